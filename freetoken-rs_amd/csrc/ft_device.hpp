@@ -1,0 +1,193 @@
+// ft_device.hpp -- device-side building blocks shared by every kernel of the
+// library: the q8 block format, the per-block integer dot, q8 quantisation,
+// the q4_0 block quantiser, the portable exp/tanh, and the seeded generator.
+//
+// The translation units that include this file are compiled with
+// -ffp-contract=off, so a*b+c stays two roundings unless fmaf()/fma() is
+// written out. That keeps every f32 expression the same as the Rust source it
+// restates (Rust never contracts).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ft {
+
+constexpr int QK = 32;
+constexpr int Q8_BLK = 40;  // {f32 d; i32 qsum; i8 qs[32]}
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    _Float16 v;
+    __builtin_memcpy(&v, &h, 2);
+    return (float)v;
+}
+
+__device__ __forceinline__ uint16_t f2h(float f) {
+    _Float16 v = (_Float16)f;  // v_cvt_f16_f32: round to nearest even
+    uint16_t h;
+    __builtin_memcpy(&h, &v, 2);
+    return h;
+}
+
+// sum_i q4u_i * q8_i over one 32-weight block. w holds the 16 packed bytes
+// (byte i = q_i | q_{i+16} << 4, ft-core/src/q4_0.rs:2-3); a points at the 8
+// dwords of the block's q8 values. v_dot4_i32_i8 treats both operands as
+// signed bytes; nibbles 0..15 are non-negative, so the products are exact.
+__device__ __forceinline__ int dot_q4u_q8(const uint4 w, const int* a) {
+    int s = 0;
+    s = __builtin_amdgcn_sdot4((int)(w.x & 0x0F0F0F0Fu), a[0], s, false);
+    s = __builtin_amdgcn_sdot4((int)(w.y & 0x0F0F0F0Fu), a[1], s, false);
+    s = __builtin_amdgcn_sdot4((int)(w.z & 0x0F0F0F0Fu), a[2], s, false);
+    s = __builtin_amdgcn_sdot4((int)(w.w & 0x0F0F0F0Fu), a[3], s, false);
+    s = __builtin_amdgcn_sdot4((int)((w.x >> 4) & 0x0F0F0F0Fu), a[4], s, false);
+    s = __builtin_amdgcn_sdot4((int)((w.y >> 4) & 0x0F0F0F0Fu), a[5], s, false);
+    s = __builtin_amdgcn_sdot4((int)((w.z >> 4) & 0x0F0F0F0Fu), a[6], s, false);
+    s = __builtin_amdgcn_sdot4((int)((w.w >> 4) & 0x0F0F0F0Fu), a[7], s, false);
+    return s;
+}
+
+// The exact per-block dot sum_i (q4_i - 8) * q8_i, with the -8 offset folded
+// out through the block's integer q8 sum (|result| <= 32*15*127, exact).
+__device__ __forceinline__ int block_dot(const uint4 w, const int* a, int qsum) {
+    return dot_q4u_q8(w, a) - 8 * qsum;
+}
+
+// ---------------------------------------------------------------------------
+// q8 quantisation of one 32-value block held one value per lane in a 32-lane
+// half of a wavefront (ft-core/src/q4_0.rs:62-78): d = amax/127 (IEEE
+// division), inv = 1/d, q = clamp(round_half_away(v*inv), -127, 127).
+// ---------------------------------------------------------------------------
+struct Q8Lane {
+    float d;
+    int q;
+    int qsum;
+};
+
+__device__ __forceinline__ Q8Lane q8_quantize_half(float v) {
+    float a = fabsf(v);
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 32));
+    float d = a > 0.0f ? a / 127.0f : 0.0f;
+    float inv = d > 0.0f ? 1.0f / d : 0.0f;
+    float r = roundf(v * inv);
+    r = fminf(127.0f, fmaxf(-127.0f, r));
+    int q = (int)r;
+    int s = q;
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) s += __shfl_xor(s, off, 32);
+    return Q8Lane{d, q, s};
+}
+
+// Store a half-wave's block: lane 0 writes the header, every lane its byte.
+__device__ __forceinline__ void q8_store_half(uint8_t* blk, int l, const Q8Lane& r) {
+    if (l == 0) {
+        reinterpret_cast<float*>(blk)[0] = r.d;
+        reinterpret_cast<int*>(blk)[1] = r.qsum;
+    }
+    blk[8 + l] = (uint8_t)(int8_t)r.q;
+}
+
+// ---------------------------------------------------------------------------
+// Portable exp / tanh: only IEEE basic operations (fma, floor, ldexp, +, -, /)
+// in a fixed order, so the host oracle computes the same bits. Cody-Waite
+// reduction x = n*ln2 + r with a two-part ln2, degree-13 Taylor polynomial of
+// e^r by Horner with fma (Cody & Waite, Software Manual for the Elementary
+// Functions, 1980).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ double exp_portable(double x) {
+    if (x > 700.0) return __builtin_huge_val();
+    if (x < -740.0) return 0.0;
+    const double LN2_HI = 6.93147180369123816490e-01;
+    const double LN2_LO = 1.90821492927058770002e-10;
+    const double INV_LN2 = 1.44269504088896338700e+00;
+    double n = floor(fma(x, INV_LN2, 0.5));
+    double r = fma(-n, LN2_HI, x);
+    r = fma(-n, LN2_LO, r);
+    double p = 1.6059043836821614599e-10;
+    p = fma(p, r, 2.0876756987868098979e-09);
+    p = fma(p, r, 2.5052108385441718775e-08);
+    p = fma(p, r, 2.7557319223985890653e-07);
+    p = fma(p, r, 2.7557319223985890653e-06);
+    p = fma(p, r, 2.4801587301587301566e-05);
+    p = fma(p, r, 1.9841269841269841253e-04);
+    p = fma(p, r, 1.3888888888888888889e-03);
+    p = fma(p, r, 8.3333333333333332177e-03);
+    p = fma(p, r, 4.1666666666666664354e-02);
+    p = fma(p, r, 1.6666666666666665741e-01);
+    p = fma(p, r, 5.0000000000000000000e-01);
+    p = fma(p, r, 1.0);
+    p = fma(p, r, 1.0);
+    return ldexp(p, (int)n);
+}
+
+__device__ __forceinline__ float tanh_portable(float z) {
+    double a = fabs((double)z);
+    double t;
+    if (a >= 9.5) t = 1.0;
+    else if (a < 0x1p-13) t = a;
+    else {
+        double e = exp_portable(2.0 * a);
+        t = 1.0 - 2.0 / (e + 1.0);
+    }
+    float tf = (float)t;
+    return signbit(z) ? -tf : tf;
+}
+
+__device__ __forceinline__ float expf_portable(float x) { return (float)exp_portable((double)x); }
+
+// gelu_tanh (ft-model/src/lib.rs:435-437), left to right, no contraction.
+__device__ __forceinline__ float gelu_tanh(float g) {
+    float c = 0.044715f * g;
+    c = c * g;
+    c = c * g;
+    float inner = g + c;
+    float t = tanh_portable(0.7978845608f * inner);
+    float h = 0.5f * g;
+    return h * (1.0f + t);
+}
+
+// ---------------------------------------------------------------------------
+// Seeded generator (same definition as the host oracle): value i of a tensor
+// is the centred sum of the four 16-bit fields of splitmix64's output, times
+// `scale`.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ float gen_value(uint64_t key, uint64_t i, float scale) {
+    uint64_t h = mix64(key + (i + 1) * 0x9E3779B97F4A7C15ULL);
+    int s = (int)(h & 0xFFFF) + (int)((h >> 16) & 0xFFFF) + (int)((h >> 32) & 0xFFFF) + (int)(h >> 48);
+    return (float)(s - 131070) * scale;
+}
+
+// ggml q4_0 block quantiser (ft-core/src/q4_0.rs:20-40) of 32 values:
+// writes the f16 scale bits and the 16 packed bytes (as 4 dwords).
+__device__ __forceinline__ void quantize_block_q4_0(const float* xb, uint16_t& dh, uint4& qs) {
+    float amax = 0.0f, maxv = 0.0f;
+    for (int i = 0; i < QK; ++i) {
+        float a = fabsf(xb[i]);
+        if (a > amax) {
+            amax = a;
+            maxv = xb[i];
+        }
+    }
+    float d = maxv / -8.0f;
+    float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+    dh = f2h(d);
+    uint32_t w[4] = {0, 0, 0, 0};
+    for (int i = 0; i < QK / 2; ++i) {
+        float t0 = xb[i] * id;
+        float t1 = xb[i + QK / 2] * id;
+        int q0 = (int)(t0 + 8.5f);
+        int q1 = (int)(t1 + 8.5f);
+        q0 = min(15, max(0, q0));
+        q1 = min(15, max(0, q1));
+        w[i >> 2] |= (uint32_t)(q0 | (q1 << 4)) << (8 * (i & 3));
+    }
+    qs = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+}  // namespace ft

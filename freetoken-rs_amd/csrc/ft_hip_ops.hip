@@ -1,0 +1,650 @@
+// ft_hip_ops.hip -- the launch-by-launch kernels of the MoE expert-FFN decode
+// section and their C ABI (include/ft_hip.h). Each kernel replaces one
+// kernel of ft-cuda/src/q4.cu; the fused whole-stack path lives in
+// ft_hip_fused.hip and reuses the device routines of ft_device.hpp.
+
+#include "ft_device.hpp"
+#include "ft_runtime.hpp"
+
+#include <algorithm>
+
+using namespace ft;
+
+// ---------------------------------------------------------------------------
+// Weight addressing shared by the grouped GEMV and the block-dot dump.
+// ---------------------------------------------------------------------------
+struct GemvArgs {
+    const uint64_t* bases;     // per-entry base pointers, or NULL
+    const uint8_t* base;       // slot form: base + slots[e] * expert_bytes
+    uint64_t expert_bytes;
+    const int32_t* slots;
+    uint64_t bank_off;
+    const int32_t* x_idx;      // per-entry q8 row, or NULL (row = e / x_div)
+    int x_div;
+    const uint8_t* q8;
+    int64_t q8_stride_blocks;
+    float* y;                  // GEMV output
+    int32_t* dots;             // block-dot dump output
+    int64_t y_stride;
+    int n_rows;
+    int k;
+};
+
+__device__ __forceinline__ const uint8_t* entry_base(const GemvArgs& a, int e) {
+    const uint8_t* p = a.bases ? reinterpret_cast<const uint8_t*>(a.bases[e])
+                               : a.base + (uint64_t)a.slots[e] * a.expert_bytes;
+    return p + a.bank_off;
+}
+
+__device__ __forceinline__ int entry_xrow(const GemvArgs& a, int e) {
+    return a.x_idx ? a.x_idx[e] : e / a.x_div;
+}
+
+// Fetch block b of a row: its f32 scale and its 16 packed bytes.
+template <int LAYOUT>
+__device__ __forceinline__ void load_block(const uint8_t* wr, int b, int qs_off, float& d4, uint4& q) {
+    if constexpr (LAYOUT == FT_LAYOUT_Q4R) {
+        d4 = h2f(reinterpret_cast<const uint16_t*>(wr)[b]);
+        q = *reinterpret_cast<const uint4*>(wr + qs_off + 16 * b);
+    } else {
+        // 18-byte blocks are only 2-byte aligned: nine u16 loads.
+        const uint16_t* p = reinterpret_cast<const uint16_t*>(wr + 18 * b);
+        d4 = h2f(p[0]);
+        q.x = (uint32_t)p[1] | ((uint32_t)p[2] << 16);
+        q.y = (uint32_t)p[3] | ((uint32_t)p[4] << 16);
+        q.z = (uint32_t)p[5] | ((uint32_t)p[6] << 16);
+        q.w = (uint32_t)p[7] | ((uint32_t)p[8] << 16);
+    }
+}
+
+__host__ __device__ __forceinline__ int64_t row_bytes_of(int layout, int k) {
+    int nb = k / 32;
+    if (layout == FT_LAYOUT_Q4R) return (int64_t)((nb * 2 + 15) / 16 * 16) + (int64_t)nb * 16;
+    return (int64_t)nb * 18;
+}
+
+// Stage an entry's q8 activation row (nb blocks of 40 B) into LDS.
+__device__ __forceinline__ void stage_q8(const GemvArgs& a, int e, int* lds) {
+    const int nb = a.k >> 5;
+    const int* src = reinterpret_cast<const int*>(a.q8 + (int64_t)entry_xrow(a, e) * a.q8_stride_blocks * Q8_BLK);
+    for (int i = threadIdx.x; i < nb * 10; i += blockDim.x) lds[i] = src[i];
+    __syncthreads();
+}
+
+// Grouped GEMV (replaces gemv_q4r_grouped_ptr/_idx, q4.cu:1497-1567, and the
+// v3 q4_0 variants, q4.cu:360-491, :1189-1241). A 256-thread workgroup owns 32
+// rows of one entry: 8 lanes per row, lane s takes blocks s, s+8, ...; the
+// activation sits in LDS. Grid: (ceil(n_rows/32), n_entries).
+template <int LAYOUT>
+__global__ __launch_bounds__(256) void k_gemv_q4_grouped(GemvArgs a) {
+    extern __shared__ int lds[];
+    const int e = blockIdx.y;
+    stage_q8(a, e, lds);
+    const int nb = a.k >> 5;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row = (blockIdx.x * 4 + wave) * 8 + (lane >> 3);
+    const int sub = lane & 7;
+    const int qs_off = (nb * 2 + 15) / 16 * 16;
+    float acc = 0.0f;
+    if (row < a.n_rows) {
+        const uint8_t* wr = entry_base(a, e) + (int64_t)row * row_bytes_of(LAYOUT, a.k);
+        for (int b = sub; b < nb; b += 8) {
+            float d4;
+            uint4 q;
+            load_block<LAYOUT>(wr, b, qs_off, d4, q);
+            const int* xb = lds + b * 10;
+            const float d8 = __int_as_float(xb[0]);
+            const int diff = block_dot(q, xb + 2, xb[1]);
+            acc = fmaf((float)diff, d4 * d8, acc);
+        }
+    }
+    acc += __shfl_xor(acc, 1);
+    acc += __shfl_xor(acc, 2);
+    acc += __shfl_xor(acc, 4);
+    if (row < a.n_rows && sub == 0) a.y[(int64_t)e * a.y_stride + row] = acc;
+}
+
+// Block-dot dump: the same addressing and block_dot() as k_gemv_q4_grouped.
+template <int LAYOUT>
+__global__ __launch_bounds__(256) void k_block_dots(GemvArgs a) {
+    extern __shared__ int lds[];
+    const int e = blockIdx.y;
+    stage_q8(a, e, lds);
+    const int nb = a.k >> 5;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row = (blockIdx.x * 4 + wave) * 8 + (lane >> 3);
+    const int sub = lane & 7;
+    const int qs_off = (nb * 2 + 15) / 16 * 16;
+    if (row >= a.n_rows) return;
+    const uint8_t* wr = entry_base(a, e) + (int64_t)row * row_bytes_of(LAYOUT, a.k);
+    int32_t* out = a.dots + ((int64_t)e * a.n_rows + row) * nb;
+    for (int b = sub; b < nb; b += 8) {
+        float d4;
+        uint4 q;
+        load_block<LAYOUT>(wr, b, qs_off, d4, q);
+        const int* xb = lds + b * 10;
+        out[b] = block_dot(q, xb + 2, xb[1]);
+    }
+}
+
+// q8 quantisation (replaces quantize_q8_grouped, q4.cu:324-355, with the
+// round-half-away rule of ft-core/src/q4_0.rs:73). 32 lanes per block.
+__global__ __launch_bounds__(256) void k_quantize_q8(const float* x, int64_t x_stride, uint8_t* q8,
+                                                     int nb, int64_t n) {
+    const int64_t g = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+    const int l = threadIdx.x & 31;
+    const bool ok = g < n * nb;
+    const int64_t gg = ok ? g : 0;
+    const int64_t e = gg / nb, b = gg % nb;
+    const float v = x[e * x_stride + b * 32 + l];
+    const Q8Lane r = q8_quantize_half(v);
+    if (ok) q8_store_half(q8 + (e * nb + b) * Q8_BLK, l, r);
+}
+
+// Fused gelu_tanh(gate)*up -> q8 (replaces gelu_mul_q8, q4.cu:255-287).
+__global__ __launch_bounds__(256) void k_gelu_mul_q8(const float* gu, uint8_t* q8, int inter, int64_t n) {
+    const int nb = inter >> 5;
+    const int64_t g = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+    const int l = threadIdx.x & 31;
+    const bool ok = g < n * nb;
+    const int64_t gg = ok ? g : 0;
+    const int64_t e = gg / nb, b = gg % nb;
+    const int j = (int)b * 32 + l;
+    const float gate = gu[e * 2 * inter + j];
+    const float up = gu[e * 2 * inter + inter + j];
+    const float v = gelu_tanh(gate) * up;
+    const Q8Lane r = q8_quantize_half(v);
+    if (ok) q8_store_half(q8 + (e * nb + b) * Q8_BLK, l, r);
+}
+
+// Router logits in the R-order (replaces gemv_f32_rows, q4.cu:1153-1174):
+// lane c computes chunk partials P_c (16-element fma chains), lanes 0..7 sum
+// their group's chunks in order, lane 0 sums the 8 groups in order.
+// Grid (n_rows, n_seqs), one wavefront per logit.
+__global__ __launch_bounds__(64) void k_router_logits(const float* W, const float* x, const float* bias,
+                                                      float* y, int dim, int n_rows) {
+    extern __shared__ float P[];  // dim/16 chunk partials
+    __shared__ float G[8];
+    const int e = blockIdx.x, s = blockIdx.y, l = threadIdx.x;
+    const float* w = W + (int64_t)e * dim;
+    const float* xs = x + (int64_t)s * dim;
+    const int nch = dim >> 4;
+    for (int c = l; c < nch; c += 64) {
+        const float4* w4 = reinterpret_cast<const float4*>(w + 16 * c);
+        const float4* x4 = reinterpret_cast<const float4*>(xs + 16 * c);
+        float p = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 a = w4[q], b = x4[q];
+            p = fmaf(a.x, b.x, p);
+            p = fmaf(a.y, b.y, p);
+            p = fmaf(a.z, b.z, p);
+            p = fmaf(a.w, b.w, p);
+        }
+        P[c] = p;
+    }
+    __syncthreads();
+    const int C = dim >> 7;
+    if (l < 8) {
+        float gs = 0.0f;
+        for (int c = l * C; c < (l + 1) * C; ++c) gs = gs + P[c];
+        G[l] = gs;
+    }
+    __syncthreads();
+    if (l == 0) {
+        float t = 0.0f;
+        for (int g = 0; g < 8; ++g) t = t + G[g];
+        if (bias) t = t + bias[e];
+        y[(int64_t)s * n_rows + e] = t;
+    }
+}
+
+// (value, index) order of the router: larger logit first, then lower index.
+__device__ __forceinline__ bool topk_better(float v1, int i1, float v2, int i2, int E) {
+    if (i2 >= E) return i1 < E;
+    if (i1 >= E) return false;
+    if (v1 > v2) return true;
+    if (v1 < v2) return false;
+    return i1 < i2;
+}
+
+// Top-k + softmax over the chosen (replaces topk_router, q4.cu:1297-1349;
+// order and weights of ft-model/src/lib.rs:1487-1504). One workgroup per seq.
+__global__ __launch_bounds__(256) void k_topk_router(const float* logits, const float* escale, int32_t* ids,
+                                                     float* wts, int E, int k) {
+    __shared__ float sv[1024];
+    __shared__ uint8_t taken[1024];
+    __shared__ float rv[256];
+    __shared__ int ri[256];
+    __shared__ float selv[32];
+    __shared__ int seli[32];
+    const int s = blockIdx.x, t = threadIdx.x;
+    for (int i = t; i < E; i += 256) {
+        sv[i] = logits[(int64_t)s * E + i];
+        taken[i] = 0;
+    }
+    __syncthreads();
+    for (int j = 0; j < k; ++j) {
+        float bv = 0.0f;
+        int bi = E;
+        for (int i = t; i < E; i += 256)
+            if (!taken[i] && topk_better(sv[i], i, bv, bi, E)) {
+                bv = sv[i];
+                bi = i;
+            }
+        rv[t] = bv;
+        ri[t] = bi;
+        __syncthreads();
+        for (int h = 128; h > 0; h >>= 1) {
+            if (t < h && topk_better(rv[t + h], ri[t + h], rv[t], ri[t], E)) {
+                rv[t] = rv[t + h];
+                ri[t] = ri[t + h];
+            }
+            __syncthreads();
+        }
+        if (t == 0) {
+            selv[j] = rv[0];
+            seli[j] = ri[0];
+            taken[ri[0]] = 1;
+        }
+        __syncthreads();
+    }
+    if (t == 0) {
+        const float mx = selv[0];
+        float ex[32];
+        float denom = 0.0f;
+        for (int j = 0; j < k; ++j) {
+            ex[j] = expf_portable(selv[j] - mx);
+            denom = denom + ex[j];
+        }
+        for (int j = 0; j < k; ++j) {
+            float w = ex[j] / denom;
+            if (escale) w = w * escale[seli[j]];
+            ids[(int64_t)s * k + j] = seli[j];
+            wts[(int64_t)s * k + j] = w;
+        }
+    }
+}
+
+// out[s][i] += sum_{p: seq_of[p]==s} wts[p]*y[p][i] (replaces
+// reduce_pairs_weighted, q4.cu:419-434; CPU order of ft-model/src/lib.rs:1641-1646).
+__global__ __launch_bounds__(256) void k_reduce_pairs(const float* y, const float* wts, const int32_t* seq_of,
+                                                      float* out, int hidden, int n_pairs) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int s = blockIdx.y;
+    if (i >= hidden) return;
+    float acc = 0.0f;
+    for (int p = 0; p < n_pairs; ++p)
+        if (seq_of[p] == s) {
+            const float part = y[(int64_t)p * hidden + i] * wts[p];
+            acc = acc + part;
+        }
+    out[(int64_t)s * hidden + i] = out[(int64_t)s * hidden + i] + acc;
+}
+
+// Residual combine over contiguous per-seq pairs [s*k, s*k+k):
+// out[s][i] = x[s][i] + ((0 + w0*y0) + w1*y1 + ...). out may alias x.
+__global__ __launch_bounds__(256) void k_combine_residual(const float* y, const float* wts, const float* x,
+                                                          float* out, int hidden, int k) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int s = blockIdx.y;
+    if (i >= hidden) return;
+    float acc = 0.0f;
+    for (int p = s * k; p < s * k + k; ++p) {
+        const float part = y[(int64_t)p * hidden + i] * wts[p];
+        acc = acc + part;
+    }
+    out[(int64_t)s * hidden + i] = x[(int64_t)s * hidden + i] + acc;
+}
+
+// Row layout conversion, one thread per (row, block).
+__global__ __launch_bounds__(256) void k_repack(const uint8_t* src, int sl, uint8_t* dst, int dl, int64_t n_rows,
+                                                int k) {
+    const int nb = k >> 5;
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n_rows * nb) return;
+    const int64_t r = g / nb;
+    const int b = (int)(g % nb);
+    const int qs_off = (nb * 2 + 15) / 16 * 16;
+    const uint8_t* s = src + r * row_bytes_of(sl, k);
+    uint8_t* d = dst + r * row_bytes_of(dl, k);
+    const uint8_t* sq = sl == FT_LAYOUT_Q4R ? s + qs_off + 16 * b : s + 18 * b + 2;
+    const uint8_t* ss = sl == FT_LAYOUT_Q4R ? s + 2 * b : s + 18 * b;
+    uint8_t* dq = dl == FT_LAYOUT_Q4R ? d + qs_off + 16 * b : d + 18 * b + 2;
+    uint8_t* ds = dl == FT_LAYOUT_Q4R ? d + 2 * b : d + 18 * b;
+    ds[0] = ss[0];
+    ds[1] = ss[1];
+    for (int i = 0; i < 16; ++i) dq[i] = sq[i];
+    if (dl == FT_LAYOUT_Q4R && b == nb - 1)  // zero the scale padding
+        for (int i = 2 * nb; i < qs_off; ++i) d[i] = 0;
+}
+
+__global__ __launch_bounds__(256) void k_gen_values(uint64_t key, int64_t start, int64_t n, float scale, float* out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = gen_value(key, (uint64_t)(start + i), scale);
+}
+
+// Seeded q4_0 rows, one thread per (row, block), written in `layout`.
+__global__ __launch_bounds__(256) void k_gen_q4_rows(uint64_t key, int64_t row0, int64_t n_rows, int k, float scale,
+                                                     uint8_t* out, int layout) {
+    const int nb = k >> 5;
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n_rows * nb) return;
+    const int64_t r = g / nb;
+    const int b = (int)(g % nb);
+    float v[QK];
+    const uint64_t base = (uint64_t)(row0 + r) * (uint64_t)k + (uint64_t)b * QK;
+    for (int i = 0; i < QK; ++i) v[i] = gen_value(key, base + i, scale);
+    uint16_t dh;
+    uint4 qs;
+    quantize_block_q4_0(v, dh, qs);
+    uint8_t* row = out + r * row_bytes_of(layout, k);
+    if (layout == FT_LAYOUT_Q4R) {
+        const int qs_off = (nb * 2 + 15) / 16 * 16;
+        reinterpret_cast<uint16_t*>(row)[b] = dh;
+        *reinterpret_cast<uint4*>(row + qs_off + 16 * b) = qs;
+        if (b == nb - 1)
+            for (int i = 2 * nb; i < qs_off; ++i) row[i] = 0;
+    } else {
+        uint16_t* p = reinterpret_cast<uint16_t*>(row + 18 * b);
+        p[0] = dh;
+        const uint32_t w[4] = {qs.x, qs.y, qs.z, qs.w};
+        for (int i = 0; i < 4; ++i) {
+            p[1 + 2 * i] = (uint16_t)(w[i] & 0xFFFF);
+            p[2 + 2 * i] = (uint16_t)(w[i] >> 16);
+        }
+    }
+}
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+static inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+static int check_layout(int layout) {
+    if (layout != FT_LAYOUT_Q4_0 && layout != FT_LAYOUT_Q4R)
+        return fail(FT_HIP_E_INVALID, "unknown layout %d", layout);
+    return FT_HIP_OK;
+}
+
+extern "C" int64_t ft_hip_row_bytes(int layout, int64_t k) {
+    if (k <= 0 || k % 32) return -1;
+    if (layout != FT_LAYOUT_Q4_0 && layout != FT_LAYOUT_Q4R) return -1;
+    return row_bytes_of(layout, (int)k);
+}
+
+extern "C" int64_t ft_hip_q4r_scales_bytes(int64_t k) {
+    if (k <= 0 || k % 32) return -1;
+    return (k / 32 * 2 + 15) / 16 * 16;
+}
+
+extern "C" int ft_hip_quantize_q8(ft_hip_ctx* ctx, void* stream, const float* x, int64_t x_stride, void* q8,
+                                  int64_t k, int64_t n) {
+    clear_error();
+    if (k <= 0 || k % 32) return fail(FT_HIP_E_SHAPE, "quantize_q8: k=%lld must be a positive multiple of 32", (long long)k);
+    if (n < 0 || x_stride < 0) return fail(FT_HIP_E_SHAPE, "quantize_q8: negative n or x_stride");
+    if (x_stride != 0 && x_stride < k) return fail(FT_HIP_E_SHAPE, "quantize_q8: x_stride < k");
+    if (!ctx || !x || !q8) return fail(FT_HIP_E_INVALID, "quantize_q8: null argument");
+    if (n == 0) return FT_HIP_OK;
+    const int nb = (int)(k / 32);
+    const int64_t threads = n * nb * 32;
+    hipLaunchKernelGGL(k_quantize_q8, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, S(stream), x, x_stride,
+                       (uint8_t*)q8, nb, n);
+    return launch_status("quantize_q8");
+}
+
+static int gemv_common(ft_hip_ctx* ctx, void* stream, GemvArgs& a, int64_t n_entries, int64_t n_rows, int64_t k,
+                       int layout, bool dots, const char* name) {
+    if (k <= 0 || k % 32) return fail(FT_HIP_E_SHAPE, "%s: k=%lld must be a positive multiple of 32", name, (long long)k);
+    if (k > 32 * 4096) return fail(FT_HIP_E_SHAPE, "%s: k=%lld exceeds 131072", name, (long long)k);
+    if (n_rows < 0 || n_entries < 0) return fail(FT_HIP_E_SHAPE, "%s: negative n_rows or n_entries", name);
+    if (n_rows > (1 << 30) || n_entries > 65535) return fail(FT_HIP_E_SHAPE, "%s: n_rows or n_entries too large", name);
+    if (!dots && a.y_stride < n_rows && n_entries > 1)
+        return fail(FT_HIP_E_SHAPE, "%s: y_stride=%lld < n_rows=%lld", name, (long long)a.y_stride, (long long)n_rows);
+    if (a.q8_stride_blocks < 0) return fail(FT_HIP_E_SHAPE, "%s: negative q8_stride_blocks", name);
+    if (int rc = check_layout(layout)) return rc;
+    if (layout == FT_LAYOUT_Q4R && !a.bases &&
+        ((reinterpret_cast<uintptr_t>(a.base) | a.expert_bytes | a.bank_off) & 15))
+        return fail(FT_HIP_E_SHAPE, "%s: q4r banks need 16-byte aligned base, expert_bytes and bank_off", name);
+    if (!ctx || !a.q8 || (!dots && !a.y) || (dots && !a.dots)) return fail(FT_HIP_E_INVALID, "%s: null argument", name);
+    if (!a.bases && (!a.base || !a.slots)) return fail(FT_HIP_E_INVALID, "%s: null weight addressing", name);
+    if (n_entries == 0 || n_rows == 0) return FT_HIP_OK;
+    a.n_rows = (int)n_rows;
+    a.k = (int)k;
+    const size_t lds = (size_t)(k / 32) * Q8_BLK;
+    dim3 grid((unsigned)((n_rows + 31) / 32), (unsigned)n_entries);
+    if (dots) {
+        if (layout == FT_LAYOUT_Q4R) hipLaunchKernelGGL(k_block_dots<FT_LAYOUT_Q4R>, grid, dim3(256), lds, S(stream), a);
+        else hipLaunchKernelGGL(k_block_dots<FT_LAYOUT_Q4_0>, grid, dim3(256), lds, S(stream), a);
+    } else {
+        if (layout == FT_LAYOUT_Q4R) hipLaunchKernelGGL(k_gemv_q4_grouped<FT_LAYOUT_Q4R>, grid, dim3(256), lds, S(stream), a);
+        else hipLaunchKernelGGL(k_gemv_q4_grouped<FT_LAYOUT_Q4_0>, grid, dim3(256), lds, S(stream), a);
+    }
+    return launch_status(name);
+}
+
+extern "C" int ft_hip_gemv_q4_grouped_ptr(ft_hip_ctx* ctx, void* stream, const uint64_t* bases, uint64_t bank_off,
+                                          const int32_t* x_idx, int64_t n_entries, const void* q8,
+                                          int64_t q8_stride_blocks, float* y, int64_t y_stride, int64_t n_rows,
+                                          int64_t k, int layout) {
+    clear_error();
+    if (!bases) return fail(FT_HIP_E_INVALID, "gemv_q4_grouped_ptr: null bases");
+    GemvArgs a{};
+    a.bases = bases;
+    a.bank_off = bank_off;
+    a.x_idx = x_idx;
+    a.x_div = 1;
+    a.q8 = (const uint8_t*)q8;
+    a.q8_stride_blocks = q8_stride_blocks;
+    a.y = y;
+    a.y_stride = y_stride;
+    return gemv_common(ctx, stream, a, n_entries, n_rows, k, layout, false, "gemv_q4_grouped_ptr");
+}
+
+extern "C" int ft_hip_gemv_q4_grouped_slots(ft_hip_ctx* ctx, void* stream, const void* base, uint64_t expert_bytes,
+                                            uint64_t bank_off, const int32_t* slots, const int32_t* x_idx,
+                                            int64_t n_entries, const void* q8, int64_t q8_stride_blocks, float* y,
+                                            int64_t y_stride, int64_t n_rows, int64_t k, int layout) {
+    clear_error();
+    GemvArgs a{};
+    a.base = (const uint8_t*)base;
+    a.expert_bytes = expert_bytes;
+    a.slots = slots;
+    a.bank_off = bank_off;
+    a.x_idx = x_idx;
+    a.x_div = 1;
+    a.q8 = (const uint8_t*)q8;
+    a.q8_stride_blocks = q8_stride_blocks;
+    a.y = y;
+    a.y_stride = y_stride;
+    return gemv_common(ctx, stream, a, n_entries, n_rows, k, layout, false, "gemv_q4_grouped_slots");
+}
+
+extern "C" int ft_hip_q4q8_block_dots(ft_hip_ctx* ctx, void* stream, const void* base, uint64_t expert_bytes,
+                                      uint64_t bank_off, const int32_t* slots, const int32_t* x_idx, int64_t n_entries,
+                                      const void* q8, int64_t q8_stride_blocks, int32_t* out, int64_t n_rows,
+                                      int64_t k, int layout) {
+    clear_error();
+    GemvArgs a{};
+    a.base = (const uint8_t*)base;
+    a.expert_bytes = expert_bytes;
+    a.slots = slots;
+    a.bank_off = bank_off;
+    a.x_idx = x_idx;
+    a.x_div = 1;
+    a.q8 = (const uint8_t*)q8;
+    a.q8_stride_blocks = q8_stride_blocks;
+    a.dots = out;
+    return gemv_common(ctx, stream, a, n_entries, n_rows, k, layout, true, "q4q8_block_dots");
+}
+
+extern "C" int ft_hip_gelu_mul_q8(ft_hip_ctx* ctx, void* stream, const float* gu, void* q8, int64_t inter, int64_t n) {
+    clear_error();
+    if (inter <= 0 || inter % 32) return fail(FT_HIP_E_SHAPE, "gelu_mul_q8: inter=%lld must be a positive multiple of 32", (long long)inter);
+    if (n < 0) return fail(FT_HIP_E_SHAPE, "gelu_mul_q8: negative n");
+    if (!ctx || !gu || !q8) return fail(FT_HIP_E_INVALID, "gelu_mul_q8: null argument");
+    if (n == 0) return FT_HIP_OK;
+    const int64_t threads = n * (inter / 32) * 32;
+    hipLaunchKernelGGL(k_gelu_mul_q8, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, S(stream), gu,
+                       (uint8_t*)q8, (int)inter, n);
+    return launch_status("gelu_mul_q8");
+}
+
+extern "C" int ft_hip_router_logits(ft_hip_ctx* ctx, void* stream, const float* w, const float* x, const float* bias,
+                                    float* y, int64_t dim, int64_t n_rows, int64_t n_seqs) {
+    clear_error();
+    if (dim <= 0 || dim % 128) return fail(FT_HIP_E_SHAPE, "router_logits: dim=%lld must be a positive multiple of 128", (long long)dim);
+    if (dim > 65536) return fail(FT_HIP_E_SHAPE, "router_logits: dim=%lld exceeds 65536", (long long)dim);
+    if (n_rows < 0 || n_seqs < 0 || n_rows > 65535 || n_seqs > 65535)
+        return fail(FT_HIP_E_SHAPE, "router_logits: n_rows/n_seqs out of range");
+    if (!ctx || !w || !x || !y) return fail(FT_HIP_E_INVALID, "router_logits: null argument");
+    if (n_rows == 0 || n_seqs == 0) return FT_HIP_OK;
+    hipLaunchKernelGGL(k_router_logits, dim3((unsigned)n_rows, (unsigned)n_seqs), dim3(64), (size_t)(dim / 16) * 4,
+                       S(stream), w, x, bias, y, (int)dim, (int)n_rows);
+    return launch_status("router_logits");
+}
+
+extern "C" int ft_hip_topk_router(ft_hip_ctx* ctx, void* stream, const float* logits, const float* expert_scale,
+                                  int32_t* ids, float* wts, int64_t e_count, int64_t k, int64_t n_seqs) {
+    clear_error();
+    if (e_count <= 0 || e_count > 1024) return fail(FT_HIP_E_SHAPE, "topk_router: e_count=%lld not in [1, 1024]", (long long)e_count);
+    if (k <= 0 || k > 32 || k > e_count) return fail(FT_HIP_E_SHAPE, "topk_router: k=%lld not in [1, min(32, e_count)]", (long long)k);
+    if (n_seqs < 0 || n_seqs > 65535) return fail(FT_HIP_E_SHAPE, "topk_router: n_seqs out of range");
+    if (!ctx || !logits || !ids || !wts) return fail(FT_HIP_E_INVALID, "topk_router: null argument");
+    if (n_seqs == 0) return FT_HIP_OK;
+    hipLaunchKernelGGL(k_topk_router, dim3((unsigned)n_seqs), dim3(256), 0, S(stream), logits, expert_scale, ids, wts,
+                       (int)e_count, (int)k);
+    return launch_status("topk_router");
+}
+
+extern "C" int ft_hip_reduce_pairs_weighted(ft_hip_ctx* ctx, void* stream, const float* y, const float* wts,
+                                            const int32_t* seq_of, float* out, int64_t hidden, int64_t n_pairs,
+                                            int64_t n_seqs) {
+    clear_error();
+    if (hidden <= 0 || n_pairs < 0 || n_seqs < 0 || n_seqs > 65535 || hidden > (1 << 30))
+        return fail(FT_HIP_E_SHAPE, "reduce_pairs_weighted: bad hidden/n_pairs/n_seqs");
+    if (!ctx || !y || !wts || !seq_of || !out) return fail(FT_HIP_E_INVALID, "reduce_pairs_weighted: null argument");
+    if (n_seqs == 0) return FT_HIP_OK;
+    hipLaunchKernelGGL(k_reduce_pairs, dim3((unsigned)((hidden + 255) / 256), (unsigned)n_seqs), dim3(256), 0,
+                       S(stream), y, wts, seq_of, out, (int)hidden, (int)n_pairs);
+    return launch_status("reduce_pairs_weighted");
+}
+
+extern "C" int ft_hip_repack_rows(ft_hip_ctx* ctx, void* stream, const void* src, int src_layout, void* dst,
+                                  int dst_layout, int64_t n_rows, int64_t k) {
+    clear_error();
+    if (k <= 0 || k % 32 || n_rows < 0) return fail(FT_HIP_E_SHAPE, "repack_rows: bad k or n_rows");
+    if (int rc = check_layout(src_layout)) return rc;
+    if (int rc = check_layout(dst_layout)) return rc;
+    if (!ctx || !src || !dst) return fail(FT_HIP_E_INVALID, "repack_rows: null argument");
+    if (n_rows == 0) return FT_HIP_OK;
+    const int64_t threads = n_rows * (k / 32);
+    hipLaunchKernelGGL(k_repack, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, S(stream),
+                       (const uint8_t*)src, src_layout, (uint8_t*)dst, dst_layout, n_rows, (int)k);
+    return launch_status("repack_rows");
+}
+
+extern "C" int ft_hip_gen_values(ft_hip_ctx* ctx, void* stream, uint64_t key, int64_t start, int64_t n, float scale,
+                                 float* out) {
+    clear_error();
+    if (n < 0 || start < 0) return fail(FT_HIP_E_SHAPE, "gen_values: negative n or start");
+    if (!ctx || !out) return fail(FT_HIP_E_INVALID, "gen_values: null argument");
+    if (n == 0) return FT_HIP_OK;
+    hipLaunchKernelGGL(k_gen_values, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, S(stream), key, start, n, scale, out);
+    return launch_status("gen_values");
+}
+
+extern "C" int ft_hip_gen_q4_rows(ft_hip_ctx* ctx, void* stream, uint64_t key, int64_t row0, int64_t n_rows, int64_t k,
+                                  float scale, void* out, int layout) {
+    clear_error();
+    if (k <= 0 || k % 32 || n_rows < 0 || row0 < 0) return fail(FT_HIP_E_SHAPE, "gen_q4_rows: bad k, row0 or n_rows");
+    if (int rc = check_layout(layout)) return rc;
+    if (!ctx || !out) return fail(FT_HIP_E_INVALID, "gen_q4_rows: null argument");
+    if (n_rows == 0) return FT_HIP_OK;
+    const int64_t threads = n_rows * (k / 32);
+    hipLaunchKernelGGL(k_gen_q4_rows, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, S(stream), key, row0,
+                       n_rows, (int)k, scale, (uint8_t*)out, layout);
+    return launch_status("gen_q4_rows");
+}
+
+// ---------------------------------------------------------------------------
+// One layer through the launch-by-launch kernels.
+// ---------------------------------------------------------------------------
+struct LayerWs {
+    float* logits;
+    uint8_t* q8x;
+    float* ygu;
+    uint8_t* q8a;
+    float* ydn;
+    size_t bytes;
+};
+
+static LayerWs layer_ws(void* base, int64_t B, int64_t H, int64_t I, int64_t E, int64_t K) {
+    auto up = [](size_t v) { return (v + 255) / 256 * 256; };
+    size_t off = 0;
+    LayerWs w{};
+    uint8_t* p = (uint8_t*)base;
+    w.logits = (float*)(p + off); off += up(sizeof(float) * B * E);
+    w.q8x = p + off; off += up((size_t)B * (H / 32) * Q8_BLK);
+    w.ygu = (float*)(p + off); off += up(sizeof(float) * B * K * 2 * I);
+    w.q8a = p + off; off += up((size_t)B * K * (I / 32) * Q8_BLK);
+    w.ydn = (float*)(p + off); off += up(sizeof(float) * B * K * H);
+    w.bytes = off;
+    return w;
+}
+
+extern "C" size_t ft_hip_moe_layer_workspace_bytes(int64_t n_seqs, int64_t hidden, int64_t inter, int64_t n_experts,
+                                                   int64_t top_k) {
+    if (n_seqs < 0 || hidden <= 0 || inter <= 0 || n_experts <= 0 || top_k <= 0) return 0;
+    return layer_ws(nullptr, n_seqs, hidden, inter, n_experts, top_k).bytes;
+}
+
+extern "C" int ft_hip_moe_layer(ft_hip_ctx* ctx, void* stream, const float* x, float* x_out, int64_t n_seqs,
+                                int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k,
+                                const float* router_w, const float* router_bias, const float* expert_scale,
+                                const void* bank, uint64_t expert_bytes, int layout, int32_t* ids, float* wts,
+                                void* workspace, size_t workspace_bytes) {
+    clear_error();
+    const char* nm = "moe_layer";
+    if (hidden <= 0 || hidden % 128) return fail(FT_HIP_E_SHAPE, "%s: hidden=%lld must be a positive multiple of 128", nm, (long long)hidden);
+    if (inter <= 0 || inter % 32) return fail(FT_HIP_E_SHAPE, "%s: inter=%lld must be a positive multiple of 32", nm, (long long)inter);
+    if (n_experts <= 0 || n_experts > 1024) return fail(FT_HIP_E_SHAPE, "%s: n_experts not in [1, 1024]", nm);
+    if (top_k <= 0 || top_k > 32 || top_k > n_experts) return fail(FT_HIP_E_SHAPE, "%s: top_k not in [1, min(32, n_experts)]", nm);
+    if (n_seqs < 0 || n_seqs * top_k > 65535) return fail(FT_HIP_E_SHAPE, "%s: n_seqs out of range", nm);
+    if (int rc = check_layout(layout)) return rc;
+    const int64_t gu_bytes = 2 * inter * row_bytes_of(layout, (int)hidden);
+    const int64_t need = gu_bytes + hidden * row_bytes_of(layout, (int)inter);
+    if ((int64_t)expert_bytes < need) return fail(FT_HIP_E_SHAPE, "%s: expert_bytes=%llu < %lld", nm, (unsigned long long)expert_bytes, (long long)need);
+    const LayerWs w = layer_ws(workspace, n_seqs, hidden, inter, n_experts, top_k);
+    if (workspace_bytes < w.bytes) return fail(FT_HIP_E_SHAPE, "%s: workspace_bytes=%zu < %zu", nm, workspace_bytes, w.bytes);
+    if (!ctx || !x || !x_out || !router_w || !bank || !ids || !wts || !workspace) return fail(FT_HIP_E_INVALID, "%s: null argument", nm);
+    if (n_seqs == 0) return FT_HIP_OK;
+    int rc;
+    if ((rc = ft_hip_router_logits(ctx, stream, router_w, x, router_bias, w.logits, hidden, n_experts, n_seqs))) return rc;
+    if ((rc = ft_hip_topk_router(ctx, stream, w.logits, expert_scale, ids, wts, n_experts, top_k, n_seqs))) return rc;
+    if ((rc = ft_hip_quantize_q8(ctx, stream, x, hidden, w.q8x, hidden, n_seqs))) return rc;
+    const int64_t n_pairs = n_seqs * top_k;
+    GemvArgs a{};
+    a.base = (const uint8_t*)bank;
+    a.expert_bytes = expert_bytes;
+    a.slots = ids;
+    a.bank_off = 0;
+    a.x_idx = nullptr;
+    a.x_div = (int)top_k;  // pair p reads token p / top_k
+    a.q8 = w.q8x;
+    a.q8_stride_blocks = hidden / 32;
+    a.y = w.ygu;
+    a.y_stride = 2 * inter;
+    if ((rc = gemv_common(ctx, stream, a, n_pairs, 2 * inter, hidden, layout, false, "moe_layer/gate_up"))) return rc;
+    if ((rc = ft_hip_gelu_mul_q8(ctx, stream, w.ygu, w.q8a, inter, n_pairs))) return rc;
+    a.bank_off = (uint64_t)gu_bytes;
+    a.x_div = 1;
+    a.q8 = w.q8a;
+    a.q8_stride_blocks = inter / 32;
+    a.y = w.ydn;
+    a.y_stride = hidden;
+    if ((rc = gemv_common(ctx, stream, a, n_pairs, hidden, inter, layout, false, "moe_layer/down"))) return rc;
+    hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)((hidden + 255) / 256), (unsigned)n_seqs), dim3(256), 0,
+                       S(stream), w.ydn, wts, x, x_out, (int)hidden, (int)top_k);
+    return launch_status("moe_layer/combine");
+}

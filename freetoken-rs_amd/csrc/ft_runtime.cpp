@@ -1,0 +1,66 @@
+// ft_runtime.cpp -- context creation (the counterpart of Q4Gemv::new,
+// ft-cuda/src/lib.rs:111-150), thread-local error text, launch checks.
+#include "ft_runtime.hpp"
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+
+namespace ft {
+
+static thread_local char g_err[512] = "";
+
+void clear_error() { g_err[0] = 0; }
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int launch_status(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(FT_HIP_E_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+    return FT_HIP_OK;
+}
+
+}  // namespace ft
+
+extern "C" int ft_hip_version(void) { return 100; }
+
+extern "C" const char* ft_hip_last_error(void) { return ft::g_err; }
+
+extern "C" int ft_hip_create(int device, ft_hip_ctx** out) {
+    clear_error();
+    if (!out) return fail(FT_HIP_E_INVALID, "create: null out");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0)
+        return fail(FT_HIP_E_DEVICE, "create: no HIP device (%s)", e != hipSuccess ? hipGetErrorString(e) : "count 0");
+    if (device < 0 || device >= n) return fail(FT_HIP_E_DEVICE, "create: device %d out of range [0, %d)", device, n);
+    hipDeviceProp_t p;
+    if ((e = hipGetDeviceProperties(&p, device)) != hipSuccess)
+        return fail(FT_HIP_E_DEVICE, "create: %s", hipGetErrorString(e));
+    if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        return fail(FT_HIP_E_DEVICE, "create: device %d is %s; this library is built for gfx950 only", device,
+                    p.gcnArchName);
+    if ((e = hipSetDevice(device)) != hipSuccess) return fail(FT_HIP_E_DEVICE, "create: %s", hipGetErrorString(e));
+    ft_hip_ctx* c = new (std::nothrow) ft_hip_ctx{};
+    if (!c) return fail(FT_HIP_E_INVALID, "create: out of host memory");
+    c->device = device;
+    c->num_cus = p.multiProcessorCount;
+    c->num_xcds = 8;  // MI355X: 8 XCDs of 32 CUs
+    std::snprintf(c->arch, sizeof c->arch, "%s", p.gcnArchName);
+    *out = c;
+    return FT_HIP_OK;
+}
+
+extern "C" int ft_hip_destroy(ft_hip_ctx* ctx) {
+    clear_error();
+    delete ctx;
+    return FT_HIP_OK;
+}

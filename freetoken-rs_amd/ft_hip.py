@@ -1,0 +1,209 @@
+"""Python host binding of libfthip.so (include/ft_hip.h) over ctypes.
+
+`Q4Gemv` mirrors the reference's ft_cuda::Q4Gemv (ft-cuda/src/lib.rs:69-150):
+same method names, same argument meaning, device buffers owned by the caller
+(torch tensors on the GPU here), launches asynchronous on a stream. Where the
+reference panics on a violated shape (assert!), these methods raise
+FtHipError carrying the library's status code and message.
+
+PyTorch is used only for device memory and streams. There is no CPU fallback:
+if libfthip.so is missing or no gfx950 GPU is present, construction fails.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libfthip.so")
+
+OK, E_INVALID, E_SHAPE, E_DEVICE, E_LAUNCH, E_TIMEOUT = 0, -1, -2, -3, -4, -5
+Q8_BLK = 40
+LAYOUT_Q4_0, LAYOUT_Q4R = 0, 1
+
+_lib = None
+
+# Exported symbols and their signatures (kept in step with include/ft_hip.h).
+_P, _I, _I64, _U64, _F, _SZ = (ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint64,
+                               ctypes.c_float, ctypes.c_size_t)
+SIGNATURES = {
+    "ft_hip_version": (_I, []),
+    "ft_hip_last_error": (ctypes.c_char_p, []),
+    "ft_hip_create": (_I, [_I, ctypes.POINTER(_P)]),
+    "ft_hip_destroy": (_I, [_P]),
+    "ft_hip_row_bytes": (_I64, [_I, _I64]),
+    "ft_hip_q4r_scales_bytes": (_I64, [_I64]),
+    "ft_hip_quantize_q8": (_I, [_P, _P, _P, _I64, _P, _I64, _I64]),
+    "ft_hip_gemv_q4_grouped_ptr": (_I, [_P, _P, _P, _U64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I]),
+    "ft_hip_gemv_q4_grouped_slots": (_I, [_P, _P, _P, _U64, _U64, _P, _P, _I64, _P, _I64, _P, _I64, _I64,
+                                          _I64, _I]),
+    "ft_hip_q4q8_block_dots": (_I, [_P, _P, _P, _U64, _U64, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _I]),
+    "ft_hip_gelu_mul_q8": (_I, [_P, _P, _P, _P, _I64, _I64]),
+    "ft_hip_router_logits": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64]),
+    "ft_hip_topk_router": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64]),
+    "ft_hip_reduce_pairs_weighted": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64]),
+    "ft_hip_repack_rows": (_I, [_P, _P, _P, _I, _P, _I, _I64, _I64]),
+    "ft_hip_gen_values": (_I, [_P, _P, _U64, _I64, _I64, _F, _P]),
+    "ft_hip_gen_q4_rows": (_I, [_P, _P, _U64, _I64, _I64, _I64, _F, _P, _I]),
+    "ft_hip_moe_layer_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
+    "ft_hip_moe_layer": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _U64, _I, _P, _P,
+                              _P, _SZ]),
+}
+
+
+class FtHipError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"ft_hip error {code}: {msg}")
+        self.code = code
+
+
+def lib():
+    """Load libfthip.so; raise if it has not been built (no fallback)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FtHipError(E_DEVICE, f"{LIB_PATH} is missing: run freetoken-rs_amd/build.py")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != OK:
+        raise FtHipError(rc, lib().ft_hip_last_error().decode())
+    return rc
+
+
+def row_bytes(k, layout=LAYOUT_Q4_0):
+    return lib().ft_hip_row_bytes(layout, k)
+
+
+def q4r_scales_bytes(k):
+    return lib().ft_hip_q4r_scales_bytes(k)
+
+
+def _ptr(t):
+    """Raw device pointer of a tensor (None -> NULL)."""
+    if t is None:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+class Q4Gemv:
+    """Counterpart of ft_cuda::Q4Gemv on one gfx950 device."""
+
+    def __init__(self, device=0):
+        self._ctx = ctypes.c_void_p()
+        check(lib().ft_hip_create(device, ctypes.byref(self._ctx)))
+        self.device = device
+
+    def close(self):
+        if self._ctx:
+            lib().ft_hip_destroy(self._ctx)
+            self._ctx = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- ft-cuda/src/lib.rs:898-921 --
+    def quantize_q8(self, x, x_stride, q8, k, n, stream=None):
+        check(lib().ft_hip_quantize_q8(self._ctx, _stream(stream), _ptr(x), x_stride, _ptr(q8), k, n))
+
+    # -- ft-cuda/src/lib.rs:593-623 (q4_0) and :736-767 (q4r) --
+    def gemv_grouped_ptr(self, bases, bank_off, x_idx, n_entries, q8, q8_stride_blocks, y, y_stride,
+                         n_rows, k, layout=LAYOUT_Q4R, stream=None):
+        check(lib().ft_hip_gemv_q4_grouped_ptr(self._ctx, _stream(stream), _ptr(bases), bank_off, _ptr(x_idx),
+                                               n_entries, _ptr(q8), q8_stride_blocks, _ptr(y), y_stride, n_rows,
+                                               k, layout))
+
+    def gemv_grouped_q8_ptr(self, bases, bank_off, x_idx, n_entries, q8, q8_stride_blocks, y, y_stride,
+                            n_rows, k, stream=None):
+        self.gemv_grouped_ptr(bases, bank_off, x_idx, n_entries, q8, q8_stride_blocks, y, y_stride, n_rows, k,
+                              LAYOUT_Q4_0, stream)
+
+    def gemv_q4r_ptr(self, bases, bank_off, x_idx, n_entries, q8, q8_stride_blocks, y, y_stride, n_rows, k,
+                     stream=None):
+        self.gemv_grouped_ptr(bases, bank_off, x_idx, n_entries, q8, q8_stride_blocks, y, y_stride, n_rows, k,
+                              LAYOUT_Q4R, stream)
+
+    # -- ft-cuda/src/lib.rs:926-957, :772-804 (q4_0) and :699-732 (q4r) --
+    def gemv_grouped_slots(self, cache, expert_bytes, bank_off, slots, x_idx, n_entries, q8, q8_stride_blocks,
+                           y, y_stride, n_rows, k, layout=LAYOUT_Q4R, stream=None):
+        check(lib().ft_hip_gemv_q4_grouped_slots(self._ctx, _stream(stream), _ptr(cache), expert_bytes, bank_off,
+                                                 _ptr(slots), _ptr(x_idx), n_entries, _ptr(q8), q8_stride_blocks,
+                                                 _ptr(y), y_stride, n_rows, k, layout))
+
+    def gemv_grouped_q8(self, cache, expert_bytes, bank_off, slots, n_experts, q8, q8_stride_blocks, y,
+                        y_stride, n_rows, k, stream=None):
+        self.gemv_grouped_slots(cache, expert_bytes, bank_off, slots, None, n_experts, q8, q8_stride_blocks, y,
+                                y_stride, n_rows, k, LAYOUT_Q4_0, stream)
+
+    def gemv_grouped_q8_idx(self, cache, expert_bytes, bank_off, slots, x_idx, n_entries, q8, q8_stride_blocks,
+                            y, y_stride, n_rows, k, stream=None):
+        self.gemv_grouped_slots(cache, expert_bytes, bank_off, slots, x_idx, n_entries, q8, q8_stride_blocks, y,
+                                y_stride, n_rows, k, LAYOUT_Q4_0, stream)
+
+    def gemv_q4r_idx(self, cache, expert_bytes, bank_off, slots, x_idx, n_entries, q8, q8_stride_blocks, y,
+                     y_stride, n_rows, k, stream=None):
+        self.gemv_grouped_slots(cache, expert_bytes, bank_off, slots, x_idx, n_entries, q8, q8_stride_blocks, y,
+                                y_stride, n_rows, k, LAYOUT_Q4R, stream)
+
+    def block_dots(self, cache, expert_bytes, bank_off, slots, x_idx, n_entries, q8, q8_stride_blocks, out,
+                   n_rows, k, layout=LAYOUT_Q4R, stream=None):
+        check(lib().ft_hip_q4q8_block_dots(self._ctx, _stream(stream), _ptr(cache), expert_bytes, bank_off,
+                                           _ptr(slots), _ptr(x_idx), n_entries, _ptr(q8), q8_stride_blocks,
+                                           _ptr(out), n_rows, k, layout))
+
+    # -- ft-cuda/src/lib.rs:354-374 --
+    def gelu_mul_q8(self, gu, q8, inter, n, stream=None):
+        check(lib().ft_hip_gelu_mul_q8(self._ctx, _stream(stream), _ptr(gu), _ptr(q8), inter, n))
+
+    # -- ft-cuda/src/lib.rs:674-694 --
+    def gemv_f32_rows_dev(self, w, x, y, dim, n_rows, n_seqs, bias=None, stream=None):
+        check(lib().ft_hip_router_logits(self._ctx, _stream(stream), _ptr(w), _ptr(x), _ptr(bias), _ptr(y), dim,
+                                         n_rows, n_seqs))
+
+    # -- ft-cuda/src/lib.rs:472-494 --
+    def topk_router_dev(self, logits, expert_scale, ids, wts, e_count, k, n_seqs, stream=None):
+        check(lib().ft_hip_topk_router(self._ctx, _stream(stream), _ptr(logits), _ptr(expert_scale), _ptr(ids),
+                                       _ptr(wts), e_count, k, n_seqs))
+
+    # -- ft-cuda/src/lib.rs:808-829 --
+    def reduce_pairs_weighted(self, y, wts, seq_of, out, hidden, n_pairs, n_seqs, stream=None):
+        check(lib().ft_hip_reduce_pairs_weighted(self._ctx, _stream(stream), _ptr(y), _ptr(wts), _ptr(seq_of),
+                                                 _ptr(out), hidden, n_pairs, n_seqs))
+
+    # -- setup: ft-core/src/q4_0.rs:248-258 on the device --
+    def repack_rows(self, src, src_layout, dst, dst_layout, n_rows, k, stream=None):
+        check(lib().ft_hip_repack_rows(self._ctx, _stream(stream), _ptr(src), src_layout, _ptr(dst), dst_layout,
+                                       n_rows, k))
+
+    def gen_values(self, key, start, n, scale, out, stream=None):
+        check(lib().ft_hip_gen_values(self._ctx, _stream(stream), key, start, n, scale, _ptr(out)))
+
+    def gen_q4_rows(self, key, row0, n_rows, k, scale, out, layout=LAYOUT_Q4R, stream=None):
+        check(lib().ft_hip_gen_q4_rows(self._ctx, _stream(stream), key, row0, n_rows, k, scale, _ptr(out), layout))
+
+    # -- the whole layer (ft-model/src/lib.rs:1406-1476 composition) --
+    @staticmethod
+    def moe_layer_workspace_bytes(n_seqs, hidden, inter, n_experts, top_k):
+        return lib().ft_hip_moe_layer_workspace_bytes(n_seqs, hidden, inter, n_experts, top_k)
+
+    def moe_layer(self, x, x_out, n_seqs, hidden, inter, n_experts, top_k, router_w, router_bias, expert_scale,
+                  bank, expert_bytes, layout, ids, wts, workspace, stream=None):
+        check(lib().ft_hip_moe_layer(self._ctx, _stream(stream), _ptr(x), _ptr(x_out), n_seqs, hidden, inter,
+                                     n_experts, top_k, _ptr(router_w), _ptr(router_bias), _ptr(expert_scale),
+                                     _ptr(bank), expert_bytes, layout, _ptr(ids), _ptr(wts), _ptr(workspace),
+                                     workspace.numel() * workspace.element_size()))

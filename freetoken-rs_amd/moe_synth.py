@@ -1,0 +1,150 @@
+"""Seeded synthetic MoE expert stacks resident in HBM, and the layer chain.
+
+This is the host side of the benchmark configurations: it owns the device
+buffers (expert banks, routers, hidden states) and drives the library
+through ft_hip.Q4Gemv, like ft-bench's decode microbenchmark does through
+ft_cuda::Q4Gemv (ft-bench/src/bin/decode.rs:93-331). Unlike that bench, whose
+weights are one template block (:111-116), every expert of every layer here
+is distinct seeded N(0, sigma) data quantized to q4_0, generated on the GPU.
+
+Bank layout (the reference's q4r bank layout, ft-model/src/lib.rs:570-609):
+expert (l, e) occupies bytes [(l*E + e) * expert_bytes, +expert_bytes) of one
+device allocation: gate rows (I x H), then up rows (I x H), then down rows
+(H x I), each row in the chosen layout. All banks stay resident: with 288 GB
+of HBM there is no slot cache and no host split.
+"""
+import math
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+import ft_hip
+
+SEED = 0xF7EE2026
+T_HIDDEN, T_GU, T_DN, T_ROUTER = 1, 2, 3, 4
+MASK64 = (1 << 64) - 1
+
+
+@dataclass(frozen=True)
+class Shape:
+    name: str
+    hidden: int
+    inter: int
+    n_experts: int
+    top_k: int
+    n_layers: int
+    cfg_id: int
+
+
+# G (configs 1-4) and X (config 5).
+GEMMA = Shape("gemma4-26b-a4b-moe", 2816, 704, 128, 8, 30, 1)
+LARGE = Shape("large-expert-h4096-i14336", 4096, 14336, 8, 2, 32, 5)
+
+
+def _mix64(z):
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & MASK64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & MASK64
+    return z ^ (z >> 31)
+
+
+def tensor_key(cfg, layer, expert, tensor, seed=SEED):
+    """Key of one seeded tensor (the same chain as the device generator's callers)."""
+    h = _mix64((seed + 0x9E3779B97F4A7C15) & MASK64)
+    h = _mix64(h ^ ((cfg << 32) | tensor))
+    h = _mix64(h ^ ((layer << 32) | expert))
+    return h
+
+
+def gen_scale(sigma):
+    """sigma*sqrt(3)/65536 rounded to f32: the Irwin-Hall(4) sum then has sd sigma."""
+    return float(np.float32(sigma * math.sqrt(3.0) / 65536.0))
+
+
+def expert_geometry(shape, layout):
+    rb_h = ft_hip.row_bytes(shape.hidden, layout)
+    rb_i = ft_hip.row_bytes(shape.inter, layout)
+    gu_bytes = 2 * shape.inter * rb_h
+    dn_bytes = shape.hidden * rb_i
+    return gu_bytes, dn_bytes, gu_bytes + dn_bytes
+
+
+def algorithmic_expert_bytes(shape):
+    """q4_0 bytes of one expert (18 B per 32 weights): 3*H*I*18/32."""
+    return 3 * shape.hidden * shape.inter * 18 // 32
+
+
+class SyntheticMoE:
+    """All layers of one config, resident on the GPU."""
+
+    def __init__(self, gemv, shape, n_layers=None, layout=ft_hip.LAYOUT_Q4R, zipf_s=None, device="cuda",
+                 w_sigma=0.02, r_sigma=0.02, progress=None):
+        self.g = gemv
+        self.shape = shape
+        self.L = n_layers or shape.n_layers
+        self.layout = layout
+        self.device = device
+        H, I, E = shape.hidden, shape.inter, shape.n_experts
+        self.gu_bytes, self.dn_bytes, self.expert_bytes = expert_geometry(shape, layout)
+        self.banks = torch.empty(self.L * E * self.expert_bytes, dtype=torch.uint8, device=device)
+        self.routers = torch.empty((self.L, E, H), dtype=torch.float32, device=device)
+        ws, ss = gen_scale(w_sigma), gen_scale(r_sigma)
+        for l in range(self.L):
+            for e in range(E):
+                off = (l * E + e) * self.expert_bytes
+                gemv.gen_q4_rows(tensor_key(shape.cfg_id, l, e, T_GU), 0, 2 * I, H, ws,
+                                 self.banks[off:off + self.gu_bytes], layout)
+                gemv.gen_q4_rows(tensor_key(shape.cfg_id, l, e, T_DN), 0, H, I, ws,
+                                 self.banks[off + self.gu_bytes:off + self.expert_bytes], layout)
+            gemv.gen_values(tensor_key(shape.cfg_id, l, 0, T_ROUTER), 0, E * H, ss, self.routers[l])
+            if progress:
+                progress(l)
+        self.bias = None
+        if zipf_s is not None:
+            self.bias = torch.from_numpy(zipf_router_bias(shape, self.L, zipf_s)).to(device)
+
+    def hidden(self, token, out=None):
+        """Seeded ~N(0,1) hidden state of one decode token."""
+        H = self.shape.hidden
+        if out is None:
+            out = torch.empty(H, dtype=torch.float32, device=self.device)
+        self.g.gen_values(tensor_key(self.shape.cfg_id, 0, token, T_HIDDEN), 0, H, gen_scale(1.0), out)
+        return out
+
+    def bank_of(self, layer, expert):
+        off = (layer * self.shape.n_experts + expert) * self.expert_bytes
+        return self.banks[off:off + self.expert_bytes]
+
+    def layer_bias(self, layer):
+        return None if self.bias is None else self.bias[layer]
+
+    def workspace(self, n_seqs):
+        s = self.shape
+        nbytes = ft_hip.Q4Gemv.moe_layer_workspace_bytes(n_seqs, s.hidden, s.inter, s.n_experts, s.top_k)
+        return torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+
+    def layer(self, l, x, x_out, ids, wts, ws, n_seqs=1, stream=None):
+        """One layer through the launch-by-launch kernels: x_out = x + MoE_l(x)."""
+        s = self.shape
+        E = s.n_experts
+        bank = self.banks[l * E * self.expert_bytes:(l + 1) * E * self.expert_bytes]
+        self.g.moe_layer(x, x_out, n_seqs, s.hidden, s.inter, E, s.top_k, self.routers[l], self.layer_bias(l),
+                         None, bank, self.expert_bytes, self.layout, ids, wts, ws, stream)
+
+
+def zipf_router_bias(shape, n_layers, s=1.1, tau=None, seed=SEED):
+    """Per-layer router bias for the skewed-routing config: expert at popularity
+    rank r (a seeded permutation per layer) gets tau * ln(r^-s), so the router
+    favours experts in Zipf(s) order. tau is in units of the logit spread
+    (router sd 0.02 * sqrt(H) for ~N(0,1) hidden states)."""
+    E, H = shape.n_experts, shape.hidden
+    if tau is None:
+        tau = 0.02 * math.sqrt(H)
+    out = np.zeros((n_layers, E), np.float32)
+    for l in range(n_layers):
+        rng = np.random.default_rng([seed, shape.cfg_id, l, 7])
+        perm = rng.permutation(E)
+        ranks = np.empty(E, np.int64)
+        ranks[perm] = np.arange(1, E + 1)
+        out[l] = (tau * (-s) * np.log(ranks)).astype(np.float32)
+    return out

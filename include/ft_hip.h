@@ -1,0 +1,182 @@
+/* ft_hip.h -- C ABI of the MI355X (gfx950) MoE expert-FFN decode library.
+ *
+ * This is the drop-in boundary for freeToken-rs's GPU expert section. Each
+ * entry point names the reference interface it replaces (paths relative to
+ * the freeToken-rs repository root). Conventions, mirroring ft_cuda::Q4Gemv
+ * (ft-cuda/src/lib.rs:69-150):
+ *   - the caller owns every device buffer; no entry point allocates device
+ *     memory during a launch (ft-cuda/src/lib.rs:989-990), so launches can be
+ *     captured into a HIP graph;
+ *   - launches are asynchronous on the given stream (a hipStream_t passed as
+ *     void*; NULL is the null stream) and never synchronise the host;
+ *   - where the reference panics on a violated shape precondition
+ *     (assert!, e.g. ft-cuda/src/lib.rs:171-173), these entry points return
+ *     FT_HIP_E_SHAPE before touching the GPU, and ft_hip_last_error() names
+ *     the violated condition. Runtime failures return FT_HIP_E_LAUNCH (the
+ *     reference's Err via `?`, lib.rs:184);
+ *   - one context is used by one host thread at a time (the reference keeps
+ *     Model and its Q4Gemv on one worker thread, ft-model/src/bin/serve.rs:635).
+ *
+ * Data formats:
+ *   q4_0 rows : ggml block_q4_0, 18 B per 32 weights {f16 d; u8 qs[16]},
+ *               byte i = q_i | q_{i+16} << 4, w = (q - 8) * d
+ *               (ft-core/src/q4_0.rs:1-16).
+ *   q4r rows  : [nb f16 scales, zero-padded to 16 B][nb x 16 B qs]
+ *               (ft-core/src/q4_0.rs:234-258).
+ *   q8 blocks : FT_Q8_BLK = 40 B per 32 activations {f32 d; i32 qsum; i8 qs[32]}.
+ *               The reference's 40-B block is {f32 d; f32 d*sum(qs); i8 qs[32]}
+ *               (ft-cuda/src/q4.cu:316-320); this build keeps the exact integer
+ *               sum so the -8 offset folds out in integer arithmetic. q8 buffers
+ *               are only produced and consumed by this library.
+ */
+#ifndef FT_HIP_H
+#define FT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FT_HIP_OK 0
+#define FT_HIP_E_INVALID (-1) /* null pointer or bad enum value */
+#define FT_HIP_E_SHAPE (-2)   /* a shape precondition does not hold */
+#define FT_HIP_E_DEVICE (-3)  /* no usable gfx950 device */
+#define FT_HIP_E_LAUNCH (-4)  /* HIP runtime or launch failure */
+#define FT_HIP_E_TIMEOUT (-5) /* the fused kernel's bounded wait expired */
+
+#define FT_Q8_BLK 40
+
+/* weight row layouts */
+#define FT_LAYOUT_Q4_0 0
+#define FT_LAYOUT_Q4R 1
+
+typedef struct ft_hip_ctx ft_hip_ctx;
+
+/* Library version (major*10000 + minor*100 + patch). */
+int ft_hip_version(void);
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* ft_hip_last_error(void);
+
+/* Replaces Q4Gemv::new (ft-cuda/src/lib.rs:111-150): binds `device`, checks
+ * that it is gfx950 and records its compute-unit count. */
+int ft_hip_create(int device, ft_hip_ctx** out);
+int ft_hip_destroy(ft_hip_ctx* ctx);
+
+/* Byte sizes of one row of k weights (ft-core/src/q4_0.rs:13-16, :238-245).
+ * Return -1 if k is not a multiple of 32. */
+int64_t ft_hip_row_bytes(int layout, int64_t k);
+int64_t ft_hip_q4r_scales_bytes(int64_t k);
+
+/* Replaces Q4Gemv::quantize_q8 / quantize_q8_view (ft-cuda/src/lib.rs:898-921,
+ * :871-894) with the arithmetic of ft-core's Q8Vec::quantize
+ * (ft-core/src/q4_0.rs:62-78: d = amax/127, round half away from zero).
+ * x: [n, x_stride] f32 (x_stride 0 shares one vector), q8: [n, k/32] blocks. */
+int ft_hip_quantize_q8(ft_hip_ctx* ctx, void* stream, const float* x, int64_t x_stride,
+                       void* q8, int64_t k, int64_t n);
+
+/* Grouped q4 x q8 GEMV over per-entry weight pointers. Replaces
+ * gemv_grouped_q8_ptr (ft-cuda/src/lib.rs:593-623, layout q4_0) and
+ * gemv_q4r_ptr (ft-cuda/src/lib.rs:736-767, layout q4r).
+ *   bases   : device u64 [n_entries], entry e's weights at bases[e] + bank_off
+ *   x_idx   : device i32 [n_entries] (entry e reads q8 row x_idx[e]) or NULL
+ *             (entry e reads q8 row e)
+ *   q8 row r starts at q8 + r * q8_stride_blocks * 40 (stride 0 shares one)
+ *   y[e * y_stride + row] = dot(W_e[row], q8 row)  for row < n_rows */
+int ft_hip_gemv_q4_grouped_ptr(ft_hip_ctx* ctx, void* stream, const uint64_t* bases,
+                               uint64_t bank_off, const int32_t* x_idx, int64_t n_entries,
+                               const void* q8, int64_t q8_stride_blocks, float* y,
+                               int64_t y_stride, int64_t n_rows, int64_t k, int layout);
+
+/* Same over a slot-indexed bank: entry e's weights at
+ * base + slots[e] * expert_bytes + bank_off. Replaces gemv_grouped_q8
+ * (ft-cuda/src/lib.rs:926-957), gemv_grouped_q8_idx (:772-804) and
+ * gemv_q4r_idx (:699-732). */
+int ft_hip_gemv_q4_grouped_slots(ft_hip_ctx* ctx, void* stream, const void* base,
+                                 uint64_t expert_bytes, uint64_t bank_off, const int32_t* slots,
+                                 const int32_t* x_idx, int64_t n_entries, const void* q8,
+                                 int64_t q8_stride_blocks, float* y, int64_t y_stride,
+                                 int64_t n_rows, int64_t k, int layout);
+
+/* Test entry (no reference counterpart): dumps the per-(entry, row, block)
+ * int32 dots sum_i (q4_i - 8) * q8_i computed by the same device routine the
+ * GEMVs use. out: [n_entries, n_rows, k/32] i32. Addressing as _slots. */
+int ft_hip_q4q8_block_dots(ft_hip_ctx* ctx, void* stream, const void* base,
+                           uint64_t expert_bytes, uint64_t bank_off, const int32_t* slots,
+                           const int32_t* x_idx, int64_t n_entries, const void* q8,
+                           int64_t q8_stride_blocks, int32_t* out, int64_t n_rows, int64_t k,
+                           int layout);
+
+/* Replaces gelu_mul_q8 (ft-cuda/src/lib.rs:354-374; kernel q4.cu:255-287):
+ * act = gelu_tanh(gu[:, j]) * gu[:, inter + j] (ft-model/src/lib.rs:435-437),
+ * then Q8Vec::quantize. gu: [n, 2*inter] f32, q8: [n, inter/32] blocks.
+ * tanh is the library's portable tanh (IEEE basic ops only). */
+int ft_hip_gelu_mul_q8(ft_hip_ctx* ctx, void* stream, const float* gu, void* q8, int64_t inter,
+                       int64_t n);
+
+/* Replaces gemv_f32_rows_dev (ft-cuda/src/lib.rs:674-694): router logits
+ * y[s][e] = sum_i W[e][i] * x[s][i] in this library's R-order (chunks of 16
+ * elements by fma, 8 groups of dim/128 chunks, summed in order), plus bias[e]
+ * if bias is not NULL. dim must be a multiple of 128. */
+int ft_hip_router_logits(ft_hip_ctx* ctx, void* stream, const float* w, const float* x,
+                         const float* bias, float* y, int64_t dim, int64_t n_rows,
+                         int64_t n_seqs);
+
+/* Replaces topk_router_dev (ft-cuda/src/lib.rs:472-494): per sequence, top-k
+ * logits (ties: lower expert index first), weights exp(l - lmax)/sum over the
+ * top-k, times expert_scale[e] (NULL = 1). e_count <= 1024, k <= 32. */
+int ft_hip_topk_router(ft_hip_ctx* ctx, void* stream, const float* logits,
+                       const float* expert_scale, int32_t* ids, float* wts, int64_t e_count,
+                       int64_t k, int64_t n_seqs);
+
+/* Replaces reduce_pairs_weighted (ft-cuda/src/lib.rs:808-829):
+ * out[s][i] += sum over pairs p with seq_of[p] == s, in p order, of
+ * wts[p] * y[p][i] (products rounded, then summed from 0, as the CPU pair
+ * combine of ft-model/src/lib.rs:1641-1646). */
+int ft_hip_reduce_pairs_weighted(ft_hip_ctx* ctx, void* stream, const float* y,
+                                 const float* wts, const int32_t* seq_of, float* out,
+                                 int64_t hidden, int64_t n_pairs, int64_t n_seqs);
+
+/* Row layout conversion on the device (setup, not the hot path): the
+ * reference repacks q4_0 banks to q4r at load (ft-model/src/lib.rs:570-609,
+ * ft-core/src/q4_0.rs:248-258). src and dst hold n_rows rows of k weights. */
+int ft_hip_repack_rows(ft_hip_ctx* ctx, void* stream, const void* src, int src_layout,
+                       void* dst, int dst_layout, int64_t n_rows, int64_t k);
+
+/* Seeded synthetic inputs (no reference counterpart; the reference's synthetic
+ * bench uses templated weights, ft-bench/src/bin/decode.rs:111-116).
+ * Value i of the tensor with key `key`: Irwin-Hall(4) over the 16-bit fields of
+ * splitmix64(key + (i+1)*0x9E3779B97F4A7C15), centred, times `scale`.
+ * gen_values writes n f32 values starting at index `start`; gen_q4_rows writes
+ * rows [row0, row0 + n_rows) of a seeded [*, k] matrix quantized to q4_0
+ * (ft-core/src/q4_0.rs:20-40) in `layout`. */
+int ft_hip_gen_values(ft_hip_ctx* ctx, void* stream, uint64_t key, int64_t start, int64_t n,
+                      float scale, float* out);
+int ft_hip_gen_q4_rows(ft_hip_ctx* ctx, void* stream, uint64_t key, int64_t row0,
+                       int64_t n_rows, int64_t k, float scale, void* out, int layout);
+
+/* One MoE expert-FFN layer for n_seqs tokens (the composition of
+ * ft-model/src/lib.rs:1406-1476 with host routing replaced by device routing):
+ *   logits = router(W_r, x) (+bias) -> top-k/softmax -> q8(x) -> grouped
+ *   gate|up GEMV -> gelu*up -> q8 -> grouped down GEMV -> x_out = x + combine.
+ * Expert e of this layer: gate|up rows [2I x H] at bank + e*expert_bytes,
+ * down rows [H x I] right after them (gu_bytes = 2I * row_bytes(H)), both in
+ * `layout`. x_out may equal x. workspace: device scratch of
+ * ft_hip_moe_layer_workspace_bytes() bytes. ids/wts (device [n_seqs*k]) receive
+ * the routing. */
+size_t ft_hip_moe_layer_workspace_bytes(int64_t n_seqs, int64_t hidden, int64_t inter,
+                                        int64_t n_experts, int64_t top_k);
+int ft_hip_moe_layer(ft_hip_ctx* ctx, void* stream, const float* x, float* x_out,
+                     int64_t n_seqs, int64_t hidden, int64_t inter, int64_t n_experts,
+                     int64_t top_k, const float* router_w, const float* router_bias,
+                     const float* expert_scale, const void* bank, uint64_t expert_bytes,
+                     int layout, int32_t* ids, float* wts, void* workspace,
+                     size_t workspace_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FT_HIP_H */

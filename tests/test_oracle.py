@@ -1,0 +1,459 @@
+"""CPU tests that pin the oracle (oracle/ft_oracle.cpp) before it is trusted.
+
+The reference ships no golden vectors (its tests generate data inline with
+xorshift32), so each oracle function is pinned by (a) the reference's own
+test assertions, reproduced on the same xorshift inputs, and (b) checks that
+the mathematics fixes: closed-form cases, independent numpy formulations of
+the integer arithmetic, IEEE library routines (numpy float16 / float32
+division), and f64 brute force. Each check is chosen so that a plausible slip
+(swapped nibbles, wrong rounding mode, dropped offset, wrong index) fails.
+"""
+import math
+
+import numpy as np
+import pytest
+
+
+def xorshift_row(n, seed, add_golden=True):
+    """ft-core/src/q4_0.rs:166-177 (pseudo_row); add_golden=False gives the
+    closure used by q4r_matches_q4 (:333-337) and ft-cuda/tests/*.rs."""
+    s = (seed + 0x9E3779B9) & 0xFFFFFFFF if add_golden else seed & 0xFFFFFFFF
+    out = np.empty(n, np.float32)
+    umax = np.float32(4294967295.0)
+    for i in range(n):
+        s ^= (s << 13) & 0xFFFFFFFF
+        s ^= s >> 17
+        s ^= (s << 5) & 0xFFFFFFFF
+        out[i] = (np.float32(s) / umax) * np.float32(2.0) - np.float32(1.0)
+    return out
+
+
+def unpack_q4(q, k):
+    """Independent numpy unpacking of q4_0 rows -> (nibbles [n, k] u8, d [n, k/32] f32)."""
+    q = np.asarray(q, np.uint8).reshape(-1, k // 32, 18)
+    d = q[:, :, :2].copy().view(np.float16).astype(np.float32)[:, :, 0]
+    qs = q[:, :, 2:]
+    nib = np.concatenate([qs & 0xF, qs >> 4], axis=2)  # [n, nb, 32]: lo nibbles are 0..15
+    return nib.reshape(q.shape[0], k), d
+
+
+# ---------------------------------------------------------------------------
+# The reference's own tests, on the reference's own inputs
+# ---------------------------------------------------------------------------
+
+def test_ref_roundtrip_error_is_small(orc):
+    """ft-core/src/q4_0.rs:179-189"""
+    row = xorshift_row(256, 7)
+    back = orc.dequantize_row(orc.quantize_row(row), 256)
+    assert np.all(np.abs(row - back) < 0.15)
+
+
+def test_ref_gemv_matches_f32_reference(orc):
+    """ft-core/src/q4_0.rs:191-215"""
+    k, n = 512, 16
+    x = xorshift_row(k, 1)
+    w = np.zeros((n, orc.row_bytes(k)), np.uint8)
+    wf = np.zeros((n, k), np.float32)
+    for r in range(n):
+        w[r] = orc.quantize_row(xorshift_row(k, 100 + r))
+        wf[r] = orc.dequantize_row(w[r], k)
+    y = orc.gemv(w, x, n)
+    ref = (wf * x).sum(axis=1)
+    assert np.all(np.abs(y - ref) < 0.15)
+
+
+def test_ref_avx2_matches_scalar(orc):
+    """ft-core/src/q4_0.rs:217-231"""
+    k = 4096
+    row = orc.quantize_row(xorshift_row(k, 42))
+    d, qs = orc.q8_quantize(xorshift_row(k, 7))
+    a = orc.dot_scalar(row, d, qs, k)
+    b = orc.dot_avx2(row, d, qs, k)
+    assert abs(a - b) < 1e-2 * (1.0 + abs(a))
+
+
+def test_ref_q4r_matches_q4(orc):
+    """ft-core/src/q4_0.rs:329-358 (the same xorshift stream, seed 0xC0DE)."""
+    k, n = 2816, 8
+    vals = xorshift_row(n * k + k, 0xC0DE, add_golden=False)
+    w = orc.quantize_row(vals[: n * k].reshape(n, k))
+    wr = orc.repack_q4r(w, k)
+    d, qs = orc.q8_quantize(vals[n * k:])
+    y1 = orc.gemv_q8(w, n, d, qs, k, layout=0)
+    y2 = orc.gemv_q8(wr, n, d, qs, k, layout=1)
+    assert np.all(np.abs(y1 - y2) < 1e-3 * (1.0 + np.abs(y1)))
+    # stronger: the arithmetic is identical, so the bits are
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# q4_0 quantiser (ft-core/src/q4_0.rs:20-40)
+# ---------------------------------------------------------------------------
+
+def test_q4_scale_is_f16_rne_of_signed_max_over_minus8(orc):
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal((64, 32)) * 0.02).astype(np.float32)
+    q = orc.quantize_row(x)
+    for r in range(64):
+        i = int(np.argmax(np.abs(x[r])))  # first occurrence of the largest magnitude
+        d = np.float32(x[r, i]) / np.float32(-8.0)
+        expect = np.array([d], np.float32).astype(np.float16).view(np.uint16)[0]
+        assert int(q[r, 0]) | (int(q[r, 1]) << 8) == int(expect)
+
+
+def test_q4_nibble_placement_single_spike(orc):
+    """A lone spike at position p must come back at p: pins byte i = q_i | q_{i+16}<<4."""
+    for p in range(32):
+        x = np.zeros(32, np.float32)
+        x[p] = -3.0  # maxv = -3 -> d = 0.375, the spike maps to q = 0 -> (0-8)*d = -3
+        back = orc.dequantize_row(orc.quantize_row(x), 32)
+        expect = np.zeros(32, np.float32)
+        expect[p] = -3.0
+        assert np.array_equal(back, expect), p
+
+
+def test_q4_rounding_closed_form(orc):
+    """maxv = -8 gives d = 1, id = 1, so q = clamp(trunc(x + 8.5), 0, 15)."""
+    x = np.array([-8.0, 0.4, 0.5, -0.5, -0.6, 6.49, 6.5, 7.9, 3.0, -7.5, 1.2, -1.2, 2.5, -2.5, 4.99, 5.5]
+                 + [0.0] * 16, np.float32)
+    q = orc.quantize_row(x)
+    nib, d = unpack_q4(q, 32)
+    assert d[0, 0] == 1.0
+    expect = np.clip(np.trunc(x.astype(np.float64) + 8.5), 0, 15).astype(np.uint8)
+    assert np.array_equal(nib[0], expect)
+    assert list(expect[:8]) == [0, 8, 9, 8, 7, 14, 15, 15]
+
+
+def test_q4_amax_tie_first_occurrence_wins(orc):
+    a = orc.quantize_row(np.array([0.5, -0.5] + [0.0] * 30, np.float32))
+    b = orc.quantize_row(np.array([-0.5, 0.5] + [0.0] * 30, np.float32))
+    # first: maxv = +0.5 -> d = -0.0625 (f16 0xAC00); second: maxv = -0.5 -> d = +0.0625 (0x2C00)
+    assert (int(a[0]) | (int(a[1]) << 8)) == 0xAC00 and (int(b[0]) | (int(b[1]) << 8)) == 0x2C00
+    assert (a[2] & 0xF) == 0                            # +0.5*(-16)+8.5 = 0.5 -> 0
+    assert (a[3] & 0xF) == 15                           # -0.5*(-16)+8.5 = 16.5 -> 16 -> clamp 15
+    assert (b[2] & 0xF) == 0 and (b[3] & 0xF) == 15
+
+
+def test_q4_zero_block(orc):
+    q = orc.quantize_row(np.zeros(32, np.float32))
+    # d = 0.0 / -8.0 = -0.0 (f16 0x8000); id = 0, so q = trunc(8.5) = 8 everywhere
+    assert q[0] == 0x00 and q[1] == 0x80 and np.all(q[2:] == 0x88)
+
+
+# ---------------------------------------------------------------------------
+# q8 activation quantiser (ft-core/src/q4_0.rs:62-78)
+# ---------------------------------------------------------------------------
+
+def test_q8_scale_is_ieee_amax_over_127(orc):
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal(32 * 500).astype(np.float32) * np.float32(3.0)
+    d, _ = orc.q8_quantize(x)
+    amax = np.abs(x.reshape(-1, 32)).max(axis=1)
+    assert np.array_equal(d, amax / np.float32(127.0))
+
+
+def test_q8_rounds_half_away_from_zero(orc):
+    """amax = 127 gives d = inv = 1, so q = round_half_away(v). RNE would give 2, -2, 0, 0, 126."""
+    x = np.array([127.0, 2.5, -2.5, 0.5, -0.5, 126.5, -126.5, 1.5, -1.5, 0.49, -0.51, 3.0] + [0.0] * 20,
+                 np.float32)
+    d, qs = orc.q8_quantize(x)
+    assert d[0] == 1.0
+    assert list(qs[:12]) == [127, 3, -3, 1, -1, 127, -127, 2, -2, 0, -1, 3]
+
+
+def test_q8_zero_block_and_error_bound(orc):
+    x = np.concatenate([np.zeros(32, np.float32),
+                        np.random.default_rng(3).standard_normal(32 * 200).astype(np.float32)])
+    d, qs = orc.q8_quantize(x)
+    assert d[0] == 0.0 and np.all(qs[:32] == 0)
+    deq = qs.astype(np.float64) * np.repeat(d, 32).astype(np.float64)
+    assert np.all(np.abs(deq - x) <= np.repeat(d, 32) * 0.5000001 + 1e-30)
+    assert np.all(np.abs(qs) <= 127)
+
+
+# ---------------------------------------------------------------------------
+# the dot (ft-core/src/q4_0.rs:105-160)
+# ---------------------------------------------------------------------------
+
+def _rand_case(orc, k, seed, n=4):
+    rng = np.random.default_rng(seed)
+    w = orc.quantize_row((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    d8, qs8 = orc.q8_quantize(rng.standard_normal(k).astype(np.float32))
+    return w, d8, qs8
+
+
+@pytest.mark.parametrize("k", [32, 64, 704, 2816, 4096])
+def test_block_dots_equal_numpy_integer_sum(orc, k):
+    w, d8, qs8 = _rand_case(orc, k, k)
+    got = orc.block_dots(w, qs8, k)
+    nib, _ = unpack_q4(w, k)
+    expect = ((nib.astype(np.int64) - 8) * qs8.astype(np.int64)).reshape(w.shape[0], k // 32, 32).sum(axis=2)
+    assert np.array_equal(got, expect)
+
+
+@pytest.mark.parametrize("k", [64, 704, 2816, 4096])
+def test_dot_avx2_close_to_f64_bruteforce(orc, k):
+    w, d8, qs8 = _rand_case(orc, k, 10 + k)
+    nib, d4 = unpack_q4(w, k)
+    wf = (nib.astype(np.float64) - 8) * np.repeat(d4, 32, axis=1)
+    xf = qs8.astype(np.float64) * np.repeat(d8, 32).astype(np.float64)
+    for r in range(w.shape[0]):
+        exact = float(wf[r] @ xf)
+        mag = float(np.abs(wf[r] * xf).sum())
+        got = orc.dot_avx2(w[r], d8, qs8, k)
+        assert abs(got - exact) <= 1e-5 * mag + 1e-12
+
+
+def test_dot_avx2_exact_when_arithmetic_is_exact(orc):
+    """Scales that are powers of two make every partial exact: the f32 result must
+    equal the integer closed form, whatever the summation order."""
+    k = 2816
+    rng = np.random.default_rng(5)
+    x = rng.integers(-127, 128, k).astype(np.float32)
+    x[::32] = 127.0                                  # amax = 127 -> d8 = 1
+    wv = rng.integers(-8, 8, k).astype(np.float32) * np.float32(0.0625)
+    wv[::32] = -0.5                                  # maxv = -0.5 -> d4 = 1/16
+    w = orc.quantize_row(wv)
+    d8, qs8 = orc.q8_quantize(x)
+    assert np.all(d8 == 1.0)
+    nib, d4 = unpack_q4(w, k)
+    assert np.all(d4 == 0.0625)
+    exact = float(((nib[0].astype(np.int64) - 8) * qs8.astype(np.int64)).sum()) * 0.0625
+    assert orc.dot_avx2(w[0] if w.ndim > 1 else w, d8, qs8, k) == exact
+    assert orc.dot_scalar(w[0] if w.ndim > 1 else w, d8, qs8, k) == exact
+
+
+def test_gemv_threads_do_not_change_bits(orc):
+    k, n = 2816, 300
+    rng = np.random.default_rng(6)
+    w = orc.quantize_row((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    d8, qs8 = orc.q8_quantize(rng.standard_normal(k).astype(np.float32))
+    y1 = orc.gemv_q8(w, n, d8, qs8, k, threads=1)
+    y8 = orc.gemv_q8(w, n, d8, qs8, k, threads=8)
+    assert np.array_equal(y1.view(np.uint32), y8.view(np.uint32))
+
+
+@pytest.mark.parametrize("k", [704, 2816, 4096])
+def test_q4r_layout_and_bit_identity(orc, k):
+    w, d8, qs8 = _rand_case(orc, k, 20 + k, n=3)
+    wr = orc.repack_q4r(w, k)
+    nb = k // 32
+    so = orc.q4r_scales_bytes(k)
+    assert wr.shape[1] == so + nb * 16 and so % 16 == 0
+    src = w.reshape(3, nb, 18)
+    assert np.array_equal(wr[:, :2 * nb].reshape(3, nb, 2), src[:, :, :2])
+    assert np.all(wr[:, 2 * nb:so] == 0)
+    assert np.array_equal(wr[:, so:].reshape(3, nb, 16), src[:, :, 2:])
+    for r in range(3):
+        a = orc.dot_avx2(w[r], d8, qs8, k)
+        b = orc.dot_q4r_avx2(wr[r], d8, qs8, k)
+        assert np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32)
+        assert orc.dot_scalar(w[r], d8, qs8, k) == orc.dot_q4r_scalar(wr[r], d8, qs8, k)
+
+
+# ---------------------------------------------------------------------------
+# GELU, portable exp/tanh (ft-model/src/lib.rs:435-437)
+# ---------------------------------------------------------------------------
+
+def test_exp_portable_accuracy(orc):
+    xs = np.concatenate([np.linspace(-700, 700, 20001), np.linspace(-1, 1, 20001)])
+    L = orc.lib()
+    for x in xs[::7]:
+        e = L.orc_exp_portable(float(x))
+        ref = math.exp(float(x))
+        assert abs(e - ref) <= 4e-16 * ref, x
+
+
+def test_tanh_portable_matches_correctly_rounded_tanh(orc):
+    """(float)tanh_f64(z) is correctly rounded except at near-ties; the portable
+    tanh must agree on (essentially) every f32 input of the GELU range."""
+    L = orc.lib()
+    rng = np.random.default_rng(7)
+    z = np.concatenate([rng.standard_normal(20000).astype(np.float32) * 3,
+                        np.linspace(-10, 10, 20001, dtype=np.float32),
+                        np.array([0.0, -0.0, 1e-30, -1e-30, 9.49, 9.5, -9.5, 1e-4], np.float32)])
+    bad = 0
+    for v in z:
+        got = np.float32(L.orc_tanh_portable(float(v)))
+        ref = np.float32(math.tanh(float(v)))
+        if got != ref:
+            bad += 1
+            assert abs(float(got) - math.tanh(float(v))) <= 1.0 * np.spacing(np.float32(abs(ref)) or 1e-45)
+    assert bad <= 2
+
+
+def test_gelu_special_values_and_libm_agreement(orc):
+    L = orc.lib()
+    assert L.orc_gelu_tanh_portable(0.0) == 0.0
+    assert L.orc_gelu_tanh_portable(10.0) == 10.0
+    g = L.orc_gelu_tanh_portable(-10.0)
+    assert g == 0.0 and math.copysign(1.0, g) == -1.0
+    rng = np.random.default_rng(8)
+    diff = 0
+    for g in rng.standard_normal(5000).astype(np.float32) * 2:
+        a = np.float32(L.orc_gelu_tanh_portable(float(g)))
+        b = np.float32(L.orc_gelu_tanh_libm(float(g)))
+        ref = 0.5 * float(g) * (1 + math.tanh(0.7978845608 * (float(g) + 0.044715 * float(g) ** 3)))
+        # 1 + t cancels for negative g: its f32 rounding (~6e-8 absolute) is scaled by 0.5*|g|
+        assert abs(float(a) - ref) <= 4e-7 * abs(ref) + 1.2e-7 * abs(float(g))
+        diff += a != b
+        # glibc 2.35 tanhf is not correctly rounded: the modes differ in the last bits only
+        assert abs(float(a) - float(b)) <= 4e-7 * abs(ref) + 1.2e-7 * abs(float(g))
+    assert diff < 1000  # measured ~11% of inputs on glibc 2.35
+
+
+def test_gelu_mul_q8_composition(orc):
+    """act[j] = gelu(gu[j]) * gu[I + j] (gate rows first), then q8."""
+    I = 704
+    rng = np.random.default_rng(9)
+    gu = rng.standard_normal(2 * I).astype(np.float32)
+    act, d, qs = orc.gelu_mul_q8(gu, I)
+    L = orc.lib()
+    expect = np.array([np.float32(L.orc_gelu_tanh_portable(float(gu[j]))) * gu[I + j] for j in range(I)],
+                      np.float32)
+    assert np.array_equal(act, expect)
+    d2, q2 = orc.q8_quantize(expect)
+    assert np.array_equal(d, d2) and np.array_equal(qs, q2)
+
+
+# ---------------------------------------------------------------------------
+# router logits (R-order), top-k, combine
+# ---------------------------------------------------------------------------
+
+def test_router_logits_f64_and_exact_integer_case(orc):
+    E, H = 128, 2816
+    rng = np.random.default_rng(10)
+    W = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    x = rng.standard_normal(H).astype(np.float32)
+    lg = orc.router_logits(W, x)
+    ref = W.astype(np.float64) @ x.astype(np.float64)
+    mag = np.abs(W.astype(np.float64)) @ np.abs(x.astype(np.float64))
+    assert np.all(np.abs(lg - ref) <= 1e-6 * mag)
+    # integer-valued inputs: every partial sum is exact, so the order cannot matter
+    Wi = rng.integers(-50, 51, (E, H)).astype(np.float32)
+    xi = rng.integers(-50, 51, H).astype(np.float32)
+    assert np.array_equal(orc.router_logits(Wi, xi), (Wi.astype(np.int64) @ xi.astype(np.int64)).astype(np.float32))
+    bias = rng.standard_normal(E).astype(np.float32)
+    assert np.array_equal(orc.router_logits(Wi, xi, bias),
+                          (Wi.astype(np.int64) @ xi.astype(np.int64)).astype(np.float32) + bias)
+
+
+def test_router_logits_order_is_chunked_not_sequential(orc):
+    """A case where the R-order and a plain left-to-right sum give different f32 bits,
+    with the R-order value predicted by hand: chunk 0 holds 2^24 and 1s that a
+    left-to-right sum would absorb one by one, but the chunk's own fma chain
+    absorbs them too; group/chunk sums add exactly."""
+    H = 128
+    W = np.zeros((1, H), np.float32)
+    x = np.zeros(H, np.float32)
+    W[0, 0], x[0] = 1.0, 16777216.0          # chunk 0: 2^24
+    W[0, 1], x[1] = 1.0, 1.0                 # 2^24 + 1 -> 2^24 (absorbed, RNE)
+    W[0, 16:32] = 1.0                        # chunk 1 (group 1): sixteen 1s = 16
+    x[16:32] = 1.0
+    lg = orc.router_logits(W, x)
+    assert lg[0] == np.float32(16777216.0 + 16.0)
+
+
+def test_topk_matches_stable_argsort_and_f64_softmax(orc):
+    rng = np.random.default_rng(11)
+    for trial in range(50):
+        E, k = 128, 8
+        lg = rng.standard_normal(E).astype(np.float32)
+        if trial % 5 == 0:  # force ties
+            lg[rng.integers(0, E, 20)] = lg[3]
+        ids, w = orc.topk_softmax(lg, k)
+        order = np.argsort(-lg.astype(np.float64), kind="stable")[:k]
+        assert np.array_equal(ids, order)
+        ex = np.exp(lg[order].astype(np.float64) - float(lg[order[0]]))
+        assert np.allclose(w, ex / ex.sum(), rtol=2e-6, atol=1e-9)
+        assert abs(float(w.astype(np.float64).sum()) - 1.0) < 1e-5
+
+
+def test_topk_ties_prefer_lower_index(orc):
+    lg = np.zeros(16, np.float32)
+    lg[[2, 5, 9]] = 1.0
+    ids, w = orc.topk_softmax(lg, 4)
+    assert list(ids) == [2, 5, 9, 0]
+    ids, _ = orc.topk_softmax(np.full(10, -3.0, np.float32), 3)
+    assert list(ids) == [0, 1, 2]
+
+
+def test_topk_expert_scale(orc):
+    lg = np.array([3.0, 1.0, 2.0, 0.0], np.float32)
+    es = np.array([2.0, 1.0, 0.5, 1.0], np.float32)
+    ids, w = orc.topk_softmax(lg, 2, es)
+    ids0, w0 = orc.topk_softmax(lg, 2)
+    assert list(ids) == [0, 2]
+    assert w[0] == w0[0] * 2.0 and w[1] == w0[1] * 0.5
+
+
+def test_combine_exact_and_f64(orc):
+    rng = np.random.default_rng(12)
+    y = rng.standard_normal((8, 2816)).astype(np.float32)
+    w = rng.random(8).astype(np.float32)
+    x = rng.standard_normal(2816).astype(np.float32)
+    out = orc.combine(y, w, x)
+    ref = x.astype(np.float64) + (y.astype(np.float64) * w.astype(np.float64)[:, None]).sum(axis=0)
+    assert np.allclose(out, ref, rtol=0, atol=2e-6 * np.abs(ref).max())
+    # power-of-two weights and small integers: exact
+    yi = rng.integers(-100, 100, (8, 64)).astype(np.float32)
+    wi = np.array([0.5, 0.25, 1, 2, 0.125, 4, 1, 0.5], np.float32)
+    assert np.array_equal(orc.combine(yi, wi), (yi * wi[:, None]).sum(axis=0))
+
+
+# ---------------------------------------------------------------------------
+# the layer composition (ft-model/src/lib.rs:1609-1653)
+# ---------------------------------------------------------------------------
+
+def test_moe_layer_stages_match_f64_composition(orc):
+    H, I, E, k = 256, 64, 16, 4
+    rng = np.random.default_rng(13)
+    x = rng.standard_normal(H).astype(np.float32)
+    W_r = (rng.standard_normal((E, H)) * 0.1).astype(np.float32)
+    gu = {e: orc.quantize_row((rng.standard_normal((2 * I, H)) * 0.02).astype(np.float32)) for e in range(E)}
+    dn = {e: orc.quantize_row((rng.standard_normal((H, I)) * 0.02).astype(np.float32)) for e in range(E)}
+    r = orc.moe_layer(x, W_r, gu, dn, H, I, k)
+    ids, wts = orc.topk_softmax(orc.router_logits(W_r, x), k)
+    assert np.array_equal(r["ids"], ids) and np.array_equal(r["wts"], wts)
+    d8, q8 = orc.q8_quantize(x)
+    xf = q8.astype(np.float64) * np.repeat(d8, 32)
+    out = x.astype(np.float64).copy()
+    for p, e in enumerate(ids):
+        nib, d4 = unpack_q4(gu[e], H)
+        ygu = ((nib.astype(np.float64) - 8) * np.repeat(d4, 32, axis=1)) @ xf
+        assert np.allclose(r["y_gu"][p], ygu, rtol=0, atol=1e-5 * np.abs(ygu).max())
+        # down projection from the oracle's own act quants (teacher forced)
+        af = r["act_qs"][p].astype(np.float64) * np.repeat(r["act_d"][p], 32)
+        nib, d4 = unpack_q4(dn[e], I)
+        ydn = ((nib.astype(np.float64) - 8) * np.repeat(d4, 32, axis=1)) @ af
+        assert np.allclose(r["y_dn"][p], ydn, rtol=0, atol=1e-5 * np.abs(ydn).max() + 1e-12)
+        out += float(wts[p]) * r["y_dn"][p].astype(np.float64)
+    assert np.allclose(r["x_out"], out, rtol=0, atol=1e-5 * np.abs(out).max())
+    # q4r banks give bit-identical results
+    r2 = orc.moe_layer(x, W_r, {e: orc.repack_q4r(v, H) for e, v in gu.items()},
+                       {e: orc.repack_q4r(v, I) for e, v in dn.items()}, H, I, k, layout=1)
+    assert np.array_equal(r2["x_out"], r["x_out"])
+
+
+def test_moe_layer_missing_expert_raises(orc):
+    H, I, E, k = 128, 32, 4, 2
+    x = np.ones(H, np.float32)
+    W_r = np.zeros((E, H), np.float32)
+    with pytest.raises(KeyError):
+        orc.moe_layer(x, W_r, {}, {}, H, I, k)
+
+
+# ---------------------------------------------------------------------------
+# seeded generator
+# ---------------------------------------------------------------------------
+
+def test_generator_moments_and_determinism(orc):
+    key = orc.tensor_key(1, 0, 0, orc.T_GU)
+    v = orc.gen_values(key, 0, 1 << 20, 0.02).astype(np.float64)
+    assert abs(v.mean()) < 1e-4 and abs(v.std() - 0.02) < 2e-4
+    assert np.abs(v).max() <= 0.02 * math.sqrt(3) * 2 + 1e-9  # Irwin-Hall(4) support: +-2*sqrt(3) sigma
+    assert np.array_equal(orc.gen_values(key, 1000, 10, 0.02), orc.gen_values(key, 0, 1010, 0.02)[1000:])
+    assert orc.tensor_key(1, 0, 0, orc.T_GU) != orc.tensor_key(1, 0, 1, orc.T_GU)
+    rows = orc.gen_q4_rows(key, 3, 2, 64, 0.02)
+    vals = orc.gen_values(key, 3 * 64, 2 * 64, 0.02).reshape(2, 64)
+    assert np.array_equal(rows, orc.quantize_row(vals))
