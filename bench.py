@@ -35,7 +35,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--path", choices=["multikernel"], default="multikernel")
+    ap.add_argument("--path", choices=["fused", "multikernel"], default="fused")
     ap.add_argument("--layers", type=int, default=30)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -187,14 +187,24 @@ def main():
     n_tok = args.warmup + args.steps
     H = model.shape.hidden
     hidden = torch.stack([model.hidden(t) for t in range(n_tok)])
-    C = chunk_size(args.steps, args.warmup)
-    runner = MultiKernelRunner(model, C)
     outs = torch.zeros((n_tok, H), dtype=torch.float32, device=model.device)
+    if args.path == "fused":
+        t1 = time.time()
+        stack = moe_synth.FusedStack(model)
+        torch.cuda.synchronize()
+        log(f"[setup] banks repacked for the fused kernel in {time.time() - t1:.1f}s")
 
-    def run(t0_, n):
-        for c in range(t0_, t0_ + n, C):
-            runner.run_chunk(hidden[c:c + C])
-            outs[c:c + C].copy_(runner.out)
+        def run(t0_, n):
+            for t in range(t0_, t0_ + n):
+                stack.run(hidden[t], outs[t])
+    else:
+        C = chunk_size(args.steps, args.warmup)
+        runner = MultiKernelRunner(model, C)
+
+        def run(t0_, n):
+            for c in range(t0_, t0_ + n, C):
+                runner.run_chunk(hidden[c:c + C])
+                outs[c:c + C].copy_(runner.out)
 
     run(0, args.warmup)
     torch.cuda.synchronize()
@@ -213,9 +223,16 @@ def main():
     log(f"[gpu] {us_tok:.1f} us/token (wall {wall * 1e6 / args.steps:.1f}), {gbps:.0f} GB/s expert bytes, "
         f"{(exp_bytes + router_bytes) / (us_tok * 1e-6) / 1e9:.0f} GB/s incl. router")
 
-    k_us, k_bytes = time_dominant_kernel(g, model)
+    if args.path == "fused":
+        stack.check()
+        # the fused kernel is the only kernel of a step: one launch per token
+        k_us, k_bytes = us_tok, exp_bytes + router_bytes
+        k_name = "k_moe_stack_fused (whole 30-layer section, one launch per token)"
+    else:
+        k_us, k_bytes = time_dominant_kernel(g, model)
+        k_name = "k_gemv_q4_grouped (gate|up, 8 experts)"
     k_gbps = k_bytes / (k_us * 1e-6) / 1e9
-    log(f"[kernel] gate|up grouped GEMV: {k_us:.2f} us/launch, {k_bytes} B -> {k_gbps:.0f} GB/s")
+    log(f"[kernel] {k_name}: {k_us:.2f} us/launch, {k_bytes} B -> {k_gbps:.0f} GB/s")
 
     cpu = None
     if not args.no_cpu:
@@ -250,7 +267,7 @@ def main():
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "roofline": {"bound": "hbm", "achieved": round(k_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(k_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "k_gemv_q4_grouped (gate|up, 8 experts)", "bytes_per_launch": k_bytes,
+                     "kernel": k_name, "bytes_per_launch": k_bytes,
                      "us_per_launch": round(k_us, 3)},
         "cpu_baseline": cpu,
     }

@@ -46,6 +46,14 @@ SIGNATURES = {
     "ft_hip_moe_layer_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "ft_hip_moe_layer": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _U64, _I, _P, _P,
                               _P, _SZ]),
+    "ft_hip_fused_expert_bytes": (_I64, [_I64, _I64]),
+    "ft_hip_fused_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
+    "ft_hip_fused_workspace_init": (_I, [_P, _P, _P, _SZ]),
+    "ft_hip_pack_experts_fused": (_I, [_P, _P, _P, _I, _U64, _P, _I64, _I64, _I64]),
+    "ft_hip_pack_router_fused": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
+    "ft_hip_moe_stack_fused": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P,
+                                    _SZ, _P, _P, _P, _P]),
+    "ft_hip_fused_status": (_I, [_P, _P, ctypes.POINTER(_I)]),
 }
 
 
@@ -207,3 +215,37 @@ class Q4Gemv:
                                      n_experts, top_k, _ptr(router_w), _ptr(router_bias), _ptr(expert_scale),
                                      _ptr(bank), expert_bytes, layout, _ptr(ids), _ptr(wts), _ptr(workspace),
                                      workspace.numel() * workspace.element_size()))
+
+    # -- fused whole-stack path --
+    @staticmethod
+    def fused_expert_bytes(hidden, inter):
+        return lib().ft_hip_fused_expert_bytes(hidden, inter)
+
+    @staticmethod
+    def fused_workspace_bytes(hidden, inter, n_experts, top_k):
+        return lib().ft_hip_fused_workspace_bytes(hidden, inter, n_experts, top_k)
+
+    def fused_workspace_init(self, ws, stream=None):
+        check(lib().ft_hip_fused_workspace_init(self._ctx, _stream(stream), _ptr(ws), ws.numel() * ws.element_size()))
+
+    def pack_experts_fused(self, src, src_layout, src_expert_bytes, dst, n_experts, hidden, inter, stream=None):
+        check(lib().ft_hip_pack_experts_fused(self._ctx, _stream(stream), _ptr(src), src_layout, src_expert_bytes,
+                                              _ptr(dst), n_experts, hidden, inter))
+
+    def pack_router_fused(self, src, dst, n_layers, n_experts, hidden, stream=None):
+        check(lib().ft_hip_pack_router_fused(self._ctx, _stream(stream), _ptr(src), _ptr(dst), n_layers, n_experts,
+                                             hidden))
+
+    def moe_stack_fused(self, x_in, x_out, hidden, inter, n_experts, top_k, n_layers, banks, routers, bias,
+                        expert_scale, ids, wts, ws, dbg_gu=None, dbg_act=None, dbg_x=None, dbg_trace=None,
+                        stream=None):
+        check(lib().ft_hip_moe_stack_fused(self._ctx, _stream(stream), _ptr(x_in), _ptr(x_out), hidden, inter,
+                                           n_experts, top_k, n_layers, _ptr(banks), _ptr(routers), _ptr(bias),
+                                           _ptr(expert_scale), _ptr(ids), _ptr(wts), _ptr(ws),
+                                           ws.numel() * ws.element_size(), _ptr(dbg_gu), _ptr(dbg_act),
+                                           _ptr(dbg_x), _ptr(dbg_trace)))
+
+    def fused_status(self, ws):
+        """Raise FtHipError(E_TIMEOUT) if a fused launch on `ws` gave up a wait (sync first)."""
+        ab = ctypes.c_int(0)
+        check(lib().ft_hip_fused_status(self._ctx, _ptr(ws), ctypes.byref(ab)))

@@ -148,3 +148,37 @@ def zipf_router_bias(shape, n_layers, s=1.1, tau=None, seed=SEED):
         ranks[perm] = np.arange(1, E + 1)
         out[l] = (tau * (-s) * np.log(ranks)).astype(np.float32)
     return out
+
+
+class FusedStack:
+    """A SyntheticMoE's banks and routers repacked for the fused whole-stack
+    kernel (ft_hip_moe_stack_fused): one cooperative launch runs all layers
+    of one token."""
+
+    def __init__(self, model):
+        g, s = model.g, model.shape
+        H, I, E, K = s.hidden, s.inter, s.n_experts, s.top_k
+        self.m, self.g = model, g
+        self.expert_bytes = g.fused_expert_bytes(H, I)
+        self.banks = torch.empty(model.L * E * self.expert_bytes, dtype=torch.uint8, device=model.device)
+        g.pack_experts_fused(model.banks, model.layout, model.expert_bytes, self.banks, model.L * E, H, I)
+        self.routers = torch.empty_like(model.routers)
+        g.pack_router_fused(model.routers, self.routers, model.L, E, H)
+        self.ws = torch.empty(g.fused_workspace_bytes(H, I, E, K), dtype=torch.uint8, device=model.device)
+        g.fused_workspace_init(self.ws)
+
+    def n_workgroups(self):
+        s = self.m.shape
+        return max(s.top_k * s.inter // 32, s.hidden // 16, (s.n_experts + 15) // 16)
+
+    def run(self, x_in, x_out, ids=None, wts=None, dbg_gu=None, dbg_act=None, dbg_x=None, trace=None,
+            stream=None):
+        s = self.m.shape
+        self.g.moe_stack_fused(x_in, x_out, s.hidden, s.inter, s.n_experts, s.top_k, self.m.L, self.banks,
+                               self.routers, self.m.bias, None, ids, wts, self.ws, dbg_gu, dbg_act, dbg_x, trace,
+                               stream)
+
+    def check(self):
+        """Raise if a launch gave up a bounded wait (synchronises first)."""
+        torch.cuda.synchronize()
+        self.g.fused_status(self.ws)

@@ -175,6 +175,64 @@ int ft_hip_moe_layer(ft_hip_ctx* ctx, void* stream, const float* x, float* x_out
                      int layout, int32_t* ids, float* wts, void* workspace,
                      size_t workspace_bytes);
 
+/* ---- fused whole-stack path (no single reference counterpart) ----
+ * The reference runs the section as a sequence of launches per layer
+ * (ft-model/src/lib.rs:1406-1476) and removes host launch cost with a CUDA
+ * graph over the whole stack (forward_sample_graphed, ft-model/src/lib.rs:
+ * 1062-1121). Here the L-layer section for one token is ONE persistent
+ * cooperative kernel: device-side routing, gate|up, GELU*up, q8, down and
+ * combine for every layer, with the same arithmetic as the launch-by-launch
+ * entry points (q8 quants, per-block int32 dots, router R-order and top-k are
+ * bit-identical; f32 sums may differ in order).
+ *
+ * Fused expert layout (a lossless repack of q4_0, same byte count):
+ *   expert = [gate|up tiles][down tiles];
+ *   gate|up tile jb (I/32 tiles) = 64 rows (gate rows 32jb..32jb+31, then up
+ *     rows I+32jb..): [H/32 blocks x 64 rows x f16 scale][H/32 x 64 x 16 B qs];
+ *   down tile jt (H/16 tiles) = rows 16jt..16jt+15:
+ *     [I/32 blocks x 16 rows x f16 scale][I/32 x 16 x 16 B qs].
+ * Fused router layout: [L][H/16 chunks][E][16] f32. */
+int64_t ft_hip_fused_expert_bytes(int64_t hidden, int64_t inter);
+size_t ft_hip_fused_workspace_bytes(int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k);
+
+/* Zero a fused workspace and set its epoch; call once after allocating it,
+ * and again after a launch reported FT_HIP_E_TIMEOUT. */
+int ft_hip_fused_workspace_init(ft_hip_ctx* ctx, void* stream, void* workspace, size_t workspace_bytes);
+
+/* Repack n_experts expert banks (gate rows, up rows, down rows, each in
+ * src_layout, src_expert_bytes apart) into the fused layout
+ * (ft_hip_fused_expert_bytes apart). Setup only. */
+int ft_hip_pack_experts_fused(ft_hip_ctx* ctx, void* stream, const void* src, int src_layout,
+                              uint64_t src_expert_bytes, void* dst, int64_t n_experts, int64_t hidden,
+                              int64_t inter);
+
+/* Repack routers [n_layers][E][H] f32 into the fused router layout. */
+int ft_hip_pack_router_fused(ft_hip_ctx* ctx, void* stream, const float* src, float* dst, int64_t n_layers,
+                             int64_t n_experts, int64_t hidden);
+
+/* Run the n_layers-layer section for one token: x_out = x_L where
+ * x_{l+1} = x_l + MoE_l(x_l). banks: [n_layers][E] fused experts; routers:
+ * fused [n_layers][H/16][E][16]; bias, expert_scale: [n_layers][E] or NULL;
+ * ids/wts: [n_layers][top_k] routing record or NULL. One workspace serves one
+ * launch at a time (launches on one stream may reuse it). dbg_* (NULL in
+ * normal use) receive per-layer stage values for tests: dbg_gu
+ * [L][K][2I] gate|up sums, dbg_act [L][K][I/32] q8 blocks, dbg_x [L+1][H];
+ * dbg_trace [workgroups][L+1][16] u64 receives wall-clock stamps of each
+ * workgroup's phases (slot 0 = the layer-0 router prologue), the analogue of
+ * the reference's per-section Profile counters (ft-model/src/lib.rs:252-296).
+ * The workgroup count is max(top_k*inter/32, hidden/16, ceil(E/16)). */
+int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float* x_in, float* x_out, int64_t hidden,
+                           int64_t inter, int64_t n_experts, int64_t top_k, int64_t n_layers,
+                           const void* banks, const float* routers, const float* bias,
+                           const float* expert_scale, int32_t* ids, float* wts, void* workspace,
+                           size_t workspace_bytes, float* dbg_gu, void* dbg_act, float* dbg_x,
+                           uint64_t* dbg_trace);
+
+/* Host-synchronous check of a fused workspace after the stream has been
+ * synchronised: FT_HIP_E_TIMEOUT (and *aborted = 1) if a launch gave up a
+ * bounded wait. */
+int ft_hip_fused_status(ft_hip_ctx* ctx, void* workspace, int* aborted);
+
 #ifdef __cplusplus
 }
 #endif

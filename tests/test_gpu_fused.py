@@ -1,0 +1,173 @@
+"""GPU parity tests of the fused whole-stack kernel (ft_hip_moe_stack_fused).
+
+Per layer, each stage is checked against the CPU oracle on the kernel's own
+input to that stage (teacher forcing, from the kernel's debug record):
+top-k ids and weights and the GELU*up q8 blocks bit-exact; gate|up sums and
+the layer output within max|d| <= 1e-3 * ||ref||_2. The repack to the fused
+layout is checked byte for byte against the oracle's q4_0 rows.
+"""
+import numpy as np
+import pytest
+import torch
+
+import ft_hip
+import moe_synth
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def unpack_fused_expert(buf, H, I):
+    """Invert the fused layout on the host -> (gate|up q4_0 rows [2I, H*18/32], down q4_0 rows [H, I*18/32])."""
+    nb, nbj = H // 32, I // 32
+    gu = np.zeros((2 * I, nb, 18), np.uint8)
+    tile = nb * 1152
+    for jb in range(nbj):
+        T = buf[jb * tile:(jb + 1) * tile]
+        sc = T[:nb * 128].reshape(nb, 64, 2)
+        qs = T[nb * 128:].reshape(nb, 64, 16)
+        rows = np.r_[np.arange(32) + 32 * jb, I + 32 * jb + np.arange(32)]
+        gu[rows, :, :2] = sc.transpose(1, 0, 2)
+        gu[rows, :, 2:] = qs.transpose(1, 0, 2)
+    dn = np.zeros((H, nbj, 18), np.uint8)
+    base = nbj * tile
+    dt = nbj * 288
+    for jt in range(H // 16):
+        T = buf[base + jt * dt: base + (jt + 1) * dt]
+        sc = T[:nbj * 32].reshape(nbj, 16, 2)
+        qs = T[nbj * 32:].reshape(nbj, 16, 16)
+        dn[jt * 16:(jt + 1) * 16, :, :2] = sc.transpose(1, 0, 2)
+        dn[jt * 16:(jt + 1) * 16, :, 2:] = qs.transpose(1, 0, 2)
+    return gu.reshape(2 * I, -1), dn.reshape(H, -1)
+
+
+@pytest.fixture(scope="module")
+def stack(gemv):
+    m = moe_synth.SyntheticMoE(gemv, moe_synth.GEMMA, n_layers=4)
+    return moe_synth.FusedStack(m)
+
+
+def test_fused_pack_is_lossless(gemv, orc, stack):
+    m = stack.m
+    H, I = m.shape.hidden, m.shape.inter
+    eb = stack.expert_bytes
+    assert eb == moe_synth.algorithmic_expert_bytes(m.shape)  # exactly q4_0's byte count
+    for l, e in [(0, 0), (1, 77), (3, 127)]:
+        buf = host(stack.banks[(l * m.shape.n_experts + e) * eb:(l * m.shape.n_experts + e + 1) * eb])
+        gu, dn = unpack_fused_expert(buf, H, I)
+        assert np.array_equal(gu, orc.gen_q4_rows(orc.tensor_key(1, l, e, orc.T_GU), 0, 2 * I, H, 0.02))
+        assert np.array_equal(dn, orc.gen_q4_rows(orc.tensor_key(1, l, e, orc.T_DN), 0, H, I, 0.02))
+    r = host(stack.routers[2]).reshape(H // 16, m.shape.n_experts, 16)
+    ref = host(m.routers[2])
+    assert np.array_equal(r.transpose(1, 0, 2).reshape(m.shape.n_experts, H), ref)
+
+
+def _run_debug(stack, token):
+    m = stack.m
+    s = m.shape
+    H, I, E, K, L = s.hidden, s.inter, s.n_experts, s.top_k, m.L
+    x = m.hidden(token)
+    out = torch.zeros_like(x)
+    ids = torch.zeros(L * K, dtype=torch.int32, device=DEV)
+    wts = torch.zeros(L * K, dtype=torch.float32, device=DEV)
+    dbg_gu = torch.zeros(L * K * 2 * I, dtype=torch.float32, device=DEV)
+    dbg_act = torch.zeros(L * K * (I // 32) * 40, dtype=torch.uint8, device=DEV)
+    dbg_x = torch.zeros((L + 1) * H, dtype=torch.float32, device=DEV)
+    stack.run(x, out, ids, wts, dbg_gu, dbg_act, dbg_x)
+    stack.check()
+    return dict(x=host(x), out=host(out), ids=host(ids).reshape(L, K), wts=host(wts).reshape(L, K),
+                gu=host(dbg_gu).reshape(L, K, 2 * I), act=host(dbg_act).reshape(L, K, I // 32, 40),
+                xs=host(dbg_x).reshape(L + 1, H))
+
+
+def test_fused_stack_stages_teacher_forced(gemv, orc, stack):
+    m = stack.m
+    s = m.shape
+    H, I, E, K, L = s.hidden, s.inter, s.n_experts, s.top_k, m.L
+    r = _run_debug(stack, 0)
+    assert np.array_equal(r["xs"][0], r["x"])
+    assert np.array_equal(r["xs"][L], r["out"])
+    for l in range(L):
+        xl = r["xs"][l]
+        Wr = host(m.routers[l])
+        ids, wts = orc.topk_softmax(orc.router_logits(Wr, xl), K)
+        assert np.array_equal(r["ids"][l], ids), f"layer {l}"
+        assert np.array_equal(r["wts"][l].view(np.uint32), wts.view(np.uint32)), f"layer {l}"
+        gu_b, dn_b = {}, {}
+        for e in ids:
+            b = host(m.bank_of(l, int(e)))
+            gu_b[int(e)], dn_b[int(e)] = b[:m.gu_bytes], b[m.gu_bytes:]
+        ref = orc.moe_layer(xl, Wr, gu_b, dn_b, H, I, K, layout=1)
+        out_ref = xl.astype(np.float64).copy()
+        for p in range(K):
+            yg = ref["y_gu"][p]
+            assert np.max(np.abs(r["gu"][l, p] - yg)) <= 1e-3 * np.linalg.norm(yg), (l, p)
+            # GELU*up -> q8 on the kernel's own gate|up sums: bit-exact
+            _, d, q = orc.gelu_mul_q8(r["gu"][l, p], I)
+            blk = r["act"][l, p]
+            assert np.array_equal(blk[:, :4].copy().view(np.float32)[:, 0].view(np.uint32), d.view(np.uint32))
+            assert np.array_equal(blk[:, 8:].copy().view(np.int8).ravel(), q)
+            assert np.array_equal(blk[:, 4:8].copy().view(np.int32)[:, 0], q.reshape(-1, 32).astype(np.int32).sum(1))
+            # down projection from the kernel's own q8 activations
+            ydn = orc.gemv_q8(dn_b[int(ids[p])], H, d, q, I, layout=1)
+            out_ref += np.float64(wts[p]) * ydn.astype(np.float64)
+        dx = r["xs"][l + 1].astype(np.float64) - xl
+        dref = out_ref - xl
+        assert np.max(np.abs(dx - dref)) <= 1e-3 * np.linalg.norm(dref), f"layer {l}"
+
+
+def test_fused_matches_launch_by_launch(gemv, stack):
+    """Per layer, the launch-by-launch path on the fused kernel's layer input
+    picks the same experts with the same weights; outputs agree to 1e-3."""
+    m = stack.m
+    s = m.shape
+    r = _run_debug(stack, 3)
+    ws = m.workspace(1)
+    for l in range(m.L):
+        x = torch.from_numpy(r["xs"][l]).to(DEV)
+        xo = torch.zeros_like(x)
+        ids = torch.zeros(s.top_k, dtype=torch.int32, device=DEV)
+        wts = torch.zeros(s.top_k, dtype=torch.float32, device=DEV)
+        m.layer(l, x, xo, ids, wts, ws)
+        assert np.array_equal(host(ids), r["ids"][l])
+        assert np.array_equal(host(wts), r["wts"][l])
+        d_ref = host(xo) - r["xs"][l]
+        d = r["xs"][l + 1] - r["xs"][l]
+        assert np.max(np.abs(d - d_ref)) <= 1e-3 * np.linalg.norm(d_ref)
+
+
+def test_fused_repeatable_bit_for_bit(gemv, stack):
+    """Fixed summation orders and no atomics: repeated launches (advancing
+    epochs on one workspace) give identical bits."""
+    m = stack.m
+    x = m.hidden(5)
+    outs = []
+    for _ in range(3):
+        o = torch.zeros_like(x)
+        ids = torch.zeros(m.L * m.shape.top_k, dtype=torch.int32, device=DEV)
+        stack.run(x, o, ids)
+        outs.append((host(o), host(ids)))
+    stack.check()
+    for o, i in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0][0].view(np.uint32))
+        assert np.array_equal(i, outs[0][1])
+
+
+def test_fused_rejects_bad_shapes(gemv, stack):
+    m = stack.m
+    s = m.shape
+    x = m.hidden(0)
+    with pytest.raises(ft_hip.FtHipError) as ei:
+        gemv.moe_stack_fused(x, x, 2880, s.inter, s.n_experts, s.top_k, m.L, stack.banks, stack.routers, None,
+                             None, None, None, stack.ws)
+    assert ei.value.code == ft_hip.E_SHAPE
+    small = torch.zeros(64, dtype=torch.uint8, device=DEV)
+    with pytest.raises(ft_hip.FtHipError) as ei:
+        gemv.moe_stack_fused(x, x, s.hidden, s.inter, s.n_experts, s.top_k, m.L, stack.banks, stack.routers,
+                             None, None, None, None, small)
+    assert ei.value.code == ft_hip.E_SHAPE
