@@ -39,6 +39,9 @@ def parse():
     ap.add_argument("--layers", type=int, default=30)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="before warmup, run 3 int32->f32 copies of MIB MiB each (a plain copy kernel of known "
+                         "size, read MIB and written MIB per launch) to scale rocprofv3 FETCH_SIZE/WRITE_SIZE")
     return ap.parse_args()
 
 
@@ -205,6 +208,16 @@ def main():
             for c in range(t0_, t0_ + n, C):
                 runner.run_chunk(hidden[c:c + C])
                 outs[c:c + C].copy_(runner.out)
+
+    if args.copy_calib > 0:
+        n = args.copy_calib << 18
+        src = torch.ones(n, dtype=torch.int32, device=model.device)
+        dst = torch.empty(n, dtype=torch.float32, device=model.device)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[calib] 3 copies of {n * 4} B read + {n * 4} B written each")
+        del src, dst
 
     run(0, args.warmup)
     torch.cuda.synchronize()

@@ -49,6 +49,7 @@ constexpr int NREP = 8;         // replicas of each broadcast buffer: one per XC
                                 // copy is polled by ~1/8 of the workgroups
 constexpr int CTL_EPOCH = 0;    // control words (u32 indices)
 constexpr int CTL_ABORT = 32;
+constexpr int TRACE_SLOTS = 32; // stamps per workgroup per layer in the debug trace
 
 struct FusedParams {
     const uint8_t* banks;       // [L][E][expert_bytes], fused layout
@@ -82,17 +83,24 @@ struct Misc {
     float xrow[DN_ROWS];
     float xnew[DN_ROWS];
     float gsum[64];
-    float G[9 * 16];
+    float G[8 * 16];
     float act[32];
     uint32_t actblk[10];
     float sel_v[MAX_K];
     int sel_i[MAX_K];
-    float ex[MAX_K];
-    float denom;
     int ids[MAX_K];
     float wts[MAX_K];
     int abort_flag;
 };
+
+// Orders LDS accesses between lanes of ONE wave (LDS operations of a wave
+// execute in issue order; this only stops the compiler from reordering them).
+__device__ __forceinline__ void wave_lds_order() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    asm volatile("" ::: "memory");
+}
 
 __device__ __forceinline__ uint64_t ld_tag(const uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -154,13 +162,13 @@ __device__ __forceinline__ bool wait_words(const FusedParams& P, Misc* m, uint32
 
 __device__ __forceinline__ void stamp(const FusedParams& P, int l, int ev) {
     if (P.trace && threadIdx.x == 0)
-        P.trace[((int64_t)blockIdx.x * (P.L + 1) + (l + 1)) * 16 + ev] = wall_clock64();
+        P.trace[((int64_t)blockIdx.x * (P.L + 1) + (l + 1)) * TRACE_SLOTS + ev] = wall_clock64();
 }
 // shader-clock stamp (slots 4 and 8): with the wall-clock slots it gives the
 // effective core clock over a layer
 __device__ __forceinline__ void stamp_clk(const FusedParams& P, int l, int ev) {
     if (P.trace && threadIdx.x == 0)
-        P.trace[((int64_t)blockIdx.x * (P.L + 1) + (l + 1)) * 16 + ev] = clock64();
+        P.trace[((int64_t)blockIdx.x * (P.L + 1) + (l + 1)) * TRACE_SLOTS + ev] = clock64();
 }
 
 // Lane-quad exchanges by DPP (quad_perm): a few cycles, unlike ds_bpermute.
@@ -221,58 +229,68 @@ __device__ void quantize_x_lds(const FusedParams& P, const float* x, uint8_t* q8
 
 // Top-k by rank over logits in LDS (rank = number of logits that sort before:
 // larger, or equal with a lower index, as the stable descending sort of
-// ft-model/src/lib.rs:1491-1492), then softmax over the chosen
+// ft-model/src/lib.rs:1491-1492; NaN sorts after every number, where the
+// reference would panic), then softmax over the chosen
 // (ft-model/src/lib.rs:1494-1503): exp(l - l_max), summed in rank order.
-// Four threads share one logit's comparisons (E <= 512, E % 4 == 0).
+// Four threads share one logit's comparisons (E <= 512, E % 16 == 0). LDS
+// reads are issued in batches of 8 float4 so that one wait covers them, and
+// the softmax runs in wave 0 from registers.
+__device__ __forceinline__ bool sorts_before(float u, int j, float v, int i, bool v_nan) {
+    return (u > v) || (u == v && j < i) || (v_nan && (!(u == u) ? j < i : true));
+}
+
 __device__ void topk_rank(const FusedParams& P, Misc* m, int layer) {
     const int E = P.E, K = P.K, t = threadIdx.x;
-    if (t < K) {                 // defaults keep every id in range even for NaN logits
-        m->sel_i[t] = t;
-        m->sel_v[t] = m->logits[t];
-    }
-    const int q = E >> 2;        // comparisons per thread
+    const int q = E >> 2;        // comparisons per thread, a multiple of 4
     for (int base = 0; base < E * 4; base += FT_THREADS) {
         const int k = base + t;
         const int i = k >> 2, part = k & 3;
         const bool live = i < E;
         const float v = m->logits[live ? i : 0];
-        const float4* l4 = reinterpret_cast<const float4*>(m->logits + part * q);
+        const bool v_nan = !(v == v);
         int rank = 0;
-#pragma unroll 8
-        for (int j4 = 0; j4 < (q >> 2); ++j4) {
-            const float4 u = l4[j4];
-            const int j = part * q + 4 * j4;
-            rank += (u.x > v) || (u.x == v && j < i);
-            rank += (u.y > v) || (u.y == v && j + 1 < i);
-            rank += (u.z > v) || (u.z == v && j + 2 < i);
-            rank += (u.w > v) || (u.w == v && j + 3 < i);
+        for (int c0 = 0; c0 < q; c0 += 32) {
+            const float4* l4 = reinterpret_cast<const float4*>(m->logits + part * q + c0);
+            const int n4 = min(8, (q - c0) >> 2);
+            float4 u[8];
+#pragma unroll
+            for (int j4 = 0; j4 < 8; ++j4) u[j4] = l4[min(j4, n4 - 1)];
+#pragma unroll
+            for (int j4 = 0; j4 < 8; ++j4) {
+                if (j4 < n4) {
+                    const int j = part * q + c0 + 4 * j4;
+                    rank += sorts_before(u[j4].x, j, v, i, v_nan);
+                    rank += sorts_before(u[j4].y, j + 1, v, i, v_nan);
+                    rank += sorts_before(u[j4].z, j + 2, v, i, v_nan);
+                    rank += sorts_before(u[j4].w, j + 3, v, i, v_nan);
+                }
+            }
         }
         rank += quad_xor1i(rank);
         rank += quad_xor2i(rank);
-        __syncthreads();  // the defaults above are written before any rank lands
-        if (live && part == 0 && rank < K) {
+        if (live && part == 0 && rank < K) {  // ranks are distinct: each slot written once
             m->sel_i[rank] = i;
             m->sel_v[rank] = v;
         }
     }
     __syncthreads();
-    if (t < K) m->ex[t] = expf_portable(m->sel_v[t] - m->sel_v[0]);
-    __syncthreads();
-    if (t == 0) {
+    if (t < 64) {  // wave 0: softmax from registers
+        const float v0 = m->sel_v[0];
+        const float vt = m->sel_v[min(t, K - 1)];
+        const int it = m->sel_i[min(t, K - 1)];
+        const float ex = expf_portable(vt - v0);
         float denom = 0.0f;
-        for (int j = 0; j < K; ++j) denom = denom + m->ex[j];
-        m->denom = denom;
-    }
-    __syncthreads();
-    if (t < K) {
-        float w = m->ex[t] / m->denom;
-        const int e = m->sel_i[t];
-        if (P.escale) w = w * P.escale[(int64_t)layer * E + e];
-        m->ids[t] = e;
-        m->wts[t] = w;
-        if (blockIdx.x == 0) {
-            if (P.ids_out) P.ids_out[layer * K + t] = e;
-            if (P.wts_out) P.wts_out[layer * K + t] = w;
+        for (int j = 0; j < K; ++j)  // in rank order, as the reference's iterator sum
+            denom = denom + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), j));
+        if (t < K) {
+            float w = ex / denom;
+            if (P.escale) w = w * P.escale[(int64_t)layer * E + it];
+            m->ids[t] = it;
+            m->wts[t] = w;
+            if (blockIdx.x == 0) {
+                if (P.ids_out) P.ids_out[layer * K + t] = it;
+                if (P.wts_out) P.wts_out[layer * K + t] = w;
+            }
         }
     }
     __syncthreads();
@@ -280,34 +298,41 @@ __device__ void topk_rank(const FusedParams& P, Misc* m, int layer) {
 
 // Logit unit: final logits of experts [e0, e0+16) in the R-order: chunk
 // partials summed in chunk order per group of C = H/128 chunks (from 0.0f),
-// then the 8 group sums in order (from 0.0f), then + bias.
+// then the 8 group sums in order (from 0.0f), then + bias. C is a compile-time
+// constant so that each thread's C partials are read from LDS in one batch.
+template <int C>
 __device__ bool logit_task(const FusedParams& P, Misc* m, uint32_t epoch, int task, int layer, uint32_t tag_in,
                            uint32_t tag_out, uint32_t* scratch) {
-    const int E = P.E, NC = P.H / DN_ROWS, C = P.H >> 7;
-    const int e0 = task * 16, ne = min(16, E - e0);
-    auto idx = [=](int i) { return (int64_t)(i / ne) * E + e0 + i % ne; };
-    if (!wait_words(P, m, epoch, P.part_t, NC * ne, idx, tag_in, scratch)) return false;
+    const int E = P.E, NC = P.H / DN_ROWS;
+    const int e0 = task * 16;  // E % 16 == 0: every task has 16 experts
+    auto idx = [=](int i) { return (int64_t)(i >> 4) * E + e0 + (i & 15); };
+    if (!wait_words(P, m, epoch, P.part_t, NC * 16, idx, tag_in, scratch)) return false;
+    stamp(P, layer - 1, 16);
     float* G = m->G;  // [8][16] group sums
     const int t = threadIdx.x;
     if (t < 8 * 16) {
         const int g = t >> 4, el = t & 15;
-        if (el < ne) {
-            float gs = 0.0f;
-#pragma unroll 8
-            for (int c = g * C; c < (g + 1) * C; ++c) gs = gs + __uint_as_float(scratch[c * ne + el]);
-            G[g * 16 + el] = gs;
-        }
+        float pv[C];
+#pragma unroll
+        for (int c = 0; c < C; ++c) pv[c] = __uint_as_float(scratch[(g * C + c) * 16 + el]);
+        float gs = 0.0f;
+#pragma unroll
+        for (int c = 0; c < C; ++c) gs = gs + pv[c];
+        G[g * 16 + el] = gs;
     }
     __syncthreads();
-    if (t < 16) {
+    if (t < 16 * NREP) {
+        const int el = t & 15;
+        float gv[8];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) gv[g] = G[g * 16 + el];
         float total = 0.0f;
-        for (int g = 0; g < 8; ++g) total = total + G[g * 16 + t];
-        if (P.bias && t < ne) total = total + P.bias[(int64_t)layer * E + e0 + t];
-        G[8 * 16 + t] = total;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) total = total + gv[g];
+        if (P.bias) total = total + P.bias[(int64_t)layer * E + e0 + el];
+        st_tag(P.lg_t + (t >> 4) * P.rs_lg + e0 + el, tag_out, __float_as_uint(total));
     }
-    __syncthreads();
-    if (t < 16 * NREP && (t & 15) < ne)
-        st_tag(P.lg_t + (t >> 4) * P.rs_lg + e0 + (t & 15), tag_out, __float_as_uint(G[8 * 16 + (t & 15)]));
+    stamp(P, layer - 1, 17);
     __syncthreads();
     return true;
 }
@@ -384,7 +409,8 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         if (P.dbg_x && t < DN_ROWS) P.dbg_x[w * DN_ROWS + t] = m->xrow[t];
         stamp(P, -1, 7);
     }
-    if (is_red && !logit_task(P, m, epoch, w, 0, tag_x(0), tag_g(0), reinterpret_cast<uint32_t*>(red))) return;
+    if (is_red && !logit_task<2 * BPW>(P, m, epoch, w, 0, tag_x(0), tag_g(0), reinterpret_cast<uint32_t*>(red)))
+        return;
     stamp(P, -1, 9);
     if (is_gu) {
         for (int i = t; i < H; i += FT_THREADS) x_l[i] = P.x_in[i];
@@ -415,11 +441,13 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
             const uint8_t* T = layer_banks + (int64_t)m->ids[p] * P.expert_bytes + (int64_t)jb * nb * 1152;
             const uint8_t* Ts = T + b0 * 128 + r * 2;
             const uint8_t* Tq = T + nb * 128 + b0 * 1024 + r * 16;
+            // all 16-byte loads first, then the 2-byte scales: interleaving
+            // them (35 loads a wave in flight) more than doubled the time to
+            // stream a layer in a standalone probe
 #pragma unroll
-            for (int i = 0; i < BPW; ++i) {
-                sc[i] = *reinterpret_cast<const uint16_t*>(Ts + i * 128);
-                qv[i] = *reinterpret_cast<const uint4*>(Tq + i * 1024);
-            }
+            for (int i = 0; i < BPW; ++i) qv[i] = *reinterpret_cast<const uint4*>(Tq + i * 1024);
+#pragma unroll
+            for (int i = 0; i < BPW; ++i) sc[i] = *reinterpret_cast<const uint16_t*>(Ts + i * 128);
         }
         // ---- down unit: its K tiles go straight into the registers of the
         // threads that use them (thread (pp, rr, s) holds row rr of expert pp,
@@ -436,8 +464,13 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
 #pragma unroll
             for (int k = 0; k < DB; ++k) {
                 const int b = min(s4 + 4 * k, nbj - 1);
-                dsc[k] = *reinterpret_cast<const uint16_t*>(D + b * 32 + rr * 2);
                 dq[k] = *reinterpret_cast<const uint4*>(D + nbj * 32 + b * 256 + rr * 16);
+            }
+            asm volatile("" ::: "memory");  // keep the scale loads behind the 16-byte loads
+#pragma unroll
+            for (int k = 0; k < DB; ++k) {
+                const int b = min(s4 + 4 * k, nbj - 1);
+                dsc[k] = *reinterpret_cast<const uint16_t*>(D + b * 32 + rr * 2);
             }
             const uint4* rsrc = reinterpret_cast<const uint4*>(
                 P.routers + ((int64_t)(l + 1 < L ? l + 1 : l) * (H / DN_ROWS) + wd) * E * DN_ROWS);
@@ -455,26 +488,32 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
             }
             red[wave * 64 + r] = acc;
             __syncthreads();
-            if (t < 64) {
+            if (t < 64) {  // wave 0 finishes the unit: only wave-local ordering from here
+                float rv[FT_WAVES];
+#pragma unroll
+                for (int v = 0; v < FT_WAVES; ++v) rv[v] = red[v * 64 + t];
                 float s = 0.0f;
-                for (int v = 0; v < FT_WAVES; ++v) s = s + red[v * 64 + t];
-                m->gsum[t] = s;
+#pragma unroll
+                for (int v = 0; v < FT_WAVES; ++v) s = s + rv[v];
                 if (P.dbg_gu) {
                     const int row = t < 32 ? jb * 32 + t : I + jb * 32 + (t - 32);
                     P.dbg_gu[((int64_t)l * K + p) * 2 * I + row] = s;
                 }
+                m->gsum[t] = s;
+                wave_lds_order();
+                if (t < 32) m->act[t] = gelu_tanh(s) * m->gsum[t + 32];
+                wave_lds_order();
+                if (t < 4) quantize_block_quad(m->act, t, m->actblk);
+                wave_lds_order();
+                for (int i = t; i < 10 * NREP; i += 64) {  // 80 contiguous bytes per replica
+                    const int k = i % 10, rep = i / 10;
+                    st_tag(P.act_t + rep * P.rs_act + ((int64_t)p * nbj + jb) * 10 + k, tag_a(l), m->actblk[k]);
+                    if (P.dbg_act && rep == 0)
+                        reinterpret_cast<uint32_t*>(P.dbg_act + (((int64_t)l * K + p) * nbj + jb) * Q8_BLK)[k] =
+                            m->actblk[k];
+                }
             }
-            __syncthreads();
-            if (t < 32) m->act[t] = gelu_tanh(m->gsum[t]) * m->gsum[t + 32];
-            __syncthreads();
-            if (t < 4) quantize_block_quad(m->act, t, m->actblk);
-            __syncthreads();
-            if (t < 10 * NREP) {  // 80 contiguous bytes per replica
-                const int k = t % 10, rep = t / 10;
-                st_tag(P.act_t + rep * P.rs_act + ((int64_t)p * nbj + jb) * 10 + k, tag_a(l), m->actblk[k]);
-                if (P.dbg_act && rep == 0)
-                    reinterpret_cast<uint32_t*>(P.dbg_act + (((int64_t)l * K + p) * nbj + jb) * Q8_BLK)[k] = m->actblk[k];
-            }
+            stamp(P, l, 19);
         }
         stamp(P, l, 2);
         // ---- land the router chunk in LDS (after the gate|up compute, which
@@ -511,12 +550,20 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
             acc += quad_xor1(acc);
             acc += quad_xor2(acc);
             if (s4 == 0 && pp < K) m->y[pp][rr] = acc;
+            stamp(P, l, 20);
             __syncthreads();
             if (t < DN_ROWS) {
+                float yv[MAX_K], wv[MAX_K];
+#pragma unroll
+                for (int q = 0; q < MAX_K; ++q) {
+                    yv[q] = m->y[q][t];
+                    wv[q] = m->wts[q];
+                }
                 float h = 0.0f;
-                for (int q = 0; q < K; ++q) {
-                    const float part = m->y[q][t] * m->wts[q];
-                    h = h + part;
+#pragma unroll
+                for (int q = 0; q < MAX_K; ++q) {
+                    const float part = yv[q] * wv[q];
+                    h = q < K ? h + part : h;
                 }
                 const float xn = m->xrow[t] + h;
                 m->xnew[t] = xn;
@@ -532,7 +579,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         if (l + 1 == L) break;
         // ---- logits of layer l+1; meanwhile gate|up units take x_{l+1} ----
         if (is_red &&
-            !logit_task(P, m, epoch, w, l + 1, tag_x(l + 1), tag_g(l + 1), reinterpret_cast<uint32_t*>(red)))
+            !logit_task<2 * BPW>(P, m, epoch, w, l + 1, tag_x(l + 1), tag_g(l + 1), reinterpret_cast<uint32_t*>(red)))
             return;
         stamp(P, l, 9);
         if (is_gu) {

@@ -199,12 +199,17 @@ __global__ __launch_bounds__(64) void k_router_logits(const float* W, const floa
     }
 }
 
-// (value, index) order of the router: larger logit first, then lower index.
+// (value, index) order of the router: larger logit first, then lower index;
+// NaN after every number (the reference's sort would panic on one).
 __device__ __forceinline__ bool topk_better(float v1, int i1, float v2, int i2, int E) {
     if (i2 >= E) return i1 < E;
     if (i1 >= E) return false;
-    if (v1 > v2) return true;
-    if (v1 < v2) return false;
+    const bool n1 = !(v1 == v1), n2 = !(v2 == v2);
+    if (n1 != n2) return n2;
+    if (!n1) {
+        if (v1 > v2) return true;
+        if (v1 < v2) return false;
+    }
     return i1 < i2;
 }
 

@@ -217,7 +217,7 @@ int ft_hip_pack_router_fused(ft_hip_ctx* ctx, void* stream, const float* src, fl
  * launch at a time (launches on one stream may reuse it). dbg_* (NULL in
  * normal use) receive per-layer stage values for tests: dbg_gu
  * [L][K][2I] gate|up sums, dbg_act [L][K][I/32] q8 blocks, dbg_x [L+1][H];
- * dbg_trace [workgroups][L+1][16] u64 receives wall-clock stamps of each
+ * dbg_trace [workgroups][L+1][32] u64 receives wall-clock stamps of each
  * workgroup's phases (slot 0 = the layer-0 router prologue), the analogue of
  * the reference's per-section Profile counters (ft-model/src/lib.rs:252-296).
  * The workgroup count is max(top_k*inter/32, hidden/16, ceil(E/16)). */

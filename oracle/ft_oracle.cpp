@@ -444,7 +444,14 @@ int orc_topk_softmax(const float* logits, int E, int k, const float* expert_scal
     if (k > E || k <= 0) return -1;
     std::vector<int> order((size_t)E);
     for (int i = 0; i < E; ++i) order[(size_t)i] = i;
-    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return logits[b] < logits[a]; });
+    // descending and stable (ties keep index order); NaN after every number,
+    // where the reference's partial_cmp().unwrap() would panic
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
+        const float x = logits[a], y = logits[b];
+        if (std::isnan(x)) return false;
+        if (std::isnan(y)) return true;
+        return y < x;
+    });
     float mx = logits[order[0]];
     std::vector<float> ex((size_t)k);
     float denom = 0.0f;

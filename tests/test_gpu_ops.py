@@ -202,6 +202,9 @@ def test_topk_router_bit_exact(gemv, orc, E, k):
     lg = rng.standard_normal((S, E)).astype(np.float32)
     lg[1, :] = 0.5                                  # all tied
     lg[2, rng.integers(0, E, E // 2)] = lg[2, 0]    # many ties
+    lg[3, rng.integers(0, E, max(1, E // 3))] = np.nan  # NaN ranks after every number
+    lg[4, : (E + 1) // 2] = -0.0                    # signed zeros tie
+    lg[4, (E + 1) // 2:] = 0.0
     scale = (rng.random(E) + 0.5).astype(np.float32)
     for es in (None, scale):
         ids = torch.zeros(S * k, dtype=torch.int32, device=DEV)
@@ -211,7 +214,9 @@ def test_topk_router_bit_exact(gemv, orc, E, k):
         for s in range(S):
             ie, we = orc.topk_softmax(lg[s], k, es, orc.GELU_PORTABLE)
             assert np.array_equal(ids[s], ie)
-            assert np.array_equal(wts[s].view(np.uint32), we.view(np.uint32))
+            nan = np.isnan(we)                      # a chosen NaN makes every weight NaN
+            assert np.array_equal(np.isnan(wts[s]), nan)
+            assert np.array_equal(wts[s][~nan].view(np.uint32), we[~nan].view(np.uint32))
 
 
 def test_reduce_pairs_weighted_bit_exact(gemv, orc):

@@ -378,6 +378,18 @@ def test_topk_ties_prefer_lower_index(orc):
     assert list(ids) == [0, 1, 2]
 
 
+def test_topk_nan_sorts_last_and_signed_zeros_tie(orc):
+    """The reference panics on a NaN logit (partial_cmp().unwrap()); this build
+    ranks NaN after every number, NaNs among themselves by index. -0.0 == 0.0,
+    so they tie and the lower index goes first."""
+    lg = np.array([np.nan, -5.0, np.nan, 0.0, -0.0, -np.inf, 2.0], np.float32)
+    ids, w = orc.topk_softmax(lg, 7)
+    assert list(ids) == [6, 3, 4, 1, 5, 0, 2]
+    lg = np.array([-0.0, 0.0, np.nan], np.float32)
+    ids, _ = orc.topk_softmax(lg, 2)
+    assert list(ids) == [0, 1]
+
+
 def test_topk_expert_scale(orc):
     lg = np.array([3.0, 1.0, 2.0, 0.0], np.float32)
     es = np.array([2.0, 1.0, 0.5, 1.0], np.float32)
