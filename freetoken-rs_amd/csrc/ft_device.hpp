@@ -52,6 +52,21 @@ __device__ __forceinline__ int block_dot(const uint4 w, const int* a, int qsum) 
     return dot_q4u_q8(w, a) - 8 * qsum;
 }
 
+// The same from two 16-byte halves of the q8 values (low: values 0..15,
+// high: 16..31), for operands read from LDS as 16-byte vectors.
+__device__ __forceinline__ int block_dot_v(const uint4 w, const uint4 lo, const uint4 hi, int qsum) {
+    int s = 0;
+    s = __builtin_amdgcn_sdot4((int)(w.x & 0x0F0F0F0Fu), (int)lo.x, s, false);
+    s = __builtin_amdgcn_sdot4((int)(w.y & 0x0F0F0F0Fu), (int)lo.y, s, false);
+    s = __builtin_amdgcn_sdot4((int)(w.z & 0x0F0F0F0Fu), (int)lo.z, s, false);
+    s = __builtin_amdgcn_sdot4((int)(w.w & 0x0F0F0F0Fu), (int)lo.w, s, false);
+    s = __builtin_amdgcn_sdot4((int)((w.x >> 4) & 0x0F0F0F0Fu), (int)hi.x, s, false);
+    s = __builtin_amdgcn_sdot4((int)((w.y >> 4) & 0x0F0F0F0Fu), (int)hi.y, s, false);
+    s = __builtin_amdgcn_sdot4((int)((w.z >> 4) & 0x0F0F0F0Fu), (int)hi.z, s, false);
+    s = __builtin_amdgcn_sdot4((int)((w.w >> 4) & 0x0F0F0F0Fu), (int)hi.w, s, false);
+    return s - 8 * qsum;
+}
+
 // ---------------------------------------------------------------------------
 // q8 quantisation of one 32-value block held one value per lane in a 32-lane
 // half of a wavefront (ft-core/src/q4_0.rs:62-78): d = amax/127 (IEEE
@@ -94,57 +109,76 @@ __device__ __forceinline__ void q8_store_half(uint8_t* blk, int l, const Q8Lane&
 // e^r by Horner with fma (Cody & Waite, Software Manual for the Elementary
 // Functions, 1980).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ double exp_portable(double x) {
+// Coefficients: [0] INV_LN2, [1] LN2_HI, [2] LN2_LO, [3..16] Taylor
+// coefficients of e^r from 1/13! down to 1 (Horner order).
+struct ExpTable {
+    double k[17];
+};
+
+__host__ __device__ constexpr ExpTable exp_table() {
+    return ExpTable{{1.44269504088896338700e+00, 6.93147180369123816490e-01, 1.90821492927058770002e-10,
+                     1.6059043836821614599e-10, 2.0876756987868098979e-09, 2.5052108385441718775e-08,
+                     2.7557319223985890653e-07, 2.7557319223985890653e-06, 2.4801587301587301566e-05,
+                     1.9841269841269841253e-04, 1.3888888888888888889e-03, 8.3333333333333332177e-03,
+                     4.1666666666666664354e-02, 1.6666666666666665741e-01, 5.0000000000000000000e-01, 1.0, 1.0}};
+}
+
+// T: anything indexable by [0..16] holding exp_table(): the constexpr table
+// itself, or a copy in LDS (a persistent kernel reads it from there so the
+// compiler does not keep 17 f64 constants live in registers across its loop).
+template <typename T>
+__device__ __forceinline__ double exp_portable_t(double x, const T& k) {
     if (x > 700.0) return __builtin_huge_val();
     if (x < -740.0) return 0.0;
-    const double LN2_HI = 6.93147180369123816490e-01;
-    const double LN2_LO = 1.90821492927058770002e-10;
-    const double INV_LN2 = 1.44269504088896338700e+00;
-    double n = floor(fma(x, INV_LN2, 0.5));
-    double r = fma(-n, LN2_HI, x);
-    r = fma(-n, LN2_LO, r);
-    double p = 1.6059043836821614599e-10;
-    p = fma(p, r, 2.0876756987868098979e-09);
-    p = fma(p, r, 2.5052108385441718775e-08);
-    p = fma(p, r, 2.7557319223985890653e-07);
-    p = fma(p, r, 2.7557319223985890653e-06);
-    p = fma(p, r, 2.4801587301587301566e-05);
-    p = fma(p, r, 1.9841269841269841253e-04);
-    p = fma(p, r, 1.3888888888888888889e-03);
-    p = fma(p, r, 8.3333333333333332177e-03);
-    p = fma(p, r, 4.1666666666666664354e-02);
-    p = fma(p, r, 1.6666666666666665741e-01);
-    p = fma(p, r, 5.0000000000000000000e-01);
-    p = fma(p, r, 1.0);
-    p = fma(p, r, 1.0);
+    double n = floor(fma(x, k[0], 0.5));
+    double r = fma(-n, k[1], x);
+    r = fma(-n, k[2], r);
+    double p = k[3];
+#pragma unroll
+    for (int i = 4; i < 17; ++i) p = fma(p, r, k[i]);
     return ldexp(p, (int)n);
 }
 
-__device__ __forceinline__ float tanh_portable(float z) {
+struct ExpConst {
+    __device__ __forceinline__ double operator[](int i) const { return exp_table().k[i]; }
+};
+
+__device__ __forceinline__ double exp_portable(double x) { return exp_portable_t(x, ExpConst{}); }
+
+template <typename T>
+__device__ __forceinline__ float tanh_portable_t(float z, const T& k) {
     double a = fabs((double)z);
     double t;
     if (a >= 9.5) t = 1.0;
     else if (a < 0x1p-13) t = a;
     else {
-        double e = exp_portable(2.0 * a);
+        double e = exp_portable_t(2.0 * a, k);
         t = 1.0 - 2.0 / (e + 1.0);
     }
     float tf = (float)t;
     return signbit(z) ? -tf : tf;
 }
 
-__device__ __forceinline__ float expf_portable(float x) { return (float)exp_portable((double)x); }
+__device__ __forceinline__ float tanh_portable(float z) { return tanh_portable_t(z, ExpConst{}); }
+
+template <typename T>
+__device__ __forceinline__ float expf_portable_t(float x, const T& k) { return (float)exp_portable_t((double)x, k); }
+
+__device__ __forceinline__ float expf_portable(float x) { return expf_portable_t(x, ExpConst{}); }
 
 // gelu_tanh (ft-model/src/lib.rs:435-437), left to right, no contraction.
-__device__ __forceinline__ float gelu_tanh(float g) {
+template <typename T>
+__device__ __forceinline__ float gelu_tanh_t(float g, const T& k) {
     float c = 0.044715f * g;
     c = c * g;
     c = c * g;
     float inner = g + c;
-    float t = tanh_portable(0.7978845608f * inner);
+    float t = tanh_portable_t(0.7978845608f * inner, k);
     float h = 0.5f * g;
     return h * (1.0f + t);
 }
+
+__device__ __forceinline__ float gelu_tanh(float g) { return gelu_tanh_t(g, ExpConst{}); }
 
 // ---------------------------------------------------------------------------
 // Seeded generator (same definition as the host oracle): value i of a tensor

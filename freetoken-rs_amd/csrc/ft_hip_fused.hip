@@ -4,31 +4,35 @@
 // Why one kernel: at batch 1 a Gemma-shaped layer streams only ~28 MB, i.e.
 // ~4.6 us at the MI355X's achievable HBM rate, while every kernel boundary
 // costs several us. The layer is therefore run as dataflow between resident
-// workgroups. Its all-to-all dependencies (gate|up -> down; down -> router
-// chunk partials -> logits -> top-k) are handed over through single-writer,
-// epoch-tagged 64-bit words in device memory: bits 63..32 = epoch tag,
-// bits 31..0 = payload. Producers write with device-coherent (agent-scope)
-// relaxed stores; consumers read with device-coherent loads, keep the words
-// that already carry the expected tag and re-read only the missing ones.
-// Data and flag travel in the same word, so a hand-over costs one memory
-// round trip once the producer is done, with no read-modify-write contention
-// and no cache-maintenance fences (the alternatives measured 1.4-20 us per
-// barrier on this part).
+// workgroups, handing over through single-writer, epoch-tagged 64-bit words
+// in device memory: bits 63..32 = epoch tag, bits 31..0 = payload.
+// Producers write with device-coherent (agent-scope) relaxed stores;
+// consumers read with device-coherent loads, keep the words that already
+// carry the expected tag and re-read only the missing ones. Data and flag
+// travel in the same word, so there is no read-modify-write contention and no
+// cache-maintenance fence (the alternatives measured 1.4-20 us per barrier on
+// this part).
 //
-// Work of one layer (G shape: H 2816, I 704, top-8), 176 workgroups:
-//   gate|up units : (routed expert p, 32 output columns jb) -> 64 rows (32
-//                   gate, 32 up) x H/32 blocks streamed into registers by 8
-//                   waves; GELU*up -> one q8 block published.
-//   down units    : 16 output rows x the K routed experts, weights prefetched
-//                   into LDS (global_load_lds); combine x_{l+1} = x_l + sum_p
-//                   w_p y_p in pair order; router chunk partials of layer l+1
-//                   over those 16 rows (R-order) and the 16 x values published.
-//   logit units   : 16 experts each: R-order sums of all chunk partials (+bias)
-//                   -> 16 final logits published.
-//   every WG      : reads the logits, rank-based top-k and softmax; gate|up
-//                   workgroups read x_{l+1} and quantize it while the logits
-//                   are still being reduced.
-// Weight layouts are lossless repacks of q4_0 with exactly q4_0's byte count.
+// Workgroups of one layer (G shape: H 2816, I 704, E 128, top-8): 184.
+//   expert unit (p, j), 176 of them, p = routed slot (w % K), j = w / K:
+//     gate|up : 64 rows (32 gate, 32 up) of expert ids[p] for act block j
+//               (32 columns), H/32 blocks streamed into registers by 8 waves;
+//               GELU*up -> one q8 block, published (hop A).
+//     down    : rows 128j..128j+127 of expert ids[p] (one 16-row tile per
+//               wave), weights streamed into registers with the gate|up
+//               tile; waits for the 22 act blocks of ITS expert only (hop A),
+//               publishes y_p for its 128 rows (hop B).
+//   group unit g, 8 of them (one per R-order group of H/8 rows):
+//     waits for y_p of its rows for every p (hop B); x_{l+1} = x_l + sum_p
+//     w_p y_p in pair order; router chunk partials of its H/128 chunks and
+//     their group sum for every expert (router weights of the next layer were
+//     streamed into registers meanwhile); q8 of its x rows; publishes group
+//     sums + q8 blocks (hop C), double-buffered by layer parity.
+//   every workgroup: reads the 8 group sums of every expert (and, expert
+//     units, the 88 q8 blocks of x_{l+1}) (hop C), logits = sum over groups
+//     in order + bias, top-k and softmax.
+// Three hand-overs per layer; the largest (C) carries 8 x (E + H/8/32*10)
+// words. Weight layouts are lossless repacks of q4_0 with its byte count.
 
 #include "ft_device.hpp"
 #include "ft_runtime.hpp"
@@ -41,12 +45,13 @@ constexpr int FT_THREADS = 512;
 constexpr int FT_WAVES = FT_THREADS / 64;
 constexpr int GU_BPW_MAX = 16;  // gate|up blocks per wave held in flight (H <= 4096)
 constexpr int MAX_K = 8;
-constexpr int MAX_E = 512;
-constexpr int DN_ROWS = 16;     // rows per down tile / router chunk
+constexpr int MAX_E = 128;      // group partials use four threads per expert
+constexpr int NGROUP = 8;       // R-order groups, one group unit each
+constexpr int DN_ROWS = 16;     // rows per router chunk and per down tile
+constexpr int DN_UNIT = DN_ROWS * FT_WAVES;  // rows per down unit: one tile per wave
 constexpr int WAIT_U = 8;       // tagged words per thread per wait (n <= 4096)
 constexpr int POLL_SLEEP = 1;   // s_sleep units (64 clocks) between polls
-constexpr int NREP = 8;         // replicas of each broadcast buffer: one per XCD, so each
-                                // copy is polled by ~1/8 of the workgroups
+constexpr int NREP = 8;         // replicas of the group broadcast, one per XCD
 constexpr int CTL_EPOCH = 0;    // control words (u32 indices)
 constexpr int CTL_ABORT = 32;
 constexpr int TRACE_SLOTS = 32; // stamps per workgroup per layer in the debug trace
@@ -60,33 +65,32 @@ struct FusedParams {
     float* x_out;               // [H]
     int32_t* ids_out;           // [L][K] or null
     float* wts_out;             // [L][K] or null
-    uint64_t* act_t;            // tagged [NREP][K][I/32][10]
-    uint64_t* x_t;              // tagged [NREP][H]
-    uint64_t* part_t;           // tagged [H/16][E]
-    uint64_t* lg_t;             // tagged [NREP][E]
-    int64_t rs_act, rs_x, rs_lg;  // replica strides (words)
+    uint64_t* act_t;            // tagged [K][I/32][10]
+    uint64_t* y_t;              // tagged [K][H]
+    uint64_t* gq_t;             // tagged [2][NREP][NGROUP][gq_stride]: E group sums, then qw q8 words
+    int64_t rs_gq;              // replica stride (words); the parity stride is NREP * rs_gq
     uint32_t* ctl;              // [CTL_EPOCH] epoch, [CTL_ABORT] abort epoch
     float* dbg_gu;              // [L][K][2I] or null
     uint8_t* dbg_act;           // [L][K][I/32][40] or null
     float* dbg_x;               // [L+1][H] or null
-    uint64_t* trace;            // [grid][L+1][16] wall-clock stamps or null
+    uint64_t* trace;            // [grid][L+1][TRACE_SLOTS] wall-clock stamps or null
     int64_t expert_bytes, gu_bytes;
     int H, I, E, K, L;
-    int n_gu, n_dn, n_red;
+    int n_gu, n_dn, n_unit;     // K*I/32 gate|up units, K*H/128 down units, max of the two
+    int gq_stride, qw;          // words per group in the broadcast; q8 words per group ((H/8)/32*10)
     int spin_limit;
-    int o_x, o_q8x, o_act8, o_wr, o_red, o_misc, lds_bytes;
+    int o_q8x, o_act8, o_red, o_gq, o_gx, o_gy, o_gp, o_misc, lds_bytes;
 };
 
-struct Misc {
+struct Misc {                   // placed 16-byte aligned
+    uint64_t keys[MAX_E + 8];   // rank keys of the logits, four padded rows (16-byte aligned)
+    double expk[17];            // exp_table() in LDS (see exp_portable_t)
     float logits[MAX_E];
-    float y[MAX_K][DN_ROWS];
-    float xrow[DN_ROWS];
-    float xnew[DN_ROWS];
     float gsum[64];
-    float G[8 * 16];
     float act[32];
     uint32_t actblk[10];
     float sel_v[MAX_K];
+    float sel_x[MAX_K];
     int sel_i[MAX_K];
     int ids[MAX_K];
     float wts[MAX_K];
@@ -113,8 +117,8 @@ __device__ __forceinline__ uint32_t ld_ctl(const uint32_t* p) {
 }
 
 // Block-wide wait until the n (<= 4096) tagged words src[idx(i)] all carry
-// `tag`; payloads land in dst[i] (LDS). Each thread re-reads only its words
-// still missing, so a consumer that arrives early costs little traffic.
+// `tag`; payloads land in dst[didx(i)] (LDS). Each thread re-reads only its
+// words still missing, so a consumer that arrives early costs little traffic.
 // Bounded: after spin_limit polls (or when another workgroup has aborted) it
 // records the abort and returns false.
 template <typename Idx, typename DIdx>
@@ -160,15 +164,14 @@ __device__ __forceinline__ bool wait_words(const FusedParams& P, Misc* m, uint32
     return wait_words(P, m, epoch, src, n, idx, tag, dst, [](int i) { return i; });
 }
 
+// Trace slots (per workgroup and layer; layer -1 = prologue): 0 layer start
+// (routing known), 1 loads issued, 2 gate|up data in, 3 act published,
+// 4 act read, 5 down dots, 6 y published, 8 group: y read, 9 group: x
+// combined, 10 group: partials, 11 group: published, 12 broadcast read,
+// 13 logits, 14 top-k done.
 __device__ __forceinline__ void stamp(const FusedParams& P, int l, int ev) {
     if (P.trace && threadIdx.x == 0)
         P.trace[((int64_t)blockIdx.x * (P.L + 1) + (l + 1)) * TRACE_SLOTS + ev] = wall_clock64();
-}
-// shader-clock stamp (slots 4 and 8): with the wall-clock slots it gives the
-// effective core clock over a layer
-__device__ __forceinline__ void stamp_clk(const FusedParams& P, int l, int ev) {
-    if (P.trace && threadIdx.x == 0)
-        P.trace[((int64_t)blockIdx.x * (P.L + 1) + (l + 1)) * TRACE_SLOTS + ev] = clock64();
 }
 
 // Lane-quad exchanges by DPP (quad_perm): a few cycles, unlike ds_bpermute.
@@ -217,74 +220,70 @@ __device__ __forceinline__ void quantize_block_quad(const float* v, int part, ui
     }
 }
 
-// q8-quantize x (H floats in LDS) into LDS blocks, one lane quad per block.
-__device__ void quantize_x_lds(const FusedParams& P, const float* x, uint8_t* q8x) {
-    const int nb = P.H >> 5;
-    for (int base = 0; base < nb * 4; base += FT_THREADS) {
-        const int i = base + threadIdx.x;
-        const int b = min(i >> 2, nb - 1);  // surplus quads redo the last block (same values)
-        quantize_block_quad(x + 32 * b, i & 3, reinterpret_cast<uint32_t*>(q8x + b * Q8_BLK));
-    }
+// Top-k by rank (rank = number of logits that sort before: larger, or equal
+// with a lower index, as the stable descending sort of
+// ft-model/src/lib.rs:1491-1492; NaN after every number, where the reference
+// would panic), then softmax over the chosen (ft-model/src/lib.rs:1494-1503):
+// exp(l - l_max), summed in rank order. Each logit carries a 64-bit key
+// (monotone float bits, then the complemented index) so that "sorts before"
+// is one unsigned compare; four threads share one logit's E comparisons.
+__device__ __forceinline__ uint64_t rank_key(float v, int i) {
+    v = v + 0.0f;  // -0 -> +0: equal values tie on the index
+    const uint32_t b = __float_as_uint(v);
+    uint32_t mo = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    mo = v == v ? mo : 0u;  // NaN below -inf
+    return ((uint64_t)mo << 32) | (0xFFFFFFFFu - (uint32_t)i);
 }
 
-// Top-k by rank over logits in LDS (rank = number of logits that sort before:
-// larger, or equal with a lower index, as the stable descending sort of
-// ft-model/src/lib.rs:1491-1492; NaN sorts after every number, where the
-// reference would panic), then softmax over the chosen
-// (ft-model/src/lib.rs:1494-1503): exp(l - l_max), summed in rank order.
-// Four threads share one logit's comparisons (E <= 512, E % 16 == 0). LDS
-// reads are issued in batches of 8 float4 so that one wait covers them, and
-// the softmax runs in wave 0 from registers.
-__device__ __forceinline__ bool sorts_before(float u, int j, float v, int i, bool v_nan) {
-    return (u > v) || (u == v && j < i) || (v_nan && (!(u == u) ? j < i : true));
-}
+// Rank keys sit in four rows (one per comparing thread of a logit), padded
+// by 16 bytes so the rows start in different LDS banks.
+__device__ __forceinline__ int key_slot(int i, int q) { return (i / q) * (q + 2) + i % q; }
 
 __device__ void topk_rank(const FusedParams& P, Misc* m, int layer) {
     const int E = P.E, K = P.K, t = threadIdx.x;
-    const int q = E >> 2;        // comparisons per thread, a multiple of 4
-    for (int base = 0; base < E * 4; base += FT_THREADS) {
-        const int k = base + t;
-        const int i = k >> 2, part = k & 3;
-        const bool live = i < E;
-        const float v = m->logits[live ? i : 0];
-        const bool v_nan = !(v == v);
+    const int q = E >> 2;  // comparisons per thread: even, at most 32 (E % 16 == 0, E <= 128)
+    {
+        const int i = min(t >> 2, E - 1), part = t & 3;
+        const uint64_t ki = m->keys[key_slot(i, q)];
+        const uint4* kk = reinterpret_cast<const uint4*>(m->keys + part * (q + 2));  // two keys per uint4
+        const int n2 = q >> 1;
+        uint4 u[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) u[j] = kk[min(j, n2 - 1)];
         int rank = 0;
-        for (int c0 = 0; c0 < q; c0 += 32) {
-            const float4* l4 = reinterpret_cast<const float4*>(m->logits + part * q + c0);
-            const int n4 = min(8, (q - c0) >> 2);
-            float4 u[8];
 #pragma unroll
-            for (int j4 = 0; j4 < 8; ++j4) u[j4] = l4[min(j4, n4 - 1)];
-#pragma unroll
-            for (int j4 = 0; j4 < 8; ++j4) {
-                if (j4 < n4) {
-                    const int j = part * q + c0 + 4 * j4;
-                    rank += sorts_before(u[j4].x, j, v, i, v_nan);
-                    rank += sorts_before(u[j4].y, j + 1, v, i, v_nan);
-                    rank += sorts_before(u[j4].z, j + 2, v, i, v_nan);
-                    rank += sorts_before(u[j4].w, j + 3, v, i, v_nan);
-                }
-            }
+        for (int j = 0; j < 16; ++j) {
+            const uint64_t k0 = ((uint64_t)u[j].y << 32) | u[j].x;
+            const uint64_t k1 = ((uint64_t)u[j].w << 32) | u[j].z;
+            const int c = (int)(k0 > ki) + (int)(k1 > ki);
+            rank += j < n2 ? c : 0;
         }
         rank += quad_xor1i(rank);
         rank += quad_xor2i(rank);
-        if (live && part == 0 && rank < K) {  // ranks are distinct: each slot written once
+        if ((t >> 2) < E && part == 0 && rank < K) {  // ranks are distinct: each slot written once
             m->sel_i[rank] = i;
-            m->sel_v[rank] = v;
+            m->sel_v[rank] = m->logits[i];
         }
     }
-    __syncthreads();
-    if (t < 64) {  // wave 0: softmax from registers
+    __syncthreads();  // every rank slot written before wave 0 reads them
+    stamp(P, layer - 1, 15);
+    if (t < 64) {  // wave 0: softmax
         const float v0 = m->sel_v[0];
         const float vt = m->sel_v[min(t, K - 1)];
         const int it = m->sel_i[min(t, K - 1)];
-        const float ex = expf_portable(vt - v0);
+        const float ex = expf_portable_t(vt - v0, m->expk);
+        if (t < K) m->sel_x[t] = ex;
+        wave_lds_order();
+        float xv[MAX_K];
+#pragma unroll
+        for (int j = 0; j < MAX_K; ++j) xv[j] = m->sel_x[j];
         float denom = 0.0f;
-        for (int j = 0; j < K; ++j)  // in rank order, as the reference's iterator sum
-            denom = denom + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), j));
+#pragma unroll
+        for (int j = 0; j < MAX_K; ++j)  // in rank order, as the reference's iterator sum
+            denom = j < K ? denom + xv[j] : denom;
         if (t < K) {
             float w = ex / denom;
-            if (P.escale) w = w * P.escale[(int64_t)layer * E + it];
+            if (P.escale) w = w * P.escale[(int64_t)layer * E + min(max(it, 0), E - 1)];
             m->ids[t] = it;
             m->wts[t] = w;
             if (blockIdx.x == 0) {
@@ -293,174 +292,248 @@ __device__ void topk_rank(const FusedParams& P, Misc* m, int layer) {
             }
         }
     }
+    stamp(P, layer - 1, 16);
     __syncthreads();
 }
 
-// Logit unit: final logits of experts [e0, e0+16) in the R-order: chunk
-// partials summed in chunk order per group of C = H/128 chunks (from 0.0f),
-// then the 8 group sums in order (from 0.0f), then + bias. C is a compile-time
-// constant so that each thread's C partials are read from LDS in one batch.
-template <int C>
-__device__ bool logit_task(const FusedParams& P, Misc* m, uint32_t epoch, int task, int layer, uint32_t tag_in,
-                           uint32_t tag_out, uint32_t* scratch) {
-    const int E = P.E, NC = P.H / DN_ROWS;
-    const int e0 = task * 16;  // E % 16 == 0: every task has 16 experts
-    auto idx = [=](int i) { return (int64_t)(i >> 4) * E + e0 + (i & 15); };
-    if (!wait_words(P, m, epoch, P.part_t, NC * 16, idx, tag_in, scratch)) return false;
-    stamp(P, layer - 1, 16);
-    float* G = m->G;  // [8][16] group sums
-    const int t = threadIdx.x;
-    if (t < 8 * 16) {
-        const int g = t >> 4, el = t & 15;
-        float pv[C];
+// Logits from the NGROUP group sums gs[NGROUP][E] (R-order: groups in order
+// from 0.0f, then + bias), then top-k and softmax into m->ids / m->wts.
+__device__ void route(const FusedParams& P, Misc* m, const float* gs, int layer) {
+    const int E = P.E, t = threadIdx.x;
+    if (t < E) {
+        float gv[NGROUP];
 #pragma unroll
-        for (int c = 0; c < C; ++c) pv[c] = __uint_as_float(scratch[(g * C + c) * 16 + el]);
-        float gs = 0.0f;
-#pragma unroll
-        for (int c = 0; c < C; ++c) gs = gs + pv[c];
-        G[g * 16 + el] = gs;
-    }
-    __syncthreads();
-    if (t < 16 * NREP) {
-        const int el = t & 15;
-        float gv[8];
-#pragma unroll
-        for (int g = 0; g < 8; ++g) gv[g] = G[g * 16 + el];
+        for (int g = 0; g < NGROUP; ++g) gv[g] = gs[g * E + t];
         float total = 0.0f;
 #pragma unroll
-        for (int g = 0; g < 8; ++g) total = total + gv[g];
-        if (P.bias) total = total + P.bias[(int64_t)layer * E + e0 + el];
-        st_tag(P.lg_t + (t >> 4) * P.rs_lg + e0 + el, tag_out, __float_as_uint(total));
+        for (int g = 0; g < NGROUP; ++g) total = total + gv[g];
+        if (P.bias) total = total + P.bias[(int64_t)layer * E + t];
+        m->logits[t] = total;
+        m->keys[key_slot(t, E >> 2)] = rank_key(total, t);
     }
-    stamp(P, layer - 1, 17);
     __syncthreads();
-    return true;
+    stamp(P, layer - 1, 13);
+    topk_rank(P, m, layer);
 }
 
-// Router chunk partials of one 16-row chunk (R-order: fma chain over the rows
-// in order, from 0.0f) and the chunk's x values, published with tag.
-__device__ void publish_chunk(const FusedParams& P, const float* wr, const float* xv, int chunk, uint32_t tag) {
+// Router weights of `layer` for group g into registers: thread (e = t/4,
+// q = t%4) holds chunks q, q+4, ... of the group (16 rows each).
+template <int CPT, int C>
+__device__ __forceinline__ void group_load_router(const FusedParams& P, int layer, int g, float4 (&wv)[CPT][4]) {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));  // keeps the per-thread offsets inside the layer loop
     const int E = P.E;
-    for (int e = threadIdx.x; e < E; e += FT_THREADS) {
-        const float4* w4 = reinterpret_cast<const float4*>(wr + e * DN_ROWS);
-        float p = 0.0f;
+    const int e = min(t >> 2, E - 1), q = t & 3;
+    const float* base = P.routers + (int64_t)layer * (P.H / DN_ROWS) * E * DN_ROWS;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float4 a = w4[q];
-            p = fmaf(a.x, xv[4 * q + 0], p);
-            p = fmaf(a.y, xv[4 * q + 1], p);
-            p = fmaf(a.z, xv[4 * q + 2], p);
-            p = fmaf(a.w, xv[4 * q + 3], p);
-        }
-        st_tag(P.part_t + (int64_t)chunk * E + e, tag, __float_as_uint(p));
-    }
-    if (threadIdx.x < DN_ROWS * NREP) {
-        const int r = threadIdx.x & (DN_ROWS - 1), rep = threadIdx.x / DN_ROWS;
-        st_tag(P.x_t + rep * P.rs_x + chunk * DN_ROWS + r, tag, __float_as_uint(xv[r]));
+    for (int i = 0; i < CPT; ++i) {
+        const int c = min(q + 4 * i, C - 1);
+        const float4* s = reinterpret_cast<const float4*>(base + ((int64_t)(g * C + c) * E + e) * DN_ROWS);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) wv[i][k] = s[k];
     }
 }
 
-// Copy `bytes` (multiple of 16) from global to LDS with global_load_lds: each
-// wave moves 1 KB per instruction, lanes past the end are masked off.
-__device__ __forceinline__ void prefetch_lds(const uint8_t* src, uint8_t* dst, int bytes) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int off = wave * 1024; off < bytes; off += FT_WAVES * 1024) {
-        const int o = off + lane * 16;
-        if (o < bytes)
-            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src + o),
-                                             reinterpret_cast<void*>(dst + off), 16, 0, 0);
+// Group g's share of the router for its x rows gx (H/8 floats in LDS), in
+// the R-order: chunk partials (fma chain over the chunk's 16 rows, from
+// 0.0f), summed over the group's C chunks in order (from 0.0f); and the q8
+// blocks of the rows. Publishes [E sums][qw q8 words] tagged, to each replica.
+template <int CPT, int C>
+__device__ void group_publish(const FusedParams& P, int g, const float4 (&wv)[CPT][4], const float* gx, float* gp,
+                              uint32_t* q8w, uint64_t* dst, uint32_t tag, int sl) {
+    const int E = P.E, t = threadIdx.x;
+    const int e = t >> 2, q = t & 3;
+    if (e < E) {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int c = q + 4 * i;
+            if (c < C) {
+                const float4* x4 = reinterpret_cast<const float4*>(gx + c * DN_ROWS);
+                float s = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float4 xv = x4[k];
+                    s = fmaf(wv[i][k].x, xv.x, s);
+                    s = fmaf(wv[i][k].y, xv.y, s);
+                    s = fmaf(wv[i][k].z, xv.z, s);
+                    s = fmaf(wv[i][k].w, xv.w, s);
+                }
+                gp[c * E + e] = s;
+            }
+        }
+    }
+    const int nbq = (P.H / NGROUP) >> 5;  // q8 blocks per group; one lane quad each
+    if (t < 4 * nbq) quantize_block_quad(gx + 32 * (t >> 2), t & 3, q8w + (t >> 2) * 10);
+    stamp(P, sl, 20);
+    __syncthreads();
+    stamp(P, sl, 21);
+    if (t < E) {
+        float pv[C];
+#pragma unroll
+        for (int c = 0; c < C; ++c) pv[c] = gp[c * E + t];
+        float s = 0.0f;
+#pragma unroll
+        for (int c = 0; c < C; ++c) s = s + pv[c];
+        gp[C * E + t] = s;
+    }
+    __syncthreads();
+    stamp(P, sl, 22);
+    const int n = E + P.qw;
+    for (int i = t; i < n * NREP; i += FT_THREADS) {
+        const int rep = i / n, k = i - rep * n;
+        const uint32_t v = k < E ? __float_as_uint(gp[C * E + k]) : q8w[k - E];
+        st_tag(dst + rep * P.rs_gq + (int64_t)g * P.gq_stride + k, tag, v);
     }
 }
 
 // BPW: gate|up blocks per wave, exactly H/32/8; DB: down blocks per thread,
-// ceil(I/32/4) rounded up (the loads are unconditional so they issue back to
-// back; surplus down blocks re-read a valid one and are masked).
-template <int BPW, int DB>
+// ceil(I/32/4) (surplus blocks re-read a valid one and are masked); CPT:
+// router chunks per group-unit thread, ceil(H/128/4). Loads are
+// unconditional so that they issue back to back.
+template <int BPW, int DB, int CPT>
 __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P) {
+    constexpr int C = 2 * BPW;  // router chunks per group = H/128
     extern __shared__ __align__(16) uint8_t lds[];
-    float* x_l = reinterpret_cast<float*>(lds + P.o_x);
-    uint8_t* q8x = lds + P.o_q8x;
     uint8_t* act8 = lds + P.o_act8;
-    float* wr = reinterpret_cast<float*>(lds + P.o_wr);
     float* red = reinterpret_cast<float*>(lds + P.o_red);
+    // expert units: [NGROUP][E] group sums, then the q8 of x as [H/32][8]
+    // qs words (16-byte aligned) and [H/32] (d, qsum) pairs
+    uint32_t* gq = reinterpret_cast<uint32_t*>(lds + P.o_gq);
+    const uint4* xq4 = reinterpret_cast<const uint4*>(gq + NGROUP * P.E);
+    const int2* xdp = reinterpret_cast<const int2*>(gq + NGROUP * P.E + (P.H >> 5) * 8);
+    float* gx = reinterpret_cast<float*>(lds + P.o_gx);
+    float* gy = reinterpret_cast<float*>(lds + P.o_gy);
+    float* gp = reinterpret_cast<float*>(lds + P.o_gp);
     Misc* m = reinterpret_cast<Misc*>(lds + P.o_misc);
 
     const int w = blockIdx.x, t = threadIdx.x;
     const int H = P.H, I = P.I, E = P.E, K = P.K, L = P.L;
-    const int nb = H >> 5, nbj = I >> 5;
-    const int dn_tile = nbj * 288;  // bytes of one 16-row down tile
-    const bool is_gu = w < P.n_gu, is_dn = w < P.n_dn, is_red = w < P.n_red;
+    const int nb = H >> 5, nbj = I >> 5, HG = H / NGROUP;
     if (t == 0) m->abort_flag = 0;
+    if (t < 17) m->expk[t] = exp_table().k[t];
+    __syncthreads();
     const uint32_t epoch = ld_ctl(P.ctl + CTL_EPOCH);
-    auto tag_x = [&](int l) { return epoch + 4u * l + 1u; };
-    auto tag_g = [&](int l) { return epoch + 4u * l + 2u; };
-    auto tag_a = [&](int l) { return epoch + 4u * l + 3u; };
+    auto tag_g = [&](int l) { return epoch + 4u * l + 1u; };
+    auto tag_a = [&](int l) { return epoch + 4u * l + 2u; };
+    auto tag_y = [&](int l) { return epoch + 4u * l + 3u; };
+    auto gq_buf = [&](int l) { return P.gq_t + (int64_t)(l & 1) * NREP * P.rs_gq; };
     auto ident = [](int i) { return (int64_t)i; };
+    const int rep = w % NREP;  // workgroups are dealt to the 8 XCDs round-robin
 
-    // ---- prologue: router of layer 0 on x_in ----
+    if (w >= P.n_unit) {
+        // ======================= group unit =======================
+        const int g = w - P.n_unit, r0 = g * HG;
+        uint32_t* q8w = reinterpret_cast<uint32_t*>(gp + (C + 1) * E);
+        float4 wv[CPT][4];
+        auto gidx = [=](int i) { return (int64_t)(i / E) * P.gq_stride + i % E; };
+        stamp(P, -1, 0);
+        group_load_router<CPT, C>(P, 0, g, wv);
+        for (int i = t; i < HG; i += FT_THREADS) {
+            gx[i] = P.x_in[r0 + i];
+            if (P.dbg_x) P.dbg_x[r0 + i] = gx[i];
+        }
+        __syncthreads();
+        group_publish<CPT, C>(P, g, wv, gx, gp, q8w, gq_buf(0), tag_g(0), -1);
+        stamp(P, -1, 11);
+        if (!wait_words(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(0), gq)) return;
+        stamp(P, -1, 12);
+        route(P, m, reinterpret_cast<const float*>(gq), 0);
+        stamp(P, -1, 14);
+        for (int l = 0; l < L; ++l) {
+            stamp(P, l, 0);
+            if (l + 1 < L) group_load_router<CPT, C>(P, l + 1, g, wv);
+            stamp(P, l, 1);
+            auto yidx = [=](int i) { return (int64_t)(i / HG) * H + r0 + i % HG; };
+            if (!wait_words(P, m, epoch, P.y_t, K * HG, yidx, tag_y(l), reinterpret_cast<uint32_t*>(gy))) return;
+            stamp(P, l, 8);
+            // x_{l+1} = x_l + sum_p (y_p * w_p), pairs in routing order
+            // (ft-model/src/lib.rs:1634-1646)
+            for (int r = t; r < HG; r += FT_THREADS) {
+                float yv[MAX_K], wk[MAX_K];
+#pragma unroll
+                for (int q = 0; q < MAX_K; ++q) {
+                    yv[q] = gy[min(q, K - 1) * HG + r];
+                    wk[q] = m->wts[q];
+                }
+                float h = 0.0f;
+#pragma unroll
+                for (int q = 0; q < MAX_K; ++q) {
+                    const float part = yv[q] * wk[q];
+                    h = q < K ? h + part : h;
+                }
+                const float xn = gx[r] + h;
+                gx[r] = xn;
+                if (l == L - 1) P.x_out[r0 + r] = xn;
+                if (P.dbg_x) P.dbg_x[(int64_t)(l + 1) * H + r0 + r] = xn;
+            }
+            __syncthreads();
+            stamp(P, l, 9);
+            if (l + 1 == L) break;
+            group_publish<CPT, C>(P, g, wv, gx, gp, q8w, gq_buf(l + 1), tag_g(l + 1), l);
+            stamp(P, l, 11);
+            if (!wait_words(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(l + 1), gq))
+                return;
+            stamp(P, l, 12);
+            route(P, m, reinterpret_cast<const float*>(gq), l + 1);
+            stamp(P, l, 14);
+        }
+        return;
+    }
+
+    // ======================= expert unit =======================
+    const int p = w % K, j = w / K;
+    const bool gm = w < P.n_gu, dm = w < P.n_dn;  // false: that part of the unit is idle
+    const int dn_tile = nbj * 288;               // bytes of one 16-row down tile
+    const int nq = E + P.qw;
+    auto xidx = [=](int i) {
+        const int g = i / nq;
+        return (int64_t)g * P.gq_stride + (i - g * nq);
+    };
+    auto xdst = [=](int i) {
+        const int g = i / nq, k = i - g * nq;
+        const int kk = k - E, bl = kk / 10, wd = kk - bl * 10, blk = g * (P.qw / 10) + bl;
+        return k < E ? g * E + k : NGROUP * E + (wd >= 2 ? blk * 8 + (wd - 2) : nb * 8 + blk * 2 + wd);
+    };
     stamp(P, -1, 0);
-    if (is_dn) {
-        if (t < DN_ROWS) m->xrow[t] = P.x_in[w * DN_ROWS + t];
-        prefetch_lds(reinterpret_cast<const uint8_t*>(P.routers + (int64_t)w * E * DN_ROWS),
-                     reinterpret_cast<uint8_t*>(wr), E * DN_ROWS * 4);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        publish_chunk(P, wr, m->xrow, w, tag_x(0));
-        if (P.dbg_x && t < DN_ROWS) P.dbg_x[w * DN_ROWS + t] = m->xrow[t];
-        stamp(P, -1, 7);
-    }
-    if (is_red && !logit_task<2 * BPW>(P, m, epoch, w, 0, tag_x(0), tag_g(0), reinterpret_cast<uint32_t*>(red)))
-        return;
-    stamp(P, -1, 9);
-    if (is_gu) {
-        for (int i = t; i < H; i += FT_THREADS) x_l[i] = P.x_in[i];
-        __syncthreads();
-        quantize_x_lds(P, x_l, q8x);
-    }
-    const int rep = w % NREP;  // this workgroup's XCD (workgroups are dealt to the 8 XCDs round-robin)
-    if (!wait_words(P, m, epoch, P.lg_t + rep * P.rs_lg, E, ident, tag_g(0), reinterpret_cast<uint32_t*>(m->logits)))
-        return;
-    topk_rank(P, m, 0);
-    stamp(P, -1, 15);
+    if (!wait_words(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * nq, xidx, tag_g(0), gq, xdst)) return;
+    stamp(P, -1, 12);
+    route(P, m, reinterpret_cast<const float*>(gq), 0);
+    stamp(P, -1, 14);
 
     for (int l = 0; l < L; ++l) {
         stamp(P, l, 0);
-        stamp_clk(P, l, 4);
-        const uint8_t* layer_banks = P.banks + (int64_t)l * E * P.expert_bytes;
-        // ---- gate|up unit: issue its whole tile into registers ----
-        const int wave = t >> 6, r = t & 63;
-        // The gate|up loads and the down/router loads below are issued without
-        // any branch between them (workgroups without a unit re-read a valid
-        // tile), so the compiler issues them back to back and the gate|up
-        // compute waits only for its own loads.
-        const int p = min(w / nbj, K - 1), jb = w % nbj;
+        // per-thread offsets derived from an opaque thread index: hoisted out
+        // of the layer loop they would stay live (and spill) for the kernel
+        int tl = threadIdx.x;
+        asm volatile("" : "+v"(tl));
+        // the routed id is in [0, E) by construction; the clamp keeps any
+        // future logic error from turning into an out-of-bounds weight read
+        const int eid = min(max(m->ids[p], 0), E - 1);
+        const uint8_t* xb = P.banks + ((int64_t)l * E + eid) * P.expert_bytes;
+        const int wave = tl >> 6, r = tl & 63;
+        // ---- gate|up tile j of expert ids[p]: 64 rows x BPW blocks per wave ----
         const int b0 = wave * BPW;
         uint32_t sc[BPW];  // 32-bit: 16-bit elements would be packed in pairs, forcing a wait per load
         uint4 qv[BPW];
         {
-            const uint8_t* T = layer_banks + (int64_t)m->ids[p] * P.expert_bytes + (int64_t)jb * nb * 1152;
+            // a unit without a gate|up tile re-reads tile 0 of expert 0 of
+            // layer 0 (shared by all such units, so it stays in cache)
+            const uint8_t* T = gm ? xb + (int64_t)j * nb * 1152 : P.banks;
             const uint8_t* Ts = T + b0 * 128 + r * 2;
             const uint8_t* Tq = T + nb * 128 + b0 * 1024 + r * 16;
             // all 16-byte loads first, then the 2-byte scales: interleaving
-            // them (35 loads a wave in flight) more than doubled the time to
-            // stream a layer in a standalone probe
+            // them more than doubled the time to stream a layer in a probe
 #pragma unroll
             for (int i = 0; i < BPW; ++i) qv[i] = *reinterpret_cast<const uint4*>(Tq + i * 1024);
 #pragma unroll
             for (int i = 0; i < BPW; ++i) sc[i] = *reinterpret_cast<const uint16_t*>(Ts + i * 128);
         }
-        // ---- down unit: its K tiles go straight into the registers of the
-        // threads that use them (thread (pp, rr, s) holds row rr of expert pp,
-        // blocks s, s+4, ...), and the next router chunk (one uint4 per
-        // thread), right behind the gate|up loads ----
-        const int s4 = t & 3, rr = (t >> 2) & 15, pp = t >> 6;
+        // ---- down unit j: rows 128j + 16*wave + rr, blocks s4, s4+4, ... ----
+        const int s4 = tl & 3, rr = (tl >> 2) & 15;
         uint32_t dsc[DB];
         uint4 dq[DB];
-        uint4 rv = make_uint4(0, 0, 0, 0);
         {
-            const int wd = min(w, P.n_dn - 1);
-            const uint8_t* D = layer_banks + (int64_t)m->ids[min(pp, K - 1)] * P.expert_bytes + P.gu_bytes +
-                               (int64_t)wd * dn_tile;
+            const uint8_t* D = (dm ? xb + (int64_t)(j * FT_WAVES + wave) * dn_tile : P.banks) + P.gu_bytes;
 #pragma unroll
             for (int k = 0; k < DB; ++k) {
                 const int b = min(s4 + 4 * k, nbj - 1);
@@ -472,20 +545,19 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                 const int b = min(s4 + 4 * k, nbj - 1);
                 dsc[k] = *reinterpret_cast<const uint16_t*>(D + b * 32 + rr * 2);
             }
-            const uint4* rsrc = reinterpret_cast<const uint4*>(
-                P.routers + ((int64_t)(l + 1 < L ? l + 1 : l) * (H / DN_ROWS) + wd) * E * DN_ROWS);
-            rv = rsrc[min(t, 4 * E - 1)];
         }
         stamp(P, l, 1);
-        // ---- gate|up compute -> GELU*up -> q8 block, published ----
-        if (is_gu) {
+        // ---- gate|up dots -> GELU*up -> q8 block, published ----
+        if (gm) {
             float acc = 0.0f;
 #pragma unroll
             for (int i = 0; i < BPW; ++i) {
-                const int* xb = reinterpret_cast<const int*>(q8x + (b0 + i) * Q8_BLK);
-                const int diff = block_dot(qv[i], xb + 2, xb[1]);
-                acc = fmaf((float)diff, h2f((uint16_t)sc[i]) * __int_as_float(xb[0]), acc);
+                const uint4 lo = xq4[(b0 + i) * 2], hi = xq4[(b0 + i) * 2 + 1];
+                const int2 dq8 = xdp[b0 + i];
+                const int diff = block_dot_v(qv[i], lo, hi, dq8.y);
+                acc = fmaf((float)diff, h2f((uint16_t)sc[i]) * __int_as_float(dq8.x), acc);
             }
+            stamp(P, l, 2);
             red[wave * 64 + r] = acc;
             __syncthreads();
             if (t < 64) {  // wave 0 finishes the unit: only wave-local ordering from here
@@ -496,105 +568,72 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
 #pragma unroll
                 for (int v = 0; v < FT_WAVES; ++v) s = s + rv[v];
                 if (P.dbg_gu) {
-                    const int row = t < 32 ? jb * 32 + t : I + jb * 32 + (t - 32);
+                    const int row = t < 32 ? j * 32 + t : I + j * 32 + (t - 32);
                     P.dbg_gu[((int64_t)l * K + p) * 2 * I + row] = s;
                 }
                 m->gsum[t] = s;
+                stamp(P, l, 17);
                 wave_lds_order();
-                if (t < 32) m->act[t] = gelu_tanh(s) * m->gsum[t + 32];
+                if (t < 32) m->act[t] = gelu_tanh_t(s, m->expk) * m->gsum[t + 32];
                 wave_lds_order();
+                stamp(P, l, 18);
                 if (t < 4) quantize_block_quad(m->act, t, m->actblk);
                 wave_lds_order();
-                for (int i = t; i < 10 * NREP; i += 64) {  // 80 contiguous bytes per replica
-                    const int k = i % 10, rep = i / 10;
-                    st_tag(P.act_t + rep * P.rs_act + ((int64_t)p * nbj + jb) * 10 + k, tag_a(l), m->actblk[k]);
-                    if (P.dbg_act && rep == 0)
-                        reinterpret_cast<uint32_t*>(P.dbg_act + (((int64_t)l * K + p) * nbj + jb) * Q8_BLK)[k] =
-                            m->actblk[k];
+                stamp(P, l, 19);
+                if (t < 10) {
+                    st_tag(P.act_t + ((int64_t)p * nbj + j) * 10 + t, tag_a(l), m->actblk[t]);
+                    if (P.dbg_act)
+                        reinterpret_cast<uint32_t*>(P.dbg_act + (((int64_t)l * K + p) * nbj + j) * Q8_BLK)[t] =
+                            m->actblk[t];
                 }
             }
-            stamp(P, l, 19);
+            stamp(P, l, 3);
         }
-        stamp(P, l, 2);
-        // ---- land the router chunk in LDS (after the gate|up compute, which
-        // waited only for its own, earlier loads) ----
-        if (is_dn && l + 1 < L && t < 4 * E) reinterpret_cast<uint4*>(wr)[t] = rv;
-        stamp(P, l, 3);
-        // ---- down unit: wait for all act blocks, combine, router partials ----
-        if (is_dn) {
-            // act8 in LDS: [K*nbj blocks x 32 B qs][K*nbj f32 d][K*nbj i32 qsum] (16-B aligned qs)
-            const int nblk = K * nbj;
+        // ---- down: the act blocks of expert slot p, then y_p of 128 rows ----
+        if (dm) {
+            // act8: [nbj blocks x 32 B qs][nbj (d, qsum) pairs] (16-B aligned qs)
             auto act_dst = [=](int i) {
                 const int bi = i / 10, k = i - bi * 10;
-                return k >= 2 ? bi * 8 + (k - 2) : nblk * 8 + (k == 0 ? bi : nblk + bi);
+                return k >= 2 ? bi * 8 + (k - 2) : nbj * 8 + bi * 2 + k;
             };
-            if (!wait_words(P, m, epoch, P.act_t + rep * P.rs_act, nblk * 10, ident, tag_a(l),
+            if (!wait_words(P, m, epoch, P.act_t + (int64_t)p * nbj * 10, nbj * 10, ident, tag_a(l),
                             reinterpret_cast<uint32_t*>(act8), act_dst))
                 return;
-            stamp(P, l, 5);
-            __syncthreads();
-            float acc = 0.0f;
-            {
-                const int* aqs = reinterpret_cast<const int*>(act8);
-                const float* ad = reinterpret_cast<const float*>(act8) + nblk * 8;
-                const int* asum = reinterpret_cast<const int*>(act8) + nblk * 9;
-                const int pc = min(pp, K - 1);
+            stamp(P, l, 4);
+            const uint4* aq4 = reinterpret_cast<const uint4*>(act8);
+            const int2* adp = reinterpret_cast<const int2*>(act8 + nbj * 32);
+            int s4o = threadIdx.x & 3;
+            asm volatile("" : "+v"(s4o));
+            uint4 alo[DB], ahi[DB];
+            int2 ap[DB];
 #pragma unroll
-                for (int k = 0; k < DB; ++k) {
-                    const int b = s4 + 4 * k;
-                    const int bi = pc * nbj + min(b, nbj - 1);
-                    const float v = (float)block_dot(dq[k], aqs + bi * 8, asum[bi]) * (h2f((uint16_t)dsc[k]) * ad[bi]);
-                    acc = b < nbj ? acc + v : acc;
-                }
+            for (int k = 0; k < DB; ++k) {  // all LDS operands first: one wait
+                const int bi = min(s4o + 4 * k, nbj - 1);
+                alo[k] = aq4[bi * 2];
+                ahi[k] = aq4[bi * 2 + 1];
+                ap[k] = adp[bi];
+            }
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < DB; ++k) {
+                const float v = (float)block_dot_v(dq[k], alo[k], ahi[k], ap[k].y) *
+                                (h2f((uint16_t)dsc[k]) * __int_as_float(ap[k].x));
+                acc = s4o + 4 * k < nbj ? acc + v : acc;
             }
             acc += quad_xor1(acc);
             acc += quad_xor2(acc);
-            if (s4 == 0 && pp < K) m->y[pp][rr] = acc;
-            stamp(P, l, 20);
-            __syncthreads();
-            if (t < DN_ROWS) {
-                float yv[MAX_K], wv[MAX_K];
-#pragma unroll
-                for (int q = 0; q < MAX_K; ++q) {
-                    yv[q] = m->y[q][t];
-                    wv[q] = m->wts[q];
-                }
-                float h = 0.0f;
-#pragma unroll
-                for (int q = 0; q < MAX_K; ++q) {
-                    const float part = yv[q] * wv[q];
-                    h = q < K ? h + part : h;
-                }
-                const float xn = m->xrow[t] + h;
-                m->xnew[t] = xn;
-                m->xrow[t] = xn;
-                if (l == L - 1) P.x_out[w * DN_ROWS + t] = xn;
-                if (P.dbg_x) P.dbg_x[(int64_t)(l + 1) * H + w * DN_ROWS + t] = xn;
-            }
-            __syncthreads();
+            stamp(P, l, 5);
+            if (s4 == 0)
+                st_tag(P.y_t + (int64_t)p * H + j * DN_UNIT + wave * DN_ROWS + rr, tag_y(l), __float_as_uint(acc));
             stamp(P, l, 6);
-            if (l + 1 < L) publish_chunk(P, wr, m->xnew, w, tag_x(l + 1));
-            stamp(P, l, 7);
         }
         if (l + 1 == L) break;
-        // ---- logits of layer l+1; meanwhile gate|up units take x_{l+1} ----
-        if (is_red &&
-            !logit_task<2 * BPW>(P, m, epoch, w, l + 1, tag_x(l + 1), tag_g(l + 1), reinterpret_cast<uint32_t*>(red)))
-            return;
-        stamp(P, l, 9);
-        if (is_gu) {
-            if (!wait_words(P, m, epoch, P.x_t + rep * P.rs_x, H, ident, tag_x(l + 1), reinterpret_cast<uint32_t*>(x_l)))
-                return;
-            stamp(P, l, 10);
-            quantize_x_lds(P, x_l, q8x);
-            stamp(P, l, 11);
-        }
-        if (!wait_words(P, m, epoch, P.lg_t + rep * P.rs_lg, E, ident, tag_g(l + 1), reinterpret_cast<uint32_t*>(m->logits)))
+        // ---- routing of layer l+1 and the q8 of x_{l+1}, from the group units ----
+        if (!wait_words(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * nq, xidx, tag_g(l + 1), gq, xdst))
             return;
         stamp(P, l, 12);
-        topk_rank(P, m, l + 1);
-        stamp(P, l, 15);
-        stamp_clk(P, l, 8);
+        route(P, m, reinterpret_cast<const float*>(gq), l + 1);
+        stamp(P, l, 14);
     }
     if (w == 0 && t == 0)
         __hip_atomic_store(P.ctl + CTL_EPOCH, epoch + 4u * (L + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -688,33 +727,42 @@ __global__ void k_fill_u32(uint32_t* p, int64_t n, uint32_t v) {
 // host side
 // ---------------------------------------------------------------------------
 struct WsLayout {
-    int64_t act, x, part, lg, ctl, total;
+    int64_t ctl, act, y, gq, total;
+    int gq_stride, qw;
+    int64_t rs_gq;  // words
 };
 
 WsLayout ws_layout(int64_t H, int64_t I, int64_t E, int64_t K) {
     auto up = [](int64_t v) { return (v + 255) / 256 * 256; };
     WsLayout w{};
+    w.qw = (int)(H / NGROUP / 32 * 10);
+    w.gq_stride = (int)((E + w.qw + 31) / 32 * 32);
+    w.rs_gq = NGROUP * (int64_t)w.gq_stride;
     int64_t off = 0;
     w.ctl = off; off += 256;
-    w.act = off; off += NREP * up(K * (I / 32) * 10 * 8);
-    w.x = off; off += NREP * up(H * 8);
-    w.part = off; off += up((H / DN_ROWS) * E * 8);
-    w.lg = off; off += NREP * up(E * 8);
+    w.act = off; off += up(K * (I / 32) * 10 * 8);
+    w.y = off; off += up(K * H * 8);
+    w.gq = off; off += 2 * NREP * up(w.rs_gq * 8);
     w.total = off;
     return w;
 }
 
+int fused_units(int64_t H, int64_t I, int64_t K, int* n_gu, int* n_dn) {
+    *n_gu = (int)(K * (I / 32));
+    *n_dn = (int)(K * (H / DN_UNIT));
+    return std::max(*n_gu, *n_dn);
+}
+
 int check_fused_shape(const char* nm, int64_t H, int64_t I, int64_t E, int64_t K, int64_t L) {
-    if (H <= 0 || H % 256) return fail(FT_HIP_E_SHAPE, "%s: hidden=%lld must be a positive multiple of 256", nm, (long long)H);
     if (H != 2816 && H != 4096)
         return fail(FT_HIP_E_SHAPE, "%s: hidden=%lld: the fused kernel is built for hidden 2816 and 4096", nm, (long long)H);
-    if (I <= 0 || I % 32) return fail(FT_HIP_E_SHAPE, "%s: inter=%lld must be a positive multiple of 32", nm, (long long)I);
-    if (E <= 0 || E > MAX_E) return fail(FT_HIP_E_SHAPE, "%s: n_experts=%lld not in [1, %d]", nm, (long long)E, MAX_E);
-    if (K <= 0 || K > MAX_K || K > E) return fail(FT_HIP_E_SHAPE, "%s: top_k=%lld not in [1, min(%d, n_experts)]", nm, (long long)K, MAX_K);
+    if (I <= 0 || I % 32 || I / 32 > 32)
+        return fail(FT_HIP_E_SHAPE, "%s: inter=%lld must be a multiple of 32 in [32, 1024]", nm, (long long)I);
+    if (E <= 0 || E > MAX_E || E % 16)
+        return fail(FT_HIP_E_SHAPE, "%s: n_experts=%lld must be a multiple of 16 in [16, %d]", nm, (long long)E, MAX_E);
+    if (K <= 0 || K > MAX_K || K > E)
+        return fail(FT_HIP_E_SHAPE, "%s: top_k=%lld not in [1, min(%d, n_experts)]", nm, (long long)K, MAX_K);
     if (L <= 0) return fail(FT_HIP_E_SHAPE, "%s: n_layers must be positive", nm);
-    if (E % 16) return fail(FT_HIP_E_SHAPE, "%s: n_experts=%lld must be a multiple of 16", nm, (long long)E);
-    if (K * DN_ROWS * 4 > FT_THREADS || I / 32 > 4 * 8 || 4 * E > FT_THREADS)
-        return fail(FT_HIP_E_SHAPE, "%s: needs top_k <= 8, inter <= 1024 and n_experts <= 128; use ft_hip_moe_layer", nm);
     return FT_HIP_OK;
 }
 
@@ -728,6 +776,12 @@ extern "C" int64_t ft_hip_fused_expert_bytes(int64_t hidden, int64_t inter) {
 extern "C" size_t ft_hip_fused_workspace_bytes(int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k) {
     if (hidden <= 0 || hidden % 256 || inter <= 0 || inter % 32 || n_experts <= 0 || top_k <= 0) return 0;
     return (size_t)ws_layout(hidden, inter, n_experts, top_k).total;
+}
+
+extern "C" int ft_hip_fused_workgroups(int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k) {
+    if (hidden <= 0 || hidden % 256 || inter <= 0 || inter % 32 || n_experts <= 0 || top_k <= 0) return -1;
+    int n_gu, n_dn;
+    return fused_units(hidden, inter, top_k, &n_gu, &n_dn) + NGROUP;
 }
 
 extern "C" int ft_hip_fused_workspace_init(ft_hip_ctx* ctx, void* stream, void* workspace, size_t workspace_bytes) {
@@ -804,19 +858,21 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
     P.E = (int)n_experts;
     P.K = (int)top_k;
     P.L = (int)n_layers;
-    P.n_gu = (int)(top_k * (inter / 32));
-    P.n_dn = (int)(hidden / DN_ROWS);
-    P.n_red = (int)((n_experts + 15) / 16);
-    const int nw = std::max(P.n_gu, std::max(P.n_dn, P.n_red));
-    // LDS plan
+    P.n_unit = fused_units(hidden, inter, top_k, &P.n_gu, &P.n_dn);
+    const int nw = P.n_unit + NGROUP;
+    P.gq_stride = wl.gq_stride;
+    P.qw = wl.qw;
+    P.rs_gq = (wl.rs_gq * 8 + 255) / 256 * 256 / 8;
+    // LDS plan (expert units and group units use disjoint regions)
+    const int C = (int)(hidden / 128), HG = (int)(hidden / NGROUP), nbj = (int)(inter / 32);
     auto up16 = [](int v) { return (v + 15) / 16 * 16; };
     int off = 0;
-    P.o_x = off; off += up16((int)hidden * 4);
-    P.o_q8x = off; off += up16((int)(hidden / 32) * Q8_BLK);
-    P.o_act8 = off; off += up16((int)(top_k * (inter / 32)) * Q8_BLK);
-    P.o_wr = off; off += up16((int)n_experts * DN_ROWS * 4);
-    const int red_bytes = std::max(FT_WAVES * 64 * 4, (int)(hidden / DN_ROWS) * 16 * 4);
-    P.o_red = off; off += up16(red_bytes);
+    P.o_act8 = off; off += up16(nbj * Q8_BLK);
+    P.o_red = off; off += up16(FT_WAVES * 64 * 4);
+    P.o_gq = off; off += up16((NGROUP * (int)n_experts + (int)(hidden / 32) * 10) * 4);
+    P.o_gx = off; off += up16(HG * 4);
+    P.o_gy = off; off += up16((int)top_k * HG * 4);
+    P.o_gp = off; off += up16(((C + 1) * (int)n_experts + wl.qw) * 4);
     P.o_misc = off; off += up16((int)sizeof(Misc));
     P.lds_bytes = off;
     if (off > 160 * 1024)
@@ -835,14 +891,9 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
     P.x_out = x_out;
     P.ids_out = ids;
     P.wts_out = wts;
-    auto up256 = [](int64_t v) { return (v + 255) / 256 * 256; };
     P.act_t = (uint64_t*)(ws + wl.act);
-    P.x_t = (uint64_t*)(ws + wl.x);
-    P.rs_act = up256(top_k * (inter / 32) * 10 * 8) / 8;
-    P.rs_x = up256(hidden * 8) / 8;
-    P.rs_lg = up256(n_experts * 8) / 8;
-    P.part_t = (uint64_t*)(ws + wl.part);
-    P.lg_t = (uint64_t*)(ws + wl.lg);
+    P.y_t = (uint64_t*)(ws + wl.y);
+    P.gq_t = (uint64_t*)(ws + wl.gq);
     P.ctl = (uint32_t*)(ws + wl.ctl);
     P.dbg_gu = dbg_gu;
     P.dbg_act = (uint8_t*)dbg_act;
@@ -852,14 +903,13 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
     P.gu_bytes = 2 * inter * (hidden / 32) * 18;
     P.spin_limit = 1 << 21;
     void* args[] = {&P};
-    // blocks per wave of a gate|up tile: the kernel keeps exactly that many in flight
+    // the kernel keeps exactly H/256 gate|up blocks per wave in flight
     const bool db6 = inter / 32 <= 24;
-    const void* kern = hidden == 2816 ? (db6 ? reinterpret_cast<const void*>(k_moe_stack_fused<11, 6>)
-                                             : reinterpret_cast<const void*>(k_moe_stack_fused<11, 8>))
-                                      : (db6 ? reinterpret_cast<const void*>(k_moe_stack_fused<GU_BPW_MAX, 6>)
-                                             : reinterpret_cast<const void*>(k_moe_stack_fused<GU_BPW_MAX, 8>));
-    hipError_t e = hipLaunchCooperativeKernel(kern, dim3((unsigned)nw),
-                                              dim3(FT_THREADS), args, (unsigned)P.lds_bytes,
+    const void* kern = hidden == 2816 ? (db6 ? reinterpret_cast<const void*>(k_moe_stack_fused<11, 6, 6>)
+                                             : reinterpret_cast<const void*>(k_moe_stack_fused<11, 8, 6>))
+                                      : (db6 ? reinterpret_cast<const void*>(k_moe_stack_fused<GU_BPW_MAX, 6, 8>)
+                                             : reinterpret_cast<const void*>(k_moe_stack_fused<GU_BPW_MAX, 8, 8>));
+    hipError_t e = hipLaunchCooperativeKernel(kern, dim3((unsigned)nw), dim3(FT_THREADS), args, (unsigned)P.lds_bytes,
                                               reinterpret_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(FT_HIP_E_LAUNCH, "%s: cooperative launch failed: %s", nm, hipGetErrorString(e));
     return FT_HIP_OK;

@@ -169,7 +169,7 @@ class FusedStack:
 
     def n_workgroups(self):
         s = self.m.shape
-        return max(s.top_k * s.inter // 32, s.hidden // 16, (s.n_experts + 15) // 16)
+        return self.g.fused_workgroups(s.hidden, s.inter, s.n_experts, s.top_k)
 
     def run(self, x_in, x_out, ids=None, wts=None, dbg_gu=None, dbg_act=None, dbg_x=None, trace=None,
             stream=None):

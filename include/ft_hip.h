@@ -185,6 +185,13 @@ int ft_hip_moe_layer(ft_hip_ctx* ctx, void* stream, const float* x, float* x_out
  * entry points (q8 quants, per-block int32 dots, router R-order and top-k are
  * bit-identical; f32 sums may differ in order).
  *
+ * Workgroups: K*max(I/32, H/128) expert units (routed slot p, index j: the
+ * gate|up rows of act block j and the down rows 128j..128j+127 of expert
+ * ids[p]) plus 8 group units (one per R-order group of H/8 rows: combine,
+ * router share, q8 of x) -- see ft_hip_fused_workgroups. Supported shapes:
+ * hidden 2816 or 4096, inter a multiple of 32 up to 1024, n_experts a
+ * multiple of 16 up to 128, top_k <= 8.
+ *
  * Fused expert layout (a lossless repack of q4_0, same byte count):
  *   expert = [gate|up tiles][down tiles];
  *   gate|up tile jb (I/32 tiles) = 64 rows (gate rows 32jb..32jb+31, then up
@@ -194,6 +201,10 @@ int ft_hip_moe_layer(ft_hip_ctx* ctx, void* stream, const float* x, float* x_out
  * Fused router layout: [L][H/16 chunks][E][16] f32. */
 int64_t ft_hip_fused_expert_bytes(int64_t hidden, int64_t inter);
 size_t ft_hip_fused_workspace_bytes(int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k);
+
+/* Grid size of ft_hip_moe_stack_fused for this shape (-1 on a bad shape);
+ * sizes the dbg_trace buffer. */
+int ft_hip_fused_workgroups(int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k);
 
 /* Zero a fused workspace and set its epoch; call once after allocating it,
  * and again after a launch reported FT_HIP_E_TIMEOUT. */
@@ -218,9 +229,8 @@ int ft_hip_pack_router_fused(ft_hip_ctx* ctx, void* stream, const float* src, fl
  * normal use) receive per-layer stage values for tests: dbg_gu
  * [L][K][2I] gate|up sums, dbg_act [L][K][I/32] q8 blocks, dbg_x [L+1][H];
  * dbg_trace [workgroups][L+1][32] u64 receives wall-clock stamps of each
- * workgroup's phases (slot 0 = the layer-0 router prologue), the analogue of
- * the reference's per-section Profile counters (ft-model/src/lib.rs:252-296).
- * The workgroup count is max(top_k*inter/32, hidden/16, ceil(E/16)). */
+ * workgroup's phases (row 0 = the prologue), the analogue of the
+ * reference's per-section Profile counters (ft-model/src/lib.rs:252-296). */
 int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float* x_in, float* x_out, int64_t hidden,
                            int64_t inter, int64_t n_experts, int64_t top_k, int64_t n_layers,
                            const void* banks, const float* routers, const float* bias,

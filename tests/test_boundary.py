@@ -89,3 +89,11 @@ def test_shape_errors_are_reported_before_any_gpu_call():
     rc, _ = _err(L.ft_hip_moe_layer(None, None, P, P, 1, 2816, 704, 128, 8, P, None, None, P, 1 << 30, 1, P, P,
                                     P, ws - 1))
     assert rc == ft_hip.E_SHAPE                                          # workspace too small
+
+
+def test_fused_workgroups_formula():
+    """K*max(I/32, H/128) expert units plus one unit per R-order group."""
+    assert ft_hip.Q4Gemv.fused_workgroups(2816, 704, 128, 8) == 8 * 22 + 8
+    assert ft_hip.Q4Gemv.fused_workgroups(2816, 352, 128, 4) == 4 * 22 + 8
+    assert ft_hip.Q4Gemv.fused_workgroups(4096, 512, 64, 2) == 2 * 32 + 8
+    assert ft_hip.Q4Gemv.fused_workgroups(2816, 700, 128, 8) == -1
