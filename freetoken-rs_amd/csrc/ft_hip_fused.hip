@@ -22,6 +22,10 @@
 //               wave), weights streamed into registers with the gate|up
 //               tile; waits for the 22 act blocks of ITS expert only (hop A),
 //               publishes y_p for its 128 rows (hop B).
+//     All units of slot p run on XCD p (workgroups are dealt to XCDs
+//     round-robin; each checks this at start through the XCD id register),
+//     so hop A stays in that XCD's L2: plain stores, agent-scope polls.
+//     If the placement check fails, hop A stores write through instead.
 //   group unit g, 8 of them (one per R-order group of H/8 rows):
 //     waits for y_p of its rows for every p (hop B); x_{l+1} = x_l + sum_p
 //     w_p y_p in pair order; router chunk partials of its H/128 chunks and
@@ -68,6 +72,7 @@ struct FusedParams {
     uint64_t* act_t;            // tagged [K][I/32][10]
     uint64_t* y_t;              // tagged [K][H]
     uint64_t* gq_t;             // tagged [2][NREP][NGROUP][gq_stride]: E group sums, then qw q8 words
+    uint64_t* pl_t;             // tagged [grid]: the XCD each workgroup runs on
     int64_t rs_gq;              // replica stride (words); the parity stride is NREP * rs_gq
     uint32_t* ctl;              // [CTL_EPOCH] epoch, [CTL_ABORT] abort epoch
     float* dbg_gu;              // [L][K][2I] or null
@@ -106,11 +111,28 @@ __device__ __forceinline__ void wave_lds_order() {
     asm volatile("" ::: "memory");
 }
 
+// Tagged words use system-scope (sc0 sc1) relaxed accesses: in a probe a
+// one-way hand-over took ~0.40 us this way whether or not the two workgroups
+// shared an XCD, against 0.85 us between workgroups of one XCD with
+// agent-scope (sc1) accesses.
 __device__ __forceinline__ uint64_t ld_tag(const uint64_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 __device__ __forceinline__ void st_tag(uint64_t* p, uint32_t tag, uint32_t v) {
-    __hip_atomic_store(p, ((uint64_t)tag << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+// Agent-scope (sc1) load: also sees a plain store made by a workgroup of the
+// same XCD (the line is dirty in the shared L2), which is the fastest
+// hand-over on this part (~0.27 us one-way even with HBM saturated).
+__device__ __forceinline__ uint64_t ld_tag_agent(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Plain store (stays in this XCD's L2): only for consumers on the same XCD.
+__device__ __forceinline__ void st_tag_local(uint64_t* p, uint32_t tag, uint32_t v) {
+    *p = ((uint64_t)tag << 32) | v;
+}
+__device__ __forceinline__ uint32_t xcc_id() {
+    return __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20);  // HW_REG_XCC_ID bits 3:0
 }
 __device__ __forceinline__ uint32_t ld_ctl(const uint32_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -121,9 +143,14 @@ __device__ __forceinline__ uint32_t ld_ctl(const uint32_t* p) {
 // words still missing, so a consumer that arrives early costs little traffic.
 // Bounded: after spin_limit polls (or when another workgroup has aborted) it
 // records the abort and returns false.
-template <typename Idx, typename DIdx>
+__device__ __forceinline__ void trace_value(const FusedParams& P, int l, int ev, uint64_t v) {
+    if (P.trace && threadIdx.x == 0)
+        P.trace[((int64_t)blockIdx.x * (P.L + 1) + (l + 1)) * TRACE_SLOTS + ev] = v;
+}
+
+template <bool AGENT = false, typename Idx, typename DIdx>
 __device__ bool wait_words(const FusedParams& P, Misc* m, uint32_t epoch, const uint64_t* src, int n, Idx idx,
-                           uint32_t tag, uint32_t* dst, DIdx didx) {
+                           uint32_t tag, uint32_t* dst, DIdx didx, int tl = -2, int ts = 0) {
     // An opaque copy of the thread index: keeps the compiler from hoisting the
     // per-call-site address arithmetic out of the layer loop, where it would
     // stay live (in registers) for the whole kernel.
@@ -137,14 +164,21 @@ __device__ bool wait_words(const FusedParams& P, Misc* m, uint32_t epoch, const 
         uint64_t v[WAIT_U];
 #pragma unroll
         for (int u = 0; u < WAIT_U; ++u)
-            v[u] = (pending >> u) & 1 ? ld_tag(src + idx(u * FT_THREADS + tid)) : 0;
+            v[u] = (pending >> u) & 1 ? (AGENT ? ld_tag_agent(src + idx(u * FT_THREADS + tid))
+                                               : ld_tag(src + idx(u * FT_THREADS + tid)))
+                                      : 0;
 #pragma unroll
         for (int u = 0; u < WAIT_U; ++u)
             if (((pending >> u) & 1) && (uint32_t)(v[u] >> 32) == tag) {
                 dst[didx(u * FT_THREADS + tid)] = (uint32_t)v[u];
                 pending &= ~(1u << u);
             }
-        if (__syncthreads_and(pending == 0)) return true;
+        if (it == 0 && tl > -2 && P.trace && threadIdx.x == 0)
+            P.trace[((int64_t)blockIdx.x * (P.L + 1) + (tl + 1)) * TRACE_SLOTS + ts + 4] = wall_clock64();
+        if (__syncthreads_and(pending == 0)) {
+            if (tl > -2) trace_value(P, tl, ts, (uint64_t)(it + 1));  // polls this wait took
+            return true;
+        }
         if ((it & 63) == 63) {
             if (threadIdx.x == 0) {
                 const bool ab = ld_ctl(P.ctl + CTL_ABORT) == epoch || it >= P.spin_limit;
@@ -160,15 +194,19 @@ __device__ bool wait_words(const FusedParams& P, Misc* m, uint32_t epoch, const 
 
 template <typename Idx>
 __device__ __forceinline__ bool wait_words(const FusedParams& P, Misc* m, uint32_t epoch, const uint64_t* src, int n,
-                                           Idx idx, uint32_t tag, uint32_t* dst) {
-    return wait_words(P, m, epoch, src, n, idx, tag, dst, [](int i) { return i; });
+                                           Idx idx, uint32_t tag, uint32_t* dst, int tl = -2, int ts = 0) {
+    return wait_words(P, m, epoch, src, n, idx, tag, dst, [](int i) { return i; }, tl, ts);
 }
 
-// Trace slots (per workgroup and layer; layer -1 = prologue): 0 layer start
-// (routing known), 1 loads issued, 2 gate|up data in, 3 act published,
-// 4 act read, 5 down dots, 6 y published, 8 group: y read, 9 group: x
-// combined, 10 group: partials, 11 group: published, 12 broadcast read,
-// 13 logits, 14 top-k done.
+// Trace slots (per workgroup and layer; layer -1 = prologue), wall-clock
+// stamps unless noted: 0 layer start (routing known), 1 loads issued,
+// 2 gate|up dots done, 3 act published, 4 act read, 5 down dots, 6 y
+// published, 8 group: y read, 9 group: x combined, 11 group: published,
+// 12 broadcast read, 13 logits, 14 top-k done, 15 top-k ranked, 16 softmax,
+// 17-19 gate|up tail (wave sums, GELU, q8), 20-22 group (partials, sync,
+// sums); 24-26 poll count of the broadcast / act / y waits and 28-30 the
+// return of each one's first poll; prologue row: 27 act hand-over local
+// (1/0), 28 XCD id.
 __device__ __forceinline__ void stamp(const FusedParams& P, int l, int ev) {
     if (P.trace && threadIdx.x == 0)
         P.trace[((int64_t)blockIdx.x * (P.L + 1) + (l + 1)) * TRACE_SLOTS + ev] = wall_clock64();
@@ -419,6 +457,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     auto gq_buf = [&](int l) { return P.gq_t + (int64_t)(l & 1) * NREP * P.rs_gq; };
     auto ident = [](int i) { return (int64_t)i; };
     const int rep = w % NREP;  // workgroups are dealt to the 8 XCDs round-robin
+    if (t == 0) st_tag(P.pl_t + w, tag_g(0), xcc_id());
 
     if (w >= P.n_unit) {
         // ======================= group unit =======================
@@ -444,7 +483,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
             if (l + 1 < L) group_load_router<CPT, C>(P, l + 1, g, wv);
             stamp(P, l, 1);
             auto yidx = [=](int i) { return (int64_t)(i / HG) * H + r0 + i % HG; };
-            if (!wait_words(P, m, epoch, P.y_t, K * HG, yidx, tag_y(l), reinterpret_cast<uint32_t*>(gy))) return;
+            if (!wait_words(P, m, epoch, P.y_t, K * HG, yidx, tag_y(l), reinterpret_cast<uint32_t*>(gy), l, 26)) return;
             stamp(P, l, 8);
             // x_{l+1} = x_l + sum_p (y_p * w_p), pairs in routing order
             // (ft-model/src/lib.rs:1634-1646)
@@ -471,7 +510,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
             if (l + 1 == L) break;
             group_publish<CPT, C>(P, g, wv, gx, gp, q8w, gq_buf(l + 1), tag_g(l + 1), l);
             stamp(P, l, 11);
-            if (!wait_words(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(l + 1), gq))
+            if (!wait_words(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(l + 1), gq, l, 24))
                 return;
             stamp(P, l, 12);
             route(P, m, reinterpret_cast<const float*>(gq), l + 1);
@@ -496,6 +535,18 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     };
     stamp(P, -1, 0);
     if (!wait_words(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * nq, xidx, tag_g(0), gq, xdst)) return;
+    // The act hand-over of routed slot p stays in the XCD's L2 (plain stores,
+    // agent-scope polls) when every unit of slot p runs on this workgroup's
+    // XCD; otherwise its stores write through.
+    bool act_local;
+    {
+        const int upe = P.n_unit / K;  // units per routed slot
+        uint32_t* xw = reinterpret_cast<uint32_t*>(red);
+        if (!wait_words(P, m, epoch, P.pl_t, upe, [=](int i) { return (int64_t)(p + K * i); }, tag_g(0), xw)) return;
+        act_local = __syncthreads_and(t >= upe || xw[t] == xcc_id()) != 0;
+        trace_value(P, -1, 27, act_local ? 1u : 0u);
+        trace_value(P, -1, 28, xcc_id());
+    }
     stamp(P, -1, 12);
     route(P, m, reinterpret_cast<const float*>(gq), 0);
     stamp(P, -1, 14);
@@ -581,7 +632,8 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                 wave_lds_order();
                 stamp(P, l, 19);
                 if (t < 10) {
-                    st_tag(P.act_t + ((int64_t)p * nbj + j) * 10 + t, tag_a(l), m->actblk[t]);
+                    if (act_local) st_tag_local(P.act_t + ((int64_t)p * nbj + j) * 10 + t, tag_a(l), m->actblk[t]);
+                    else st_tag(P.act_t + ((int64_t)p * nbj + j) * 10 + t, tag_a(l), m->actblk[t]);
                     if (P.dbg_act)
                         reinterpret_cast<uint32_t*>(P.dbg_act + (((int64_t)l * K + p) * nbj + j) * Q8_BLK)[t] =
                             m->actblk[t];
@@ -596,8 +648,8 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                 const int bi = i / 10, k = i - bi * 10;
                 return k >= 2 ? bi * 8 + (k - 2) : nbj * 8 + bi * 2 + k;
             };
-            if (!wait_words(P, m, epoch, P.act_t + (int64_t)p * nbj * 10, nbj * 10, ident, tag_a(l),
-                            reinterpret_cast<uint32_t*>(act8), act_dst))
+            if (!wait_words<true>(P, m, epoch, P.act_t + (int64_t)p * nbj * 10, nbj * 10, ident, tag_a(l),
+                                  reinterpret_cast<uint32_t*>(act8), act_dst, l, 25))
                 return;
             stamp(P, l, 4);
             const uint4* aq4 = reinterpret_cast<const uint4*>(act8);
@@ -629,7 +681,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         }
         if (l + 1 == L) break;
         // ---- routing of layer l+1 and the q8 of x_{l+1}, from the group units ----
-        if (!wait_words(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * nq, xidx, tag_g(l + 1), gq, xdst))
+        if (!wait_words(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * nq, xidx, tag_g(l + 1), gq, xdst, l, 24))
             return;
         stamp(P, l, 12);
         route(P, m, reinterpret_cast<const float*>(gq), l + 1);
@@ -727,7 +779,7 @@ __global__ void k_fill_u32(uint32_t* p, int64_t n, uint32_t v) {
 // host side
 // ---------------------------------------------------------------------------
 struct WsLayout {
-    int64_t ctl, act, y, gq, total;
+    int64_t ctl, act, y, gq, pl, total;
     int gq_stride, qw;
     int64_t rs_gq;  // words
 };
@@ -743,6 +795,7 @@ WsLayout ws_layout(int64_t H, int64_t I, int64_t E, int64_t K) {
     w.act = off; off += up(K * (I / 32) * 10 * 8);
     w.y = off; off += up(K * H * 8);
     w.gq = off; off += 2 * NREP * up(w.rs_gq * 8);
+    w.pl = off; off += up(((int64_t)std::max(K * (I / 32), K * (H / DN_UNIT)) + NGROUP) * 8);
     w.total = off;
     return w;
 }
@@ -894,6 +947,7 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
     P.act_t = (uint64_t*)(ws + wl.act);
     P.y_t = (uint64_t*)(ws + wl.y);
     P.gq_t = (uint64_t*)(ws + wl.gq);
+    P.pl_t = (uint64_t*)(ws + wl.pl);
     P.ctl = (uint32_t*)(ws + wl.ctl);
     P.dbg_gu = dbg_gu;
     P.dbg_act = (uint8_t*)dbg_act;
