@@ -179,7 +179,7 @@ __device__ bool wait_words(const FusedParams& P, Misc* m, uint32_t epoch, const 
             if (tl > -2) trace_value(P, tl, ts, (uint64_t)(it + 1));  // polls this wait took
             return true;
         }
-        if ((it & 63) == 63) {
+        if ((it & 63) == 63 || it >= P.spin_limit) {
             if (threadIdx.x == 0) {
                 const bool ab = ld_ctl(P.ctl + CTL_ABORT) == epoch || it >= P.spin_limit;
                 if (ab) __hip_atomic_store(P.ctl + CTL_ABORT, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -450,6 +450,10 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     if (t == 0) m->abort_flag = 0;
     if (t < 17) m->expk[t] = exp_table().k[t];
     __syncthreads();
+    // A workspace whose abort word is set (an earlier launch gave up a wait)
+    // is poisoned until ft_hip_fused_workspace_init: its epoch may not have
+    // advanced, so stale tags could match. Do nothing; the status reports it.
+    if (ld_ctl(P.ctl + CTL_ABORT) != 0) return;
     const uint32_t epoch = ld_ctl(P.ctl + CTL_EPOCH);
     auto tag_g = [&](int l) { return epoch + 4u * l + 1u; };
     auto tag_a = [&](int l) { return epoch + 4u * l + 2u; };
@@ -955,7 +959,7 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
     P.trace = dbg_trace;
     P.expert_bytes = ft_hip_fused_expert_bytes(hidden, inter);
     P.gu_bytes = 2 * inter * (hidden / 32) * 18;
-    P.spin_limit = 1 << 21;
+    P.spin_limit = ctx->fused_spin_limit;
     void* args[] = {&P};
     // the kernel keeps exactly H/256 gate|up blocks per wave in flight
     const bool db6 = inter / 32 <= 24;
@@ -963,9 +967,23 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
                                              : reinterpret_cast<const void*>(k_moe_stack_fused<11, 8, 6>))
                                       : (db6 ? reinterpret_cast<const void*>(k_moe_stack_fused<GU_BPW_MAX, 6, 8>)
                                              : reinterpret_cast<const void*>(k_moe_stack_fused<GU_BPW_MAX, 8, 8>));
-    hipError_t e = hipLaunchCooperativeKernel(kern, dim3((unsigned)nw), dim3(FT_THREADS), args, (unsigned)P.lds_bytes,
-                                              reinterpret_cast<hipStream_t>(stream));
-    if (e != hipSuccess) return fail(FT_HIP_E_LAUNCH, "%s: cooperative launch failed: %s", nm, hipGetErrorString(e));
+    // A plain launch: every workgroup must be resident at once, which holds
+    // when the kernel has the device to itself (nw <= CUs, one workgroup per
+    // CU). A cooperative launch guarantees it but costs ~19 us per launch
+    // against ~1-2 us measured here. If residency ever fails, the resident
+    // workgroups give up their bounded waits and the launch reports
+    // FT_HIP_E_TIMEOUT through ft_hip_fused_status; nothing hangs.
+    hipError_t e = hipLaunchKernel(kern, dim3((unsigned)nw), dim3(FT_THREADS), args, (size_t)P.lds_bytes,
+                                   reinterpret_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(FT_HIP_E_LAUNCH, "%s: launch failed: %s", nm, hipGetErrorString(e));
+    return FT_HIP_OK;
+}
+
+extern "C" int ft_hip_fused_set_spin_limit(ft_hip_ctx* ctx, int polls) {
+    clear_error();
+    if (!ctx) return fail(FT_HIP_E_INVALID, "fused_set_spin_limit: null ctx");
+    if (polls < 0) return fail(FT_HIP_E_SHAPE, "fused_set_spin_limit: polls=%d < 0", polls);
+    ctx->fused_spin_limit = polls;
     return FT_HIP_OK;
 }
 

@@ -10,6 +10,7 @@ struct ft_hip_ctx {
     int device;
     int num_cus;
     int num_xcds;
+    int fused_spin_limit;  // polls before a fused-kernel wait gives up
     char arch[64];
 };
 

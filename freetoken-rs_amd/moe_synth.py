@@ -178,6 +178,10 @@ class FusedStack:
                                self.routers, self.m.bias, None, ids, wts, self.ws, dbg_gu, dbg_act, dbg_x, trace,
                                stream)
 
+    def reset(self):
+        """Re-initialise the workspace (required after a launch that timed out)."""
+        self.g.fused_workspace_init(self.ws)
+
     def check(self):
         """Raise if a launch gave up a bounded wait (synchronises first)."""
         torch.cuda.synchronize()

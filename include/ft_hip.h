@@ -238,9 +238,17 @@ int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float* x_in, flo
                            size_t workspace_bytes, float* dbg_gu, void* dbg_act, float* dbg_x,
                            uint64_t* dbg_trace);
 
+/* Length of the fused kernel's bounded waits, in polls (default 2^21, about
+ * a second): a wait that has not seen its data after this many polls gives up,
+ * records the abort in the workspace and every workgroup exits. 0 makes the
+ * first incomplete poll give up (tests of the abort path). No counterpart in
+ * the reference, whose launch sequence has no cross-workgroup waits. */
+int ft_hip_fused_set_spin_limit(ft_hip_ctx* ctx, int polls);
+
 /* Host-synchronous check of a fused workspace after the stream has been
  * synchronised: FT_HIP_E_TIMEOUT (and *aborted = 1) if a launch gave up a
- * bounded wait. */
+ * bounded wait. Such a workspace stays poisoned -- later launches on it do
+ * nothing -- until ft_hip_fused_workspace_init. */
 int ft_hip_fused_status(ft_hip_ctx* ctx, void* workspace, int* aborted);
 
 #ifdef __cplusplus

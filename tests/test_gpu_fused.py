@@ -171,3 +171,36 @@ def test_fused_rejects_bad_shapes(gemv, stack):
         gemv.moe_stack_fused(x, x, s.hidden, s.inter, s.n_experts, s.top_k, m.L, stack.banks, stack.routers,
                              None, None, None, None, small)
     assert ei.value.code == ft_hip.E_SHAPE
+
+
+def test_fused_abort_poisons_workspace_until_init(gemv, stack):
+    """A wait that gives up (forced from the host with a spin limit of 0, so
+    the first incomplete poll aborts; every workgroup still exits normally)
+    records the abort; the workspace then stays poisoned -- launches on it do
+    nothing -- until ft_hip_fused_workspace_init, after which results match a
+    clean run bit for bit."""
+    m = stack.m
+    x = m.hidden(7)
+    ref = torch.zeros_like(x)
+    stack.run(x, ref)
+    stack.check()
+    gemv.fused_set_spin_limit(0)
+    try:
+        stack.run(x, torch.zeros_like(x))
+        torch.cuda.synchronize()
+    finally:
+        gemv.fused_set_spin_limit(1 << 21)
+    with pytest.raises(ft_hip.FtHipError) as ei:
+        stack.check()
+    assert ei.value.code == ft_hip.E_TIMEOUT
+    o = torch.full_like(x, 7.0)
+    stack.run(x, o)  # poisoned workspace: the launch does nothing
+    torch.cuda.synchronize()
+    assert bool(torch.all(o == 7.0))
+    with pytest.raises(ft_hip.FtHipError):
+        stack.check()
+    stack.reset()
+    o = torch.zeros_like(x)
+    stack.run(x, o)
+    stack.check()
+    assert np.array_equal(host(o).view(np.uint32), host(ref).view(np.uint32))
