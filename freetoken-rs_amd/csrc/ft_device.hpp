@@ -102,6 +102,52 @@ __device__ __forceinline__ void q8_store_half(uint8_t* blk, int l, const Q8Lane&
     blk[8 + l] = (uint8_t)(int8_t)r.q;
 }
 
+// Lane-quad exchanges by DPP (quad_perm): a few cycles, unlike ds_bpermute.
+__device__ __forceinline__ float quad_xor1(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+}
+__device__ __forceinline__ float quad_xor2(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+}
+__device__ __forceinline__ int quad_xor1i(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
+__device__ __forceinline__ int quad_xor2i(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false); }
+
+// A lane quad quantizes one 32-value block to q8 {d, qsum, qs[32]}
+// (ft-core/src/q4_0.rs:62-78; the same arithmetic as q8_quantize_half): lane
+// part (0..3) owns values 8*part..8*part+7 and writes output words 2+2*part
+// and 3+2*part; part 0 also writes d and qsum. All four lanes must be active.
+__device__ __forceinline__ void quantize_block_quad(const float* v, int part, uint32_t* out) {
+    const float4 a = reinterpret_cast<const float4*>(v)[2 * part];
+    const float4 b = reinterpret_cast<const float4*>(v)[2 * part + 1];
+    const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
+    amax = fmaxf(amax, quad_xor1(amax));
+    amax = fmaxf(amax, quad_xor2(amax));
+    const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
+    const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+    int qsum = 0;
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float r = roundf(x[i] * inv);
+        r = fminf(127.0f, fmaxf(-127.0f, r));
+        const int q = (int)r;
+        qsum += q;
+        const uint32_t byte = (uint32_t)(uint8_t)(int8_t)q << (8 * (i & 3));
+        if (i < 4) w0 |= byte; else w1 |= byte;
+    }
+    qsum += quad_xor1i(qsum);
+    qsum += quad_xor2i(qsum);
+    out[2 + 2 * part] = w0;
+    out[3 + 2 * part] = w1;
+    if (part == 0) {
+        out[0] = __float_as_uint(d);
+        out[1] = (uint32_t)qsum;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Portable exp / tanh: only IEEE basic operations (fma, floor, ldexp, +, -, /)
 // in a fixed order, so the host oracle computes the same bits. Cody-Waite

@@ -46,6 +46,9 @@ SIGNATURES = {
     "ft_hip_moe_layer_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "ft_hip_moe_layer": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _U64, _I, _P, _P,
                               _P, _SZ]),
+    "ft_hip_moe_layer_grouped_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
+    "ft_hip_moe_layer_grouped": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P,
+                                      _SZ, _P, _P]),
     "ft_hip_fused_expert_bytes": (_I64, [_I64, _I64]),
     "ft_hip_fused_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
     "ft_hip_fused_workgroups": (ctypes.c_int, [_I64, _I64, _I64, _I64]),
@@ -217,6 +220,19 @@ class Q4Gemv:
                                      n_experts, top_k, _ptr(router_w), _ptr(router_bias), _ptr(expert_scale),
                                      _ptr(bank), expert_bytes, layout, _ptr(ids), _ptr(wts), _ptr(workspace),
                                      workspace.numel() * workspace.element_size()))
+
+    # -- grouped batched layer (ft-model/src/lib.rs:1507-1606) --
+    @staticmethod
+    def moe_layer_grouped_workspace_bytes(n_seqs, hidden, inter, n_experts, top_k):
+        return lib().ft_hip_moe_layer_grouped_workspace_bytes(n_seqs, hidden, inter, n_experts, top_k)
+
+    def moe_layer_grouped(self, x, x_out, n_seqs, hidden, inter, n_experts, top_k, router_w, router_bias,
+                          expert_scale, bank, ids, wts, workspace, dbg_gu=None, dbg_act=None, stream=None):
+        check(lib().ft_hip_moe_layer_grouped(self._ctx, _stream(stream), _ptr(x), _ptr(x_out), n_seqs, hidden,
+                                             inter, n_experts, top_k, _ptr(router_w), _ptr(router_bias),
+                                             _ptr(expert_scale), _ptr(bank), _ptr(ids), _ptr(wts), _ptr(workspace),
+                                             workspace.numel() * workspace.element_size(), _ptr(dbg_gu),
+                                             _ptr(dbg_act)))
 
     # -- fused whole-stack path --
     @staticmethod

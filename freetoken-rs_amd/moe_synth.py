@@ -152,8 +152,8 @@ def zipf_router_bias(shape, n_layers, s=1.1, tau=None, seed=SEED):
 
 class FusedStack:
     """A SyntheticMoE's banks and routers repacked for the fused whole-stack
-    kernel (ft_hip_moe_stack_fused): one cooperative launch runs all layers
-    of one token."""
+    kernel (ft_hip_moe_stack_fused): one launch runs all layers of one token.
+    The packed banks also serve the grouped batched path (GroupedStack)."""
 
     def __init__(self, model):
         g, s = model.g, model.shape
@@ -186,3 +186,36 @@ class FusedStack:
         """Raise if a launch gave up a bounded wait (synchronises first)."""
         torch.cuda.synchronize()
         self.g.fused_status(self.ws)
+
+
+class GroupedStack:
+    """Batched decode through ft_hip_moe_layer_grouped: n_seqs tokens per step,
+    layer by layer, pairs grouped by expert; the banks are a FusedStack's."""
+
+    def __init__(self, fused, n_seqs):
+        self.f, self.m, self.B = fused, fused.m, n_seqs
+        g, s = self.m.g, self.m.shape
+        self.g = g
+        nbytes = g.moe_layer_grouped_workspace_bytes(n_seqs, s.hidden, s.inter, s.n_experts, s.top_k)
+        self.ws = torch.empty(nbytes, dtype=torch.uint8, device=self.m.device)
+        self.buf = [torch.zeros((n_seqs, s.hidden), dtype=torch.float32, device=self.m.device) for _ in range(2)]
+        self.ids = torch.zeros((self.m.L, n_seqs * s.top_k), dtype=torch.int32, device=self.m.device)
+        self.wts = torch.zeros((self.m.L, n_seqs * s.top_k), dtype=torch.float32, device=self.m.device)
+
+    def bank(self, l):
+        E, eb = self.m.shape.n_experts, self.f.expert_bytes
+        return self.f.banks[l * E * eb:(l + 1) * E * eb]
+
+    def layer(self, l, x, x_out, ids=None, wts=None, dbg_gu=None, dbg_act=None, stream=None):
+        s = self.m.shape
+        self.g.moe_layer_grouped(x, x_out, self.B, s.hidden, s.inter, s.n_experts, s.top_k, self.m.routers[l],
+                                 self.m.layer_bias(l), None, self.bank(l), self.ids[l] if ids is None else ids,
+                                 self.wts[l] if wts is None else wts, self.ws, dbg_gu, dbg_act, stream)
+
+    def run(self, x_in, x_out, stream=None):
+        """All layers for the batch: x_out = x_L (x_in, x_out: [n_seqs, H])."""
+        src = x_in
+        for l in range(self.m.L):
+            dst = x_out if l == self.m.L - 1 else self.buf[l & 1]
+            self.layer(l, src, dst, stream=stream)
+            src = dst

@@ -175,6 +175,28 @@ int ft_hip_moe_layer(ft_hip_ctx* ctx, void* stream, const float* x, float* x_out
                      int layout, int32_t* ids, float* wts, void* workspace,
                      size_t workspace_bytes);
 
+/* One MoE layer for n_seqs decode tokens with the (token, expert) pairs
+ * grouped by expert: replaces the batched pair section of
+ * ft-model/src/lib.rs:1507-1606 (quantize_q8, gemv_q4r_ptr over every pair,
+ * gelu_mul_q8, gemv_q4r_ptr, reduce_pairs_weighted), which re-reads an
+ * expert's weights for each of its tokens; here each routed expert's weights
+ * stream once for all of its tokens. bank: ONE layer's n_experts experts in
+ * the fused layout (ft_hip_pack_experts_fused), 16-byte aligned; router_w:
+ * [E][H] f32. ids/wts: [n_seqs][top_k] routing (written). Same arithmetic as
+ * ft_hip_moe_layer: q8 quants, block dots, routing, GELU q8 and the combine
+ * (slot order) are bit-identical; f32 GEMV sums may differ in order.
+ * dbg_gu [n_seqs*top_k][2I] f32 and dbg_act [n_seqs*top_k][I/32][40] (NULL
+ * in normal use) receive the gate|up sums and act q8 blocks per pair.
+ * Shapes: hidden 2816 or 4096, inter a multiple of 32 up to 1024,
+ * n_seqs*top_k <= 4096. */
+size_t ft_hip_moe_layer_grouped_workspace_bytes(int64_t n_seqs, int64_t hidden, int64_t inter,
+                                                int64_t n_experts, int64_t top_k);
+int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const float* x, float* x_out, int64_t n_seqs,
+                             int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k,
+                             const float* router_w, const float* router_bias, const float* expert_scale,
+                             const void* bank, int32_t* ids, float* wts, void* workspace,
+                             size_t workspace_bytes, float* dbg_gu, void* dbg_act);
+
 /* ---- fused whole-stack path (no single reference counterpart) ----
  * The reference runs the section as a sequence of launches per layer
  * (ft-model/src/lib.rs:1406-1476) and removes host launch cost with a CUDA
