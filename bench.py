@@ -37,6 +37,11 @@ def parse():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--path", choices=["fused", "multikernel"], default="fused")
     ap.add_argument("--layers", type=int, default=30)
+    ap.add_argument("--prefetch", type=int, choices=[0, 1], default=1,
+                    help="fused path: stream the early-routed experts of the next layer ahead (1) or not (0)")
+    ap.add_argument("--trace", default="", metavar="NPY",
+                    help="fused path: after timing, run one more token recording every workgroup's phase stamps "
+                         "(wall clock, 100 MHz) into this .npy file, shape [workgroups][layers+1][32]")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
@@ -193,6 +198,7 @@ def main():
     outs = torch.zeros((n_tok, H), dtype=torch.float32, device=model.device)
     if args.path == "fused":
         t1 = time.time()
+        g.fused_set_prefetch(args.prefetch)
         stack = moe_synth.FusedStack(model)
         torch.cuda.synchronize()
         log(f"[setup] banks repacked for the fused kernel in {time.time() - t1:.1f}s")
@@ -238,6 +244,13 @@ def main():
 
     if args.path == "fused":
         stack.check()
+        if args.trace:
+            nw = stack.n_workgroups()
+            tr = torch.zeros(nw * (model.L + 1) * 32, dtype=torch.int64, device=model.device)
+            stack.run(hidden[0], torch.empty_like(hidden[0]), trace=tr)
+            stack.check()
+            np.save(args.trace, tr.cpu().numpy().reshape(nw, model.L + 1, 32))
+            log(f"[trace] {nw} workgroups x {model.L + 1} rows of phase stamps -> {args.trace}")
         # the fused kernel is the only kernel of a step: one launch per token
         k_us, k_bytes = us_tok, exp_bytes + router_bytes
         k_name = "k_moe_stack_fused (whole 30-layer section, one launch per token)"
@@ -275,7 +288,8 @@ def main():
         "data": "synthetic (seeded N(0,0.02) q4_0 banks, N(0,1) hidden)",
         "config": {"workload": f"gemma-shaped MoE expert FFN, {model.L} layers, batch 1, residual chain",
                    "hidden": H, "inter": model.shape.inter, "experts": model.shape.n_experts,
-                   "top_k": model.shape.top_k, "layers": model.L, "path": args.path},
+                   "top_k": model.shape.top_k, "layers": model.L, "path": args.path,
+                   "prefetch": bool(args.prefetch) if args.path == "fused" else None},
         "achieved_GBps": round(gbps, 1),
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "roofline": {"bound": "hbm", "achieved": round(k_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",

@@ -112,6 +112,61 @@ __device__ __forceinline__ float quad_xor2(float v) {
 __device__ __forceinline__ int quad_xor1i(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
 __device__ __forceinline__ int quad_xor2i(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false); }
 
+// DPP moves by a fixed control: quad_perm broadcasts 0x00/0x55/0xAA/0xFF,
+// 0x140 row_mirror, 0x141 row_half_mirror; every lane of the row must be
+// active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+// Lane l <-> lane l ^ 16 within each 32-lane half (ds_swizzle, bit mode:
+// and 0x1F, or 0, xor 0x10).
+__device__ __forceinline__ float swz_xor16_f(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+}
+__device__ __forceinline__ int swz_xor16_i(int v) { return __builtin_amdgcn_ds_swizzle(v, 0x401F); }
+
+// All-lane max / sum over the 32 lanes of a half-wave (every one active):
+// DPP within rows of 16 (quad xor 1, quad xor 2, half-row mirror, row
+// mirror), then one swizzle across the two rows. Max is exact in any order;
+// the sum is of integers.
+__device__ __forceinline__ float half_max32(float a) {
+    a = fmaxf(a, quad_xor1(a));
+    a = fmaxf(a, quad_xor2(a));
+    a = fmaxf(a, dpp_f<0x141>(a));
+    a = fmaxf(a, dpp_f<0x140>(a));
+    return fmaxf(a, swz_xor16_f(a));
+}
+__device__ __forceinline__ int half_sum32(int s) {
+    s += quad_xor1i(s);
+    s += quad_xor2i(s);
+    s += dpp_i<0x141>(s);
+    s += dpp_i<0x140>(s);
+    return s + swz_xor16_i(s);
+}
+
+// q8 block of 32 values held one per lane by lanes 0..31 (all active), the
+// arithmetic of q8_quantize_half (ft-core/src/q4_0.rs:62-78). Returns, in
+// lane 4k, output word 2+k (the packed bytes of lanes 4k..4k+3); *d and
+// *qsum are the same in every lane.
+__device__ __forceinline__ uint32_t q8_quantize_lanes32(float v, float* d_out, int* qsum_out) {
+    const float amax = half_max32(fabsf(v));
+    const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
+    const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+    float r = roundf(v * inv);
+    r = fminf(127.0f, fmaxf(-127.0f, r));
+    const int q = (int)r;
+    *d_out = d;
+    *qsum_out = half_sum32(q);
+    const int b = q & 0xFF;
+    return (uint32_t)dpp_i<0x00>(b) | ((uint32_t)dpp_i<0x55>(b) << 8) | ((uint32_t)dpp_i<0xAA>(b) << 16) |
+           ((uint32_t)dpp_i<0xFF>(b) << 24);
+}
+
 // A lane quad quantizes one 32-value block to q8 {d, qsum, qs[32]}
 // (ft-core/src/q4_0.rs:62-78; the same arithmetic as q8_quantize_half): lane
 // part (0..3) owns values 8*part..8*part+7 and writes output words 2+2*part
@@ -187,6 +242,18 @@ __device__ __forceinline__ double exp_portable_t(double x, const T& k) {
 
 struct ExpConst {
     __device__ __forceinline__ double operator[](int i) const { return exp_table().k[i]; }
+};
+
+// The same constants, each materialised in scalar registers at its use (an
+// opaque move the compiler cannot hoist): inside a long persistent loop this
+// keeps them out of the vector registers, where hoisted copies would be
+// spilled and reloaded.
+struct ExpConstS {
+    __device__ __forceinline__ double operator[](int i) const {
+        double v = exp_table().k[i];
+        asm volatile("" : "+s"(v));
+        return v;
+    }
 };
 
 __device__ __forceinline__ double exp_portable(double x) { return exp_portable_t(x, ExpConst{}); }

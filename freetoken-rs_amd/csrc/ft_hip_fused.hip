@@ -1,42 +1,54 @@
 // ft_hip_fused.hip -- the whole MoE expert-FFN section of an L-layer stack for
-// one decode token in ONE persistent, cooperatively launched kernel.
+// one decode token in ONE persistent kernel.
 //
 // Why one kernel: at batch 1 a Gemma-shaped layer streams only ~28 MB, i.e.
 // ~4.6 us at the MI355X's achievable HBM rate, while every kernel boundary
 // costs several us. The layer is therefore run as dataflow between resident
 // workgroups, handing over through single-writer, epoch-tagged 64-bit words
 // in device memory: bits 63..32 = epoch tag, bits 31..0 = payload.
-// Producers write with device-coherent (agent-scope) relaxed stores;
-// consumers read with device-coherent loads, keep the words that already
-// carry the expected tag and re-read only the missing ones. Data and flag
-// travel in the same word, so there is no read-modify-write contention and no
-// cache-maintenance fence (the alternatives measured 1.4-20 us per barrier on
-// this part).
+// Producers write with device-coherent relaxed stores; consumers read with
+// device-coherent loads, keep the words that already carry the expected tag
+// and re-read only the missing ones. Data and flag travel in the same word,
+// so there is no read-modify-write contention and no cache-maintenance fence
+// (the alternatives measured 1.4-20 us per barrier on this part).
 //
-// Workgroups of one layer (G shape: H 2816, I 704, E 128, top-8): 184.
-//   expert unit (p, j), 176 of them, p = routed slot (w % K), j = w / K:
-//     gate|up : 64 rows (32 gate, 32 up) of expert ids[p] for act block j
-//               (32 columns), H/32 blocks streamed into registers by 8 waves;
+// Why prefetch: a layer's hand-over chain (act -> y -> routing) is several
+// us during which HBM would sit idle. The router of layer l+1 applied to x_l
+// ("early routing") picks most of layer l+1's experts, so every unit group
+// streams the tiles of its PREDICTED expert of layer l+1 into registers as
+// soon as it has finished layer l's dots, overlapping the stream with the
+// chain. When the true routing arrives, predicted experts that were routed
+// stay with the unit group that holds them; only the remaining unit groups
+// load the experts nobody predicted (a miss).
+//
+// Workgroups (G shape: H 2816, I 704, E 128, top-8): 192.
+//   expert unit (u, j), 176 of them, unit group u = w % K, j = w / K:
+//     gate|up : 64 rows (32 gate, 32 up) of its expert for act block j
+//               (32 columns), H/32 blocks held in registers by 8 waves;
 //               GELU*up -> one q8 block, published (hop A).
-//     down    : rows 128j..128j+127 of expert ids[p] (one 16-row tile per
-//               wave), weights streamed into registers with the gate|up
-//               tile; waits for the 22 act blocks of ITS expert only (hop A),
-//               publishes y_p for its 128 rows (hop B).
-//     All units of slot p run on XCD p (workgroups are dealt to XCDs
+//     down    : rows 128j..128j+127 of its expert (one 16-row tile per
+//               wave), held in registers with the gate|up tile; waits for
+//               the act blocks of ITS unit group only (hop A), publishes y
+//               for its 128 rows (hop B), then prefetches layer l+1.
+//     All units of group u run on XCD u (workgroups are dealt to XCDs
 //     round-robin; each checks this at start through the XCD id register),
 //     so hop A stays in that XCD's L2: plain stores, agent-scope polls.
 //     If the placement check fails, hop A stores write through instead.
 //   group unit g, 8 of them (one per R-order group of H/8 rows):
-//     waits for y_p of its rows for every p (hop B); x_{l+1} = x_l + sum_p
-//     w_p y_p in pair order; router chunk partials of its H/128 chunks and
-//     their group sum for every expert (router weights of the next layer were
-//     streamed into registers meanwhile); q8 of its x rows; publishes group
-//     sums + q8 blocks (hop C), double-buffered by layer parity.
-//   every workgroup: reads the 8 group sums of every expert (and, expert
-//     units, the 88 q8 blocks of x_{l+1}) (hop C), logits = sum over groups
-//     in order + bias, top-k and softmax.
-// Three hand-overs per layer; the largest (C) carries 8 x (E + H/8/32*10)
-// words. Weight layouts are lossless repacks of q4_0 with its byte count.
+//     waits for y of its rows from every routed slot (hop B); x_{l+1} =
+//     x_l + sum_p w_p y_p in routing order; router chunk partials of its
+//     H/128 chunks and their group sum for every expert (layer l+1's router
+//     weights were streamed into registers meanwhile); q8 of its x rows;
+//     publishes group sums + q8 blocks (hop C), double-buffered by parity.
+//   pred unit g, 8 of them: the same combine of group g's rows, then the
+//     group sums of layer l+2's router over x_{l+1}; the pred units exchange
+//     them, rank them (the same top-k as the true routing) and publish the
+//     predicted experts of layer l+2, one copy per XCD.
+//   every expert and group unit: reads the 8 group sums of every expert
+//     (and, expert units, the 88 q8 blocks of x_{l+1}) (hop C), logits =
+//     sum over groups in order + bias, top-k and softmax, then the
+//     assignment of routed slots to unit groups.
+// Weight layouts are lossless repacks of q4_0 with its byte count.
 
 #include "ft_device.hpp"
 #include "ft_runtime.hpp"
@@ -59,6 +71,7 @@ constexpr int NREP = 8;         // replicas of the group broadcast, one per XCD
 constexpr int CTL_EPOCH = 0;    // control words (u32 indices)
 constexpr int CTL_ABORT = 32;
 constexpr int TRACE_SLOTS = 32; // stamps per workgroup per layer in the debug trace
+constexpr int PID_STRIDE = 16;  // words per copy of the predicted experts
 
 struct FusedParams {
     const uint8_t* banks;       // [L][E][expert_bytes], fused layout
@@ -72,6 +85,8 @@ struct FusedParams {
     uint64_t* act_t;            // tagged [K][I/32][10]
     uint64_t* y_t;              // tagged [K][H]
     uint64_t* gq_t;             // tagged [2][NREP][NGROUP][gq_stride]: E group sums, then qw q8 words
+    uint64_t* pp_t;             // tagged [2][NGROUP][E]: group sums of the predicting router
+    uint64_t* pid_t;            // tagged [2][NREP][PID_STRIDE]: predicted experts, one copy per XCD
     uint64_t* pl_t;             // tagged [grid]: the XCD each workgroup runs on
     int64_t rs_gq;              // replica stride (words); the parity stride is NREP * rs_gq
     uint32_t* ctl;              // [CTL_EPOCH] epoch, [CTL_ABORT] abort epoch
@@ -82,34 +97,24 @@ struct FusedParams {
     int64_t expert_bytes, gu_bytes;
     int H, I, E, K, L;
     int n_gu, n_dn, n_unit;     // K*I/32 gate|up units, K*H/128 down units, max of the two
+    int prefetch;               // 0: every layer loads its routed experts (no prediction)
     int gq_stride, qw;          // words per group in the broadcast; q8 words per group ((H/8)/32*10)
     int spin_limit;
     int o_q8x, o_act8, o_red, o_gq, o_gx, o_gy, o_gp, o_misc, lds_bytes;
 };
 
-struct Misc {                   // placed 16-byte aligned
+struct alignas(16) Misc {       // placed 16-byte aligned
     uint64_t keys[MAX_E + 8];   // rank keys of the logits, four padded rows (16-byte aligned)
-    double expk[17];            // exp_table() in LDS (see exp_portable_t)
     float logits[MAX_E];
-    float gsum[64];
-    float act[32];
-    uint32_t actblk[10];
-    float sel_v[MAX_K];
-    float sel_x[MAX_K];
-    int sel_i[MAX_K];
-    int ids[MAX_K];
+    float sel_v[MAX_K];         // the chosen logits, in rank order
+    int sel_i[MAX_K];           // the chosen experts, in rank order
+    int ids[MAX_K];             // routed experts of the current layer, in routing order
     float wts[MAX_K];
+    alignas(16) int pid[2][MAX_K];  // by layer parity: the expert unit group u holds (predicted)
+    int uslot[MAX_K];           // slot of unit group u's held expert, -1: not routed
+    int pown[MAX_K];            // unit group that runs routed slot p
     int abort_flag;
 };
-
-// Orders LDS accesses between lanes of ONE wave (LDS operations of a wave
-// execute in issue order; this only stops the compiler from reordering them).
-__device__ __forceinline__ void wave_lds_order() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    asm volatile("" ::: "memory");
-}
 
 // Tagged words use system-scope (sc0 sc1) relaxed accesses: in a probe a
 // one-way hand-over took ~0.40 us this way whether or not the two workgroups
@@ -139,18 +144,21 @@ __device__ __forceinline__ uint32_t ld_ctl(const uint32_t* p) {
 }
 
 // Block-wide wait until the n (<= 4096) tagged words src[idx(i)] all carry
-// `tag`; payloads land in dst[didx(i)] (LDS). Each thread re-reads only its
-// words still missing, so a consumer that arrives early costs little traffic.
-// Bounded: after spin_limit polls (or when another workgroup has aborted) it
-// records the abort and returns false.
+// `tag`; payloads land in dst[didx(i)] (LDS). Each lane re-reads only its
+// words still missing, and each wave spins on its own words without
+// synchronising (a lane that is done idles under the wave's exec mask); one
+// barrier ends the wait. Bounded: after spin_limit polls (or when another
+// workgroup has aborted) the lane records the abort and the wait returns
+// false in every thread.
+template <bool DBG>
 __device__ __forceinline__ void trace_value(const FusedParams& P, int l, int ev, uint64_t v) {
-    if (P.trace && threadIdx.x == 0)
+    if (DBG && P.trace && threadIdx.x == 0)
         P.trace[((int64_t)blockIdx.x * (P.L + 1) + (l + 1)) * TRACE_SLOTS + ev] = v;
 }
 
-template <bool AGENT = false, typename Idx, typename DIdx>
-__device__ bool wait_words(const FusedParams& P, Misc* m, uint32_t epoch, const uint64_t* src, int n, Idx idx,
-                           uint32_t tag, uint32_t* dst, DIdx didx, int tl = -2, int ts = 0) {
+template <bool DBG, bool AGENT = false, typename Idx, typename DIdx>
+__device__ __forceinline__ bool wait_words(const FusedParams& P, Misc* m, uint32_t epoch, const uint64_t* src, int n,
+                                           Idx idx, uint32_t tag, uint32_t* dst, DIdx didx, int tl = -2, int ts = 0) {
     // An opaque copy of the thread index: keeps the compiler from hoisting the
     // per-call-site address arithmetic out of the layer loop, where it would
     // stay live (in registers) for the whole kernel.
@@ -160,7 +168,9 @@ __device__ bool wait_words(const FusedParams& P, Misc* m, uint32_t epoch, const 
 #pragma unroll
     for (int u = 0; u < WAIT_U; ++u)
         if (u * FT_THREADS + tid < n) pending |= 1u << u;
-    for (int it = 0;; ++it) {
+    int it = 0;
+    bool give_up = false;
+    while (pending) {
         uint64_t v[WAIT_U];
 #pragma unroll
         for (int u = 0; u < WAIT_U; ++u)
@@ -173,29 +183,27 @@ __device__ bool wait_words(const FusedParams& P, Misc* m, uint32_t epoch, const 
                 dst[didx(u * FT_THREADS + tid)] = (uint32_t)v[u];
                 pending &= ~(1u << u);
             }
-        if (it == 0 && tl > -2 && P.trace && threadIdx.x == 0)
-            P.trace[((int64_t)blockIdx.x * (P.L + 1) + (tl + 1)) * TRACE_SLOTS + ts + 4] = wall_clock64();
-        if (__syncthreads_and(pending == 0)) {
-            if (tl > -2) trace_value(P, tl, ts, (uint64_t)(it + 1));  // polls this wait took
-            return true;
-        }
-        if ((it & 63) == 63 || it >= P.spin_limit) {
-            if (threadIdx.x == 0) {
-                const bool ab = ld_ctl(P.ctl + CTL_ABORT) == epoch || it >= P.spin_limit;
-                if (ab) __hip_atomic_store(P.ctl + CTL_ABORT, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                m->abort_flag = ab;
-            }
-            __syncthreads();
-            if (m->abort_flag) return false;
+        if (!pending) break;
+        ++it;
+        if (it >= P.spin_limit || ((it & 63) == 0 && ld_ctl(P.ctl + CTL_ABORT) == epoch)) {
+            // published at once: the other lanes, waves and workgroups see it
+            // at their next check (every 64 polls) and give up too
+            __hip_atomic_store(P.ctl + CTL_ABORT, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            give_up = true;
+            break;
         }
         __builtin_amdgcn_s_sleep(POLL_SLEEP);
     }
+    if (give_up) m->abort_flag = 1;
+    if (tl > -2) trace_value<DBG>(P, tl, ts, (uint64_t)(it + 1));  // polls this wait took (thread 0)
+    __syncthreads();
+    return m->abort_flag == 0;
 }
 
-template <typename Idx>
+template <bool DBG, typename Idx>
 __device__ __forceinline__ bool wait_words(const FusedParams& P, Misc* m, uint32_t epoch, const uint64_t* src, int n,
                                            Idx idx, uint32_t tag, uint32_t* dst, int tl = -2, int ts = 0) {
-    return wait_words(P, m, epoch, src, n, idx, tag, dst, [](int i) { return i; }, tl, ts);
+    return wait_words<DBG>(P, m, epoch, src, n, idx, tag, dst, [](int i) { return i; }, tl, ts);
 }
 
 // Trace slots (per workgroup and layer; layer -1 = prologue), wall-clock
@@ -205,10 +213,12 @@ __device__ __forceinline__ bool wait_words(const FusedParams& P, Misc* m, uint32
 // 12 broadcast read, 13 logits, 14 top-k done, 15 top-k ranked, 16 softmax,
 // 17-19 gate|up tail (wave sums, GELU, q8), 20-22 group (partials, sync,
 // sums); 24-26 poll count of the broadcast / act / y waits and 28-30 the
-// return of each one's first poll; prologue row: 27 act hand-over local
-// (1/0), 28 XCD id.
+// return of each one's first poll; 7 prefetch issued, 10 miss (1/0), 23
+// shader clock at layer start, 27 poll count of the prediction wait;
+// prologue row: 27 act hand-over local (1/0), 28 XCD id.
+template <bool DBG>
 __device__ __forceinline__ void stamp(const FusedParams& P, int l, int ev) {
-    if (P.trace && threadIdx.x == 0)
+    if (DBG && P.trace && threadIdx.x == 0)
         P.trace[((int64_t)blockIdx.x * (P.L + 1) + (l + 1)) * TRACE_SLOTS + ev] = wall_clock64();
 }
 
@@ -219,6 +229,15 @@ __device__ __forceinline__ void stamp(const FusedParams& P, int l, int ev) {
 // exp(l - l_max), summed in rank order. Each logit carries a 64-bit key
 // (monotone float bits, then the complemented index) so that "sorts before"
 // is one unsigned compare; four threads share one logit's E comparisons.
+// threadIdx.x behind an opaque move: comparisons against it are recomputed
+// where they are used instead of being hoisted out of the layer loop as lane
+// masks, which would be spilled and reloaded (scalar register pressure).
+__device__ __forceinline__ int tid_here() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
 __device__ __forceinline__ uint64_t rank_key(float v, int i) {
     v = v + 0.0f;  // -0 -> +0: equal values tie on the index
     const uint32_t b = __float_as_uint(v);
@@ -227,85 +246,138 @@ __device__ __forceinline__ uint64_t rank_key(float v, int i) {
     return ((uint64_t)mo << 32) | (0xFFFFFFFFu - (uint32_t)i);
 }
 
-// Rank keys sit in four rows (one per comparing thread of a logit), padded
-// by 16 bytes so the rows start in different LDS banks.
-__device__ __forceinline__ int key_slot(int i, int q) { return (i / q) * (q + 2) + i % q; }
+// Rank keys sit in four rows of 32 (one row per comparing thread of a
+// logit), padded by 16 bytes so the rows start in different LDS banks; keys
+// of indices >= E are 0, below every real key, so every thread compares a
+// full row without masks.
+constexpr int KEY_ROW = MAX_E / 4;
+__device__ __forceinline__ int key_slot(int i) { return (i / KEY_ROW) * (KEY_ROW + 2) + i % KEY_ROW; }
 
-__device__ void topk_rank(const FusedParams& P, Misc* m, int layer) {
-    const int E = P.E, K = P.K, t = threadIdx.x;
-    const int q = E >> 2;  // comparisons per thread: even, at most 32 (E % 16 == 0, E <= 128)
-    {
-        const int i = min(t >> 2, E - 1), part = t & 3;
-        const uint64_t ki = m->keys[key_slot(i, q)];
-        const uint4* kk = reinterpret_cast<const uint4*>(m->keys + part * (q + 2));  // two keys per uint4
-        const int n2 = q >> 1;
-        uint4 u[16];
+// Routing of `layer` from the NGROUP group sums gs[E][NGROUP] in LDS.
+//   Logits: R-order, the group sums of expert e in group order from 0.0f,
+//   then + bias (bias_t: this thread's expert's bias, read ahead by the
+//   caller). Then each logit's rank, and the top K in rank order:
+//   pred >= 0 (prediction): ids alone into m->pid[pred];
+//   otherwise ids into m->sel_i, logits into m->sel_v and, for every unit
+//   group u whose held expert `held[u]` was routed, its slot into
+//   m->uslot[u] (-1: not routed). Two barriers; the caller reads after the
+//   second.
+__device__ __forceinline__ void route_rank(const FusedParams& P, Misc* m, const float* gs, float bias_t, int pred,
+                                           const int* held) {
+    static_assert(NGROUP == 8 && MAX_E == 128, "the logit and key layouts below assume these");
+    const int E = P.E, K = P.K, t = tid_here();
+    if (t < MAX_E) {
+        uint64_t key = 0;
+        if (t < E) {
+            const float4 a = reinterpret_cast<const float4*>(gs + t * NGROUP)[0];
+            const float4 b = reinterpret_cast<const float4*>(gs + t * NGROUP)[1];
+            const float gv[NGROUP] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            float total = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) u[j] = kk[min(j, n2 - 1)];
-        int rank = 0;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const uint64_t k0 = ((uint64_t)u[j].y << 32) | u[j].x;
-            const uint64_t k1 = ((uint64_t)u[j].w << 32) | u[j].z;
-            const int c = (int)(k0 > ki) + (int)(k1 > ki);
-            rank += j < n2 ? c : 0;
+            for (int g = 0; g < NGROUP; ++g) total = total + gv[g];
+            if (P.bias) total = total + bias_t;
+            m->logits[t] = total;
+            key = rank_key(total, t);
         }
-        rank += quad_xor1i(rank);
-        rank += quad_xor2i(rank);
-        if ((t >> 2) < E && part == 0 && rank < K) {  // ranks are distinct: each slot written once
+        m->keys[key_slot(t)] = key;
+    }
+    if (t < MAX_K) m->uslot[t] = -1;
+    __syncthreads();
+    const int i = min(t >> 2, E - 1), part = t & 3;
+    const uint64_t ki = m->keys[key_slot(i)];
+    const uint4* kk = reinterpret_cast<const uint4*>(m->keys + part * (KEY_ROW + 2));  // two keys per uint4
+    int rank = 0;
+#pragma unroll
+    for (int j0 = 0; j0 < KEY_ROW / 2; j0 += 8) {  // two batches of LDS reads: fewer registers live
+        uint4 kv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) kv[j] = kk[j0 + j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint64_t k0 = ((uint64_t)kv[j].y << 32) | kv[j].x;
+            const uint64_t k1 = ((uint64_t)kv[j].w << 32) | kv[j].z;
+            rank += (int)(k0 > ki) + (int)(k1 > ki);
+        }
+    }
+    rank += quad_xor1i(rank);
+    rank += quad_xor2i(rank);
+    // the held experts, two 16-byte LDS reads issued with the rank's (MAX_K == 8)
+    int4 h0 = make_int4(-1, -1, -1, -1), h1 = h0;
+    if (held) {
+        h0 = reinterpret_cast<const int4*>(held)[0];
+        h1 = reinterpret_cast<const int4*>(held)[1];
+    }
+    const float li = m->logits[i];
+    if ((t >> 2) < E && part == 0 && rank < K) {  // ranks are distinct: each slot written once
+        if (pred >= 0) {
+            m->pid[pred][rank] = i;
+        } else {
             m->sel_i[rank] = i;
-            m->sel_v[rank] = m->logits[i];
+            m->sel_v[rank] = li;
+            const int hv[MAX_K] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+            for (int u = 0; u < MAX_K; ++u)
+                if (u < K && hv[u] == i) m->uslot[u] = rank;
         }
     }
-    __syncthreads();  // every rank slot written before wave 0 reads them
-    stamp(P, layer - 1, 15);
-    if (t < 64) {  // wave 0: softmax
-        const float v0 = m->sel_v[0];
-        const float vt = m->sel_v[min(t, K - 1)];
-        const int it = m->sel_i[min(t, K - 1)];
-        const float ex = expf_portable_t(vt - v0, m->expk);
-        if (t < K) m->sel_x[t] = ex;
-        wave_lds_order();
-        float xv[MAX_K];
-#pragma unroll
-        for (int j = 0; j < MAX_K; ++j) xv[j] = m->sel_x[j];
-        float denom = 0.0f;
-#pragma unroll
-        for (int j = 0; j < MAX_K; ++j)  // in rank order, as the reference's iterator sum
-            denom = j < K ? denom + xv[j] : denom;
-        if (t < K) {
-            float w = ex / denom;
-            if (P.escale) w = w * P.escale[(int64_t)layer * E + min(max(it, 0), E - 1)];
-            m->ids[t] = it;
-            m->wts[t] = w;
-            if (blockIdx.x == 0) {
-                if (P.ids_out) P.ids_out[layer * K + t] = it;
-                if (P.wts_out) P.wts_out[layer * K + t] = w;
-            }
-        }
-    }
-    stamp(P, layer - 1, 16);
     __syncthreads();
 }
 
-// Logits from the NGROUP group sums gs[NGROUP][E] (R-order: groups in order
-// from 0.0f, then + bias), then top-k and softmax into m->ids / m->wts.
-__device__ void route(const FusedParams& P, Misc* m, const float* gs, int layer) {
-    const int E = P.E, t = threadIdx.x;
-    if (t < E) {
-        float gv[NGROUP];
+// Slot that unit group u runs (after route_rank with `held`): the slot of
+// its held expert if that was routed; otherwise the r-th routed slot that no
+// unit group holds, r = u's rank among the unit groups whose held expert was
+// not routed. first (nothing held): slot u. Every workgroup computes the same
+// assignment from the same routing and prediction.
+__device__ __forceinline__ int unit_slot(const Misc* m, int K, int u, bool first) {
+    if (first) return u;
+    int us[MAX_K];
 #pragma unroll
-        for (int g = 0; g < NGROUP; ++g) gv[g] = gs[g * E + t];
-        float total = 0.0f;
+    for (int q = 0; q < MAX_K; ++q) us[q] = m->uslot[q];
+    uint32_t held = 0, hit = 0;
+    int mine = -1;
 #pragma unroll
-        for (int g = 0; g < NGROUP; ++g) total = total + gv[g];
-        if (P.bias) total = total + P.bias[(int64_t)layer * E + t];
-        m->logits[t] = total;
-        m->keys[key_slot(t, E >> 2)] = rank_key(total, t);
+    for (int q = 0; q < MAX_K; ++q) {
+        if (q < K && us[q] >= 0) {
+            held |= 1u << us[q];
+            hit |= 1u << q;
+        }
+        mine = q == u ? us[q] : mine;
     }
-    __syncthreads();
-    stamp(P, layer - 1, 13);
-    topk_rank(P, m, layer);
+    if (mine >= 0) return mine;
+    const int r = __popc(~hit & ((1u << u) - 1));
+    uint32_t fr = ~held & ((1u << K) - 1);
+#pragma unroll
+    for (int k = 0; k < MAX_K; ++k)
+        if (k < r) fr &= fr - 1;
+    return fr ? (int)__builtin_ctz(fr) : 0;
+}
+
+// Group and pred units, wave 0, after route_rank: softmax over the chosen in
+// rank order (weights into m->wts, ids into m->ids; the routing record when
+// `record`), and pown[p] = the unit group running slot p. The caller
+// synchronizes before other waves read them.
+__device__ __forceinline__ void route_weights(const FusedParams& P, Misc* m, int layer, bool first, bool record) {
+    const int E = P.E, K = P.K, t = tid_here();
+    if (t >= 64) return;
+    const float v0 = m->sel_v[0];
+    const float vt = m->sel_v[min(t, K - 1)];
+    const int it = m->sel_i[min(t, K - 1)];
+    const float ex = expf_portable_t(vt - v0, ExpConstS{});
+    float denom = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MAX_K; ++j)  // in rank order, as the reference's iterator sum
+        denom = j < K ? denom + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), j)) : denom;
+    if (t < K) {
+        float w = ex / denom;
+        if (P.escale) w = w * P.escale[(int64_t)layer * E + min(max(it, 0), E - 1)];
+        m->ids[t] = it;
+        m->wts[t] = w;
+        if (record) {
+            if (P.ids_out) P.ids_out[layer * K + t] = it;
+            if (P.wts_out) P.wts_out[layer * K + t] = w;
+        }
+        m->pown[unit_slot(m, K, t, first)] = t;
+    }
 }
 
 // Router weights of `layer` for group g into registers: thread (e = t/4,
@@ -329,11 +401,16 @@ __device__ __forceinline__ void group_load_router(const FusedParams& P, int laye
 // Group g's share of the router for its x rows gx (H/8 floats in LDS), in
 // the R-order: chunk partials (fma chain over the chunk's 16 rows, from
 // 0.0f), summed over the group's C chunks in order (from 0.0f); and the q8
-// blocks of the rows. Publishes [E sums][qw q8 words] tagged, to each replica.
-template <int CPT, int C>
-__device__ void group_publish(const FusedParams& P, int g, const float4 (&wv)[CPT][4], const float* gx, float* gp,
-                              uint32_t* q8w, uint64_t* dst, uint32_t tag, int sl) {
-    const int E = P.E, t = threadIdx.x;
+// blocks of the rows. Publishes [E sums][qw q8 words] tagged, to each replica;
+// pred: only the E sums, to dst[g * E + e] (no q8, one copy).
+template <int CPT, int C, bool DBG>
+__device__ __forceinline__ void group_publish(const FusedParams& P, int g, const float4 (&wv)[CPT][4], const float* gx, float* gp,
+                              uint32_t* q8w, uint64_t* dst, uint32_t tag, int sl, bool pred = false) {
+    // E behind an opaque move: the C chunk offsets c*E are formed here, not
+    // hoisted to the kernel's start and kept (spilled) for its lifetime
+    int E = P.E;
+    asm volatile("" : "+s"(E));
+    const int t = tid_here();
     const int e = t >> 2, q = t & 3;
     if (e < E) {
 #pragma unroll
@@ -355,10 +432,10 @@ __device__ void group_publish(const FusedParams& P, int g, const float4 (&wv)[CP
         }
     }
     const int nbq = (P.H / NGROUP) >> 5;  // q8 blocks per group; one lane quad each
-    if (t < 4 * nbq) quantize_block_quad(gx + 32 * (t >> 2), t & 3, q8w + (t >> 2) * 10);
-    stamp(P, sl, 20);
+    if (!pred && t < 4 * nbq) quantize_block_quad(gx + 32 * (t >> 2), t & 3, q8w + (t >> 2) * 10);
+    stamp<DBG>(P, sl, 20);
     __syncthreads();
-    stamp(P, sl, 21);
+    stamp<DBG>(P, sl, 21);
     if (t < E) {
         float pv[C];
 #pragma unroll
@@ -369,7 +446,11 @@ __device__ void group_publish(const FusedParams& P, int g, const float4 (&wv)[CP
         gp[C * E + t] = s;
     }
     __syncthreads();
-    stamp(P, sl, 22);
+    stamp<DBG>(P, sl, 22);
+    if (pred) {
+        if (t < E) st_tag(dst + g * E + t, tag, __float_as_uint(gp[C * E + t]));
+        return;
+    }
     const int n = E + P.qw;
     for (int i = t; i < n * NREP; i += FT_THREADS) {
         const int rep = i / n, k = i - rep * n;
@@ -378,17 +459,24 @@ __device__ void group_publish(const FusedParams& P, int g, const float4 (&wv)[CP
     }
 }
 
+// The bias of thread t's expert (t < E) for `layer`, or 0 without a bias;
+// issued early so that the load is back by the time routing needs it.
+__device__ __forceinline__ float ld_bias(const FusedParams& P, int layer) {
+    const int t = threadIdx.x;
+    return (P.bias && t < P.E) ? P.bias[(int64_t)layer * P.E + t] : 0.0f;
+}
+
 // BPW: gate|up blocks per wave, exactly H/32/8; DB: down blocks per thread,
 // ceil(I/32/4) (surplus blocks re-read a valid one and are masked); CPT:
 // router chunks per group-unit thread, ceil(H/128/4). Loads are
 // unconditional so that they issue back to back.
-template <int BPW, int DB, int CPT>
+template <int BPW, int DB, int CPT, bool DBG>
 __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P) {
     constexpr int C = 2 * BPW;  // router chunks per group = H/128
     extern __shared__ __align__(16) uint8_t lds[];
     uint8_t* act8 = lds + P.o_act8;
     float* red = reinterpret_cast<float*>(lds + P.o_red);
-    // expert units: [NGROUP][E] group sums, then the q8 of x as [H/32][8]
+    // expert units: [E][NGROUP] group sums, then the q8 of x as [H/32][8]
     // qs words (16-byte aligned) and [H/32] (d, qsum) pairs
     uint32_t* gq = reinterpret_cast<uint32_t*>(lds + P.o_gq);
     const uint4* xq4 = reinterpret_cast<const uint4*>(gq + NGROUP * P.E);
@@ -402,7 +490,6 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     const int H = P.H, I = P.I, E = P.E, K = P.K, L = P.L;
     const int nb = H >> 5, nbj = I >> 5, HG = H / NGROUP;
     if (t == 0) m->abort_flag = 0;
-    if (t < 17) m->expk[t] = exp_table().k[t];
     __syncthreads();
     // A workspace whose abort word is set (an earlier launch gave up a wait)
     // is poisoned until ft_hip_fused_workspace_init: its epoch may not have
@@ -413,43 +500,74 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     auto tag_a = [&](int l) { return epoch + 4u * l + 2u; };
     auto tag_y = [&](int l) { return epoch + 4u * l + 3u; };
     auto gq_buf = [&](int l) { return P.gq_t + (int64_t)(l & 1) * NREP * P.rs_gq; };
+    auto pp_buf = [&](int l) { return P.pp_t + (int64_t)(l & 1) * NGROUP * E; };
+    auto pid_buf = [&](int l) { return P.pid_t + (int64_t)(l & 1) * NREP * PID_STRIDE; };
     auto ident = [](int i) { return (int64_t)i; };
     const int rep = w % NREP;  // workgroups are dealt to the 8 XCDs round-robin
+    const bool pf = P.prefetch != 0;
     if (t == 0) st_tag(P.pl_t + w, tag_g(0), xcc_id());
 
     if (w >= P.n_unit) {
-        // ======================= group unit =======================
-        const int g = w - P.n_unit, r0 = g * HG;
+        // ============ group unit (routing) or pred unit (prediction) ============
+        // Both combine the same rows bit for bit. A group unit then applies the
+        // router of layer l+1 (true routing of l+1, q8 of x_{l+1}); a pred unit
+        // the router of layer l+2 (the prediction of layer l+2). Ordering of
+        // the double-buffered words: a pred unit publishes the prediction of
+        // layer l+2 only after reading every group unit's routing of layer
+        // l+1, which each group unit publishes after reading the prediction
+        // of layer l from the same buffer parity.
+        const bool pu = w >= P.n_unit + NGROUP;
+        const int g = w - P.n_unit - (pu ? NGROUP : 0), r0 = g * HG;
+        const bool record = !pu && g == 0;  // group unit 0 writes ids/wts
+        if (pu && (!pf || L < 2)) return;    // nothing to predict
         uint32_t* q8w = reinterpret_cast<uint32_t*>(gp + (C + 1) * E);
         float4 wv[CPT][4];
         auto gidx = [=](int i) { return (int64_t)(i / E) * P.gq_stride + i % E; };
-        stamp(P, -1, 0);
-        group_load_router<CPT, C>(P, 0, g, wv);
+        auto gdst = [=](int i) { return (i % E) * NGROUP + i / E; };  // group sums -> LDS [E][NGROUP]
+        stamp<DBG>(P, -1, 0);
+        group_load_router<CPT, C>(P, pu ? 1 : 0, g, wv);
+        float bias_n = ld_bias(P, 0), bias_p = pu ? ld_bias(P, 1) : 0.0f;
         for (int i = t; i < HG; i += FT_THREADS) {
             gx[i] = P.x_in[r0 + i];
-            if (P.dbg_x) P.dbg_x[r0 + i] = gx[i];
+            if (DBG && P.dbg_x && !pu) P.dbg_x[r0 + i] = gx[i];
         }
         __syncthreads();
-        group_publish<CPT, C>(P, g, wv, gx, gp, q8w, gq_buf(0), tag_g(0), -1);
-        stamp(P, -1, 11);
-        if (!wait_words(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(0), gq)) return;
-        stamp(P, -1, 12);
-        route(P, m, reinterpret_cast<const float*>(gq), 0);
-        stamp(P, -1, 14);
+        if (pu) {
+            group_publish<CPT, C, DBG>(P, g, wv, gx, gp, q8w, pp_buf(1), tag_g(1), -1, true);
+            if (!wait_words<DBG>(P, m, epoch, pp_buf(1), NGROUP * E, ident, tag_g(1), gq, gdst)) return;
+            route_rank(P, m, reinterpret_cast<const float*>(gq), bias_p, 1, nullptr);
+            if (!wait_words<DBG>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(0), gq, gdst)) return;
+            if (t < K) st_tag(pid_buf(1) + rep * PID_STRIDE + t, tag_g(1), (uint32_t)m->pid[1][t]);
+        } else {
+            group_publish<CPT, C, DBG>(P, g, wv, gx, gp, q8w, gq_buf(0), tag_g(0), -1);
+            stamp<DBG>(P, -1, 11);
+            if (!wait_words<DBG>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(0), gq, gdst)) return;
+        }
+        stamp<DBG>(P, -1, 12);
+        route_rank(P, m, reinterpret_cast<const float*>(gq), bias_n, -1, nullptr);
+        route_weights(P, m, 0, true, record);
+        stamp<DBG>(P, -1, 14);
         for (int l = 0; l < L; ++l) {
-            stamp(P, l, 0);
-            if (l + 1 < L) group_load_router<CPT, C>(P, l + 1, g, wv);
-            stamp(P, l, 1);
+            stamp<DBG>(P, l, 0);
+            const int rl = pu ? l + 2 : l + 1;  // the router layer applied after this layer's combine
+            if (rl < L) group_load_router<CPT, C>(P, rl, g, wv);
+            if (l + 1 < L) bias_n = ld_bias(P, l + 1);
+            if (pu && l + 2 < L) bias_p = ld_bias(P, l + 2);
+            stamp<DBG>(P, l, 1);
+            // y of every unit group for this group's rows, [u][HG] in LDS
             auto yidx = [=](int i) { return (int64_t)(i / HG) * H + r0 + i % HG; };
-            if (!wait_words(P, m, epoch, P.y_t, K * HG, yidx, tag_y(l), reinterpret_cast<uint32_t*>(gy), l, 26)) return;
-            stamp(P, l, 8);
+            if (!wait_words<DBG>(P, m, epoch, P.y_t, K * HG, yidx, tag_y(l), reinterpret_cast<uint32_t*>(gy), l, 26)) return;
+            stamp<DBG>(P, l, 8);
             // x_{l+1} = x_l + sum_p (y_p * w_p), pairs in routing order
-            // (ft-model/src/lib.rs:1634-1646)
+            // (ft-model/src/lib.rs:1634-1646); slot p ran on unit group pown[p]
+            int own[MAX_K];
+#pragma unroll
+            for (int q = 0; q < MAX_K; ++q) own[q] = m->pown[min(q, K - 1)];
             for (int r = t; r < HG; r += FT_THREADS) {
                 float yv[MAX_K], wk[MAX_K];
 #pragma unroll
                 for (int q = 0; q < MAX_K; ++q) {
-                    yv[q] = gy[min(q, K - 1) * HG + r];
+                    yv[q] = gy[own[q] * HG + r];
                     wk[q] = m->wts[q];
                 }
                 float h = 0.0f;
@@ -460,25 +578,47 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                 }
                 const float xn = gx[r] + h;
                 gx[r] = xn;
-                if (l == L - 1) P.x_out[r0 + r] = xn;
-                if (P.dbg_x) P.dbg_x[(int64_t)(l + 1) * H + r0 + r] = xn;
+                if (!pu) {
+                    if (l == L - 1) P.x_out[r0 + r] = xn;
+                    if (DBG && P.dbg_x) P.dbg_x[(int64_t)(l + 1) * H + r0 + r] = xn;
+                }
             }
             __syncthreads();
-            stamp(P, l, 9);
+            stamp<DBG>(P, l, 9);
             if (l + 1 == L) break;
-            group_publish<CPT, C>(P, g, wv, gx, gp, q8w, gq_buf(l + 1), tag_g(l + 1), l);
-            stamp(P, l, 11);
-            if (!wait_words(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(l + 1), gq, l, 24))
-                return;
-            stamp(P, l, 12);
-            route(P, m, reinterpret_cast<const float*>(gq), l + 1);
-            stamp(P, l, 14);
+            if (pu) {
+                if (l + 2 < L) {
+                    group_publish<CPT, C, DBG>(P, g, wv, gx, gp, q8w, pp_buf(l + 2), tag_g(l + 2), l, true);
+                    stamp<DBG>(P, l, 11);
+                    if (!wait_words<DBG>(P, m, epoch, pp_buf(l + 2), NGROUP * E, ident, tag_g(l + 2), gq, gdst, l, 24)) return;
+                    route_rank(P, m, reinterpret_cast<const float*>(gq), bias_p, l & 1, nullptr);
+                }
+                if (!wait_words<DBG>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(l + 1), gq, gdst))
+                    return;
+                stamp<DBG>(P, l, 12);
+                if (l + 2 < L && t < K)
+                    st_tag(pid_buf(l + 2) + rep * PID_STRIDE + t, tag_g(l + 2), (uint32_t)m->pid[l & 1][t]);
+            } else {
+                group_publish<CPT, C, DBG>(P, g, wv, gx, gp, q8w, gq_buf(l + 1), tag_g(l + 1), l);
+                stamp<DBG>(P, l, 11);
+                if (!wait_words<DBG>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(l + 1), gq, gdst, l,
+                                24))
+                    return;
+                stamp<DBG>(P, l, 12);
+                // the prediction of layer l+1, for the slot -> unit group map
+                if (pf && !wait_words<DBG>(P, m, epoch, pid_buf(l + 1) + rep * PID_STRIDE, K, ident, tag_g(l + 1),
+                                      reinterpret_cast<uint32_t*>(m->pid[(l + 1) & 1]), l, 27))
+                    return;
+            }
+            route_rank(P, m, reinterpret_cast<const float*>(gq), bias_n, -1, pf ? m->pid[(l + 1) & 1] : nullptr);
+            route_weights(P, m, l + 1, !pf, record);
+            stamp<DBG>(P, l, 14);
         }
         return;
     }
 
     // ======================= expert unit =======================
-    const int p = w % K, j = w / K;
+    const int u = w % K, j = w / K;
     const bool gm = w < P.n_gu, dm = w < P.n_dn;  // false: that part of the unit is idle
     const int dn_tile = nbj * 288;               // bytes of one 16-row down tile
     const int nq = E + P.qw;
@@ -489,41 +629,43 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     auto xdst = [=](int i) {
         const int g = i / nq, k = i - g * nq;
         const int kk = k - E, bl = kk / 10, wd = kk - bl * 10, blk = g * (P.qw / 10) + bl;
-        return k < E ? g * E + k : NGROUP * E + (wd >= 2 ? blk * 8 + (wd - 2) : nb * 8 + blk * 2 + wd);
+        return k < E ? k * NGROUP + g : NGROUP * E + (wd >= 2 ? blk * 8 + (wd - 2) : nb * 8 + blk * 2 + wd);
     };
-    stamp(P, -1, 0);
-    if (!wait_words(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * nq, xidx, tag_g(0), gq, xdst)) return;
-    // The act hand-over of routed slot p stays in the XCD's L2 (plain stores,
-    // agent-scope polls) when every unit of slot p runs on this workgroup's
+    stamp<DBG>(P, -1, 0);
+    float bias_n = ld_bias(P, 0);
+    if (!wait_words<DBG>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * nq, xidx, tag_g(0), gq, xdst)) return;
+    // The act hand-over of unit group u stays in the XCD's L2 (plain stores,
+    // agent-scope polls) when every unit of group u runs on this workgroup's
     // XCD; otherwise its stores write through.
     bool act_local;
     {
-        const int upe = P.n_unit / K;  // units per routed slot
+        const int upe = P.n_unit / K;  // units per unit group
         uint32_t* xw = reinterpret_cast<uint32_t*>(red);
-        if (!wait_words(P, m, epoch, P.pl_t, upe, [=](int i) { return (int64_t)(p + K * i); }, tag_g(0), xw)) return;
+        if (!wait_words<DBG>(P, m, epoch, P.pl_t, upe, [=](int i) { return (int64_t)(u + K * i); }, tag_g(0), xw)) return;
         act_local = __syncthreads_and(t >= upe || xw[t] == xcc_id()) != 0;
-        trace_value(P, -1, 27, act_local ? 1u : 0u);
-        trace_value(P, -1, 28, xcc_id());
+        trace_value<DBG>(P, -1, 27, act_local ? 1u : 0u);
+        trace_value<DBG>(P, -1, 28, xcc_id());
     }
-    stamp(P, -1, 12);
-    route(P, m, reinterpret_cast<const float*>(gq), 0);
-    stamp(P, -1, 14);
+    stamp<DBG>(P, -1, 12);
+    route_rank(P, m, reinterpret_cast<const float*>(gq), bias_n, -1, nullptr);
 
-    for (int l = 0; l < L; ++l) {
-        stamp(P, l, 0);
-        // per-thread offsets derived from an opaque thread index: hoisted out
-        // of the layer loop they would stay live (and spill) for the kernel
+    // This unit's share of its expert, in registers from the load to the dots
+    // (a prefetch holds it across the end of the previous layer):
+    //   gate|up tile j, 64 rows x BPW blocks per wave: qv (16 B of nibbles per
+    //   row and block), sc (the f16 scale, widened to 32 bits so that loads
+    //   do not pair up and wait for each other);
+    //   down rows 128j + 16*wave + rr, blocks s4, s4+4, ...: dq, dsc.
+    uint32_t sc[BPW];
+    uint4 qv[BPW];
+    uint32_t dsc[DB];
+    uint4 dq[DB];
+    auto load_tiles = [&](int layer, int eid) __attribute__((always_inline)) {
+        // per-thread offsets from an opaque thread index: hoisted out of the
+        // layer loop they would stay live (and spill) for the whole kernel
         int tl = threadIdx.x;
         asm volatile("" : "+v"(tl));
-        // the routed id is in [0, E) by construction; the clamp keeps any
-        // future logic error from turning into an out-of-bounds weight read
-        const int eid = min(max(m->ids[p], 0), E - 1);
-        const uint8_t* xb = P.banks + ((int64_t)l * E + eid) * P.expert_bytes;
-        const int wave = tl >> 6, r = tl & 63;
-        // ---- gate|up tile j of expert ids[p]: 64 rows x BPW blocks per wave ----
-        const int b0 = wave * BPW;
-        uint32_t sc[BPW];  // 32-bit: 16-bit elements would be packed in pairs, forcing a wait per load
-        uint4 qv[BPW];
+        const uint8_t* xb = P.banks + ((int64_t)layer * E + eid) * P.expert_bytes;
+        const int wave = tl >> 6, r = tl & 63, b0 = wave * BPW;
         {
             // a unit without a gate|up tile re-reads tile 0 of expert 0 of
             // layer 0 (shared by all such units, so it stays in cache)
@@ -537,11 +679,8 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
 #pragma unroll
             for (int i = 0; i < BPW; ++i) sc[i] = *reinterpret_cast<const uint16_t*>(Ts + i * 128);
         }
-        // ---- down unit j: rows 128j + 16*wave + rr, blocks s4, s4+4, ... ----
-        const int s4 = tl & 3, rr = (tl >> 2) & 15;
-        uint32_t dsc[DB];
-        uint4 dq[DB];
         {
+            const int s4 = tl & 3, rr = (tl >> 2) & 15;
             const uint8_t* D = (dm ? xb + (int64_t)(j * FT_WAVES + wave) * dn_tile : P.banks) + P.gu_bytes;
 #pragma unroll
             for (int k = 0; k < DB; ++k) {
@@ -555,7 +694,22 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                 dsc[k] = *reinterpret_cast<const uint16_t*>(D + b * 32 + rr * 2);
             }
         }
-        stamp(P, l, 1);
+        asm volatile("" ::: "memory");  // issued here, not sunk towards the first use
+    };
+    // layer 0: nothing held; slot u runs on unit group u
+    int p = u;
+    // the routed id is in [0, E) by construction; the clamp keeps any future
+    // logic error from turning into an out-of-bounds weight read
+    int eid = min(max(m->sel_i[p], 0), E - 1);
+    load_tiles(0, eid);
+    trace_value<DBG>(P, 0, 10, 1u);
+    stamp<DBG>(P, -1, 14);
+
+    for (int l = 0; l < L; ++l) {
+        stamp<DBG>(P, l, 0);
+        int tl = threadIdx.x;
+        asm volatile("" : "+v"(tl));
+        const int wave = tl >> 6, r = tl & 63, b0 = wave * BPW, s4 = tl & 3, rr = (tl >> 2) & 15;
         // ---- gate|up dots -> GELU*up -> q8 block, published ----
         if (gm) {
             float acc = 0.0f;
@@ -566,50 +720,67 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                 const int diff = block_dot_v(qv[i], lo, hi, dq8.y);
                 acc = fmaf((float)diff, h2f((uint16_t)sc[i]) * __int_as_float(dq8.x), acc);
             }
-            stamp(P, l, 2);
+            stamp<DBG>(P, l, 2);
             red[wave * 64 + r] = acc;
             __syncthreads();
-            if (t < 64) {  // wave 0 finishes the unit: only wave-local ordering from here
-                float rv[FT_WAVES];
+            if (t < 32) {
+                // lane t: gate row j*32+t and up row I+j*32+t, the 8 wave
+                // partials summed in wave order; GELU*up; the q8 block of the
+                // 32 lanes, published as {d, qsum, 8 words of qs}
+                float gv[FT_WAVES], uv[FT_WAVES];
 #pragma unroll
-                for (int v = 0; v < FT_WAVES; ++v) rv[v] = red[v * 64 + t];
-                float s = 0.0f;
+                for (int v = 0; v < FT_WAVES; ++v) {
+                    gv[v] = red[v * 64 + t];
+                    uv[v] = red[v * 64 + 32 + t];
+                }
+                float sg = 0.0f, su = 0.0f;
 #pragma unroll
-                for (int v = 0; v < FT_WAVES; ++v) s = s + rv[v];
-                if (P.dbg_gu) {
-                    const int row = t < 32 ? j * 32 + t : I + j * 32 + (t - 32);
-                    P.dbg_gu[((int64_t)l * K + p) * 2 * I + row] = s;
+                for (int v = 0; v < FT_WAVES; ++v) {
+                    sg = sg + gv[v];
+                    su = su + uv[v];
                 }
-                m->gsum[t] = s;
-                stamp(P, l, 17);
-                wave_lds_order();
-                if (t < 32) m->act[t] = gelu_tanh_t(s, m->expk) * m->gsum[t + 32];
-                wave_lds_order();
-                stamp(P, l, 18);
-                if (t < 4) quantize_block_quad(m->act, t, m->actblk);
-                wave_lds_order();
-                stamp(P, l, 19);
-                if (t < 10) {
-                    if (act_local) st_tag_local(P.act_t + ((int64_t)p * nbj + j) * 10 + t, tag_a(l), m->actblk[t]);
-                    else st_tag(P.act_t + ((int64_t)p * nbj + j) * 10 + t, tag_a(l), m->actblk[t]);
-                    if (P.dbg_act)
-                        reinterpret_cast<uint32_t*>(P.dbg_act + (((int64_t)l * K + p) * nbj + j) * Q8_BLK)[t] =
-                            m->actblk[t];
+                if (DBG && P.dbg_gu) {
+                    float* dg = P.dbg_gu + ((int64_t)l * K + p) * 2 * I;
+                    dg[j * 32 + t] = sg;
+                    dg[I + j * 32 + t] = su;
                 }
+                stamp<DBG>(P, l, 17);
+                const float a = gelu_tanh_t(sg, ExpConstS{}) * su;
+                stamp<DBG>(P, l, 18);
+                float d;
+                int qsum;
+                const uint32_t wq = q8_quantize_lanes32(a, &d, &qsum);
+                uint64_t* dst = P.act_t + ((int64_t)u * nbj + j) * 10;
+                const int k = (t & 3) == 0 ? 2 + (t >> 2) : (t == 1 ? 0 : (t == 2 ? 1 : -1));
+                const uint32_t v = t == 1 ? __float_as_uint(d) : (t == 2 ? (uint32_t)qsum : wq);
+                if (k >= 0) {
+                    if (act_local) st_tag_local(dst + k, tag_a(l), v);
+                    else st_tag(dst + k, tag_a(l), v);
+                    if (DBG && P.dbg_act)
+                        reinterpret_cast<uint32_t*>(P.dbg_act + (((int64_t)l * K + p) * nbj + j) * Q8_BLK)[k] = v;
+                }
+                stamp<DBG>(P, l, 19);
             }
-            stamp(P, l, 3);
+            stamp<DBG>(P, l, 3);
         }
-        // ---- down: the act blocks of expert slot p, then y_p of 128 rows ----
+        // the prediction of layer l+1 (published during layer l-1): read while
+        // the act blocks are on their way, so the prefetch can follow the y
+        // publish directly
+        if (pf && l + 1 < L &&
+            !wait_words<DBG>(P, m, epoch, pid_buf(l + 1) + rep * PID_STRIDE, K, ident, tag_g(l + 1),
+                             reinterpret_cast<uint32_t*>(m->pid[(l + 1) & 1]), l, 27))
+            return;
+        // ---- down: the act blocks of unit group u, then y of 128 rows ----
         if (dm) {
             // act8: [nbj blocks x 32 B qs][nbj (d, qsum) pairs] (16-B aligned qs)
             auto act_dst = [=](int i) {
                 const int bi = i / 10, k = i - bi * 10;
                 return k >= 2 ? bi * 8 + (k - 2) : nbj * 8 + bi * 2 + k;
             };
-            if (!wait_words<true>(P, m, epoch, P.act_t + (int64_t)p * nbj * 10, nbj * 10, ident, tag_a(l),
+            if (!wait_words<DBG, true>(P, m, epoch, P.act_t + (int64_t)u * nbj * 10, nbj * 10, ident, tag_a(l),
                                   reinterpret_cast<uint32_t*>(act8), act_dst, l, 25))
                 return;
-            stamp(P, l, 4);
+            stamp<DBG>(P, l, 4);
             const uint4* aq4 = reinterpret_cast<const uint4*>(act8);
             const int2* adp = reinterpret_cast<const int2*>(act8 + nbj * 32);
             int s4o = threadIdx.x & 3;
@@ -632,18 +803,30 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
             }
             acc += quad_xor1(acc);
             acc += quad_xor2(acc);
-            stamp(P, l, 5);
+            stamp<DBG>(P, l, 5);
             if (s4 == 0)
-                st_tag(P.y_t + (int64_t)p * H + j * DN_UNIT + wave * DN_ROWS + rr, tag_y(l), __float_as_uint(acc));
-            stamp(P, l, 6);
+                st_tag(P.y_t + (int64_t)u * H + j * DN_UNIT + wave * DN_ROWS + rr, tag_y(l), __float_as_uint(acc));
+            stamp<DBG>(P, l, 6);
         }
         if (l + 1 == L) break;
+        bias_n = ld_bias(P, l + 1);
+        // ---- prefetch: the predicted expert of layer l+1 for this unit group ----
+        if (pf) {
+            load_tiles(l + 1, min(max(m->pid[(l + 1) & 1][u], 0), E - 1));
+            stamp<DBG>(P, l, 7);
+        }
         // ---- routing of layer l+1 and the q8 of x_{l+1}, from the group units ----
-        if (!wait_words(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * nq, xidx, tag_g(l + 1), gq, xdst, l, 24))
+        if (!wait_words<DBG>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * nq, xidx, tag_g(l + 1), gq, xdst, l, 24))
             return;
-        stamp(P, l, 12);
-        route(P, m, reinterpret_cast<const float*>(gq), l + 1);
-        stamp(P, l, 14);
+        stamp<DBG>(P, l, 12);
+        route_rank(P, m, reinterpret_cast<const float*>(gq), bias_n, -1, pf ? m->pid[(l + 1) & 1] : nullptr);
+        stamp<DBG>(P, l, 13);
+        p = unit_slot(m, K, u, !pf);
+        eid = min(max(m->sel_i[p], 0), E - 1);
+        const bool miss = !pf || eid != m->pid[(l + 1) & 1][u];
+        if (miss) load_tiles(l + 1, eid);
+        trace_value<DBG>(P, l + 1, 10, miss ? 1u : 0u);
+        stamp<DBG>(P, l, 14);
     }
     if (w == 0 && t == 0)
         __hip_atomic_store(P.ctl + CTL_EPOCH, epoch + 4u * (L + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -737,7 +920,7 @@ __global__ void k_fill_u32(uint32_t* p, int64_t n, uint32_t v) {
 // host side
 // ---------------------------------------------------------------------------
 struct WsLayout {
-    int64_t ctl, act, y, gq, pl, total;
+    int64_t ctl, act, y, gq, pp, pid, pl, total;
     int gq_stride, qw;
     int64_t rs_gq;  // words
 };
@@ -753,7 +936,9 @@ WsLayout ws_layout(int64_t H, int64_t I, int64_t E, int64_t K) {
     w.act = off; off += up(K * (I / 32) * 10 * 8);
     w.y = off; off += up(K * H * 8);
     w.gq = off; off += 2 * NREP * up(w.rs_gq * 8);
-    w.pl = off; off += up(((int64_t)std::max(K * (I / 32), K * (H / DN_UNIT)) + NGROUP) * 8);
+    w.pp = off; off += 2 * up(NGROUP * E * 8);
+    w.pid = off; off += 2 * up(NREP * PID_STRIDE * 8);
+    w.pl = off; off += up(((int64_t)std::max(K * (I / 32), K * (H / DN_UNIT)) + 2 * NGROUP) * 8);
     w.total = off;
     return w;
 }
@@ -792,7 +977,7 @@ extern "C" size_t ft_hip_fused_workspace_bytes(int64_t hidden, int64_t inter, in
 extern "C" int ft_hip_fused_workgroups(int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k) {
     if (hidden <= 0 || hidden % 256 || inter <= 0 || inter % 32 || n_experts <= 0 || top_k <= 0) return -1;
     int n_gu, n_dn;
-    return fused_units(hidden, inter, top_k, &n_gu, &n_dn) + NGROUP;
+    return fused_units(hidden, inter, top_k, &n_gu, &n_dn) + 2 * NGROUP;
 }
 
 extern "C" int ft_hip_fused_workspace_init(ft_hip_ctx* ctx, void* stream, void* workspace, size_t workspace_bytes) {
@@ -870,7 +1055,7 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
     P.K = (int)top_k;
     P.L = (int)n_layers;
     P.n_unit = fused_units(hidden, inter, top_k, &P.n_gu, &P.n_dn);
-    const int nw = P.n_unit + NGROUP;
+    const int nw = P.n_unit + 2 * NGROUP;
     P.gq_stride = wl.gq_stride;
     P.qw = wl.qw;
     P.rs_gq = (wl.rs_gq * 8 + 255) / 256 * 256 / 8;
@@ -905,6 +1090,8 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
     P.act_t = (uint64_t*)(ws + wl.act);
     P.y_t = (uint64_t*)(ws + wl.y);
     P.gq_t = (uint64_t*)(ws + wl.gq);
+    P.pp_t = (uint64_t*)(ws + wl.pp);
+    P.pid_t = (uint64_t*)(ws + wl.pid);
     P.pl_t = (uint64_t*)(ws + wl.pl);
     P.ctl = (uint32_t*)(ws + wl.ctl);
     P.dbg_gu = dbg_gu;
@@ -914,13 +1101,22 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
     P.expert_bytes = ft_hip_fused_expert_bytes(hidden, inter);
     P.gu_bytes = 2 * inter * (hidden / 32) * 18;
     P.spin_limit = ctx->fused_spin_limit;
+    P.prefetch = ctx->fused_prefetch;
     void* args[] = {&P};
     // the kernel keeps exactly H/256 gate|up blocks per wave in flight
     const bool db6 = inter / 32 <= 24;
-    const void* kern = hidden == 2816 ? (db6 ? reinterpret_cast<const void*>(k_moe_stack_fused<11, 6, 6>)
-                                             : reinterpret_cast<const void*>(k_moe_stack_fused<11, 8, 6>))
-                                      : (db6 ? reinterpret_cast<const void*>(k_moe_stack_fused<GU_BPW_MAX, 6, 8>)
-                                             : reinterpret_cast<const void*>(k_moe_stack_fused<GU_BPW_MAX, 8, 8>));
+    // debug records and the phase trace are compiled in only when asked for
+    const bool dbg = dbg_gu || dbg_act || dbg_x || dbg_trace;
+    const void* kern =
+        hidden == 2816
+            ? (db6 ? (dbg ? reinterpret_cast<const void*>(k_moe_stack_fused<11, 6, 6, true>)
+                          : reinterpret_cast<const void*>(k_moe_stack_fused<11, 6, 6, false>))
+                   : (dbg ? reinterpret_cast<const void*>(k_moe_stack_fused<11, 8, 6, true>)
+                          : reinterpret_cast<const void*>(k_moe_stack_fused<11, 8, 6, false>)))
+            : (db6 ? (dbg ? reinterpret_cast<const void*>(k_moe_stack_fused<GU_BPW_MAX, 6, 8, true>)
+                          : reinterpret_cast<const void*>(k_moe_stack_fused<GU_BPW_MAX, 6, 8, false>))
+                   : (dbg ? reinterpret_cast<const void*>(k_moe_stack_fused<GU_BPW_MAX, 8, 8, true>)
+                          : reinterpret_cast<const void*>(k_moe_stack_fused<GU_BPW_MAX, 8, 8, false>)));
     // A plain launch: every workgroup must be resident at once, which holds
     // when the kernel has the device to itself (nw <= CUs, one workgroup per
     // CU). A cooperative launch guarantees it but costs ~19 us per launch
@@ -938,6 +1134,14 @@ extern "C" int ft_hip_fused_set_spin_limit(ft_hip_ctx* ctx, int polls) {
     if (!ctx) return fail(FT_HIP_E_INVALID, "fused_set_spin_limit: null ctx");
     if (polls < 0) return fail(FT_HIP_E_SHAPE, "fused_set_spin_limit: polls=%d < 0", polls);
     ctx->fused_spin_limit = polls;
+    return FT_HIP_OK;
+}
+
+extern "C" int ft_hip_fused_set_prefetch(ft_hip_ctx* ctx, int on) {
+    clear_error();
+    if (!ctx) return fail(FT_HIP_E_INVALID, "fused_set_prefetch: null ctx");
+    if (on != 0 && on != 1) return fail(FT_HIP_E_SHAPE, "fused_set_prefetch: on=%d is not 0 or 1", on);
+    ctx->fused_prefetch = on;
     return FT_HIP_OK;
 }
 

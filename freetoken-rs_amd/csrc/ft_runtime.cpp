@@ -55,6 +55,7 @@ extern "C" int ft_hip_create(int device, ft_hip_ctx** out) {
     c->num_cus = p.multiProcessorCount;
     c->num_xcds = 8;  // MI355X: 8 XCDs of 32 CUs
     c->fused_spin_limit = 1 << 21;
+    c->fused_prefetch = 1;
     std::snprintf(c->arch, sizeof c->arch, "%s", p.gcnArchName);
     *out = c;
     return FT_HIP_OK;

@@ -11,6 +11,7 @@ struct ft_hip_ctx {
     int num_cus;
     int num_xcds;
     int fused_spin_limit;  // polls before a fused-kernel wait gives up
+    int fused_prefetch;    // fused kernel: stream predicted experts ahead (1) or not (0)
     char arch[64];
 };
 

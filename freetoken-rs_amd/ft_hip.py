@@ -53,6 +53,7 @@ SIGNATURES = {
     "ft_hip_fused_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
     "ft_hip_fused_workgroups": (ctypes.c_int, [_I64, _I64, _I64, _I64]),
     "ft_hip_fused_set_spin_limit": (_I, [_P, _I]),
+    "ft_hip_fused_set_prefetch": (_I, [_P, _I]),
     "ft_hip_fused_workspace_init": (_I, [_P, _P, _P, _SZ]),
     "ft_hip_pack_experts_fused": (_I, [_P, _P, _P, _I, _U64, _P, _I64, _I64, _I64]),
     "ft_hip_pack_router_fused": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
@@ -249,6 +250,10 @@ class Q4Gemv:
 
     def fused_set_spin_limit(self, polls):
         check(lib().ft_hip_fused_set_spin_limit(self._ctx, polls))
+
+    def fused_set_prefetch(self, on):
+        """1: stream early-routed experts ahead (default); 0: load each layer's experts once routed."""
+        check(lib().ft_hip_fused_set_prefetch(self._ctx, int(on)))
 
     def fused_workspace_init(self, ws, stream=None):
         check(lib().ft_hip_fused_workspace_init(self._ctx, _stream(stream), _ptr(ws), ws.numel() * ws.element_size()))

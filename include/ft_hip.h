@@ -267,6 +267,16 @@ int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float* x_in, flo
  * the reference, whose launch sequence has no cross-workgroup waits. */
 int ft_hip_fused_set_spin_limit(ft_hip_ctx* ctx, int polls);
 
+/* Fused kernel, 1 (default): while layer l finishes, every unit group streams
+ * the tiles of the expert that early routing (layer l+1's router applied to
+ * x_l) predicts, and only mispredicted experts are loaded after the true
+ * routing of l+1; 0: each layer loads its routed experts once routed.
+ * Results are identical either way. A performance choice with no reference
+ * counterpart (the reference's SlotCache, ft-core/src/lib.rs:61-91, keeps
+ * recently routed experts in device slots and copies misses over PCIe after
+ * routing; it predicts nothing). */
+int ft_hip_fused_set_prefetch(ft_hip_ctx* ctx, int on);
+
 /* Host-synchronous check of a fused workspace after the stream has been
  * synchronised: FT_HIP_E_TIMEOUT (and *aborted = 1) if a launch gave up a
  * bounded wait. Such a workspace stays poisoned -- later launches on it do

@@ -85,24 +85,47 @@ def _run_debug(stack, token):
                 xs=host(dbg_x).reshape(L + 1, H))
 
 
+@pytest.fixture(scope="module")
+def zstack(gemv):
+    """Zipf(1.1)-skewed routing (BASELINE config 3's router bias)."""
+    m = moe_synth.SyntheticMoE(gemv, moe_synth.GEMMA, n_layers=4, zipf_s=1.1)
+    return moe_synth.FusedStack(m)
+
+
 def test_fused_stack_stages_teacher_forced(gemv, orc, stack):
+    _check_teacher_forced(orc, stack, 0)
+
+
+def test_fused_zipf_stages_teacher_forced(gemv, orc, zstack):
+    _check_teacher_forced(orc, zstack, 1)
+
+
+def test_fused_zipf_prefetch_does_not_change_results(gemv, zstack):
+    a = _run_plain(zstack, 2, 1)
+    b = _run_plain(zstack, 2, 0)
+    for u, v in zip(a, b):
+        assert np.array_equal(u.view(np.uint32), v.view(np.uint32))
+
+
+def _check_teacher_forced(orc, stack, token):
     m = stack.m
     s = m.shape
     H, I, E, K, L = s.hidden, s.inter, s.n_experts, s.top_k, m.L
-    r = _run_debug(stack, 0)
+    r = _run_debug(stack, token)
     assert np.array_equal(r["xs"][0], r["x"])
     assert np.array_equal(r["xs"][L], r["out"])
     for l in range(L):
         xl = r["xs"][l]
         Wr = host(m.routers[l])
-        ids, wts = orc.topk_softmax(orc.router_logits(Wr, xl), K)
+        bias = None if m.bias is None else host(m.bias[l])
+        ids, wts = orc.topk_softmax(orc.router_logits(Wr, xl, bias), K)
         assert np.array_equal(r["ids"][l], ids), f"layer {l}"
         assert np.array_equal(r["wts"][l].view(np.uint32), wts.view(np.uint32)), f"layer {l}"
         gu_b, dn_b = {}, {}
         for e in ids:
             b = host(m.bank_of(l, int(e)))
             gu_b[int(e)], dn_b[int(e)] = b[:m.gu_bytes], b[m.gu_bytes:]
-        ref = orc.moe_layer(xl, Wr, gu_b, dn_b, H, I, K, layout=1)
+        ref = orc.moe_layer(xl, Wr, gu_b, dn_b, H, I, K, bias=bias, layout=1)
         out_ref = xl.astype(np.float64).copy()
         for p in range(K):
             yg = ref["y_gu"][p]
@@ -156,6 +179,56 @@ def test_fused_repeatable_bit_for_bit(gemv, stack):
     for o, i in outs[1:]:
         assert np.array_equal(o.view(np.uint32), outs[0][0].view(np.uint32))
         assert np.array_equal(i, outs[0][1])
+
+
+def _run_plain(stack, token, prefetch):
+    m = stack.m
+    x = m.hidden(token)
+    o = torch.zeros_like(x)
+    ids = torch.zeros(m.L * m.shape.top_k, dtype=torch.int32, device=DEV)
+    wts = torch.zeros(m.L * m.shape.top_k, dtype=torch.float32, device=DEV)
+    stack.m.g.fused_set_prefetch(prefetch)
+    try:
+        stack.run(x, o, ids, wts)
+        stack.check()
+    finally:
+        stack.m.g.fused_set_prefetch(1)
+    return host(o), host(ids), host(wts)
+
+
+@pytest.mark.parametrize("token", [11, 12, 13])
+def test_fused_prefetch_does_not_change_results(gemv, stack, token):
+    """Prediction only decides which unit group holds which expert and what
+    is streamed ahead: outputs, ids and weights are bit-identical with and
+    without it (hits and misses both occur over these tokens)."""
+    a = _run_plain(stack, token, 1)
+    b = _run_plain(stack, token, 0)
+    for u, v in zip(a, b):
+        assert np.array_equal(u.view(np.uint32), v.view(np.uint32))
+
+
+@pytest.mark.parametrize("n_layers", [1, 2, 3])
+def test_fused_short_stacks(gemv, orc, n_layers):
+    """Stacks too short to predict (1 layer), predicting one layer ahead only
+    (2), and an odd layer count (3): same results as the launch-by-launch
+    layers on the fused kernel's own layer inputs."""
+    m = moe_synth.SyntheticMoE(gemv, moe_synth.GEMMA, n_layers=n_layers)
+    st = moe_synth.FusedStack(m)
+    r = _run_debug(st, 21 + n_layers)
+    s = m.shape
+    ws = m.workspace(1)
+    for l in range(m.L):
+        x = torch.from_numpy(r["xs"][l]).to(DEV)
+        xo = torch.zeros_like(x)
+        ids = torch.zeros(s.top_k, dtype=torch.int32, device=DEV)
+        wts = torch.zeros(s.top_k, dtype=torch.float32, device=DEV)
+        m.layer(l, x, xo, ids, wts, ws)
+        assert np.array_equal(host(ids), r["ids"][l])
+        assert np.array_equal(host(wts), r["wts"][l])
+        d_ref = host(xo) - r["xs"][l]
+        d = r["xs"][l + 1] - r["xs"][l]
+        assert np.max(np.abs(d - d_ref)) <= 1e-3 * np.linalg.norm(d_ref)
+    assert np.array_equal(r["xs"][m.L], r["out"])
 
 
 def test_fused_rejects_bad_shapes(gemv, stack):
