@@ -67,7 +67,7 @@ constexpr int DN_ROWS = 16;     // rows per router chunk and per down tile
 constexpr int DN_UNIT = DN_ROWS * FT_WAVES;  // rows per down unit: one tile per wave
 constexpr int WAIT_U = 8;       // tagged words per thread per wait (n <= 4096)
 constexpr int POLL_SLEEP = 1;   // s_sleep units (64 clocks) between polls
-constexpr int NREP = 8;         // replicas of the group broadcast, one per XCD
+constexpr int NREP = 1;         // replicas of the group broadcast
 constexpr int CTL_EPOCH = 0;    // control words (u32 indices)
 constexpr int CTL_ABORT = 32;
 constexpr int TRACE_SLOTS = 32; // stamps per workgroup per layer in the debug trace
@@ -83,10 +83,11 @@ struct FusedParams {
     int32_t* ids_out;           // [L][K] or null
     float* wts_out;             // [L][K] or null
     uint64_t* act_t;            // tagged [K][I/32][10]
-    uint64_t* y_t;              // tagged [K][H]
+    uint64_t* hp_t;             // tagged [K][I/32][8 wave slices][64 rows]: gate|up partials of missed tiles
+    uint64_t* y_t;              // tagged [2][K][H], by layer parity
     uint64_t* gq_t;             // tagged [2][NREP][NGROUP][gq_stride]: E group sums, then qw q8 words
     uint64_t* pp_t;             // tagged [2][NGROUP][E]: group sums of the predicting router
-    uint64_t* pid_t;            // tagged [2][NREP][PID_STRIDE]: predicted experts, one copy per XCD
+    uint64_t* pid_t;            // tagged [2][NGROUP][PID_STRIDE]: predicted experts, one copy per pred unit
     uint64_t* pl_t;             // tagged [grid]: the XCD each workgroup runs on
     int64_t rs_gq;              // replica stride (words); the parity stride is NREP * rs_gq
     uint32_t* ctl;              // [CTL_EPOCH] epoch, [CTL_ABORT] abort epoch
@@ -113,6 +114,9 @@ struct alignas(16) Misc {       // placed 16-byte aligned
     alignas(16) int pid[2][MAX_K];  // by layer parity: the expert unit group u holds (predicted)
     int uslot[MAX_K];           // slot of unit group u's held expert, -1: not routed
     int pown[MAX_K];            // unit group that runs routed slot p
+    int mlist[MAX_K];           // unit groups whose held expert was not routed (misses), ascending
+    int mexp[MAX_K];            // the expert each of them runs instead
+    int mcount;
     int abort_flag;
 };
 
@@ -143,67 +147,92 @@ __device__ __forceinline__ uint32_t ld_ctl(const uint32_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Block-wide wait until the n (<= 4096) tagged words src[idx(i)] all carry
-// `tag`; payloads land in dst[didx(i)] (LDS). Each lane re-reads only its
-// words still missing, and each wave spins on its own words without
-// synchronising (a lane that is done idles under the wave's exec mask); one
-// barrier ends the wait. Bounded: after spin_limit polls (or when another
-// workgroup has aborted) the lane records the abort and the wait returns
-// false in every thread.
+// threadIdx.x behind an opaque move: comparisons against it are recomputed
+// where they are used instead of being hoisted out of the layer loop as lane
+// masks, which would be spilled and reloaded (scalar register pressure).
+__device__ __forceinline__ int tid_here() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
 template <bool DBG>
 __device__ __forceinline__ void trace_value(const FusedParams& P, int l, int ev, uint64_t v) {
     if (DBG && P.trace && threadIdx.x == 0)
         P.trace[((int64_t)blockIdx.x * (P.L + 1) + (l + 1)) * TRACE_SLOTS + ev] = v;
 }
 
-template <bool DBG, bool AGENT = false, typename Idx, typename DIdx>
+// Block-wide wait until the n (<= U * FT_THREADS) tagged words src[idx(i)]
+// all carry `tag`; payloads land in dst[didx(i)] (LDS). Each lane owns words
+// tid, tid + FT_THREADS, ... and each wave spins on its own words without
+// synchronising; one barrier ends the wait.
+// Two poll rounds are kept in flight: a round is issued before the previous
+// one is checked, so a word is seen about half a memory round trip after it
+// lands instead of up to a whole one. Every round issues exactly U loads per
+// lane (a lane's finished or surplus words re-read a valid word), so the
+// compiler waits for the older round only.
+// Bounded: after spin_limit rounds (or when another workgroup has aborted)
+// the lane records the abort and the wait returns false in every thread.
+template <bool DBG, int U, bool AGENT = false, int NPOLL = FT_THREADS, typename Idx, typename DIdx>
 __device__ __forceinline__ bool wait_words(const FusedParams& P, Misc* m, uint32_t epoch, const uint64_t* src, int n,
                                            Idx idx, uint32_t tag, uint32_t* dst, DIdx didx, int tl = -2, int ts = 0) {
     // An opaque copy of the thread index: keeps the compiler from hoisting the
     // per-call-site address arithmetic out of the layer loop, where it would
     // stay live (in registers) for the whole kernel.
-    int tid = threadIdx.x;
-    asm volatile("" : "+v"(tid));
+    const int tid = tid_here();
     uint32_t pending = 0;
 #pragma unroll
-    for (int u = 0; u < WAIT_U; ++u)
-        if (u * FT_THREADS + tid < n) pending |= 1u << u;
-    int it = 0;
-    bool give_up = false;
-    while (pending) {
-        uint64_t v[WAIT_U];
+    for (int u = 0; u < U; ++u)
+        if (tid < NPOLL && u * NPOLL + tid < n) pending |= 1u << u;
+    auto issue = [&](uint64_t (&v)[U]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int u = 0; u < WAIT_U; ++u)
-            v[u] = (pending >> u) & 1 ? (AGENT ? ld_tag_agent(src + idx(u * FT_THREADS + tid))
-                                               : ld_tag(src + idx(u * FT_THREADS + tid)))
-                                      : 0;
+        for (int u = 0; u < U; ++u) {
+            const int64_t a = idx(min(u * NPOLL + tid, n - 1));
+            v[u] = AGENT ? ld_tag_agent(src + a) : ld_tag(src + a);
+        }
+    };
+    auto check = [&](const uint64_t (&v)[U]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int u = 0; u < WAIT_U; ++u)
+        for (int u = 0; u < U; ++u)
             if (((pending >> u) & 1) && (uint32_t)(v[u] >> 32) == tag) {
-                dst[didx(u * FT_THREADS + tid)] = (uint32_t)v[u];
+                dst[didx(u * NPOLL + tid)] = (uint32_t)v[u];
                 pending &= ~(1u << u);
             }
-        if (!pending) break;
+    };
+    int it = 0;
+    bool give_up = false;
+    auto bounded = [&]() __attribute__((always_inline)) {
         ++it;
         if (it >= P.spin_limit || ((it & 63) == 0 && ld_ctl(P.ctl + CTL_ABORT) == epoch)) {
             // published at once: the other lanes, waves and workgroups see it
-            // at their next check (every 64 polls) and give up too
+            // at their next check (every 64 rounds) and give up too
             __hip_atomic_store(P.ctl + CTL_ABORT, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             give_up = true;
-            break;
         }
+        return give_up;
+    };
+    uint64_t va[U], vb[U];
+    if (pending) issue(va);
+    while (pending) {
         __builtin_amdgcn_s_sleep(POLL_SLEEP);
+        issue(vb);
+        check(va);
+        if (!pending || bounded()) break;
+        __builtin_amdgcn_s_sleep(POLL_SLEEP);
+        issue(va);
+        check(vb);
+        if (!pending || bounded()) break;
     }
     if (give_up) m->abort_flag = 1;
-    if (tl > -2) trace_value<DBG>(P, tl, ts, (uint64_t)(it + 1));  // polls this wait took (thread 0)
+    if (tl > -2) trace_value<DBG>(P, tl, ts, (uint64_t)(it + 1));  // rounds this wait took (thread 0)
     __syncthreads();
     return m->abort_flag == 0;
 }
 
-template <bool DBG, typename Idx>
+template <bool DBG, int U, typename Idx>
 __device__ __forceinline__ bool wait_words(const FusedParams& P, Misc* m, uint32_t epoch, const uint64_t* src, int n,
                                            Idx idx, uint32_t tag, uint32_t* dst, int tl = -2, int ts = 0) {
-    return wait_words<DBG>(P, m, epoch, src, n, idx, tag, dst, [](int i) { return i; }, tl, ts);
+    return wait_words<DBG, U>(P, m, epoch, src, n, idx, tag, dst, [](int i) { return i; }, tl, ts);
 }
 
 // Trace slots (per workgroup and layer; layer -1 = prologue), wall-clock
@@ -229,15 +258,6 @@ __device__ __forceinline__ void stamp(const FusedParams& P, int l, int ev) {
 // exp(l - l_max), summed in rank order. Each logit carries a 64-bit key
 // (monotone float bits, then the complemented index) so that "sorts before"
 // is one unsigned compare; four threads share one logit's E comparisons.
-// threadIdx.x behind an opaque move: comparisons against it are recomputed
-// where they are used instead of being hoisted out of the layer loop as lane
-// masks, which would be spilled and reloaded (scalar register pressure).
-__device__ __forceinline__ int tid_here() {
-    int t = threadIdx.x;
-    asm volatile("" : "+v"(t));
-    return t;
-}
-
 __device__ __forceinline__ uint64_t rank_key(float v, int i) {
     v = v + 0.0f;  // -0 -> +0: equal values tie on the index
     const uint32_t b = __float_as_uint(v);
@@ -350,6 +370,22 @@ __device__ __forceinline__ int unit_slot(const Misc* m, int K, int u, bool first
     for (int k = 0; k < MAX_K; ++k)
         if (k < r) fr &= fr - 1;
     return fr ? (int)__builtin_ctz(fr) : 0;
+}
+
+// Expert units, wave 0, after route_rank: the unit groups whose held expert
+// was not routed (every group when `first`), ascending, with the expert each
+// runs instead, into m->mlist / m->mexp / m->mcount. The caller synchronizes.
+__device__ __forceinline__ void miss_list(Misc* m, int K, bool first) {
+    const int t = tid_here();
+    if (t >= 64) return;
+    const bool mis = t < K && (first || m->uslot[t] < 0);
+    const uint64_t mm = __ballot(mis);
+    if (mis) {
+        const int mi = __popcll(mm & ((1ull << t) - 1));
+        m->mlist[mi] = t;
+        m->mexp[mi] = m->sel_i[unit_slot(m, K, t, first)];
+    }
+    if (t == 0) m->mcount = __popcll(mm);
 }
 
 // Group and pred units, wave 0, after route_rank: softmax over the chosen in
@@ -473,6 +509,10 @@ __device__ __forceinline__ float ld_bias(const FusedParams& P, int layer) {
 template <int BPW, int DB, int CPT, bool DBG>
 __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P) {
     constexpr int C = 2 * BPW;  // router chunks per group = H/128
+    // words per thread of each wait (H = 256 * BPW, E <= 128, K <= 8):
+    constexpr int UW_G = NGROUP * MAX_E / FT_THREADS;                              // group sums
+    constexpr int UW_Y = (BPW + 1) / 2;                                            // y of a group's rows
+    constexpr int UW_X = (NGROUP * (MAX_E + 10 * BPW) + FT_THREADS - 1) / FT_THREADS;  // sums + q8 of x
     extern __shared__ __align__(16) uint8_t lds[];
     uint8_t* act8 = lds + P.o_act8;
     float* red = reinterpret_cast<float*>(lds + P.o_red);
@@ -501,7 +541,11 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     auto tag_y = [&](int l) { return epoch + 4u * l + 3u; };
     auto gq_buf = [&](int l) { return P.gq_t + (int64_t)(l & 1) * NREP * P.rs_gq; };
     auto pp_buf = [&](int l) { return P.pp_t + (int64_t)(l & 1) * NGROUP * E; };
-    auto pid_buf = [&](int l) { return P.pid_t + (int64_t)(l & 1) * NREP * PID_STRIDE; };
+    // the prediction: one copy per pred unit g (on XCD g), read by the units
+    // of the same XCD
+    auto pid_buf = [&](int l) { return P.pid_t + (int64_t)(l & 1) * NGROUP * PID_STRIDE; };
+    auto y_buf = [&](int l) { return P.y_t + (int64_t)(l & 1) * K * H; };
+    const int prep = w % NGROUP;  // the pred unit whose copy this workgroup reads
     auto ident = [](int i) { return (int64_t)i; };
     const int rep = w % NREP;  // workgroups are dealt to the 8 XCDs round-robin
     const bool pf = P.prefetch != 0;
@@ -511,11 +555,23 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         // ============ group unit (routing) or pred unit (prediction) ============
         // Both combine the same rows bit for bit. A group unit then applies the
         // router of layer l+1 (true routing of l+1, q8 of x_{l+1}); a pred unit
-        // the router of layer l+2 (the prediction of layer l+2). Ordering of
-        // the double-buffered words: a pred unit publishes the prediction of
-        // layer l+2 only after reading every group unit's routing of layer
-        // l+1, which each group unit publishes after reading the prediction
-        // of layer l from the same buffer parity.
+        // the router of layer l+2 (the prediction of layer l+2).
+        // Reused words are rewritten only after every reader has read them:
+        //   act_t, hp_t (one buffer): rewritten for l+1 after the routing of
+        //     l+1, which needs every y of l, produced after the reads;
+        //   y_t (by parity): rewritten for l+2 after the writer saw the
+        //     prediction of l+2, which its pred unit publishes after every
+        //     pred unit's sums of l+2, each computed after reading y(l); group
+        //     units read y(l) before publishing the routing of l+1;
+        //   gq_t (by parity): rewritten for l+2 after every y(l+1), i.e. after
+        //     every expert unit took the prediction of l+1 from its XCD's pred
+        //     unit, which publishes it after reading gq(l);
+        //   pp_t (by parity): rewritten for l+2 after y(l), i.e. after the
+        //     prediction of l was read from all 8 copies, each published after
+        //     its pred unit read pp(l);
+        //   pid_t (by parity): rewritten for l+2 after the routing of l+1 from
+        //     every group unit (each read pid(l) before publishing it), and so
+        //     after every y(l), i.e. after every expert unit took pid(l).
         const bool pu = w >= P.n_unit + NGROUP;
         const int g = w - P.n_unit - (pu ? NGROUP : 0), r0 = g * HG;
         const bool record = !pu && g == 0;  // group unit 0 writes ids/wts
@@ -534,14 +590,14 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         __syncthreads();
         if (pu) {
             group_publish<CPT, C, DBG>(P, g, wv, gx, gp, q8w, pp_buf(1), tag_g(1), -1, true);
-            if (!wait_words<DBG>(P, m, epoch, pp_buf(1), NGROUP * E, ident, tag_g(1), gq, gdst)) return;
+            if (!wait_words<DBG, UW_G>(P, m, epoch, pp_buf(1), NGROUP * E, ident, tag_g(1), gq, gdst)) return;
             route_rank(P, m, reinterpret_cast<const float*>(gq), bias_p, 1, nullptr);
-            if (!wait_words<DBG>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(0), gq, gdst)) return;
-            if (t < K) st_tag(pid_buf(1) + rep * PID_STRIDE + t, tag_g(1), (uint32_t)m->pid[1][t]);
+            if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(0), gq, gdst)) return;
+            if (t < K) st_tag(pid_buf(1) + g * PID_STRIDE + t, tag_g(1), (uint32_t)m->pid[1][t]);
         } else {
             group_publish<CPT, C, DBG>(P, g, wv, gx, gp, q8w, gq_buf(0), tag_g(0), -1);
             stamp<DBG>(P, -1, 11);
-            if (!wait_words<DBG>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(0), gq, gdst)) return;
+            if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(0), gq, gdst)) return;
         }
         stamp<DBG>(P, -1, 12);
         route_rank(P, m, reinterpret_cast<const float*>(gq), bias_n, -1, nullptr);
@@ -556,7 +612,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
             stamp<DBG>(P, l, 1);
             // y of every unit group for this group's rows, [u][HG] in LDS
             auto yidx = [=](int i) { return (int64_t)(i / HG) * H + r0 + i % HG; };
-            if (!wait_words<DBG>(P, m, epoch, P.y_t, K * HG, yidx, tag_y(l), reinterpret_cast<uint32_t*>(gy), l, 26)) return;
+            if (!wait_words<DBG, UW_Y>(P, m, epoch, y_buf(l), K * HG, yidx, tag_y(l), reinterpret_cast<uint32_t*>(gy), l, 26)) return;
             stamp<DBG>(P, l, 8);
             // x_{l+1} = x_l + sum_p (y_p * w_p), pairs in routing order
             // (ft-model/src/lib.rs:1634-1646); slot p ran on unit group pown[p]
@@ -590,23 +646,23 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                 if (l + 2 < L) {
                     group_publish<CPT, C, DBG>(P, g, wv, gx, gp, q8w, pp_buf(l + 2), tag_g(l + 2), l, true);
                     stamp<DBG>(P, l, 11);
-                    if (!wait_words<DBG>(P, m, epoch, pp_buf(l + 2), NGROUP * E, ident, tag_g(l + 2), gq, gdst, l, 24)) return;
+                    if (!wait_words<DBG, UW_G>(P, m, epoch, pp_buf(l + 2), NGROUP * E, ident, tag_g(l + 2), gq, gdst, l, 24)) return;
                     route_rank(P, m, reinterpret_cast<const float*>(gq), bias_p, l & 1, nullptr);
                 }
-                if (!wait_words<DBG>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(l + 1), gq, gdst))
+                if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(l + 1), gq, gdst))
                     return;
                 stamp<DBG>(P, l, 12);
                 if (l + 2 < L && t < K)
-                    st_tag(pid_buf(l + 2) + rep * PID_STRIDE + t, tag_g(l + 2), (uint32_t)m->pid[l & 1][t]);
+                    st_tag(pid_buf(l + 2) + g * PID_STRIDE + t, tag_g(l + 2), (uint32_t)m->pid[l & 1][t]);
             } else {
                 group_publish<CPT, C, DBG>(P, g, wv, gx, gp, q8w, gq_buf(l + 1), tag_g(l + 1), l);
                 stamp<DBG>(P, l, 11);
-                if (!wait_words<DBG>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(l + 1), gq, gdst, l,
+                if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(l + 1), gq, gdst, l,
                                 24))
                     return;
                 stamp<DBG>(P, l, 12);
                 // the prediction of layer l+1, for the slot -> unit group map
-                if (pf && !wait_words<DBG>(P, m, epoch, pid_buf(l + 1) + rep * PID_STRIDE, K, ident, tag_g(l + 1),
+                if (pf && !wait_words<DBG, 1>(P, m, epoch, pid_buf(l + 1) + prep * PID_STRIDE, K, ident, tag_g(l + 1),
                                       reinterpret_cast<uint32_t*>(m->pid[(l + 1) & 1]), l, 27))
                     return;
             }
@@ -633,7 +689,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     };
     stamp<DBG>(P, -1, 0);
     float bias_n = ld_bias(P, 0);
-    if (!wait_words<DBG>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * nq, xidx, tag_g(0), gq, xdst)) return;
+    if (!wait_words<DBG, UW_X>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * nq, xidx, tag_g(0), gq, xdst)) return;
     // The act hand-over of unit group u stays in the XCD's L2 (plain stores,
     // agent-scope polls) when every unit of group u runs on this workgroup's
     // XCD; otherwise its stores write through.
@@ -641,7 +697,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     {
         const int upe = P.n_unit / K;  // units per unit group
         uint32_t* xw = reinterpret_cast<uint32_t*>(red);
-        if (!wait_words<DBG>(P, m, epoch, P.pl_t, upe, [=](int i) { return (int64_t)(u + K * i); }, tag_g(0), xw)) return;
+        if (!wait_words<DBG, 1>(P, m, epoch, P.pl_t, upe, [=](int i) { return (int64_t)(u + K * i); }, tag_g(0), xw)) return;
         act_local = __syncthreads_and(t >= upe || xw[t] == xcc_id()) != 0;
         trace_value<DBG>(P, -1, 27, act_local ? 1u : 0u);
         trace_value<DBG>(P, -1, 28, xcc_id());
@@ -655,78 +711,103 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     //   row and block), sc (the f16 scale, widened to 32 bits so that loads
     //   do not pair up and wait for each other);
     //   down rows 128j + 16*wave + rr, blocks s4, s4+4, ...: dq, dsc.
+    // Missed tiles (K == 8): the gate|up tile j of a unit group whose held
+    // expert was not routed is computed by the 8 units with index j, one wave
+    // slice (64 rows x BPW blocks) each, in a wave of theirs otherwise idle
+    // (hq, hs); each publishes its slice's per-row partial, the fma chain of
+    // exactly that wave of the unit that owns the tile, and the owner sums the
+    // 8 partials in wave order as for its own dots: the same bits. A missed
+    // tile's 101 KB thus arrives as 8 loads of 12.7 KB on 8 CUs instead of one
+    // 101 KB load on one CU (a CU keeps only ~40 KB of loads in flight).
     uint32_t sc[BPW];
     uint4 qv[BPW];
     uint32_t dsc[DB];
     uint4 dq[DB];
-    auto load_tiles = [&](int layer, int eid) __attribute__((always_inline)) {
-        // per-thread offsets from an opaque thread index: hoisted out of the
-        // layer loop they would stay live (and spill) for the whole kernel
-        int tl = threadIdx.x;
-        asm volatile("" : "+v"(tl));
+    uint32_t hs[BPW];
+    uint4 hq[BPW];
+    const bool helpers = K == FT_WAVES;
+    // per-thread offsets from an opaque thread index: hoisted out of the layer
+    // loop they would stay live (and spill) for the whole kernel
+    auto load_gu = [&](int layer, int eid, int s, uint4 (&q)[BPW], uint32_t (&c)[BPW])
+                       __attribute__((always_inline)) {
+        const int tl = tid_here();
         const uint8_t* xb = P.banks + ((int64_t)layer * E + eid) * P.expert_bytes;
-        const int wave = tl >> 6, r = tl & 63, b0 = wave * BPW;
-        {
-            // a unit without a gate|up tile re-reads tile 0 of expert 0 of
-            // layer 0 (shared by all such units, so it stays in cache)
-            const uint8_t* T = gm ? xb + (int64_t)j * nb * 1152 : P.banks;
-            const uint8_t* Ts = T + b0 * 128 + r * 2;
-            const uint8_t* Tq = T + nb * 128 + b0 * 1024 + r * 16;
-            // all 16-byte loads first, then the 2-byte scales: interleaving
-            // them more than doubled the time to stream a layer in a probe
+        const int r = tl & 63, b0 = s * BPW;
+        // a unit without a gate|up tile re-reads tile 0 of expert 0 of layer 0
+        // (shared by all such units, so it stays in cache)
+        const uint8_t* T = gm ? xb + (int64_t)j * nb * 1152 : P.banks;
+        const uint8_t* Ts = T + b0 * 128 + r * 2;
+        const uint8_t* Tq = T + nb * 128 + b0 * 1024 + r * 16;
+        // all 16-byte loads first, then the 2-byte scales: interleaving them
+        // more than doubled the time to stream a layer in a probe
 #pragma unroll
-            for (int i = 0; i < BPW; ++i) qv[i] = *reinterpret_cast<const uint4*>(Tq + i * 1024);
+        for (int i = 0; i < BPW; ++i) q[i] = *reinterpret_cast<const uint4*>(Tq + i * 1024);
 #pragma unroll
-            for (int i = 0; i < BPW; ++i) sc[i] = *reinterpret_cast<const uint16_t*>(Ts + i * 128);
-        }
-        {
-            const int s4 = tl & 3, rr = (tl >> 2) & 15;
-            const uint8_t* D = (dm ? xb + (int64_t)(j * FT_WAVES + wave) * dn_tile : P.banks) + P.gu_bytes;
-#pragma unroll
-            for (int k = 0; k < DB; ++k) {
-                const int b = min(s4 + 4 * k, nbj - 1);
-                dq[k] = *reinterpret_cast<const uint4*>(D + nbj * 32 + b * 256 + rr * 16);
-            }
-            asm volatile("" ::: "memory");  // keep the scale loads behind the 16-byte loads
-#pragma unroll
-            for (int k = 0; k < DB; ++k) {
-                const int b = min(s4 + 4 * k, nbj - 1);
-                dsc[k] = *reinterpret_cast<const uint16_t*>(D + b * 32 + rr * 2);
-            }
-        }
+        for (int i = 0; i < BPW; ++i) c[i] = *reinterpret_cast<const uint16_t*>(Ts + i * 128);
         asm volatile("" ::: "memory");  // issued here, not sunk towards the first use
     };
-    // layer 0: nothing held; slot u runs on unit group u
-    int p = u;
-    // the routed id is in [0, E) by construction; the clamp keeps any future
-    // logic error from turning into an out-of-bounds weight read
-    int eid = min(max(m->sel_i[p], 0), E - 1);
-    load_tiles(0, eid);
-    trace_value<DBG>(P, 0, 10, 1u);
+    auto load_dn = [&](int layer, int eid) __attribute__((always_inline)) {
+        const int tl = tid_here();
+        const uint8_t* xb = P.banks + ((int64_t)layer * E + eid) * P.expert_bytes;
+        const int wave = tl >> 6, s4 = tl & 3, rr = (tl >> 2) & 15;
+        const uint8_t* D = (dm ? xb + (int64_t)(j * FT_WAVES + wave) * dn_tile : P.banks) + P.gu_bytes;
+#pragma unroll
+        for (int k = 0; k < DB; ++k) {
+            const int b = min(s4 + 4 * k, nbj - 1);
+            dq[k] = *reinterpret_cast<const uint4*>(D + nbj * 32 + b * 256 + rr * 16);
+        }
+        asm volatile("" ::: "memory");  // keep the scale loads behind the 16-byte loads
+#pragma unroll
+        for (int k = 0; k < DB; ++k) {
+            const int b = min(s4 + 4 * k, nbj - 1);
+            dsc[k] = *reinterpret_cast<const uint16_t*>(D + b * 32 + rr * 2);
+        }
+        asm volatile("" ::: "memory");
+    };
+    // Routing of `layer` known (after route_rank): this unit's slot and
+    // expert, the missed unit groups, and the wave slice this unit computes
+    // for a missed tile (loaded now: it is on the critical path). With no
+    // helpers a missed unit loads its whole tile now; with helpers its down
+    // tile is loaded after its slice is computed (a CU keeps ~40 KB of loads
+    // in flight, and the down tile is needed only after the act hand-over).
+    int p = u, eid = 0, hug = 0;
+    bool own_miss = true, hm = false;
+    auto decide = [&](int layer, bool first) __attribute__((always_inline)) {
+        miss_list(m, K, first);
+        __syncthreads();
+        p = unit_slot(m, K, u, first);
+        // the routed id is in [0, E) by construction; the clamp keeps any
+        // future logic error from turning into an out-of-bounds weight read
+        eid = min(max(m->sel_i[p], 0), E - 1);
+        own_miss = first || m->uslot[u] < 0;
+        hm = false;
+        if (helpers) {
+            const int mc = m->mcount, wv = tid_here() >> 6;
+            const int mi = mc == FT_WAVES ? wv : wv - 1;  // wave 0 keeps the GELU tail unless all missed
+            if (mi >= 0 && mi < mc) {
+                hm = true;
+                hug = m->mlist[mi];
+                load_gu(layer, min(max(m->mexp[mi], 0), E - 1), (u - hug) & (FT_WAVES - 1), hq, hs);
+            }
+        } else if (own_miss) {
+            load_gu(layer, eid, tid_here() >> 6, qv, sc);
+            load_dn(layer, eid);
+        }
+    };
+    decide(0, true);
+    trace_value<DBG>(P, 0, 10, own_miss ? 1u : 0u);
     stamp<DBG>(P, -1, 14);
 
     for (int l = 0; l < L; ++l) {
         stamp<DBG>(P, l, 0);
-        int tl = threadIdx.x;
-        asm volatile("" : "+v"(tl));
-        const int wave = tl >> 6, r = tl & 63, b0 = wave * BPW, s4 = tl & 3, rr = (tl >> 2) & 15;
+        const int tl = tid_here();
+        const int wave = tl >> 6, r = tl & 63, s4 = tl & 3, rr = (tl >> 2) & 15;
         // ---- gate|up dots -> GELU*up -> q8 block, published ----
         if (gm) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int i = 0; i < BPW; ++i) {
-                const uint4 lo = xq4[(b0 + i) * 2], hi = xq4[(b0 + i) * 2 + 1];
-                const int2 dq8 = xdp[b0 + i];
-                const int diff = block_dot_v(qv[i], lo, hi, dq8.y);
-                acc = fmaf((float)diff, h2f((uint16_t)sc[i]) * __int_as_float(dq8.x), acc);
-            }
-            stamp<DBG>(P, l, 2);
-            red[wave * 64 + r] = acc;
-            __syncthreads();
-            if (t < 32) {
-                // lane t: gate row j*32+t and up row I+j*32+t, the 8 wave
-                // partials summed in wave order; GELU*up; the q8 block of the
-                // 32 lanes, published as {d, qsum, 8 words of qs}
+            // lane t < 32: gate row j*32+t and up row I+j*32+t, the 8 wave
+            // partials in red summed in wave order; GELU*up; the q8 block of
+            // the 32 lanes, published as {d, qsum, 8 words of qs}
+            auto tail = [&]() __attribute__((always_inline)) {
                 float gv[FT_WAVES], uv[FT_WAVES];
 #pragma unroll
                 for (int v = 0; v < FT_WAVES; ++v) {
@@ -760,16 +841,54 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                         reinterpret_cast<uint32_t*>(P.dbg_act + (((int64_t)l * K + p) * nbj + j) * Q8_BLK)[k] = v;
                 }
                 stamp<DBG>(P, l, 19);
+            };
+            // one wave's partial for row r: the fma chain over the BPW blocks
+            // s*BPW.. of the tile in (q, c) against q8(x)
+            auto wave_partial = [&](const uint4 (&q)[BPW], const uint32_t (&c)[BPW], int s)
+                                    __attribute__((always_inline)) {
+                const int b0 = s * BPW;
+                float acc = 0.0f;
+#pragma unroll
+                for (int i = 0; i < BPW; ++i) {
+                    const uint4 lo = xq4[(b0 + i) * 2], hi = xq4[(b0 + i) * 2 + 1];
+                    const int2 dq8 = xdp[b0 + i];
+                    const int diff = block_dot_v(q[i], lo, hi, dq8.y);
+                    acc = fmaf((float)diff, h2f((uint16_t)c[i]) * __int_as_float(dq8.x), acc);
+                }
+                return acc;
+            };
+            // the slice this wave computes for a missed tile, to its owner
+            auto help = [&]() __attribute__((always_inline)) {
+                if (hm) {
+                    const int sl = (u - hug) & (FT_WAVES - 1);
+                    const float a2 = wave_partial(hq, hs, sl);
+                    st_tag(P.hp_t + (((int64_t)hug * nbj + j) * FT_WAVES + sl) * 64 + r, tag_a(l), __float_as_uint(a2));
+                    if (DBG && P.trace && r == 0 && wave == 1)  // slot 29: wave 1's slice published
+                        P.trace[((int64_t)blockIdx.x * (P.L + 1) + (l + 1)) * TRACE_SLOTS + 29] = wall_clock64();
+                }
+            };
+            if (!(helpers && own_miss)) {
+                red[wave * 64 + r] = wave_partial(qv, sc, wave);
+                stamp<DBG>(P, l, 2);
+                __syncthreads();
+                if (t < 32) tail();
+                help();
+            } else {
+                help();
+                load_dn(l, eid);
+                if (!wait_words<DBG, 1>(P, m, epoch, P.hp_t + ((int64_t)u * nbj + j) * FT_WAVES * 64, FT_WAVES * 64,
+                                        ident, tag_a(l), reinterpret_cast<uint32_t*>(red), l, 26))
+                    return;
+                stamp<DBG>(P, l, 2);
+                if (t < 32) tail();
             }
             stamp<DBG>(P, l, 3);
         }
-        // the prediction of layer l+1 (published during layer l-1): read while
-        // the act blocks are on their way, so the prefetch can follow the y
-        // publish directly
-        if (pf && l + 1 < L &&
-            !wait_words<DBG>(P, m, epoch, pid_buf(l + 1) + rep * PID_STRIDE, K, ident, tag_g(l + 1),
-                             reinterpret_cast<uint32_t*>(m->pid[(l + 1) & 1]), l, 27))
-            return;
+        // the prediction of layer l+1 (published early in this layer): loaded
+        // now, checked after the down dots, when every older load of this wave
+        // has landed anyway, so it never stalls the chain
+        uint64_t pid_raw = 0;
+        if (pf && l + 1 < L && t < K) pid_raw = ld_tag(pid_buf(l + 1) + prep * PID_STRIDE + t);
         // ---- down: the act blocks of unit group u, then y of 128 rows ----
         if (dm) {
             // act8: [nbj blocks x 32 B qs][nbj (d, qsum) pairs] (16-B aligned qs)
@@ -777,8 +896,8 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                 const int bi = i / 10, k = i - bi * 10;
                 return k >= 2 ? bi * 8 + (k - 2) : nbj * 8 + bi * 2 + k;
             };
-            if (!wait_words<DBG, true>(P, m, epoch, P.act_t + (int64_t)u * nbj * 10, nbj * 10, ident, tag_a(l),
-                                  reinterpret_cast<uint32_t*>(act8), act_dst, l, 25))
+            if (!wait_words<DBG, 1, true>(P, m, epoch, P.act_t + (int64_t)u * nbj * 10, nbj * 10, ident, tag_a(l),
+                                       reinterpret_cast<uint32_t*>(act8), act_dst, l, 25))
                 return;
             stamp<DBG>(P, l, 4);
             const uint4* aq4 = reinterpret_cast<const uint4*>(act8);
@@ -805,27 +924,36 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
             acc += quad_xor2(acc);
             stamp<DBG>(P, l, 5);
             if (s4 == 0)
-                st_tag(P.y_t + (int64_t)u * H + j * DN_UNIT + wave * DN_ROWS + rr, tag_y(l), __float_as_uint(acc));
+                st_tag(y_buf(l) + (int64_t)u * H + j * DN_UNIT + wave * DN_ROWS + rr, tag_y(l), __float_as_uint(acc));
             stamp<DBG>(P, l, 6);
         }
         if (l + 1 == L) break;
         bias_n = ld_bias(P, l + 1);
         // ---- prefetch: the predicted expert of layer l+1 for this unit group ----
         if (pf) {
-            load_tiles(l + 1, min(max(m->pid[(l + 1) & 1][u], 0), E - 1));
+            bool ok = true;
+            if (t < K) {
+                ok = (uint32_t)(pid_raw >> 32) == tag_g(l + 1);
+                m->pid[(l + 1) & 1][t] = (int)(uint32_t)pid_raw;
+            }
+            // not yet published (late pred units): the bounded wait
+            if (!__syncthreads_and(ok) &&
+                !wait_words<DBG, 1>(P, m, epoch, pid_buf(l + 1) + prep * PID_STRIDE, K, ident, tag_g(l + 1),
+                                 reinterpret_cast<uint32_t*>(m->pid[(l + 1) & 1]), l, 27))
+                return;
+            const int pe = min(max(m->pid[(l + 1) & 1][u], 0), E - 1);
+            load_gu(l + 1, pe, wave, qv, sc);
+            load_dn(l + 1, pe);
             stamp<DBG>(P, l, 7);
         }
         // ---- routing of layer l+1 and the q8 of x_{l+1}, from the group units ----
-        if (!wait_words<DBG>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * nq, xidx, tag_g(l + 1), gq, xdst, l, 24))
+        if (!wait_words<DBG, UW_X>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * nq, xidx, tag_g(l + 1), gq, xdst, l, 24))
             return;
         stamp<DBG>(P, l, 12);
         route_rank(P, m, reinterpret_cast<const float*>(gq), bias_n, -1, pf ? m->pid[(l + 1) & 1] : nullptr);
         stamp<DBG>(P, l, 13);
-        p = unit_slot(m, K, u, !pf);
-        eid = min(max(m->sel_i[p], 0), E - 1);
-        const bool miss = !pf || eid != m->pid[(l + 1) & 1][u];
-        if (miss) load_tiles(l + 1, eid);
-        trace_value<DBG>(P, l + 1, 10, miss ? 1u : 0u);
+        decide(l + 1, !pf);
+        trace_value<DBG>(P, l + 1, 10, own_miss ? 1u : 0u);
         stamp<DBG>(P, l, 14);
     }
     if (w == 0 && t == 0)
@@ -920,7 +1048,7 @@ __global__ void k_fill_u32(uint32_t* p, int64_t n, uint32_t v) {
 // host side
 // ---------------------------------------------------------------------------
 struct WsLayout {
-    int64_t ctl, act, y, gq, pp, pid, pl, total;
+    int64_t ctl, act, hp, y, gq, pp, pid, pl, total;
     int gq_stride, qw;
     int64_t rs_gq;  // words
 };
@@ -934,10 +1062,11 @@ WsLayout ws_layout(int64_t H, int64_t I, int64_t E, int64_t K) {
     int64_t off = 0;
     w.ctl = off; off += 256;
     w.act = off; off += up(K * (I / 32) * 10 * 8);
-    w.y = off; off += up(K * H * 8);
+    w.hp = off; off += up(K * (I / 32) * FT_WAVES * 64 * 8);
+    w.y = off; off += 2 * up(K * H * 8);
     w.gq = off; off += 2 * NREP * up(w.rs_gq * 8);
     w.pp = off; off += 2 * up(NGROUP * E * 8);
-    w.pid = off; off += 2 * up(NREP * PID_STRIDE * 8);
+    w.pid = off; off += 2 * up(NGROUP * PID_STRIDE * 8);
     w.pl = off; off += up(((int64_t)std::max(K * (I / 32), K * (H / DN_UNIT)) + 2 * NGROUP) * 8);
     w.total = off;
     return w;
@@ -1088,6 +1217,7 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
     P.ids_out = ids;
     P.wts_out = wts;
     P.act_t = (uint64_t*)(ws + wl.act);
+    P.hp_t = (uint64_t*)(ws + wl.hp);
     P.y_t = (uint64_t*)(ws + wl.y);
     P.gq_t = (uint64_t*)(ws + wl.gq);
     P.pp_t = (uint64_t*)(ws + wl.pp);
