@@ -169,8 +169,8 @@ __device__ __forceinline__ void trace_value(const FusedParams& P, int l, int ev,
 // Two poll rounds are kept in flight: a round is issued before the previous
 // one is checked, so a word is seen about half a memory round trip after it
 // lands instead of up to a whole one. Every round issues exactly U loads per
-// lane (a lane's finished or surplus words re-read a valid word), so the
-// compiler waits for the older round only.
+// polling lane (a lane's finished or surplus words re-read one of its own),
+// so the compiler waits for the older round only.
 // Bounded: after spin_limit rounds (or when another workgroup has aborted)
 // the lane records the abort and the wait returns false in every thread.
 template <bool DBG, int U, bool AGENT = false, int NPOLL = FT_THREADS, typename Idx, typename DIdx>
@@ -187,7 +187,9 @@ __device__ __forceinline__ bool wait_words(const FusedParams& P, Misc* m, uint32
     auto issue = [&](uint64_t (&v)[U]) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int64_t a = idx(min(u * NPOLL + tid, n - 1));
+            // a slot beyond n re-reads the lane's first word (spread over the
+            // payload: many lanes re-reading one word would make it a hot spot)
+            const int64_t a = idx(u * NPOLL + tid < n ? u * NPOLL + tid : min(tid, n - 1));
             v[u] = AGENT ? ld_tag_agent(src + a) : ld_tag(src + a);
         }
     };
