@@ -12,6 +12,12 @@ Prints one JSON line: value = mean us/token (lower is better), plus achieved
 HBM GB/s over the algorithmic expert bytes (802,897,920 B/token), the
 roofline of the dominant kernel, and a CPU baseline (the oracle's restatement
 of ft-core's AVX2 path, timed on this host's cores on a bounded sample).
+
+--config picks one of BASELINE.json's other configurations instead (cfg3 Zipf
+routing, cfg4 batched decode at 16/64 tokens, cfg5 the large-expert shape at
+batch 1 and 32). One step is then one batch of B tokens through all layers;
+value stays us/token (step time / B) and GB/s counts each step's unique
+experts once per layer (the bytes a grouped product has to stream).
 """
 import argparse
 import json
@@ -24,6 +30,15 @@ sys.path.insert(0, os.path.join(ROOT, "freetoken-rs_amd"))
 
 HBM_PEAK_GBPS = 8000.0
 METRIC = "MoE expert-FFN µs/token at batch 1 + achieved HBM GB/s (% of MI355X peak)"
+# name -> (shape, tokens per step, Zipf exponent of the router bias, BASELINE.json config)
+CONFIGS = {
+    "gemma30": ("GEMMA", 1, None, 2),
+    "zipf": ("GEMMA", 1, 1.1, 3),
+    "batch16": ("GEMMA", 16, None, 4),
+    "batch64": ("GEMMA", 64, None, 4),
+    "large1": ("LARGE", 1, None, 5),
+    "large32": ("LARGE", 32, None, 5),
+}
 
 
 def log(*a):
@@ -35,8 +50,12 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--path", choices=["fused", "multikernel"], default="fused")
-    ap.add_argument("--layers", type=int, default=30)
+    ap.add_argument("--config", choices=list(CONFIGS), default="gemma30",
+                    help="gemma30 = the headline (cfg2); zipf = cfg3; batch16/batch64 = cfg4; large1/large32 = cfg5")
+    ap.add_argument("--path", choices=["auto", "fused", "grouped", "multikernel"], default="auto",
+                    help="auto: fused whole-stack kernel at batch 1 of the Gemma shape, grouped layers for batched "
+                         "Gemma, launch-by-launch layers for the large-expert shape")
+    ap.add_argument("--layers", type=int, default=0, help="0 = the config's layer count")
     ap.add_argument("--prefetch", type=int, choices=[0, 1], default=1,
                     help="fused path: stream the early-routed experts of the next layer ahead (1) or not (0)")
     ap.add_argument("--trace", default="", metavar="NPY",
@@ -57,20 +76,22 @@ def chunk_size(steps, warmup):
     return 1
 
 
-class MultiKernelRunner:
-    """Launch-by-launch path: 7 kernels per layer, C tokens per captured HIP graph."""
+class GraphRunner:
+    """Layer-by-layer paths: C steps of B tokens through all layers per
+    captured HIP graph. layer(l, src, dst, ids, wts, stream) enqueues one
+    layer for the B tokens of src ([B, H]) into dst. The routing of every
+    step of a chunk lands in ids/wts [C, L, B*k] (read after timing only)."""
 
-    def __init__(self, model, chunk):
+    def __init__(self, model, B, chunk, layer):
         import torch
-        self.m, self.C = model, chunk
+        self.m, self.B, self.C, self.layer = model, B, chunk, layer
         H, k = model.shape.hidden, model.shape.top_k
         dev = model.device
-        self.xin = torch.zeros((chunk, H), dtype=torch.float32, device=dev)
-        self.out = torch.zeros((chunk, H), dtype=torch.float32, device=dev)
-        self.state = torch.zeros(H, dtype=torch.float32, device=dev)
-        self.ids = torch.zeros((model.L, chunk, k), dtype=torch.int32, device=dev)
-        self.wts = torch.zeros((model.L, chunk, k), dtype=torch.float32, device=dev)
-        self.ws = model.workspace(1)
+        self.xin = torch.zeros((chunk, B, H), dtype=torch.float32, device=dev)
+        self.out = torch.zeros((chunk, B, H), dtype=torch.float32, device=dev)
+        self.state = [torch.zeros((B, H), dtype=torch.float32, device=dev) for _ in range(2)]
+        self.ids = torch.zeros((chunk, model.L, B * k), dtype=torch.int32, device=dev)
+        self.wts = torch.zeros((chunk, model.L, B * k), dtype=torch.float32, device=dev)
         self.stream = torch.cuda.Stream()
         self.graph = torch.cuda.CUDAGraph()
         self._enqueue(self.stream)  # one eager pass before capture
@@ -80,14 +101,16 @@ class MultiKernelRunner:
         torch.cuda.synchronize()
 
     def _enqueue(self, stream):
-        m = self.m
-        for t in range(self.C):
-            for l in range(m.L):
-                src = self.xin[t] if l == 0 else self.state
-                dst = self.out[t] if l == m.L - 1 else self.state
-                m.layer(l, src, dst, self.ids[l, t], self.wts[l, t], self.ws, 1, stream)
+        L = self.m.L
+        for c in range(self.C):
+            src = self.xin[c]
+            for l in range(L):
+                dst = self.out[c] if l == L - 1 else self.state[l & 1]
+                self.layer(l, src, dst, self.ids[c, l], self.wts[c, l], stream)
+                src = dst
 
     def run_chunk(self, hidden_rows):
+        """hidden_rows: [C, B, H]; the outputs land in self.out."""
         self.xin.copy_(hidden_rows)
         self.graph.replay()
 
@@ -143,6 +166,7 @@ def cpu_baseline(model, hidden, seconds, threads):
     banks = model.banks.cpu().numpy()
     routers = model.routers.cpu().numpy()
     log(f"[cpu] banks copied to host in {time.time() - t0:.1f}s")
+    bias = None if model.bias is None else model.bias.cpu().numpy()
     eb, gb = model.expert_bytes, model.gu_bytes
     base = banks.ctypes.data
     gu_ptrs = [(ctypes.c_void_p * E)(*[base + (l * E + e) * eb for e in range(E)]) for l in range(model.L)]
@@ -156,7 +180,8 @@ def cpu_baseline(model, hidden, seconds, threads):
     while True:
         x = hidden[n_tok].copy()
         for l in range(model.L):
-            rc = L.orc_moe_layer(x.ctypes.data_as(P), H, I, E, k, routers[l].ctypes.data_as(P), None, None,
+            b = None if bias is None else bias[l].ctypes.data_as(P)
+            rc = L.orc_moe_layer(x.ctypes.data_as(P), H, I, E, k, routers[l].ctypes.data_as(P), b, None,
                                  ctypes.cast(gu_ptrs[l], P), ctypes.cast(dn_ptrs[l], P), model.layout, threads,
                                  orc.GELU_LIBM, x_out.ctypes.data_as(P), None, None, None, None, None, None,
                                  None, None)
@@ -181,22 +206,34 @@ def main():
     import ft_hip
     import moe_synth
 
+    shape_name, B, zipf_s, cfg_id = CONFIGS[args.config]
+    shape = getattr(moe_synth, shape_name)
+    path = args.path
+    if path == "auto":
+        path = "multikernel" if shape is moe_synth.LARGE else ("fused" if B == 1 else "grouped")
+    if path == "fused" and B != 1:
+        sys.exit("the fused whole-stack kernel decodes one token per launch: use --path grouped or multikernel")
+    if path in ("fused", "grouped") and shape is not moe_synth.GEMMA:
+        sys.exit(f"--path {path} is built for the Gemma shape only: use --path multikernel")
+
     g = ft_hip.Q4Gemv(0)
     t0 = time.time()
+
     def progress(l):
         if l % 10 == 9:
             torch.cuda.synchronize()
             log(f"[setup] layer {l + 1} generated ({time.time() - t0:.1f}s)")
 
-    model = moe_synth.SyntheticMoE(g, moe_synth.GEMMA, n_layers=args.layers, progress=progress)
+    model = moe_synth.SyntheticMoE(g, shape, n_layers=args.layers or None, zipf_s=zipf_s, progress=progress)
     torch.cuda.synchronize()
-    log(f"[setup] {model.L} layers x {model.shape.n_experts} experts generated on the GPU in {time.time() - t0:.1f}s "
-        f"({model.banks.numel() / 1e9:.2f} GB of banks)")
-    n_tok = args.warmup + args.steps
-    H = model.shape.hidden
-    hidden = torch.stack([model.hidden(t) for t in range(n_tok)])
-    outs = torch.zeros((n_tok, H), dtype=torch.float32, device=model.device)
-    if args.path == "fused":
+    log(f"[setup] {args.config}: {model.L} layers x {shape.n_experts} experts generated on the GPU in "
+        f"{time.time() - t0:.1f}s ({model.banks.numel() / 1e9:.2f} GB of banks), {B} token(s) per step, path {path}")
+    H, I, E, k = shape.hidden, shape.inter, shape.n_experts, shape.top_k
+    n_steps = args.warmup + args.steps
+    hidden = torch.stack([model.hidden(t) for t in range(n_steps * B)]).view(n_steps, B, H)
+    outs = torch.zeros((n_steps, B, H), dtype=torch.float32, device=model.device)
+    runner = None
+    if path == "fused":
         t1 = time.time()
         g.fused_set_prefetch(args.prefetch)
         stack = moe_synth.FusedStack(model)
@@ -205,10 +242,21 @@ def main():
 
         def run(t0_, n):
             for t in range(t0_, t0_ + n):
-                stack.run(hidden[t], outs[t])
+                stack.run(hidden[t, 0], outs[t, 0])
     else:
+        if path == "grouped":
+            gstack = moe_synth.GroupedStack(moe_synth.FusedStack(model), B)
+
+            def layer(l, src, dst, ids, wts, stream):
+                gstack.layer(l, src, dst, ids, wts, stream=stream)
+        else:
+            ws = model.workspace(B)
+
+            def layer(l, src, dst, ids, wts, stream):
+                model.layer(l, src, dst, ids, wts, ws, n_seqs=B, stream=stream)
         C = chunk_size(args.steps, args.warmup)
-        runner = MultiKernelRunner(model, C)
+        runner = GraphRunner(model, B, C, layer)
+        log(f"[setup] {C} step(s) per captured HIP graph")
 
         def run(t0_, n):
             for c in range(t0_, t0_ + n, C):
@@ -235,44 +283,65 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall
     ms = ev0.elapsed_time(ev1)
-    us_tok = ms * 1000.0 / args.steps
-    exp_bytes = moe_synth.algorithmic_expert_bytes(model.shape) * model.shape.top_k * model.L
-    router_bytes = model.shape.n_experts * H * 4 * model.L
-    gbps = exp_bytes / (us_tok * 1e-6) / 1e9
-    log(f"[gpu] {us_tok:.1f} us/token (wall {wall * 1e6 / args.steps:.1f}), {gbps:.0f} GB/s expert bytes, "
-        f"{(exp_bytes + router_bytes) / (us_tok * 1e-6) / 1e9:.0f} GB/s incl. router")
+    us_step = ms * 1000.0 / args.steps
+    us_tok = us_step / B
+    e_bytes = moe_synth.algorithmic_expert_bytes(shape)
+    router_bytes = E * H * 4 * model.L
+    if B == 1:
+        uniq = float(k)
+    else:  # unique experts per layer, averaged over the timed steps (replayed untimed: same inputs, same ids)
+        counts = []
+        for c in range(args.warmup, args.warmup + args.steps, runner.C):
+            runner.run_chunk(hidden[c:c + runner.C])
+            ids = runner.ids.cpu().numpy()
+            counts += [len(np.unique(ids[i, l])) for i in range(runner.C) for l in range(model.L)]
+        uniq = float(np.mean(counts))
+    step_bytes = int(round(uniq * e_bytes * model.L))
+    gbps = step_bytes / (us_step * 1e-6) / 1e9
+    log(f"[gpu] {us_tok:.1f} us/token, {us_step:.1f} us/step (wall {wall * 1e6 / args.steps:.1f}), "
+        f"{uniq:.2f} unique experts/layer, {gbps:.0f} GB/s expert bytes, "
+        f"{(step_bytes + router_bytes) / (us_step * 1e-6) / 1e9:.0f} GB/s incl. router")
 
-    if args.path == "fused":
+    if path == "fused":
         stack.check()
         if args.trace:
             nw = stack.n_workgroups()
             tr = torch.zeros(nw * (model.L + 1) * 32, dtype=torch.int64, device=model.device)
-            stack.run(hidden[0], torch.empty_like(hidden[0]), trace=tr)
+            stack.run(hidden[0, 0], torch.empty_like(hidden[0, 0]), trace=tr)
             stack.check()
             np.save(args.trace, tr.cpu().numpy().reshape(nw, model.L + 1, 32))
             log(f"[trace] {nw} workgroups x {model.L + 1} rows of phase stamps -> {args.trace}")
         # the fused kernel is the only kernel of a step: one launch per token
-        k_us, k_bytes = us_tok, exp_bytes + router_bytes
-        k_name = "k_moe_stack_fused (whole 30-layer section, one launch per token)"
-    else:
+        k_us, k_bytes = us_tok, step_bytes + router_bytes
+        k_name = f"k_moe_stack_fused (whole {model.L}-layer section, one launch per token)"
+    elif B == 1:
         k_us, k_bytes = time_dominant_kernel(g, model)
-        k_name = "k_gemv_q4_grouped (gate|up, 8 experts)"
+        k_name = f"k_gemv_q4_grouped (gate|up, {k} experts)"
+    else:  # the step's graph as a whole: its expert bytes over the step time
+        k_us, k_bytes = us_step, step_bytes
+        k_name = f"whole step ({model.L} {path} layers of {B} tokens in one HIP graph; not a single kernel)"
     k_gbps = k_bytes / (k_us * 1e-6) / 1e9
     log(f"[kernel] {k_name}: {k_us:.2f} us/launch, {k_bytes} B -> {k_gbps:.0f} GB/s")
 
     cpu = None
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
-        hid = hidden.cpu().numpy()
+        hid = hidden.view(n_steps * B, H).cpu().numpy()
         cpu_us, cpu_n, cpu_outs = cpu_baseline(model, hid, args.cpu_seconds, threads)
-        gpu_outs = outs.cpu().numpy()
-        errs = [float(np.max(np.abs(gpu_outs[i] - cpu_outs[i])) / np.linalg.norm(cpu_outs[i] - hid[i]))
-                for i in range(cpu_n)]
+        gpu_outs = outs.view(n_steps * B, H).cpu().numpy()
+        errs = np.array([np.max(np.abs(gpu_outs[i] - cpu_outs[i])) / np.linalg.norm(cpu_outs[i] - hid[i])
+                         for i in range(cpu_n)])
+        bad_gpu = int((~np.isfinite(gpu_outs[:cpu_n])).sum())
+        bad_cpu = int(sum((~np.isfinite(o)).sum() for o in cpu_outs))
         log(f"[cpu] {cpu_us:.0f} us/token over {cpu_n} tokens on {threads} threads; "
-            f"GPU vs CPU max|dx|/||dx_ref|| = {max(errs):.2e}")
+            f"GPU vs CPU max|dx|/||dx_ref|| = {np.nanmax(errs):.2e} (median {np.nanmedian(errs):.2e}; "
+            f"non-finite values: GPU {bad_gpu}, CPU {bad_cpu}, first bad token "
+            f"{int(np.argmax(~np.isfinite(errs))) if not np.isfinite(errs).all() else -1})")
         cpu = {"value": round(cpu_us, 1), "unit": "us/token", "cores": threads, "kind": "port",
-               "sample": f"{cpu_n} tokens x {model.L} layers of the same workload (libm GELU mode)"}
+               "sample": f"{cpu_n} tokens x {model.L} layers of the same workload, one token at a time "
+                         f"(libm GELU mode)"}
 
+    workload = {1: "", 2: "", 3: ", Zipf(1.1) router bias", 4: "", 5: ""}[cfg_id]
     res = {
         "metric": METRIC,
         "value": round(us_tok, 2),
@@ -286,10 +355,11 @@ def main():
         "vs_baseline": None,
         "dtype": "q4_0 x q8 (int8 dot, f32 accumulate)",
         "data": "synthetic (seeded N(0,0.02) q4_0 banks, N(0,1) hidden)",
-        "config": {"workload": f"gemma-shaped MoE expert FFN, {model.L} layers, batch 1, residual chain",
-                   "hidden": H, "inter": model.shape.inter, "experts": model.shape.n_experts,
-                   "top_k": model.shape.top_k, "layers": model.L, "path": args.path,
-                   "prefetch": bool(args.prefetch) if args.path == "fused" else None},
+        "config": {"workload": f"{shape.name} MoE expert FFN, {model.L} layers, batch {B}, residual chain{workload}",
+                   "baseline_config": cfg_id, "name": args.config,
+                   "hidden": H, "inter": I, "experts": E, "top_k": k, "layers": model.L, "batch": B,
+                   "path": path, "prefetch": bool(args.prefetch) if path == "fused" else None,
+                   "unique_experts_per_layer": round(uniq, 2)},
         "achieved_GBps": round(gbps, 1),
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "roofline": {"bound": "hbm", "achieved": round(k_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
