@@ -4,8 +4,11 @@
 Workload: the 30-layer Gemma-4-26B-A4B-shaped
 expert section (H 2816, I 704, 128 experts, top-8, q4_0 banks of seeded
 N(0, 0.02) weights, f32 routers of N(0, 0.02)), decoding tokens at batch 1
-with the residual chain x <- x + MoE_l(x) between layers (attention stubbed
-as identity). One step = one token through all 30 layers; inputs (banks,
+with the residual chain x <- x + MoE_l(rmsnorm(x)) between layers (attention
+stubbed as identity; the unweighted pre-norm is the reference model's, and
+without it (--input-norm 0) the chain's GELU*up, quadratic in the scale of x,
+overflows to inf within the 30 layers of the Zipf stack and 3 of the
+large-expert stack). One step = one token through all 30 layers; inputs (banks,
 routers, the tokens' hidden states) are resident in HBM before timing.
 
 Prints one JSON line: value = mean us/token (lower is better), plus achieved
@@ -61,6 +64,9 @@ def parse():
     ap.add_argument("--trace", default="", metavar="NPY",
                     help="fused path: after timing, run one more token recording every workgroup's phase stamps "
                          "(wall clock, 100 MHz) into this .npy file, shape [workgroups][layers+1][32]")
+    ap.add_argument("--input-norm", type=int, choices=[0, 1], default=1,
+                    help="1: each layer runs on rmsnorm(x) (the reference model's pre-norm; keeps the 30/32-layer "
+                         "residual chains finite); 0: on x as is")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
@@ -152,7 +158,7 @@ def time_dominant_kernel(g, model, reps=3):
     return us, nbytes
 
 
-def cpu_baseline(model, hidden, seconds, threads):
+def cpu_baseline(model, hidden, seconds, threads, input_norm):
     """The oracle's restatement of ft-core's AVX2 CPU path (row-parallel over
     `threads` host threads, as rayon's par_iter_mut) over the same section,
     on a time-bounded sample of the same tokens."""
@@ -183,7 +189,7 @@ def cpu_baseline(model, hidden, seconds, threads):
             b = None if bias is None else bias[l].ctypes.data_as(P)
             rc = L.orc_moe_layer(x.ctypes.data_as(P), H, I, E, k, routers[l].ctypes.data_as(P), b, None,
                                  ctypes.cast(gu_ptrs[l], P), ctypes.cast(dn_ptrs[l], P), model.layout, threads,
-                                 orc.GELU_LIBM, x_out.ctypes.data_as(P), None, None, None, None, None, None,
+                                 orc.GELU_LIBM, int(input_norm), x_out.ctypes.data_as(P), None, None, None, None, None, None,
                                  None, None)
             assert rc == 0
             x, x_out = x_out, x
@@ -217,6 +223,7 @@ def main():
         sys.exit(f"--path {path} is built for the Gemma shape only: use --path multikernel")
 
     g = ft_hip.Q4Gemv(0)
+    g.set_input_norm(args.input_norm)
     t0 = time.time()
 
     def progress(l):
@@ -327,7 +334,7 @@ def main():
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
         hid = hidden.view(n_steps * B, H).cpu().numpy()
-        cpu_us, cpu_n, cpu_outs = cpu_baseline(model, hid, args.cpu_seconds, threads)
+        cpu_us, cpu_n, cpu_outs = cpu_baseline(model, hid, args.cpu_seconds, threads, args.input_norm)
         gpu_outs = outs.view(n_steps * B, H).cpu().numpy()
         errs = np.array([np.max(np.abs(gpu_outs[i] - cpu_outs[i])) / np.linalg.norm(cpu_outs[i] - hid[i])
                          for i in range(cpu_n)])
@@ -355,10 +362,12 @@ def main():
         "vs_baseline": None,
         "dtype": "q4_0 x q8 (int8 dot, f32 accumulate)",
         "data": "synthetic (seeded N(0,0.02) q4_0 banks, N(0,1) hidden)",
-        "config": {"workload": f"{shape.name} MoE expert FFN, {model.L} layers, batch {B}, residual chain{workload}",
+        "config": {"workload": f"{shape.name} MoE expert FFN, {model.L} layers, batch {B}, residual chain"
+                               f"{' on rmsnorm(x)' if args.input_norm else ''}{workload}",
                    "baseline_config": cfg_id, "name": args.config,
                    "hidden": H, "inter": I, "experts": E, "top_k": k, "layers": model.L, "batch": B,
                    "path": path, "prefetch": bool(args.prefetch) if path == "fused" else None,
+                   "input_norm": bool(args.input_norm),
                    "unique_experts_per_layer": round(uniq, 2)},
         "achieved_GBps": round(gbps, 1),
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),

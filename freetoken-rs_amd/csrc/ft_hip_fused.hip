@@ -85,8 +85,10 @@ struct FusedParams {
     uint64_t* act_t;            // tagged [K][I/32][10]
     uint64_t* hp_t;             // tagged [K][I/32][8 wave slices][64 rows]: gate|up partials of missed tiles
     uint64_t* y_t;              // tagged [2][K][H], by layer parity
-    uint64_t* gq_t;             // tagged [2][NREP][NGROUP][gq_stride]: E group sums, then qw q8 words
-    uint64_t* pp_t;             // tagged [2][NGROUP][E]: group sums of the predicting router
+    uint64_t* gq_t;             // tagged [2][NREP][NGROUP][gq_stride]: E group sums, the group's sum of
+                                // squares of x, then qw q8 words
+    uint64_t* pp_t;             // tagged [2][NGROUP][E+1]: group sums of the predicting router, then the
+                                // group's sum of squares of x
     uint64_t* pid_t;            // tagged [2][NGROUP][PID_STRIDE]: predicted experts, one copy per pred unit
     uint64_t* pl_t;             // tagged [grid]: the XCD each workgroup runs on
     int64_t rs_gq;              // replica stride (words); the parity stride is NREP * rs_gq
@@ -99,6 +101,7 @@ struct FusedParams {
     int H, I, E, K, L;
     int n_gu, n_dn, n_unit;     // K*I/32 gate|up units, K*H/128 down units, max of the two
     int prefetch;               // 0: every layer loads its routed experts (no prediction)
+    int input_norm;             // 1: each layer runs on rmsnorm(x) (logits and gate|up sums times inv_r)
     int gq_stride, qw;          // words per group in the broadcast; q8 words per group ((H/8)/32*10)
     int spin_limit;
     int o_q8x, o_act8, o_red, o_gq, o_gx, o_gy, o_gp, o_misc, lds_bytes;
@@ -118,6 +121,7 @@ struct alignas(16) Misc {       // placed 16-byte aligned
     int mexp[MAX_K];            // the expert each of them runs instead
     int mcount;
     int abort_flag;
+    float inv_r;                // the input RMS norm's scale of the current layer (1 without the norm)
 };
 
 // Tagged words use system-scope (sc0 sc1) relaxed accesses: in a probe a
@@ -268,6 +272,20 @@ __device__ __forceinline__ uint64_t rank_key(float v, int i) {
     return ((uint64_t)mo << 32) | (0xFFFFFFFFu - (uint32_t)i);
 }
 
+// Scale of the input RMS norm from the 8 groups' sums of squares (R-order,
+// like a router row with W = x): ss = the group sums in order from 0.0f,
+// inv_r = 1 / sqrt(ss / H + 1e-6), each op rounded once. Whole wavefronts:
+// lane g < 8 reads group g's sum and the sum runs over lane reads, which
+// keeps one register live instead of eight.
+__device__ __forceinline__ float rms_inv_groups(const float* gss, int H) {
+    asm volatile("" : "+s"(H));  // (float)H formed here, not hoisted to the kernel's start and spilled
+    const float p = gss[__lane_id() & (NGROUP - 1)];
+    float ss = 0.0f;
+#pragma unroll
+    for (int g = 0; g < NGROUP; ++g) ss = ss + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), g));
+    return 1.0f / sqrtf(ss / (float)H + 1e-6f);  // correctly rounded (HIP default)
+}
+
 // Rank keys sit in four rows of 32 (one row per comparing thread of a
 // logit), padded by 16 bytes so the rows start in different LDS banks; keys
 // of indices >= E are 0, below every real key, so every thread compares a
@@ -277,8 +295,10 @@ __device__ __forceinline__ int key_slot(int i) { return (i / KEY_ROW) * (KEY_ROW
 
 // Routing of `layer` from the NGROUP group sums gs[E][NGROUP] in LDS.
 //   Logits: R-order, the group sums of expert e in group order from 0.0f,
-//   then + bias (bias_t: this thread's expert's bias, read ahead by the
-//   caller). Then each logit's rank, and the top K in rank order:
+//   times inv_r of the input RMS norm (routing, with the norm on: inv_r from
+//   the groups' sums of squares in row E of gs; else 1), then + bias (bias_t:
+//   this thread's expert's bias, read ahead by the caller). inv_r goes to
+//   m->inv_r (routing only). Then each logit's rank, and the top K in rank order:
 //   pred >= 0 (prediction): ids alone into m->pid[pred];
 //   otherwise ids into m->sel_i, logits into m->sel_v and, for every unit
 //   group u whose held expert `held[u]` was routed, its slot into
@@ -288,7 +308,13 @@ __device__ __forceinline__ void route_rank(const FusedParams& P, Misc* m, const 
                                            const int* held) {
     static_assert(NGROUP == 8 && MAX_E == 128, "the logit and key layouts below assume these");
     const int E = P.E, K = P.K, t = tid_here();
-    if (t < MAX_E) {
+    if (t < MAX_E) {  // whole wavefronts (MAX_E is a multiple of 64)
+        float ir = 1.0f;
+        if (pred < 0 && P.input_norm) ir = rms_inv_groups(gs + E * NGROUP, P.H);
+        // done before the group sums are read (its temporaries and those sums
+        // are never live together) and kept in a scalar register (uniform)
+        ir = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(ir)));
+        asm volatile("" : "+s"(ir)::"memory");
         uint64_t key = 0;
         if (t < E) {
             const float4 a = reinterpret_cast<const float4*>(gs + t * NGROUP)[0];
@@ -297,8 +323,10 @@ __device__ __forceinline__ void route_rank(const FusedParams& P, Misc* m, const 
             float total = 0.0f;
 #pragma unroll
             for (int g = 0; g < NGROUP; ++g) total = total + gv[g];
+            total = total * ir;
             if (P.bias) total = total + bias_t;
             m->logits[t] = total;
+            if (t == 0 && pred < 0) m->inv_r = ir;
             key = rank_key(total, t);
         }
         m->keys[key_slot(t)] = key;
@@ -439,8 +467,10 @@ __device__ __forceinline__ void group_load_router(const FusedParams& P, int laye
 // Group g's share of the router for its x rows gx (H/8 floats in LDS), in
 // the R-order: chunk partials (fma chain over the chunk's 16 rows, from
 // 0.0f), summed over the group's C chunks in order (from 0.0f); and the q8
-// blocks of the rows. Publishes [E sums][qw q8 words] tagged, to each replica;
-// pred: only the E sums, to dst[g * E + e] (no q8, one copy).
+// blocks of the rows; and the sum of squares of the rows in the same order
+// (chunk fma chains of x*x). Publishes [E sums][sum of squares][qw q8 words]
+// tagged, to each replica; pred: [E sums][sum of squares] to
+// dst[g * (E + 1) + k] (no q8, one copy).
 template <int CPT, int C, bool DBG>
 __device__ __forceinline__ void group_publish(const FusedParams& P, int g, const float4 (&wv)[CPT][4], const float* gx, float* gp,
                               uint32_t* q8w, uint64_t* dst, uint32_t tag, int sl, bool pred = false) {
@@ -470,7 +500,26 @@ __device__ __forceinline__ void group_publish(const FusedParams& P, int g, const
         }
     }
     const int nbq = (P.H / NGROUP) >> 5;  // q8 blocks per group; one lane quad each
+    float* sq = reinterpret_cast<float*>(q8w + P.qw);  // [C] chunk partials of x*x, then their sum
     if (!pred && t < 4 * nbq) quantize_block_quad(gx + 32 * (t >> 2), t & 3, q8w + (t >> 2) * 10);
+    // sum of squares: chunk c on thread SQ0 + c, in the last wavefront (the
+    // q8 quads are in the first)
+    constexpr int SQ0 = FT_THREADS - 64;
+    static_assert(C <= 64, "one thread per chunk");
+    if (t >= SQ0 && t < SQ0 + C) {
+        const int c = t - SQ0;
+        const float4* x4 = reinterpret_cast<const float4*>(gx + c * DN_ROWS);
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 xv = x4[k];
+            s = fmaf(xv.x, xv.x, s);
+            s = fmaf(xv.y, xv.y, s);
+            s = fmaf(xv.z, xv.z, s);
+            s = fmaf(xv.w, xv.w, s);
+        }
+        sq[c] = s;
+    }
     stamp<DBG>(P, sl, 20);
     __syncthreads();
     stamp<DBG>(P, sl, 21);
@@ -483,16 +532,21 @@ __device__ __forceinline__ void group_publish(const FusedParams& P, int g, const
         for (int c = 0; c < C; ++c) s = s + pv[c];
         gp[C * E + t] = s;
     }
+    if (t == MAX_E) {
+        float s = 0.0f;
+        for (int c = 0; c < C; ++c) s = s + sq[c];
+        sq[C] = s;
+    }
     __syncthreads();
     stamp<DBG>(P, sl, 22);
     if (pred) {
-        if (t < E) st_tag(dst + g * E + t, tag, __float_as_uint(gp[C * E + t]));
+        if (t <= E) st_tag(dst + g * (E + 1) + t, tag, __float_as_uint(t < E ? gp[C * E + t] : sq[C]));
         return;
     }
-    const int n = E + P.qw;
+    const int n = E + 1 + P.qw;
     for (int i = t; i < n * NREP; i += FT_THREADS) {
         const int rep = i / n, k = i - rep * n;
-        const uint32_t v = k < E ? __float_as_uint(gp[C * E + k]) : q8w[k - E];
+        const uint32_t v = k < E ? __float_as_uint(gp[C * E + k]) : (k == E ? __float_as_uint(sq[C]) : q8w[k - E - 1]);
         st_tag(dst + rep * P.rs_gq + (int64_t)g * P.gq_stride + k, tag, v);
     }
 }
@@ -512,17 +566,18 @@ template <int BPW, int DB, int CPT, bool DBG>
 __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P) {
     constexpr int C = 2 * BPW;  // router chunks per group = H/128
     // words per thread of each wait (H = 256 * BPW, E <= 128, K <= 8):
-    constexpr int UW_G = NGROUP * MAX_E / FT_THREADS;                              // group sums
+    constexpr int UW_G = NGROUP * MAX_E / FT_THREADS;                              // group sums (prediction)
+    static_assert((NGROUP - 1) * (MAX_E + 1) <= UW_G * FT_THREADS, "group units poll 7 groups' sums in UW_G rounds");
     constexpr int UW_Y = (BPW + 1) / 2;                                            // y of a group's rows
-    constexpr int UW_X = (NGROUP * (MAX_E + 10 * BPW) + FT_THREADS - 1) / FT_THREADS;  // sums + q8 of x
+    constexpr int UW_X = (NGROUP * (MAX_E + 1 + 10 * BPW) + FT_THREADS - 1) / FT_THREADS;  // sums + q8 of x
     extern __shared__ __align__(16) uint8_t lds[];
     uint8_t* act8 = lds + P.o_act8;
     float* red = reinterpret_cast<float*>(lds + P.o_red);
-    // expert units: [E][NGROUP] group sums, then the q8 of x as [H/32][8]
-    // qs words (16-byte aligned) and [H/32] (d, qsum) pairs
+    // expert units: [E+1][NGROUP] group sums (row E: sums of squares), then
+    // the q8 of x as [H/32][8] qs words (16-byte aligned) and [H/32] (d, qsum) pairs
     uint32_t* gq = reinterpret_cast<uint32_t*>(lds + P.o_gq);
-    const uint4* xq4 = reinterpret_cast<const uint4*>(gq + NGROUP * P.E);
-    const int2* xdp = reinterpret_cast<const int2*>(gq + NGROUP * P.E + (P.H >> 5) * 8);
+    const uint4* xq4 = reinterpret_cast<const uint4*>(gq + NGROUP * (P.E + 1));
+    const int2* xdp = reinterpret_cast<const int2*>(gq + NGROUP * (P.E + 1) + (P.H >> 5) * 8);
     float* gx = reinterpret_cast<float*>(lds + P.o_gx);
     float* gy = reinterpret_cast<float*>(lds + P.o_gy);
     float* gp = reinterpret_cast<float*>(lds + P.o_gp);
@@ -542,7 +597,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     auto tag_a = [&](int l) { return epoch + 4u * l + 2u; };
     auto tag_y = [&](int l) { return epoch + 4u * l + 3u; };
     auto gq_buf = [&](int l) { return P.gq_t + (int64_t)(l & 1) * NREP * P.rs_gq; };
-    auto pp_buf = [&](int l) { return P.pp_t + (int64_t)(l & 1) * NGROUP * E; };
+    auto pp_buf = [&](int l) { return P.pp_t + (int64_t)(l & 1) * NGROUP * (E + 1); };
     // the prediction: one copy per pred unit g (on XCD g), read by the units
     // of the same XCD
     auto pid_buf = [&](int l) { return P.pid_t + (int64_t)(l & 1) * NGROUP * PID_STRIDE; };
@@ -580,8 +635,24 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         if (pu && (!pf || L < 2)) return;    // nothing to predict
         uint32_t* q8w = reinterpret_cast<uint32_t*>(gp + (C + 1) * E);
         float4 wv[CPT][4];
-        auto gidx = [=](int i) { return (int64_t)(i / E) * P.gq_stride + i % E; };
-        auto gdst = [=](int i) { return (i % E) * NGROUP + i / E; };  // group sums -> LDS [E][NGROUP]
+        // Group sums and sums of squares -> LDS [E+1][NGROUP] (row E: the
+        // sums of squares). A unit takes its own group's row from gp
+        // (own_sums, before the wait) and polls the 7 other groups: group
+        // units the broadcast (oidx), pred units the prediction exchange
+        // (opidx), which carries the same sums of squares (both combine the
+        // same x); pred units then poll the broadcast's E sums alone (gidx_e,
+        // into rows < E, keeping row E).
+        const int ES = E + 1;
+        auto ogrp = [=](int i) { const int o = i / ES; return o < g ? o : o + 1; };
+        auto oidx = [=](int i) { return (int64_t)ogrp(i) * P.gq_stride + i % ES; };
+        auto opidx = [=](int i) { return (int64_t)ogrp(i) * ES + i % ES; };
+        auto odst = [=](int i) { return (i % ES) * NGROUP + ogrp(i); };
+        auto gidx_e = [=](int i) { return (int64_t)(i / E) * P.gq_stride + i % E; };
+        auto own_sums = [&]() __attribute__((always_inline)) {
+            const float* sq = reinterpret_cast<const float*>(q8w + P.qw);
+            if (t <= E) gq[t * NGROUP + g] = __float_as_uint(t < E ? gp[C * E + t] : sq[C]);
+        };
+        auto pdst = [=](int i) { return (i % E) * NGROUP + i / E; };  // E sums of 8 groups -> LDS rows < E
         stamp<DBG>(P, -1, 0);
         group_load_router<CPT, C>(P, pu ? 1 : 0, g, wv);
         float bias_n = ld_bias(P, 0), bias_p = pu ? ld_bias(P, 1) : 0.0f;
@@ -592,20 +663,26 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         __syncthreads();
         if (pu) {
             group_publish<CPT, C, DBG>(P, g, wv, gx, gp, q8w, pp_buf(1), tag_g(1), -1, true);
-            if (!wait_words<DBG, UW_G>(P, m, epoch, pp_buf(1), NGROUP * E, ident, tag_g(1), gq, gdst)) return;
+            own_sums();
+            if (!wait_words<DBG, UW_G>(P, m, epoch, pp_buf(1), (NGROUP - 1) * ES, opidx, tag_g(1), gq, odst)) return;
             route_rank(P, m, reinterpret_cast<const float*>(gq), bias_p, 1, nullptr);
-            if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(0), gq, gdst)) return;
+            if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * E, gidx_e, tag_g(0), gq, pdst)) return;
             if (t < K) st_tag(pid_buf(1) + g * PID_STRIDE + t, tag_g(1), (uint32_t)m->pid[1][t]);
         } else {
             group_publish<CPT, C, DBG>(P, g, wv, gx, gp, q8w, gq_buf(0), tag_g(0), -1);
             stamp<DBG>(P, -1, 11);
-            if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(0), gq, gdst)) return;
+            own_sums();
+            if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, (NGROUP - 1) * ES, oidx, tag_g(0), gq, odst))
+                return;
         }
         stamp<DBG>(P, -1, 12);
         route_rank(P, m, reinterpret_cast<const float*>(gq), bias_n, -1, nullptr);
         route_weights(P, m, 0, true, record);
         stamp<DBG>(P, -1, 14);
         for (int l = 0; l < L; ++l) {
+            // a pred unit's last prediction (of layer L-1) was published at
+            // l = L-3: nothing of its work after that is read
+            if (pu && l + 2 >= L) return;
             stamp<DBG>(P, l, 0);
             const int rl = pu ? l + 2 : l + 1;  // the router layer applied after this layer's combine
             if (rl < L) group_load_router<CPT, C>(P, rl, g, wv);
@@ -644,23 +721,25 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
             __syncthreads();
             stamp<DBG>(P, l, 9);
             if (l + 1 == L) break;
-            if (pu) {
-                if (l + 2 < L) {
-                    group_publish<CPT, C, DBG>(P, g, wv, gx, gp, q8w, pp_buf(l + 2), tag_g(l + 2), l, true);
-                    stamp<DBG>(P, l, 11);
-                    if (!wait_words<DBG, UW_G>(P, m, epoch, pp_buf(l + 2), NGROUP * E, ident, tag_g(l + 2), gq, gdst, l, 24)) return;
-                    route_rank(P, m, reinterpret_cast<const float*>(gq), bias_p, l & 1, nullptr);
-                }
-                if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(l + 1), gq, gdst))
+            if (pu) {  // here l + 2 < L
+                group_publish<CPT, C, DBG>(P, g, wv, gx, gp, q8w, pp_buf(l + 2), tag_g(l + 2), l, true);
+                stamp<DBG>(P, l, 11);
+                own_sums();
+                if (!wait_words<DBG, UW_G>(P, m, epoch, pp_buf(l + 2), (NGROUP - 1) * ES, opidx, tag_g(l + 2), gq, odst, l,
+                                           24))
+                    return;
+                route_rank(P, m, reinterpret_cast<const float*>(gq), bias_p, l & 1, nullptr);
+                if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * E, gidx_e, tag_g(l + 1), gq,
+                                           pdst))
                     return;
                 stamp<DBG>(P, l, 12);
-                if (l + 2 < L && t < K)
-                    st_tag(pid_buf(l + 2) + g * PID_STRIDE + t, tag_g(l + 2), (uint32_t)m->pid[l & 1][t]);
+                if (t < K) st_tag(pid_buf(l + 2) + g * PID_STRIDE + t, tag_g(l + 2), (uint32_t)m->pid[l & 1][t]);
             } else {
                 group_publish<CPT, C, DBG>(P, g, wv, gx, gp, q8w, gq_buf(l + 1), tag_g(l + 1), l);
                 stamp<DBG>(P, l, 11);
-                if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * E, gidx, tag_g(l + 1), gq, gdst, l,
-                                24))
+                own_sums();
+                if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, (NGROUP - 1) * ES, oidx, tag_g(l + 1),
+                                           gq, odst, l, 24))
                     return;
                 stamp<DBG>(P, l, 12);
                 // the prediction of layer l+1, for the slot -> unit group map
@@ -679,15 +758,15 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     const int u = w % K, j = w / K;
     const bool gm = w < P.n_gu, dm = w < P.n_dn;  // false: that part of the unit is idle
     const int dn_tile = nbj * 288;               // bytes of one 16-row down tile
-    const int nq = E + P.qw;
+    const int ES = E + 1, nq = ES + P.qw;  // per group: E sums, the sum of squares, q8 words
     auto xidx = [=](int i) {
         const int g = i / nq;
         return (int64_t)g * P.gq_stride + (i - g * nq);
     };
     auto xdst = [=](int i) {
         const int g = i / nq, k = i - g * nq;
-        const int kk = k - E, bl = kk / 10, wd = kk - bl * 10, blk = g * (P.qw / 10) + bl;
-        return k < E ? k * NGROUP + g : NGROUP * E + (wd >= 2 ? blk * 8 + (wd - 2) : nb * 8 + blk * 2 + wd);
+        const int kk = k - ES, bl = kk / 10, wd = kk - bl * 10, blk = g * (P.qw / 10) + bl;
+        return k < ES ? k * NGROUP + g : NGROUP * ES + (wd >= 2 ? blk * 8 + (wd - 2) : nb * 8 + blk * 2 + wd);
     };
     stamp<DBG>(P, -1, 0);
     float bias_n = ld_bias(P, 0);
@@ -822,6 +901,9 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                     sg = sg + gv[v];
                     su = su + uv[v];
                 }
+                const float ir = m->inv_r;  // input RMS norm: the sums of rmsnorm(x)
+                sg = sg * ir;
+                su = su * ir;
                 if (DBG && P.dbg_gu) {
                     float* dg = P.dbg_gu + ((int64_t)l * K + p) * 2 * I;
                     dg[j * 32 + t] = sg;
@@ -1059,7 +1141,7 @@ WsLayout ws_layout(int64_t H, int64_t I, int64_t E, int64_t K) {
     auto up = [](int64_t v) { return (v + 255) / 256 * 256; };
     WsLayout w{};
     w.qw = (int)(H / NGROUP / 32 * 10);
-    w.gq_stride = (int)((E + w.qw + 31) / 32 * 32);
+    w.gq_stride = (int)((E + 1 + w.qw + 31) / 32 * 32);
     w.rs_gq = NGROUP * (int64_t)w.gq_stride;
     int64_t off = 0;
     w.ctl = off; off += 256;
@@ -1067,7 +1149,7 @@ WsLayout ws_layout(int64_t H, int64_t I, int64_t E, int64_t K) {
     w.hp = off; off += up(K * (I / 32) * FT_WAVES * 64 * 8);
     w.y = off; off += 2 * up(K * H * 8);
     w.gq = off; off += 2 * NREP * up(w.rs_gq * 8);
-    w.pp = off; off += 2 * up(NGROUP * E * 8);
+    w.pp = off; off += 2 * up(NGROUP * (E + 1) * 8);
     w.pid = off; off += 2 * up(NGROUP * PID_STRIDE * 8);
     w.pl = off; off += up(((int64_t)std::max(K * (I / 32), K * (H / DN_UNIT)) + 2 * NGROUP) * 8);
     w.total = off;
@@ -1196,10 +1278,10 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
     int off = 0;
     P.o_act8 = off; off += up16(nbj * Q8_BLK);
     P.o_red = off; off += up16(FT_WAVES * 64 * 4);
-    P.o_gq = off; off += up16((NGROUP * (int)n_experts + (int)(hidden / 32) * 10) * 4);
+    P.o_gq = off; off += up16((NGROUP * ((int)n_experts + 1) + (int)(hidden / 32) * 10) * 4);
     P.o_gx = off; off += up16(HG * 4);
     P.o_gy = off; off += up16((int)top_k * HG * 4);
-    P.o_gp = off; off += up16(((C + 1) * (int)n_experts + wl.qw) * 4);
+    P.o_gp = off; off += up16(((C + 1) * (int)n_experts + wl.qw + C + 1) * 4);
     P.o_misc = off; off += up16((int)sizeof(Misc));
     P.lds_bytes = off;
     if (off > 160 * 1024)
@@ -1234,6 +1316,7 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
     P.gu_bytes = 2 * inter * (hidden / 32) * 18;
     P.spin_limit = ctx->fused_spin_limit;
     P.prefetch = ctx->fused_prefetch;
+    P.input_norm = ctx->input_norm;
     void* args[] = {&P};
     // the kernel keeps exactly H/256 gate|up blocks per wave in flight
     const bool db6 = inter / 32 <= 24;

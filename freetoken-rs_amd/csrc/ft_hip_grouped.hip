@@ -40,6 +40,7 @@ struct GroupWs {
     int32_t* ppos;      // [P] scratch
     uint8_t* q8a;       // [P][I/32][40]
     float* ydn;         // [P][H]
+    float* inv;         // [B] input RMS norm scales
     size_t bytes;
 };
 
@@ -56,6 +57,7 @@ GroupWs group_ws(void* base, int64_t B, int64_t H, int64_t I, int64_t E, int64_t
     w.ppos = (int32_t*)(p + off); off += up(sizeof(int32_t) * P);
     w.q8a = p + off; off += up((size_t)P * (I / 32) * Q8_BLK);
     w.ydn = (float*)(p + off); off += up(sizeof(float) * P * H);
+    w.inv = (float*)(p + off); off += up(sizeof(float) * B);
     w.bytes = off;
     return w;
 }
@@ -104,11 +106,14 @@ __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t* ids, int P,
 }
 
 // Gate|up tile j of active expert g for all of its tokens, then GELU*up and
-// the q8 of act block j per token. BPW = H/32/8 blocks per wave.
+// the q8 of act block j per token. BPW = H/32/8 blocks per wave. in_scale
+// (input RMS norm, or null): a token's gate|up sums are first multiplied by
+// in_scale[token].
 template <int BPW>
 __global__ __launch_bounds__(GT, 1) void k_grouped_gu(const uint8_t* bank, int64_t expert_bytes, const int32_t* meta,
                                                       const int32_t* plist, const uint8_t* q8x, uint8_t* q8a,
-                                                      float* dbg_gu, int H, int I, int E, int K) {
+                                                      float* dbg_gu, const float* in_scale, int H, int I, int E,
+                                                      int K) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int nb = H >> 5, nbj = I >> 5;
     const int j = blockIdx.x, g = blockIdx.y;
@@ -160,6 +165,7 @@ __global__ __launch_bounds__(GT, 1) void k_grouped_gu(const uint8_t* bank, int64
             float sv = 0.0f;
 #pragma unroll
             for (int v = 0; v < GW; ++v) sv = sv + red[(v * NT + tt) * 64 + rr];
+            if (in_scale) sv = sv * in_scale[plist[s0 + c0 + tt] / K];
             rows[tt * 64 + rr] = sv;
             if (dbg_gu) {
                 const int p = plist[s0 + c0 + tt];
@@ -298,7 +304,10 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
     const int64_t eb = ft_hip_fused_expert_bytes(hidden, inter);
     const int64_t gu_bytes = 2LL * I * nb * 18;
     int rc;
-    if ((rc = ft_hip_router_logits(ctx, stream, router_w, x, router_bias, w.logits, hidden, n_experts, n_seqs))) return rc;
+    const float* inv = ctx->input_norm ? w.inv : nullptr;
+    if (inv && (rc = ft::launch_rms_inv(stream, x, w.inv, hidden, n_seqs))) return rc;
+    if ((rc = ft::launch_router_logits(stream, router_w, x, router_bias, inv, w.logits, hidden, n_experts, n_seqs)))
+        return rc;
     if ((rc = ft_hip_topk_router(ctx, stream, w.logits, expert_scale, ids, wts, n_experts, top_k, n_seqs))) return rc;
     if ((rc = ft_hip_quantize_q8(ctx, stream, x, hidden, w.q8x, hidden, n_seqs))) return rc;
     hipLaunchKernelGGL(k_group_pairs, dim3(1), dim3(1024), 0, s, (const int32_t*)ids, P, E, w.meta, w.plist, w.ppos);
@@ -307,10 +316,10 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
     const size_t lds_gu = (size_t)NT * nb * 40 + sizeof(float) * (GW * NT * 64 + NT * 64 + NT * 32) + 4 * NT * 10;
     if (H == 2816)
         hipLaunchKernelGGL(k_grouped_gu<11>, dim3(nbj, gmax), dim3(GT), lds_gu, s, (const uint8_t*)bank, eb,
-                           (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8x, w.q8a, dbg_gu, H, I, E, K);
+                           (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8x, w.q8a, dbg_gu, inv, H, I, E, K);
     else
         hipLaunchKernelGGL(k_grouped_gu<16>, dim3(nbj, gmax), dim3(GT), lds_gu, s, (const uint8_t*)bank, eb,
-                           (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8x, w.q8a, dbg_gu, H, I, E, K);
+                           (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8x, w.q8a, dbg_gu, inv, H, I, E, K);
     if ((rc = launch_status("moe_layer_grouped/gate_up"))) return rc;
     if (dbg_act && hipMemcpyAsync(dbg_act, w.q8a, (size_t)P * nbj * Q8_BLK, hipMemcpyDeviceToDevice, s) != hipSuccess)
         return fail(FT_HIP_E_LAUNCH, "%s: debug copy failed", nm);

@@ -142,7 +142,10 @@ __global__ __launch_bounds__(256) void k_quantize_q8(const float* x, int64_t x_s
 }
 
 // Fused gelu_tanh(gate)*up -> q8 (replaces gelu_mul_q8, q4.cu:255-287).
-__global__ __launch_bounds__(256) void k_gelu_mul_q8(const float* gu, uint8_t* q8, int inter, int64_t n) {
+// in_scale (input RMS norm, or null): pair e's gate and up sums are first
+// multiplied by in_scale[e / div].
+__global__ __launch_bounds__(256) void k_gelu_mul_q8(const float* gu, uint8_t* q8, int inter, int64_t n,
+                                                     const float* in_scale, int div) {
     const int nb = inter >> 5;
     const int64_t g = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 5;
     const int l = threadIdx.x & 31;
@@ -150,24 +153,23 @@ __global__ __launch_bounds__(256) void k_gelu_mul_q8(const float* gu, uint8_t* q
     const int64_t gg = ok ? g : 0;
     const int64_t e = gg / nb, b = gg % nb;
     const int j = (int)b * 32 + l;
-    const float gate = gu[e * 2 * inter + j];
-    const float up = gu[e * 2 * inter + inter + j];
+    float gate = gu[e * 2 * inter + j];
+    float up = gu[e * 2 * inter + inter + j];
+    if (in_scale) {
+        const float sc = in_scale[e / div];
+        gate = gate * sc;
+        up = up * sc;
+    }
     const float v = gelu_tanh(gate) * up;
     const Q8Lane r = q8_quantize_half(v);
     if (ok) q8_store_half(q8 + (e * nb + b) * Q8_BLK, l, r);
 }
 
-// Router logits in the R-order (replaces gemv_f32_rows, q4.cu:1153-1174):
+// R-order dot w.xs of one wavefront (the value is returned in lane 0):
 // lane c computes chunk partials P_c (16-element fma chains), lanes 0..7 sum
 // their group's chunks in order, lane 0 sums the 8 groups in order.
-// Grid (n_rows, n_seqs), one wavefront per logit.
-__global__ __launch_bounds__(64) void k_router_logits(const float* W, const float* x, const float* bias,
-                                                      float* y, int dim, int n_rows) {
-    extern __shared__ float P[];  // dim/16 chunk partials
-    __shared__ float G[8];
-    const int e = blockIdx.x, s = blockIdx.y, l = threadIdx.x;
-    const float* w = W + (int64_t)e * dim;
-    const float* xs = x + (int64_t)s * dim;
+__device__ __forceinline__ float rorder_dot(const float* w, const float* xs, int dim, float* P, float* G) {
+    const int l = threadIdx.x;
     const int nch = dim >> 4;
     for (int c = l; c < nch; c += 64) {
         const float4* w4 = reinterpret_cast<const float4*>(w + 16 * c);
@@ -191,12 +193,37 @@ __global__ __launch_bounds__(64) void k_router_logits(const float* W, const floa
         G[l] = gs;
     }
     __syncthreads();
-    if (l == 0) {
-        float t = 0.0f;
+    float t = 0.0f;
+    if (l == 0)
         for (int g = 0; g < 8; ++g) t = t + G[g];
+    return t;
+}
+
+// Router logits in the R-order (replaces gemv_f32_rows, q4.cu:1153-1174),
+// times in_scale[s] (input RMS norm) when given, then + bias.
+// Grid (n_rows, n_seqs), one wavefront per logit.
+__global__ __launch_bounds__(64) void k_router_logits(const float* W, const float* x, const float* bias,
+                                                      const float* in_scale, float* y, int dim, int n_rows) {
+    extern __shared__ float P[];  // dim/16 chunk partials
+    __shared__ float G[8];
+    const int e = blockIdx.x, s = blockIdx.y;
+    float t = rorder_dot(W + (int64_t)e * dim, x + (int64_t)s * dim, dim, P, G);
+    if (threadIdx.x == 0) {
+        if (in_scale) t = t * in_scale[s];
         if (bias) t = t + bias[e];
         y[(int64_t)s * n_rows + e] = t;
     }
+}
+
+// Scale of the input RMS norm per seq: inv[s] = 1 / sqrt(ss / dim + 1e-6),
+// ss = x_s.x_s in the R-order, each op rounded once. Grid n_seqs.
+__global__ __launch_bounds__(64) void k_rms_inv(const float* x, float* inv, int dim) {
+    extern __shared__ float P[];
+    __shared__ float G[8];
+    const int s = blockIdx.x;
+    const float* xs = x + (int64_t)s * dim;
+    const float ss = rorder_dot(xs, xs, dim, P, G);
+    if (threadIdx.x == 0) inv[s] = 1.0f / sqrtf(ss / (float)dim + 1e-6f);  // correctly rounded (HIP default)
 }
 
 // (value, index) order of the router: larger logit first, then lower index;
@@ -491,7 +518,7 @@ extern "C" int ft_hip_gelu_mul_q8(ft_hip_ctx* ctx, void* stream, const float* gu
     if (n == 0) return FT_HIP_OK;
     const int64_t threads = n * (inter / 32) * 32;
     hipLaunchKernelGGL(k_gelu_mul_q8, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, S(stream), gu,
-                       (uint8_t*)q8, (int)inter, n);
+                       (uint8_t*)q8, (int)inter, n, (const float*)nullptr, 1);
     return launch_status("gelu_mul_q8");
 }
 
@@ -503,11 +530,25 @@ extern "C" int ft_hip_router_logits(ft_hip_ctx* ctx, void* stream, const float* 
     if (n_rows < 0 || n_seqs < 0 || n_rows > 65535 || n_seqs > 65535)
         return fail(FT_HIP_E_SHAPE, "router_logits: n_rows/n_seqs out of range");
     if (!ctx || !w || !x || !y) return fail(FT_HIP_E_INVALID, "router_logits: null argument");
+    return ft::launch_router_logits(stream, w, x, bias, nullptr, y, dim, n_rows, n_seqs);
+}
+
+namespace ft {
+int launch_router_logits(void* stream, const float* w, const float* x, const float* bias, const float* in_scale,
+                         float* y, int64_t dim, int64_t n_rows, int64_t n_seqs) {
     if (n_rows == 0 || n_seqs == 0) return FT_HIP_OK;
     hipLaunchKernelGGL(k_router_logits, dim3((unsigned)n_rows, (unsigned)n_seqs), dim3(64), (size_t)(dim / 16) * 4,
-                       S(stream), w, x, bias, y, (int)dim, (int)n_rows);
+                       S(stream), w, x, bias, in_scale, y, (int)dim, (int)n_rows);
     return launch_status("router_logits");
 }
+
+int launch_rms_inv(void* stream, const float* x, float* inv, int64_t dim, int64_t n_seqs) {
+    if (n_seqs == 0) return FT_HIP_OK;
+    hipLaunchKernelGGL(k_rms_inv, dim3((unsigned)n_seqs), dim3(64), (size_t)(dim / 16) * 4, S(stream), x, inv,
+                       (int)dim);
+    return launch_status("rms_inv");
+}
+}  // namespace ft
 
 extern "C" int ft_hip_topk_router(ft_hip_ctx* ctx, void* stream, const float* logits, const float* expert_scale,
                                   int32_t* ids, float* wts, int64_t e_count, int64_t k, int64_t n_seqs) {
@@ -581,6 +622,7 @@ struct LayerWs {
     float* ygu;
     uint8_t* q8a;
     float* ydn;
+    float* inv;         // [B] input RMS norm scales
     size_t bytes;
 };
 
@@ -594,6 +636,7 @@ static LayerWs layer_ws(void* base, int64_t B, int64_t H, int64_t I, int64_t E, 
     w.ygu = (float*)(p + off); off += up(sizeof(float) * B * K * 2 * I);
     w.q8a = p + off; off += up((size_t)B * K * (I / 32) * Q8_BLK);
     w.ydn = (float*)(p + off); off += up(sizeof(float) * B * K * H);
+    w.inv = (float*)(p + off); off += up(sizeof(float) * B);
     w.bytes = off;
     return w;
 }
@@ -625,7 +668,10 @@ extern "C" int ft_hip_moe_layer(ft_hip_ctx* ctx, void* stream, const float* x, f
     if (!ctx || !x || !x_out || !router_w || !bank || !ids || !wts || !workspace) return fail(FT_HIP_E_INVALID, "%s: null argument", nm);
     if (n_seqs == 0) return FT_HIP_OK;
     int rc;
-    if ((rc = ft_hip_router_logits(ctx, stream, router_w, x, router_bias, w.logits, hidden, n_experts, n_seqs))) return rc;
+    const float* inv = ctx->input_norm ? w.inv : nullptr;
+    if (inv && (rc = ft::launch_rms_inv(stream, x, w.inv, hidden, n_seqs))) return rc;
+    if ((rc = ft::launch_router_logits(stream, router_w, x, router_bias, inv, w.logits, hidden, n_experts, n_seqs)))
+        return rc;
     if ((rc = ft_hip_topk_router(ctx, stream, w.logits, expert_scale, ids, wts, n_experts, top_k, n_seqs))) return rc;
     if ((rc = ft_hip_quantize_q8(ctx, stream, x, hidden, w.q8x, hidden, n_seqs))) return rc;
     const int64_t n_pairs = n_seqs * top_k;
@@ -641,7 +687,9 @@ extern "C" int ft_hip_moe_layer(ft_hip_ctx* ctx, void* stream, const float* x, f
     a.y = w.ygu;
     a.y_stride = 2 * inter;
     if ((rc = gemv_common(ctx, stream, a, n_pairs, 2 * inter, hidden, layout, false, "moe_layer/gate_up"))) return rc;
-    if ((rc = ft_hip_gelu_mul_q8(ctx, stream, w.ygu, w.q8a, inter, n_pairs))) return rc;
+    hipLaunchKernelGGL(k_gelu_mul_q8, dim3((unsigned)((n_pairs * inter + 255) / 256)), dim3(256), 0, S(stream),
+                       (const float*)w.ygu, w.q8a, (int)inter, n_pairs, inv, (int)top_k);
+    if ((rc = launch_status("moe_layer/gelu_mul_q8"))) return rc;
     a.bank_off = (uint64_t)gu_bytes;
     a.x_div = 1;
     a.q8 = w.q8a;

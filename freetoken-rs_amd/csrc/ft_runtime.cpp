@@ -61,6 +61,14 @@ extern "C" int ft_hip_create(int device, ft_hip_ctx** out) {
     return FT_HIP_OK;
 }
 
+extern "C" int ft_hip_set_input_norm(ft_hip_ctx* ctx, int on) {
+    clear_error();
+    if (!ctx) return fail(FT_HIP_E_INVALID, "set_input_norm: null ctx");
+    if (on != 0 && on != 1) return fail(FT_HIP_E_SHAPE, "set_input_norm: on=%d is not 0 or 1", on);
+    ctx->input_norm = on;
+    return FT_HIP_OK;
+}
+
 extern "C" int ft_hip_destroy(ft_hip_ctx* ctx) {
     clear_error();
     delete ctx;

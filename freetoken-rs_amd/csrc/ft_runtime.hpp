@@ -12,6 +12,7 @@ struct ft_hip_ctx {
     int num_xcds;
     int fused_spin_limit;  // polls before a fused-kernel wait gives up
     int fused_prefetch;    // fused kernel: stream predicted experts ahead (1) or not (0)
+    int input_norm;        // layer entry points run on rmsnorm(x) (1) or x (0)
     char arch[64];
 };
 
@@ -21,6 +22,12 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // Status of the launch just issued: FT_HIP_OK, or FT_HIP_E_LAUNCH with the
 // HIP error text.
 int launch_status(const char* what);
+// Router logits in the R-order, times in_scale[s] when given, + bias (shapes
+// already checked by the caller).
+int launch_router_logits(void* stream, const float* w, const float* x, const float* bias, const float* in_scale,
+                         float* y, int64_t dim, int64_t n_rows, int64_t n_seqs);
+// Input RMS norm scale per seq: inv[s] = 1 / sqrt(R-order(x_s . x_s) / dim + 1e-6).
+int launch_rms_inv(void* stream, const float* x, float* inv, int64_t dim, int64_t n_seqs);
 }  // namespace ft
 
 using ft::clear_error;

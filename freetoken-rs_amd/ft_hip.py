@@ -54,6 +54,7 @@ SIGNATURES = {
     "ft_hip_fused_workgroups": (ctypes.c_int, [_I64, _I64, _I64, _I64]),
     "ft_hip_fused_set_spin_limit": (_I, [_P, _I]),
     "ft_hip_fused_set_prefetch": (_I, [_P, _I]),
+    "ft_hip_set_input_norm": (_I, [_P, _I]),
     "ft_hip_fused_workspace_init": (_I, [_P, _P, _P, _SZ]),
     "ft_hip_pack_experts_fused": (_I, [_P, _P, _P, _I, _U64, _P, _I64, _I64, _I64]),
     "ft_hip_pack_router_fused": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
@@ -254,6 +255,11 @@ class Q4Gemv:
     def fused_set_prefetch(self, on):
         """1: stream early-routed experts ahead (default); 0: load each layer's experts once routed."""
         check(lib().ft_hip_fused_set_prefetch(self._ctx, int(on)))
+
+    def set_input_norm(self, on):
+        """1: the layer entry points run on rmsnorm(x) (logits and gate|up sums times
+        1/sqrt(mean(x*x) + 1e-6)); 0 (default): on x as given."""
+        check(lib().ft_hip_set_input_norm(self._ctx, int(on)))
 
     def fused_workspace_init(self, ws, stream=None):
         check(lib().ft_hip_fused_workspace_init(self._ctx, _stream(stream), _ptr(ws), ws.numel() * ws.element_size()))

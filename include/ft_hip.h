@@ -197,6 +197,18 @@ int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const float* x, floa
                              const void* bank, int32_t* ids, float* wts, void* workspace,
                              size_t workspace_bytes, float* dbg_gu, void* dbg_act);
 
+/* Input RMS norm of the layer entry points (ft_hip_moe_layer,
+ * ft_hip_moe_layer_grouped, ft_hip_moe_stack_fused); off (0) after create.
+ * On (1), each layer runs on rmsnorm(x) = x * inv_r with
+ *   inv_r = 1 / sqrt(ss / H + 1e-6),  ss = x.x in the R-order of the router
+ * (each op rounded once, f32), applied where the layer is linear in its
+ * input: router logits = R-order(W_r, x) * inv_r (+ bias), gate|up sums
+ * times inv_r before GELU*up. q8 quants and int32 dots stay those of x; the
+ * residual stays x. Replaces the caller-side norms that feed the reference's
+ * router and routed experts (rmsnorm_rows_dev, ft-model/src/lib.rs:1362-1365
+ * and :1398-1399; unweighted here), which keeps a layer chain bounded. */
+int ft_hip_set_input_norm(ft_hip_ctx* ctx, int on);
+
 /* ---- fused whole-stack path (no single reference counterpart) ----
  * The reference runs the section as a sequence of launches per layer
  * (ft-model/src/lib.rs:1406-1476) and removes host launch cost with a CUDA

@@ -435,6 +435,23 @@ int orc_router_logits(const float* W, const float* x, int E, int H, const float*
     return 0;
 }
 
+// Input RMS norm of the synthetic layer chain (definition of this build).
+// The reference model feeds its router and its routed experts rmsnorm(x)
+// (router: unweighted, ft-model/src/lib.rs:1398-1399; experts: :1362-1365);
+// the stack here is unweighted on both. The scale of x is
+//   ss    = R-order dot of x with itself (orc_router_logits with W = x)
+//   inv_r = 1.0f / sqrtf(ss / (float)H + 1e-6f)   (each op rounded once, f32)
+// and orc_moe_layer with input_norm applies it where the section is linear
+// in its input (router logits, gate|up sums), so that the q8 quants and the
+// int32 dots stay those of x itself.
+// ---------------------------------------------------------------------------
+float orc_rms_inv(const float* x, int H) {
+    if (H % 128) return -1.0f;
+    float ss = 0.0f;
+    orc_router_logits(x, x, 1, H, nullptr, &ss);
+    return 1.0f / std::sqrt(ss / (float)H + 1e-6f);
+}
+
 // ft-model/src/lib.rs:1487-1504: stable sort by descending logit (ties keep
 // the lower expert index first), take k, w_j = exp(l_j - l_max) / sum (sum in
 // top-k order from 0.0f), times per_expert_scale[e] (NULL = 1).
@@ -491,20 +508,29 @@ void orc_combine(const float* y, const float* w, int n_pairs, int64_t H, const f
 // the synthetic stack: x_out = x + sum_p w_p * down_p(q8(gelu(gate_p)*up_p))).
 //   gu[e], dn[e]: expert e's gate|up rows ([2I x H]) and down rows ([H x I]) in
 //   `layout` (0 q4_0, 1 q4r); NULL for experts that are not available.
+// input_norm != 0: the layer runs on rmsnorm(x) in the form of orc_rms_inv:
+//   logits[e] = R-order(W_r[e], x) * inv_r (+ bias[e]), and the gate|up sums
+//   y_gu = gemv_q8(W_gu, q8(x)) * inv_r (f32 mul) before GELU*up; the
+//   residual stays x.
 // Optional stage outputs (NULL to skip): logits[E], ids[k], wts[k],
-//   y_gu[k][2I], act[k][I], act_d[k][I/32], act_qs[k][I], y_dn[k][H].
+//   y_gu[k][2I] (after the scale), act[k][I], act_d[k][I/32], act_qs[k][I], y_dn[k][H].
 // Returns 0, or -1 on a bad shape, -2 if a routed expert's bytes are missing.
 // ---------------------------------------------------------------------------
 int orc_moe_layer(const float* x, int H, int I, int E, int k,
                   const float* W_r, const float* bias, const float* expert_scale,
                   const uint8_t* const* gu, const uint8_t* const* dn, int layout,
-                  int threads, int gelu_mode,
+                  int threads, int gelu_mode, int input_norm,
                   float* x_out, float* logits, int32_t* ids, float* wts,
                   float* y_gu, float* act, float* act_d, int8_t* act_qs, float* y_dn) {
     if (H % 128 || I % 32 || k <= 0 || k > E) return -1;
     std::vector<float> lg((size_t)E), w((size_t)k);
     std::vector<int32_t> id((size_t)k);
-    if (orc_router_logits(W_r, x, E, H, bias, lg.data())) return -1;
+    const float inv_r = input_norm ? orc_rms_inv(x, H) : 1.0f;
+    if (orc_router_logits(W_r, x, E, H, nullptr, lg.data())) return -1;
+    for (int e = 0; e < E; ++e) {
+        if (input_norm) lg[(size_t)e] = lg[(size_t)e] * inv_r;
+        if (bias) lg[(size_t)e] = lg[(size_t)e] + bias[e];
+    }
     orc_topk_softmax(lg.data(), E, k, expert_scale, gelu_mode, id.data(), w.data());
     for (int j = 0; j < k; ++j)
         if (!gu[id[(size_t)j]] || !dn[id[(size_t)j]]) return -2;
@@ -517,6 +543,8 @@ int orc_moe_layer(const float* x, int H, int I, int E, int k,
         int e = id[(size_t)p];
         float* yg = ygu.data() + (size_t)p * 2 * I;
         orc_gemv_q8(gu[e], 2 * I, layout, xd.data(), xq.data(), H, yg, threads);
+        if (input_norm)
+            for (int r = 0; r < 2 * I; ++r) yg[r] = yg[r] * inv_r;
         orc_gelu_mul_q8(yg, I, gelu_mode, av.data() + (size_t)p * I, ad.data() + (size_t)p * I / 32,
                         aq.data() + (size_t)p * I);
         orc_gemv_q8(dn[e], H, layout, ad.data() + (size_t)p * I / 32, aq.data() + (size_t)p * I, I,

@@ -68,8 +68,9 @@ def _declare(L):
         "orc_router_logits": (i32, [P, P, i32, i32, P, P]),
         "orc_topk_softmax": (i32, [P, i32, i32, P, i32, P, P]),
         "orc_combine": (None, [P, P, i32, i64, P, P]),
-        "orc_moe_layer": (i32, [P, i32, i32, i32, i32, P, P, P, P, P, i32, i32, i32,
+        "orc_moe_layer": (i32, [P, i32, i32, i32, i32, P, P, P, P, P, i32, i32, i32, i32,
                                 P, P, P, P, P, P, P, P, P]),
+        "orc_rms_inv": (f32, [P, i32]),
         "orc_tensor_key": (u64, [u64, u32, u32, u32, u32]),
         "orc_gen_scale": (f32, [f64]),
         "orc_gen_values": (None, [u64, i64, i64, f32, P]),
@@ -241,9 +242,19 @@ def combine(y, w, resid=None):
     return out
 
 
+def rms_inv(x):
+    """Scale of the stack's input RMS norm: 1/sqrt(R-order(x.x)/H + 1e-6) in f32
+    (definition of this build; the reference model's router and experts take
+    rmsnorm(x), ft-model/src/lib.rs:1362-1365, :1398-1399)."""
+    x = _f32(x).ravel()
+    return np.float32(lib().orc_rms_inv(_p(x), x.size))
+
+
 def moe_layer(x, W_r, gu_banks, dn_banks, H, I, k, bias=None, expert_scale=None,
-              layout=0, threads=1, gelu_mode=GELU_PORTABLE):
+              layout=0, threads=1, gelu_mode=GELU_PORTABLE, input_norm=False):
     """One MoE layer for one token (ft-model/src/lib.rs:1487-1504, :1609-1653).
+    input_norm: run on rmsnorm(x) in the form of rms_inv (logits and gate|up
+    sums scaled by it; q8 quants and int32 dots those of x).
 
     gu_banks / dn_banks: dict expert -> uint8 array (that expert's gate|up rows /
     down rows in `layout`); experts the router may pick must be present.
@@ -274,7 +285,7 @@ def moe_layer(x, W_r, gu_banks, dn_banks, H, I, k, bias=None, expert_scale=None,
     rc = lib().orc_moe_layer(
         _p(x), H, I, E, k, _p(W_r), _p(b), _p(es),
         ctypes.cast(gu_ptrs, ctypes.c_void_p), ctypes.cast(dn_ptrs, ctypes.c_void_p),
-        layout, threads, gelu_mode,
+        layout, threads, gelu_mode, int(bool(input_norm)),
         _p(r["x_out"]), _p(r["logits"]), _p(r["ids"]), _p(r["wts"]), _p(r["y_gu"]),
         _p(r["act"]), _p(r["act_d"]), _p(r["act_qs"]), _p(r["y_dn"]))
     if rc == -2:

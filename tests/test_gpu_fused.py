@@ -4,8 +4,12 @@ Per layer, each stage is checked against the CPU oracle on the kernel's own
 input to that stage (teacher forcing, from the kernel's debug record):
 top-k ids and weights and the GELU*up q8 blocks bit-exact; gate|up sums and
 the layer output within max|d| <= 1e-3 * ||ref||_2. The repack to the fused
-layout is checked byte for byte against the oracle's q4_0 rows.
+layout is checked byte for byte against the oracle's q4_0 rows. The input
+RMS norm (ft_hip_set_input_norm) is covered the same way: its scale enters
+the logits (ids and weights still bit-exact) and the gate|up sums.
 """
+import contextlib
+
 import numpy as np
 import pytest
 import torch
@@ -67,7 +71,27 @@ def test_fused_pack_is_lossless(gemv, orc, stack):
     assert np.array_equal(r.transpose(1, 0, 2).reshape(m.shape.n_experts, H), ref)
 
 
-def _run_debug(stack, token):
+@contextlib.contextmanager
+def input_norm(gemv, on):
+    gemv.set_input_norm(on)
+    try:
+        yield
+    finally:
+        gemv.set_input_norm(0)
+
+
+def route(orc, Wr, x, bias, K, norm):
+    """The oracle's routing of one token: R-order logits, times the input RMS
+    norm's scale when on, + bias; top-k and softmax."""
+    lg = orc.router_logits(Wr, x)
+    if norm:
+        lg = (lg * orc.rms_inv(x)).astype(np.float32)
+    if bias is not None:
+        lg = (lg + bias).astype(np.float32)
+    return orc.topk_softmax(lg, K)
+
+
+def _run_debug(stack, token, norm=False):
     m = stack.m
     s = m.shape
     H, I, E, K, L = s.hidden, s.inter, s.n_experts, s.top_k, m.L
@@ -78,7 +102,8 @@ def _run_debug(stack, token):
     dbg_gu = torch.zeros(L * K * 2 * I, dtype=torch.float32, device=DEV)
     dbg_act = torch.zeros(L * K * (I // 32) * 40, dtype=torch.uint8, device=DEV)
     dbg_x = torch.zeros((L + 1) * H, dtype=torch.float32, device=DEV)
-    stack.run(x, out, ids, wts, dbg_gu, dbg_act, dbg_x)
+    with input_norm(m.g, norm):
+        stack.run(x, out, ids, wts, dbg_gu, dbg_act, dbg_x)
     stack.check()
     return dict(x=host(x), out=host(out), ids=host(ids).reshape(L, K), wts=host(wts).reshape(L, K),
                 gu=host(dbg_gu).reshape(L, K, 2 * I), act=host(dbg_act).reshape(L, K, I // 32, 40),
@@ -100,6 +125,22 @@ def test_fused_zipf_stages_teacher_forced(gemv, orc, zstack):
     _check_teacher_forced(orc, zstack, 1)
 
 
+def test_fused_norm_stages_teacher_forced(gemv, orc, stack):
+    _check_teacher_forced(orc, stack, 4, norm=True)
+
+
+def test_fused_zipf_norm_stages_teacher_forced(gemv, orc, zstack):
+    _check_teacher_forced(orc, zstack, 5, norm=True)
+
+
+def test_fused_norm_prefetch_does_not_change_results(gemv, zstack):
+    with input_norm(gemv, 1):
+        a = _run_plain(zstack, 6, 1)
+        b = _run_plain(zstack, 6, 0)
+    for u, v in zip(a, b):
+        assert np.array_equal(u.view(np.uint32), v.view(np.uint32))
+
+
 def test_fused_zipf_prefetch_does_not_change_results(gemv, zstack):
     a = _run_plain(zstack, 2, 1)
     b = _run_plain(zstack, 2, 0)
@@ -107,25 +148,44 @@ def test_fused_zipf_prefetch_does_not_change_results(gemv, zstack):
         assert np.array_equal(u.view(np.uint32), v.view(np.uint32))
 
 
-def _check_teacher_forced(orc, stack, token):
+def _weights_diag(orc, Wr, x, bias, K, got, want):
+    """Which scale of the logits reproduces the kernel's weights (a failure report)."""
+    lg = orc.router_logits(Wr, x)
+    ir = orc.rms_inv(x)
+    hits = []
+    for k in range(-4, 5):
+        c = ir
+        for _ in range(abs(k)):
+            c = np.nextafter(c, np.float32(np.inf if k > 0 else -np.inf), dtype=np.float32)
+        v = (lg * c).astype(np.float32)
+        if bias is not None:
+            v = (v + bias).astype(np.float32)
+        if np.array_equal(orc.topk_softmax(v, K)[1].view(np.uint32), got.view(np.uint32)):
+            hits.append(k)
+    return f"got {got.tolist()} want {want.tolist()} inv_r {float(ir)!r}; ulp offsets of inv_r that match: {hits}"
+
+
+def _check_teacher_forced(orc, stack, token, norm=False):
     m = stack.m
     s = m.shape
     H, I, E, K, L = s.hidden, s.inter, s.n_experts, s.top_k, m.L
-    r = _run_debug(stack, token)
+    r = _run_debug(stack, token, norm)
     assert np.array_equal(r["xs"][0], r["x"])
     assert np.array_equal(r["xs"][L], r["out"])
     for l in range(L):
         xl = r["xs"][l]
         Wr = host(m.routers[l])
         bias = None if m.bias is None else host(m.bias[l])
-        ids, wts = orc.topk_softmax(orc.router_logits(Wr, xl, bias), K)
+        ids, wts = route(orc, Wr, xl, bias, K, norm)
         assert np.array_equal(r["ids"][l], ids), f"layer {l}"
-        assert np.array_equal(r["wts"][l].view(np.uint32), wts.view(np.uint32)), f"layer {l}"
+        assert np.array_equal(r["wts"][l].view(np.uint32), wts.view(np.uint32)), \
+            f"layer {l}: " + _weights_diag(orc, Wr, xl, bias, K, r["wts"][l], wts)
         gu_b, dn_b = {}, {}
         for e in ids:
             b = host(m.bank_of(l, int(e)))
             gu_b[int(e)], dn_b[int(e)] = b[:m.gu_bytes], b[m.gu_bytes:]
-        ref = orc.moe_layer(xl, Wr, gu_b, dn_b, H, I, K, bias=bias, layout=1)
+        ref = orc.moe_layer(xl, Wr, gu_b, dn_b, H, I, K, bias=bias, layout=1, input_norm=norm)
+        assert np.array_equal(ref["ids"], ids) and np.array_equal(ref["wts"].view(np.uint32), wts.view(np.uint32))
         out_ref = xl.astype(np.float64).copy()
         for p in range(K):
             yg = ref["y_gu"][p]
@@ -144,19 +204,21 @@ def _check_teacher_forced(orc, stack, token):
         assert np.max(np.abs(dx - dref)) <= 1e-3 * np.linalg.norm(dref), f"layer {l}"
 
 
-def test_fused_matches_launch_by_launch(gemv, stack):
+@pytest.mark.parametrize("norm", [False, True])
+def test_fused_matches_launch_by_launch(gemv, stack, norm):
     """Per layer, the launch-by-launch path on the fused kernel's layer input
     picks the same experts with the same weights; outputs agree to 1e-3."""
     m = stack.m
     s = m.shape
-    r = _run_debug(stack, 3)
+    r = _run_debug(stack, 3, norm)
     ws = m.workspace(1)
     for l in range(m.L):
         x = torch.from_numpy(r["xs"][l]).to(DEV)
         xo = torch.zeros_like(x)
         ids = torch.zeros(s.top_k, dtype=torch.int32, device=DEV)
         wts = torch.zeros(s.top_k, dtype=torch.float32, device=DEV)
-        m.layer(l, x, xo, ids, wts, ws)
+        with input_norm(gemv, norm):
+            m.layer(l, x, xo, ids, wts, ws)
         assert np.array_equal(host(ids), r["ids"][l])
         assert np.array_equal(host(wts), r["wts"][l])
         d_ref = host(xo) - r["xs"][l]

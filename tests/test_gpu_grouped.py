@@ -8,7 +8,8 @@ GELU*up q8 of the kernel's own gate|up sums (teacher forcing); gate|up sums
 and layer outputs within max|d| <= 1e-3 * ||ref||_2.
 The ungrouped launch-by-launch layer (one GEMV per pair, as the reference's
 batched path, ft-model/src/lib.rs:1507-1606) must pick the same experts with
-the same weights.
+the same weights. With the input RMS norm on, its scale enters the logits
+and the gate|up sums; the same checks hold.
 """
 import numpy as np
 import pytest
@@ -46,8 +47,8 @@ def _banks(m, layer, ids):
     return gu, dn
 
 
-@pytest.mark.parametrize("B,zipf", [(16, False), (64, False), (64, True)])
-def test_grouped_layer_matches_oracle(gemv, orc, gstack, B, zipf):
+@pytest.mark.parametrize("B,zipf,norm", [(16, False, False), (64, False, False), (64, True, False), (16, True, True)])
+def test_grouped_layer_matches_oracle(gemv, orc, gstack, B, zipf, norm):
     m = gstack.m
     s = m.shape
     H, I, E, K = s.hidden, s.inter, s.n_experts, s.top_k
@@ -63,6 +64,7 @@ def test_grouped_layer_matches_oracle(gemv, orc, gstack, B, zipf):
         dgu = torch.zeros((B * K, 2 * I), dtype=torch.float32, device=DEV)
         dact = torch.zeros((B * K, I // 32, 40), dtype=torch.uint8, device=DEV)
         layer = 1
+        gemv.set_input_norm(norm)
         gs.layer(layer, x, xo, ids, wts, dgu, dact)
         X, XO, IDS, WTS = host(x), host(xo), host(ids).reshape(B, K), host(wts).reshape(B, K)
         GU, ACT = host(dgu).reshape(B, K, 2 * I), host(dact).reshape(B, K, I // 32, 40)
@@ -70,7 +72,11 @@ def test_grouped_layer_matches_oracle(gemv, orc, gstack, B, zipf):
         bias = None if m.bias is None else host(m.bias[layer])
         # routing: bit-exact per token
         for t in range(B):
-            lg = orc.router_logits(W_r, X[t], bias)
+            lg = orc.router_logits(W_r, X[t])
+            if norm:
+                lg = (lg * orc.rms_inv(X[t])).astype(np.float32)
+            if bias is not None:
+                lg = (lg + bias).astype(np.float32)
             ie, we = orc.topk_softmax(lg, K)
             assert np.array_equal(IDS[t], ie), f"token {t}"
             assert np.array_equal(WTS[t].view(np.uint32), we.view(np.uint32)), f"token {t}"
@@ -88,8 +94,11 @@ def test_grouped_layer_matches_oracle(gemv, orc, gstack, B, zipf):
                 assert np.array_equal(blk[:, 0:4].copy().view(np.float32)[:, 0].view(np.uint32), ad.view(np.uint32))
                 assert np.array_equal(blk[:, 8:40].copy().view(np.int8).ravel(), aq)
                 ref = orc.gemv_q8(gub[e].reshape(2 * I, -1), 2 * I, d8, q8, H, layout=m.layout)
+                if norm:
+                    ref = (ref * orc.rms_inv(X[t])).astype(np.float32)
                 assert np.max(np.abs(GU[t, k] - ref)) <= 1e-3 * np.linalg.norm(ref)
-            r = orc.moe_layer(X[t], W_r, gub, dnb, H, I, K, bias=bias, layout=m.layout, gelu_mode=orc.GELU_PORTABLE)
+            r = orc.moe_layer(X[t], W_r, gub, dnb, H, I, K, bias=bias, layout=m.layout, gelu_mode=orc.GELU_PORTABLE,
+                              input_norm=norm)
             assert np.array_equal(r["ids"], IDS[t])
             dref = r["x_out"] - X[t]
             assert np.max(np.abs((XO[t] - X[t]) - dref)) <= 1e-3 * np.linalg.norm(dref), f"token {t}"
@@ -107,6 +116,7 @@ def test_grouped_layer_matches_oracle(gemv, orc, gstack, B, zipf):
             assert np.max(np.abs((XO[t] - X[t]) - d2)) <= 1e-3 * np.linalg.norm(d2)
     finally:
         m.bias = saved
+        gemv.set_input_norm(0)
 
 
 def test_grouped_repeatable_and_empty(gemv, gstack):

@@ -359,10 +359,12 @@ def test_moe_layer_batched_two_layers(gemv, orc, gemma_layers):
         x = xo
 
 
-def test_moe_layer_large_expert(gemv, orc):
+@pytest.mark.parametrize("norm", [False, True])
+def test_moe_layer_large_expert(gemv, orc, norm):
     """Config 5's shape (H 4096, 8 experts of I 14336, top-2): one layer, 3 tokens
     (the batched launch), per token ids/weights exact against the oracle and the
-    output within tolerance; gate|up of the long rows within tolerance per pair."""
+    output within tolerance (with and without the input RMS norm); gate|up of
+    the long rows within tolerance per pair."""
     m = moe_synth.SyntheticMoE(gemv, moe_synth.LARGE, n_layers=1)
     s = m.shape
     H, I, E, k, B = s.hidden, s.inter, s.n_experts, s.top_k, 3
@@ -371,11 +373,15 @@ def test_moe_layer_large_expert(gemv, orc):
     ids = torch.zeros(B * k, dtype=torch.int32, device=DEV)
     wts = torch.zeros(B * k, dtype=torch.float32, device=DEV)
     xo = torch.zeros_like(x)
-    m.layer(0, x, xo, ids, wts, ws, n_seqs=B)
+    gemv.set_input_norm(norm)
+    try:
+        m.layer(0, x, xo, ids, wts, ws, n_seqs=B)
+    finally:
+        gemv.set_input_norm(0)
     xin, ids_h, wts_h, xo_h = host(x), host(ids).reshape(B, k), host(wts).reshape(B, k), host(xo)
     Wr = host(m.routers[0])
     gu_b, dn_b = _oracle_banks(m, 0, sorted(set(ids_h.ravel().tolist())))
-    refs = [orc.moe_layer(xin[t], Wr, gu_b, dn_b, H, I, k, layout=1, threads=8) for t in range(B)]
+    refs = [orc.moe_layer(xin[t], Wr, gu_b, dn_b, H, I, k, layout=1, threads=8, input_norm=norm) for t in range(B)]
     for t, ref in enumerate(refs):
         assert np.array_equal(ids_h[t], ref["ids"]) and np.array_equal(wts_h[t], ref["wts"]), t
         d_ref = ref["x_out"] - xin[t]
@@ -385,4 +391,5 @@ def test_moe_layer_large_expert(gemv, orc):
     gemv.quantize_q8(x[0], 0, q8x, H, 1)
     ygu = torch.zeros(2 * I, dtype=torch.float32, device=DEV)
     gemv.gemv_q4r_idx(m.banks, m.expert_bytes, 0, ids[:1], None, 1, q8x, 0, ygu, 2 * I, 2 * I, H)
-    assert np.max(np.abs(host(ygu) - refs[0]["y_gu"][0])) <= 1e-3 * np.linalg.norm(refs[0]["y_gu"][0])
+    ygu_h = host(ygu) * (orc.rms_inv(xin[0]) if norm else np.float32(1))
+    assert np.max(np.abs(ygu_h - refs[0]["y_gu"][0])) <= 1e-3 * np.linalg.norm(refs[0]["y_gu"][0])

@@ -447,6 +447,58 @@ def test_moe_layer_stages_match_f64_composition(orc):
     assert np.array_equal(r2["x_out"], r["x_out"])
 
 
+def test_rms_inv_closed_forms(orc):
+    """The input RMS norm's scale: f64 closed form 1/sqrt(mean(x^2) + 1e-6) to
+    f32 accuracy; exact on a constant power-of-two vector (every partial sum
+    exact); and its sum of squares is the R-order router dot of x with itself."""
+    rng = np.random.default_rng(21)
+    for H in (128, 2816, 4096):
+        x = (rng.standard_normal(H) * rng.uniform(0.1, 30)).astype(np.float32)
+        ir = orc.rms_inv(x)
+        ref = 1.0 / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-6)
+        assert abs(float(ir) - ref) <= 4e-7 * ref, H
+        ss = orc.router_logits(x[None, :], x)[0]
+        assert ir == np.float32(1.0) / np.sqrt(ss / np.float32(H) + np.float32(1e-6))
+    x = np.full(2816, 0.25, np.float32)  # ss = 176 exactly, mean = 1/16
+    assert orc.rms_inv(x) == np.float32(1.0) / np.sqrt(np.float32(0.0625) + np.float32(1e-6))
+    assert np.isclose(orc.rms_inv(np.zeros(256, np.float32)), 1000.0, rtol=1e-6)
+
+
+def test_moe_layer_input_norm_is_layer_on_rmsnorm_x(orc):
+    """input_norm runs the layer on rmsnorm(x): against the plain layer on
+    u = x * inv_r (u quantized itself), the routing is the same and the MoE
+    update agrees to rounding; scaling x by any c > 0 leaves the update of the
+    normed layer unchanged up to rounding (the norm removes the scale); and
+    the logits are the plain logits times inv_r, bit for bit."""
+    H, I, E, k = 256, 64, 16, 4
+    rng = np.random.default_rng(17)
+    x = (rng.standard_normal(H) * 3.0).astype(np.float32)
+    W_r = (rng.standard_normal((E, H)) * 0.1).astype(np.float32)
+    gu = {e: orc.repack_q4r(orc.quantize_row((rng.standard_normal((2 * I, H)) * 0.02).astype(np.float32)), H)
+          for e in range(E)}
+    dn = {e: orc.repack_q4r(orc.quantize_row((rng.standard_normal((H, I)) * 0.02).astype(np.float32)), I)
+          for e in range(E)}
+    ir = orc.rms_inv(x)
+    rn = orc.moe_layer(x, W_r, gu, dn, H, I, k, layout=1, input_norm=True)
+    assert np.array_equal(rn["logits"].view(np.uint32), (orc.router_logits(W_r, x) * ir).astype(np.float32).view(np.uint32))
+    u = (x * ir).astype(np.float32)
+    ru = orc.moe_layer(u, W_r, gu, dn, H, I, k, layout=1)
+    assert np.array_equal(rn["ids"], ru["ids"])
+    assert np.allclose(rn["wts"], ru["wts"], rtol=1e-5, atol=0)
+    dn_ = rn["x_out"].astype(np.float64) - x
+    du = ru["x_out"].astype(np.float64) - u
+    assert np.max(np.abs(dn_ - du)) <= 2e-2 * np.linalg.norm(du)
+    for c in (0.125, 7.0):
+        rc = orc.moe_layer((x * np.float32(c)).astype(np.float32), W_r, gu, dn, H, I, k, layout=1, input_norm=True)
+        assert np.array_equal(rc["ids"], rn["ids"])
+        dc = rc["x_out"].astype(np.float64) - (x * np.float32(c))
+        assert np.max(np.abs(dc - dn_)) <= 2e-2 * np.linalg.norm(dn_)
+    # off: identical bits to the layer without the argument
+    r0 = orc.moe_layer(x, W_r, gu, dn, H, I, k, layout=1, input_norm=False)
+    r1 = orc.moe_layer(x, W_r, gu, dn, H, I, k, layout=1)
+    assert np.array_equal(r0["x_out"].view(np.uint32), r1["x_out"].view(np.uint32))
+
+
 def test_moe_layer_missing_expert_raises(orc):
     H, I, E, k = 128, 32, 4, 2
     x = np.ones(H, np.float32)
