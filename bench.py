@@ -56,8 +56,11 @@ def parse():
     ap.add_argument("--config", choices=list(CONFIGS), default="gemma30",
                     help="gemma30 = the headline (cfg2); zipf = cfg3; batch16/batch64 = cfg4; large1/large32 = cfg5")
     ap.add_argument("--path", choices=["auto", "fused", "grouped", "multikernel"], default="auto",
-                    help="auto: fused whole-stack kernel at batch 1 of the Gemma shape, grouped layers for batched "
-                         "Gemma, launch-by-launch layers for the large-expert shape")
+                    help="auto: fused whole-stack kernel at batch 1 of the Gemma shape, grouped layers (dot4 and "
+                         "int8 MFMA kernels) for batched decode, launch-by-launch layers for the large-expert "
+                         "shape at batch 1")
+    ap.add_argument("--mfma-min", type=int, default=16,
+                    help="grouped path: experts with at least this many tokens take the int8 MFMA kernels")
     ap.add_argument("--layers", type=int, default=0, help="0 = the config's layer count")
     ap.add_argument("--prefetch", type=int, choices=[0, 1], default=1,
                     help="fused path: stream the early-routed experts of the next layer ahead (1) or not (0)")
@@ -216,14 +219,15 @@ def main():
     shape = getattr(moe_synth, shape_name)
     path = args.path
     if path == "auto":
-        path = "multikernel" if shape is moe_synth.LARGE else ("fused" if B == 1 else "grouped")
+        path = "grouped" if B > 1 else ("fused" if shape is moe_synth.GEMMA else "multikernel")
     if path == "fused" and B != 1:
         sys.exit("the fused whole-stack kernel decodes one token per launch: use --path grouped or multikernel")
-    if path in ("fused", "grouped") and shape is not moe_synth.GEMMA:
-        sys.exit(f"--path {path} is built for the Gemma shape only: use --path multikernel")
+    if path == "fused" and shape is not moe_synth.GEMMA:
+        sys.exit("--path fused is built for the Gemma shape only: use --path grouped or multikernel")
 
     g = ft_hip.Q4Gemv(0)
     g.set_input_norm(args.input_norm)
+    g.set_grouped_mfma_min(args.mfma_min)
     t0 = time.time()
 
     def progress(l):
@@ -252,7 +256,7 @@ def main():
                 stack.run(hidden[t, 0], outs[t, 0])
     else:
         if path == "grouped":
-            gstack = moe_synth.GroupedStack(moe_synth.FusedStack(model), B)
+            gstack = moe_synth.GroupedStack(moe_synth.FusedStack(model, workspace=False), B)
 
             def layer(l, src, dst, ids, wts, stream):
                 gstack.layer(l, src, dst, ids, wts, stream=stream)
@@ -368,6 +372,7 @@ def main():
                    "hidden": H, "inter": I, "experts": E, "top_k": k, "layers": model.L, "batch": B,
                    "path": path, "prefetch": bool(args.prefetch) if path == "fused" else None,
                    "input_norm": bool(args.input_norm),
+                   "mfma_min_tokens": args.mfma_min if path == "grouped" else None,
                    "unique_experts_per_layer": round(uniq, 2)},
         "achieved_GBps": round(gbps, 1),
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),

@@ -35,7 +35,7 @@ constexpr int MAX_PAIRS = 4096;
 struct GroupWs {
     float* logits;      // [B][E]
     uint8_t* q8x;       // [B][H/32][40]
-    int32_t* meta;      // [0] active experts; [1..] gexp[E], gstart[E], gcount[E]
+    int32_t* meta;      // [0] active experts; [1..] gexp[E], gstart[E], gcount[E]; [1+3E] MFMA groups
     int32_t* plist;     // [P] pairs grouped by expert
     int32_t* ppos;      // [P] scratch
     uint8_t* q8a;       // [P][I/32][40]
@@ -52,7 +52,7 @@ GroupWs group_ws(void* base, int64_t B, int64_t H, int64_t I, int64_t E, int64_t
     uint8_t* p = (uint8_t*)base;
     w.logits = (float*)(p + off); off += up(sizeof(float) * B * E);
     w.q8x = p + off; off += up((size_t)B * (H / 32) * Q8_BLK);
-    w.meta = (int32_t*)(p + off); off += up(sizeof(int32_t) * (1 + 3 * E));
+    w.meta = (int32_t*)(p + off); off += up(sizeof(int32_t) * (2 + 3 * E));
     w.plist = (int32_t*)(p + off); off += up(sizeof(int32_t) * P);
     w.ppos = (int32_t*)(p + off); off += up(sizeof(int32_t) * P);
     w.q8a = p + off; off += up((size_t)P * (I / 32) * Q8_BLK);
@@ -62,14 +62,39 @@ GroupWs group_ws(void* base, int64_t B, int64_t H, int64_t I, int64_t E, int64_t
     return w;
 }
 
+// Global -> LDS copy of n 32-bit items: item i is ld(i), stored by st(i, v).
+// Each thread issues up to R loads before its first store, so the copy
+// costs ceil(n / (R * GT)) load latencies rather than ceil(n / GT).
+template <int R, typename Ld, typename St>
+__device__ __forceinline__ void stage(int n, Ld ld, St st) {
+    const int t = threadIdx.x;
+    for (int base = 0; base < n; base += R * GT) {
+        uint32_t v[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int i = base + r * GT + t;
+            v[r] = i < n ? ld(i) : 0u;
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int i = base + r * GT + t;
+            if (i < n) st(i, v[r]);
+        }
+    }
+}
+
 // Pairs p = t*K + k grouped by expert ids[p]. The order inside a group does
 // not matter: every (row, token) dot is independent and outputs are written
 // to the pair's own slot, so results are the same for any order.
-__global__ __launch_bounds__(1024) void k_group_pairs(const int32_t* ids, int P, int E, int32_t* meta, int32_t* plist,
-                                                      int32_t* ppos) {
+// Groups are numbered with the experts of >= n_mfma tokens first (meta[1 +
+// 3E] of them, for the MFMA kernels), then the others (for the dot4
+// kernels), each in expert order.
+__global__ __launch_bounds__(1024) void k_group_pairs(const int32_t* ids, int P, int E, int n_mfma, int32_t* meta,
+                                                      int32_t* plist, int32_t* ppos) {
     __shared__ int cnt[1024];
     __shared__ int scan[1024];
     __shared__ int act[1024];
+    __shared__ int big[1024];
     const int t = threadIdx.x;
     for (int e = t; e < E; e += 1024) cnt[e] = 0;
     __syncthreads();
@@ -82,22 +107,28 @@ __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t* ids, int P,
     const int c = t < E ? cnt[t] : 0;
     scan[t] = c;
     act[t] = c > 0;
+    big[t] = c > 0 && c >= n_mfma;
     __syncthreads();
     for (int d = 1; d < 1024; d <<= 1) {
         const int a = t >= d ? scan[t - d] : 0;
         const int b = t >= d ? act[t - d] : 0;
+        const int f = t >= d ? big[t - d] : 0;
         __syncthreads();
         scan[t] += a;
         act[t] += b;
+        big[t] += f;
         __syncthreads();
     }
     if (t < E && c > 0) {
-        const int g = act[t] - 1;
+        const int g = c >= n_mfma ? big[t] - 1 : big[1023] + (act[t] - big[t]) - 1;
         meta[1 + g] = t;                 // gexp
         meta[1 + E + g] = scan[t] - c;   // gstart
         meta[1 + 2 * E + g] = c;         // gcount
     }
-    if (t == 0) meta[0] = act[1023];
+    if (t == 0) {
+        meta[0] = act[1023];
+        meta[1 + 3 * E] = big[1023];
+    }
     __syncthreads();
     for (int p = t; p < P; p += 1024) {
         const int e = min(max(ids[p], 0), E - 1);
@@ -113,12 +144,13 @@ template <int BPW>
 __global__ __launch_bounds__(GT, 1) void k_grouped_gu(const uint8_t* bank, int64_t expert_bytes, const int32_t* meta,
                                                       const int32_t* plist, const uint8_t* q8x, uint8_t* q8a,
                                                       float* dbg_gu, const float* in_scale, int H, int I, int E,
-                                                      int K) {
+                                                      int K, int n_mfma) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int nb = H >> 5, nbj = I >> 5;
-    const int j = blockIdx.x, g = blockIdx.y;
+    const int j = blockIdx.x, g = blockIdx.y + meta[1 + 3 * E];  // after the MFMA kernels' groups
     if (g >= meta[0]) return;
     const int e = meta[1 + g], s0 = meta[1 + E + g], n = meta[1 + 2 * E + g];
+    if (n >= n_mfma) return;
     // LDS: x q8 of NT tokens as [NT][nb][8 words] qs + [NT][nb] (d, qsum) pairs;
     // wave partial sums [GW][NT][64]; row sums [NT][64]; act [NT][32]
     uint4* xq = reinterpret_cast<uint4*>(lds);
@@ -140,13 +172,18 @@ __global__ __launch_bounds__(GT, 1) void k_grouped_gu(const uint8_t* bank, int64
     for (int c0 = 0; c0 < n; c0 += NT) {
         const int nt = min(NT, n - c0);
         __syncthreads();  // the previous chunk's LDS is consumed
-        for (int i = t; i < nt * nb * 10; i += GT) {  // stage x q8 of this chunk's tokens
-            const int tt = i / (nb * 10), rem = i - tt * nb * 10, b = rem / 10, wd = rem - b * 10;
-            const int tok = plist[s0 + c0 + tt] / K;
-            const uint32_t v = reinterpret_cast<const uint32_t*>(q8x + ((int64_t)tok * nb + b) * Q8_BLK)[wd];
-            if (wd >= 2) reinterpret_cast<uint32_t*>(xq)[(tt * nb + b) * 8 + (wd - 2)] = v;
-            else reinterpret_cast<uint32_t*>(xp)[(tt * nb + b) * 2 + wd] = v;
-        }
+        stage<16>(  // x q8 of this chunk's tokens
+            nt * nb * 10,
+            [&](int i) {
+                const int tt = i / (nb * 10), rem = i - tt * nb * 10;
+                const int tok = plist[s0 + c0 + tt] / K;
+                return reinterpret_cast<const uint32_t*>(q8x + (int64_t)tok * nb * Q8_BLK)[rem];
+            },
+            [&](int i, uint32_t v) {
+                const int tt = i / (nb * 10), rem = i - tt * nb * 10, b = rem / 10, wd = rem - b * 10;
+                if (wd >= 2) reinterpret_cast<uint32_t*>(xq)[(tt * nb + b) * 8 + (wd - 2)] = v;
+                else reinterpret_cast<uint32_t*>(xp)[(tt * nb + b) * 2 + wd] = v;
+            });
         __syncthreads();
         for (int tt = 0; tt < nt; ++tt) {  // one token at a time: its BPW blocks' LDS reads in one batch
             float acc = 0.0f;
@@ -194,12 +231,13 @@ __global__ __launch_bounds__(GT, 1) void k_grouped_gu(const uint8_t* bank, int64
 template <int DB>
 __global__ __launch_bounds__(GT, 1) void k_grouped_down(const uint8_t* bank, int64_t expert_bytes, int64_t gu_bytes,
                                                         const int32_t* meta, const int32_t* plist, const uint8_t* q8a,
-                                                        float* ydn, int H, int I, int E) {
+                                                        float* ydn, int H, int I, int E, int n_mfma) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int nbj = I >> 5;
-    const int u = blockIdx.x, g = blockIdx.y;
+    const int u = blockIdx.x, g = blockIdx.y + meta[1 + 3 * E];  // after the MFMA kernels' groups
     if (g >= meta[0]) return;
     const int e = meta[1 + g], s0 = meta[1 + E + g], n = meta[1 + 2 * E + g];
+    if (n >= n_mfma) return;
     uint4* aq = reinterpret_cast<uint4*>(lds);                  // [NTD][nbj][2 uint4]
     int2* ap = reinterpret_cast<int2*>(lds + NTD * nbj * 32);   // [NTD][nbj]
     const int t = threadIdx.x, wave = t >> 6, s4 = t & 3, rr = (t >> 2) & 15;
@@ -222,13 +260,18 @@ __global__ __launch_bounds__(GT, 1) void k_grouped_down(const uint8_t* bank, int
     for (int c0 = 0; c0 < n; c0 += NTD) {
         const int nt = min(NTD, n - c0);
         __syncthreads();
-        for (int i = t; i < nt * nbj * 10; i += GT) {
-            const int tt = i / (nbj * 10), rem = i - tt * nbj * 10, b = rem / 10, wd = rem - b * 10;
-            const int p = plist[s0 + c0 + tt];
-            const uint32_t v = reinterpret_cast<const uint32_t*>(q8a + ((int64_t)p * nbj + b) * Q8_BLK)[wd];
-            if (wd >= 2) reinterpret_cast<uint32_t*>(aq)[(tt * nbj + b) * 8 + (wd - 2)] = v;
-            else reinterpret_cast<uint32_t*>(ap)[(tt * nbj + b) * 2 + wd] = v;
-        }
+        stage<8>(  // act q8 of this chunk's pairs
+            nt * nbj * 10,
+            [&](int i) {
+                const int tt = i / (nbj * 10), rem = i - tt * nbj * 10;
+                const int p = plist[s0 + c0 + tt];
+                return reinterpret_cast<const uint32_t*>(q8a + (int64_t)p * nbj * Q8_BLK)[rem];
+            },
+            [&](int i, uint32_t v) {
+                const int tt = i / (nbj * 10), rem = i - tt * nbj * 10, b = rem / 10, wd = rem - b * 10;
+                if (wd >= 2) reinterpret_cast<uint32_t*>(aq)[(tt * nbj + b) * 8 + (wd - 2)] = v;
+                else reinterpret_cast<uint32_t*>(ap)[(tt * nbj + b) * 2 + wd] = v;
+            });
         __syncthreads();
         for (int tt = 0; tt < nt; ++tt) {
             float acc = 0.0f;
@@ -251,6 +294,285 @@ __global__ __launch_bounds__(GT, 1) void k_grouped_down(const uint8_t* bank, int
     }
 }
 
+// ---------------------------------------------------------------------------
+// int8 MFMA tile path, for groups of at least n_min tokens.
+//
+// v_mfma_i32_16x16x32_i8: D[16 rows][16 tokens] += A[16 rows][32] *
+// B[32][16 tokens]; lane l holds A row l%16 and B column l%16 at k =
+// 8*(l/16)..+7, and D rows 4*(l/16)..+3 of column l%16. One MFMA is one q4_0
+// block (32 weights) of 16 rows against the q8 blocks of 16 tokens. The 32 k
+// of a block are ordered so that lane group g = l/16 takes elements
+// 4g..4g+3 and 16+4g..16+4g+3: for the weights the low and the high nibbles
+// of qs word g (one dword, two masks), for the activations q8 words g and
+// 4+g. The nibbles enter unsigned (0..15) and the accumulator starts at
+// -8 * qsum of the token's block, so D is exactly the block's int32 dot
+// sum (q-8)*q8 (ft-core/src/q4_0.rs:105-118). Per (row, token) the blocks
+// then accumulate as acc = fma(float(D), d4 * d8, acc), in block order.
+// ---------------------------------------------------------------------------
+typedef int v4i __attribute__((ext_vector_type(4)));
+constexpr int MT = 16;  // tokens per MFMA tile
+
+struct ActOp {
+    long b;    // B operand: q8 words g and 4+g
+    float d;   // the block's d
+    int qsum;  // the block's sum of q
+};
+
+// Raw buffer loads: a per-lane 32-bit offset plus a uniform one (scalar
+// register or immediate), so per-block addresses cost no vector registers;
+// an offset past num_records reads 0.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint32_t buf_ld(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+
+// The q8 block at byte soff + vd of buffer r ({d, qsum, qs[32]}) for lane
+// group g (vq = vd + 8 + 4g); zeros if !ok (loads unconditional, then selects).
+__device__ __forceinline__ ActOp act_op(__amdgpu_buffer_rsrc_t r, uint32_t vq, uint32_t vd, uint32_t soff, bool ok) {
+    const uint32_t lo = buf_ld(r, vq, soff), hi = buf_ld(r, vq + 16, soff);
+    const u32x2 dq = __builtin_amdgcn_raw_buffer_load_b64(r, vd, soff, 0);
+    ActOp a;
+    a.b = (long)(((uint64_t)(ok ? hi : 0u) << 32) | (ok ? lo : 0u));
+    a.d = ok ? __uint_as_float(dq.x) : 0.0f;
+    a.qsum = ok ? (int)dq.y : 0;
+    return a;
+}
+
+// A operand from qs word g of a row's block: low nibbles, then high nibbles.
+__device__ __forceinline__ long nib_op(uint32_t w) {
+    return (long)(((uint64_t)((w >> 4) & 0x0F0F0F0Fu) << 32) | (w & 0x0F0F0F0Fu));
+}
+
+__device__ __forceinline__ v4i c_init(int qsum) {
+    const int c = -8 * qsum;
+    const v4i v = {c, c, c, c};
+    return v;
+}
+
+// Four f16 scales (8 bytes) at p, widened.
+__device__ __forceinline__ void scales4(const uint16_t* p, float (&sc)[4]) {
+    const uint2 s2 = *reinterpret_cast<const uint2*>(p);
+    sc[0] = h2f((uint16_t)(s2.x & 0xFFFF));
+    sc[1] = h2f((uint16_t)(s2.x >> 16));
+    sc[2] = h2f((uint16_t)(s2.y & 0xFFFF));
+    sc[3] = h2f((uint16_t)(s2.y >> 16));
+}
+
+// Gate|up tile j (64 rows: gate rows 32j.., up rows I+32j..) of active expert
+// g for its tokens, 16 at a time. Wave w takes blocks [w*BPW, (w+1)*BPW) of
+// the 64 rows as four 16-row MFMA tiles (qs dwords loaded per token tile,
+// every load of a tile issued before the first MFMA; the tile's scales in
+// LDS); the 8 wave partials of a (row, token) are summed in wave order;
+// then, as k_grouped_gu, the input-norm scale, GELU*up and the q8 of act
+// block j per token.
+template <int BPW>
+__global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* bank, int64_t expert_bytes, const int32_t* meta,
+                                                   const int32_t* plist, const uint8_t* q8x, uint32_t q8x_bytes,
+                                                   uint8_t* q8a, float* dbg_gu, const float* in_scale, int H, int I,
+                                                   int E, int K, int n_min) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int nb = H >> 5, nbj = I >> 5;
+    const int j = blockIdx.x, g = blockIdx.y;
+    if (g >= meta[1 + 3 * E]) return;  // groups of >= n_min tokens come first
+    const int e = meta[1 + g], s0 = meta[1 + E + g], n = meta[1 + 2 * E + g];
+    if (n < n_min) return;
+    // LDS: the tile's scales [nb][64] f16; wave partials [GW][64][MT]; sums
+    // [MT][64]; act [MT][32]; act q8 [MT][10]
+    uint16_t* scl = reinterpret_cast<uint16_t*>(lds);
+    float* red = reinterpret_cast<float*>(lds + nb * 128);
+    float* rows = red + GW * 64 * MT;
+    float* actv = rows + MT * 64;
+    uint32_t* ablk = reinterpret_cast<uint32_t*>(actv + MT * 32);
+    // the wave index in a scalar register: buffer offsets built from it stay uniform
+    const int t = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(t >> 6), li = t & 15, lg = (t >> 4) & 3;
+    const int b0 = wave * BPW;
+    const uint8_t* T = bank + (int64_t)e * expert_bytes + (int64_t)j * nb * 1152;
+    // qs of the tile: lane offset li*16 + 4*lg (row li of an MFMA tile, word
+    // lg), uniform offset block*1024 + m*256
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(T + nb * 128, (uint32_t)nb * 1024);
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(q8x, q8x_bytes);
+    const uint32_t vw = li * 16 + 4 * lg;
+    for (int c0 = 0; c0 < n; c0 += MT) {
+        const int nt = min(MT, n - c0);
+        const int p = plist[s0 + c0 + min(li, nt - 1)];
+        const uint32_t vd = (uint32_t)((p / K) * nb + b0) * Q8_BLK, vq = vd + 8 + 4 * lg;
+        // blocks in NBB-block batches, the next batch's loads issued before
+        // the current batch's MFMAs (two register buffers)
+        constexpr int NBB = BPW > 12 ? 4 : BPW, NBATCH = (BPW + NBB - 1) / NBB;
+        uint32_t aw[2][NBB][4];
+        ActOp av[2][NBB];
+        auto load = [&](int k, int buf) __attribute__((always_inline)) {
+#pragma unroll
+            for (int b = 0; b < NBB; ++b) {
+                const int bb = min(k * NBB + b, BPW - 1);
+#pragma unroll
+                for (int m = 0; m < 4; ++m) aw[buf][b][m] = buf_ld(rw, vw + m * 256, (b0 + bb) * 1024);
+                av[buf][b] = act_op(rx, vq, vd, bb * Q8_BLK, li < nt);
+            }
+        };
+        float acc[4][4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[m][v] = 0.0f;
+        load(0, 0);
+        if (c0 == 0) {  // the tile's scales to LDS, with the first batch in flight
+            stage<8>(
+                nb * 32, [&](int i) { return reinterpret_cast<const uint32_t*>(T)[i]; },
+                [&](int i, uint32_t v) { reinterpret_cast<uint32_t*>(scl)[i] = v; });
+            __syncthreads();
+        }
+#pragma unroll
+        for (int k = 0; k < NBATCH; ++k) {
+            if (k + 1 < NBATCH) load(k + 1, (k + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int b = 0; b < NBB; ++b) {
+                if (k * NBB + b < BPW) {
+                    const ActOp a = av[k & 1][b];
+                    const v4i c = c_init(a.qsum);
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) {
+                        const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib_op(aw[k & 1][b][m]), a.b, c, 0, 0, 0);
+                        float sc[4];
+                        scales4(scl + (b0 + k * NBB + b) * 64 + 16 * m + 4 * lg, sc);
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) acc[m][v] = fmaf((float)d[v], sc[v] * a.d, acc[m][v]);
+                    }
+                    // one block's MFMA results live at a time
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) red[(wave * 64 + 16 * m + 4 * lg + v) * MT + li] = acc[m][v];
+        __syncthreads();
+        for (int i = t; i < nt * 64; i += GT) {  // (token, row) sums over the waves, in wave order
+            const int tt = i >> 6, rr = i & 63;
+            float sv = 0.0f;
+#pragma unroll
+            for (int v = 0; v < GW; ++v) sv = sv + red[(v * 64 + rr) * MT + tt];
+            const int pp = plist[s0 + c0 + tt];
+            if (in_scale) sv = sv * in_scale[pp / K];
+            rows[tt * 64 + rr] = sv;
+            if (dbg_gu) dbg_gu[(int64_t)pp * 2 * I + (rr < 32 ? j * 32 + rr : I + j * 32 + (rr - 32))] = sv;
+        }
+        __syncthreads();
+        for (int i = t; i < nt * 32; i += GT) {
+            const int tt = i >> 5, cc = i & 31;
+            actv[tt * 32 + cc] = gelu_tanh(rows[tt * 64 + cc]) * rows[tt * 64 + 32 + cc];
+        }
+        __syncthreads();
+        if (t < 4 * nt) quantize_block_quad(actv + (t >> 2) * 32, t & 3, ablk + (t >> 2) * 10);
+        __syncthreads();
+        for (int i = t; i < nt * 10; i += GT) {
+            const int tt = i / 10, wd = i - tt * 10;
+            const int pp = plist[s0 + c0 + tt];
+            reinterpret_cast<uint32_t*>(q8a + ((int64_t)pp * nbj + j) * Q8_BLK)[wd] = ablk[tt * 10 + wd];
+        }
+    }
+}
+
+// Down rows of active expert g for its tokens, 16 at a time. The workgroup
+// takes GW/KS 16-row down tiles; wave w works on tile u*(GW/KS) + w/KS, K
+// slice w%KS (blocks [s*BW, s*BW+BW) below nbj); the KS slice partials of a
+// (row, token) are summed in slice order into y[pair][row].
+template <int KS, int BW>
+__global__ __launch_bounds__(GT, 1) void k_mfma_down(const uint8_t* bank, int64_t expert_bytes, int64_t gu_bytes,
+                                                     const int32_t* meta, const int32_t* plist, const uint8_t* q8a,
+                                                     uint32_t q8a_bytes, float* ydn, int H, int I, int E, int n_min) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int TPW = GW / KS;  // tiles per workgroup
+    const int nbj = I >> 5, dn_tile = nbj * 288;
+    const int u = blockIdx.x, g = blockIdx.y;
+    if (g >= meta[1 + 3 * E]) return;  // groups of >= n_min tokens come first
+    const int e = meta[1 + g], s0 = meta[1 + E + g], n = meta[1 + 2 * E + g];
+    if (n < n_min) return;
+    // LDS: the tiles' scales [TPW][nbj][16] f16; slice partials [GW][16][MT]
+    uint16_t* scl = reinterpret_cast<uint16_t*>(lds);
+    float* red = reinterpret_cast<float*>(lds + TPW * nbj * 32);
+    const int t = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(t >> 6), li = t & 15, lg = (t >> 4) & 3;
+    const int tl = wave / KS, sl = wave % KS, bs = sl * BW;
+    const int tile = u * TPW + tl;
+    const uint8_t* Dt = bank + (int64_t)e * expert_bytes + gu_bytes + (int64_t)tile * dn_tile;
+    const uint16_t* st = scl + tl * nbj * 16;
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(Dt + nbj * 32, (uint32_t)nbj * 256);  // the tile's qs
+    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(q8a, q8a_bytes);
+    const uint32_t vw = li * 16 + 4 * lg;
+    for (int c0 = 0; c0 < n; c0 += MT) {
+        const int nt = min(MT, n - c0);
+        const int p = plist[s0 + c0 + min(li, nt - 1)];
+        const uint32_t vd = (uint32_t)p * nbj * Q8_BLK, vq = vd + 8 + 4 * lg;
+        // blocks in NBB-block batches, the next batch's loads issued before
+        // the current batch's MFMAs (two register buffers)
+        constexpr int NBB = BW > 32 ? 16 : BW, NBATCH = BW / NBB;
+        uint32_t aw[2][NBB];
+        ActOp av[2][NBB];
+        auto load = [&](int k, int buf) __attribute__((always_inline)) {
+#pragma unroll
+            for (int b = 0; b < NBB; ++b) {
+                const int bb = min(bs + k * NBB + b, nbj - 1);
+                aw[buf][b] = buf_ld(rw, vw, bb * 256);
+                av[buf][b] = act_op(ra, vq, vd, bb * Q8_BLK, li < nt);
+            }
+        };
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        load(0, 0);
+        if (c0 == 0) {  // the tiles' scales to LDS, with the first batch in flight
+            stage<8>(
+                TPW * nbj * 8,
+                [&](int i) {
+                    const int k = i / (nbj * 8), r = i - k * nbj * 8;
+                    return reinterpret_cast<const uint32_t*>(bank + (int64_t)e * expert_bytes + gu_bytes +
+                                                             (int64_t)(u * TPW + k) * dn_tile)[r];
+                },
+                [&](int i, uint32_t v) { reinterpret_cast<uint32_t*>(scl)[i] = v; });
+            __syncthreads();
+        }
+#pragma unroll
+        for (int k = 0; k < NBATCH; ++k) {
+            if (bs + k * NBB >= nbj) break;  // uniform: this slice ends here
+            if (k + 1 < NBATCH && bs + (k + 1) * NBB < nbj) load(k + 1, (k + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int b = 0; b < NBB; ++b) {
+                if (bs + k * NBB + b < nbj) {  // uniform
+                    const ActOp a = av[k & 1][b];
+                    const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib_op(aw[k & 1][b]), a.b, c_init(a.qsum), 0, 0, 0);
+                    float sc[4];
+                    scales4(st + (bs + k * NBB + b) * 16 + 4 * lg, sc);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) acc[v] = fmaf((float)d[v], sc[v] * a.d, acc[v]);
+                }
+                __builtin_amdgcn_sched_barrier(0);  // one block's MFMA result live at a time
+            }
+        }
+        if (KS == 1) {
+            if (li < nt) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) ydn[(int64_t)p * H + tile * 16 + 4 * lg + v] = acc[v];
+            }
+        } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) red[(wave * 16 + 4 * lg + v) * MT + li] = acc[v];
+            __syncthreads();
+            for (int i = t; i < TPW * 16 * nt; i += GT) {  // (tile, row, token) sums over the slices in order
+                const int k = i / (16 * nt), r = (i / nt) % 16, tt = i % nt;
+                float sv = 0.0f;
+#pragma unroll
+                for (int q = 0; q < KS; ++q) sv = sv + red[((k * KS + q) * 16 + r) * MT + tt];
+                ydn[(int64_t)plist[s0 + c0 + tt] * H + (u * TPW + k) * 16 + r] = sv;
+            }
+            __syncthreads();
+        }
+    }
+}
+
 // x_out[t] = x[t] + sum_k (y[t*K+k] * w[t*K+k]), slots in order
 // (ft-model/src/lib.rs:1634-1646).
 __global__ __launch_bounds__(256) void k_grouped_combine(const float* y, const float* wts, const float* x, float* out,
@@ -268,8 +590,8 @@ __global__ __launch_bounds__(256) void k_grouped_combine(const float* y, const f
 int check_grouped_shape(const char* nm, int64_t B, int64_t H, int64_t I, int64_t E, int64_t K) {
     if (H != 2816 && H != 4096)
         return fail(FT_HIP_E_SHAPE, "%s: hidden=%lld: built for hidden 2816 and 4096", nm, (long long)H);
-    if (I <= 0 || I % 32 || I / 32 > 32)
-        return fail(FT_HIP_E_SHAPE, "%s: inter=%lld must be a multiple of 32 in [32, 1024]", nm, (long long)I);
+    if (I <= 0 || I % 32 || I / 32 > 512)
+        return fail(FT_HIP_E_SHAPE, "%s: inter=%lld must be a multiple of 32 in [32, 16384]", nm, (long long)I);
     if (E <= 0 || E > 1024) return fail(FT_HIP_E_SHAPE, "%s: n_experts not in [1, 1024]", nm);
     if (K <= 0 || K > 32 || K > E) return fail(FT_HIP_E_SHAPE, "%s: top_k not in [1, min(32, n_experts)]", nm);
     if (B < 0 || B * K > MAX_PAIRS) return fail(FT_HIP_E_SHAPE, "%s: n_seqs*top_k must be <= %d", nm, MAX_PAIRS);
@@ -310,27 +632,68 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
         return rc;
     if ((rc = ft_hip_topk_router(ctx, stream, w.logits, expert_scale, ids, wts, n_experts, top_k, n_seqs))) return rc;
     if ((rc = ft_hip_quantize_q8(ctx, stream, x, hidden, w.q8x, hidden, n_seqs))) return rc;
-    hipLaunchKernelGGL(k_group_pairs, dim3(1), dim3(1024), 0, s, (const int32_t*)ids, P, E, w.meta, w.plist, w.ppos);
+    // groups of >= n_mfma tokens take the MFMA tile kernels, the others the
+    // dot4 kernels; rows longer than 32 blocks (I > 1024) only the former
+    const int n_mfma = nbj > 32 ? 1 : std::max(1, ctx->grouped_mfma_min);
+    hipLaunchKernelGGL(k_group_pairs, dim3(1), dim3(1024), 0, s, (const int32_t*)ids, P, E, n_mfma, w.meta, w.plist,
+                       w.ppos);
     if ((rc = launch_status("moe_layer_grouped/group"))) return rc;
     const int gmax = std::min(E, P);
-    const size_t lds_gu = (size_t)NT * nb * 40 + sizeof(float) * (GW * NT * 64 + NT * 64 + NT * 32) + 4 * NT * 10;
-    if (H == 2816)
-        hipLaunchKernelGGL(k_grouped_gu<11>, dim3(nbj, gmax), dim3(GT), lds_gu, s, (const uint8_t*)bank, eb,
-                           (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8x, w.q8a, dbg_gu, inv, H, I, E, K);
-    else
-        hipLaunchKernelGGL(k_grouped_gu<16>, dim3(nbj, gmax), dim3(GT), lds_gu, s, (const uint8_t*)bank, eb,
-                           (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8x, w.q8a, dbg_gu, inv, H, I, E, K);
-    if ((rc = launch_status("moe_layer_grouped/gate_up"))) return rc;
+    const int gbig = std::min(gmax, P / n_mfma);  // at most this many groups of >= n_mfma tokens
+    const bool dot4 = n_mfma > 1, mfma = n_seqs >= n_mfma;
+    const uint32_t q8x_bytes = (uint32_t)(n_seqs * nb * Q8_BLK), q8a_bytes = (uint32_t)((int64_t)P * nbj * Q8_BLK);
+    if (dot4) {
+        const size_t lds_gu = (size_t)NT * nb * 40 + sizeof(float) * (GW * NT * 64 + NT * 64 + NT * 32) + 4 * NT * 10;
+        if (H == 2816)
+            hipLaunchKernelGGL(k_grouped_gu<11>, dim3(nbj, gmax), dim3(GT), lds_gu, s, (const uint8_t*)bank, eb,
+                               (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8x, w.q8a, dbg_gu, inv,
+                               H, I, E, K, n_mfma);
+        else
+            hipLaunchKernelGGL(k_grouped_gu<16>, dim3(nbj, gmax), dim3(GT), lds_gu, s, (const uint8_t*)bank, eb,
+                               (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8x, w.q8a, dbg_gu, inv,
+                               H, I, E, K, n_mfma);
+        if ((rc = launch_status("moe_layer_grouped/gate_up"))) return rc;
+    }
+    if (mfma) {
+        const size_t lds_mg = (size_t)nb * 128 + sizeof(float) * (GW * 64 * MT + MT * 64 + MT * 32) + 4 * MT * 10;
+        if (H == 2816)
+            hipLaunchKernelGGL(k_mfma_gu<11>, dim3(nbj, gbig), dim3(GT), lds_mg, s, (const uint8_t*)bank, eb,
+                               (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8x, q8x_bytes, w.q8a,
+                               dbg_gu, inv, H, I, E, K, n_mfma);
+        else
+            hipLaunchKernelGGL(k_mfma_gu<16>, dim3(nbj, gbig), dim3(GT), lds_mg, s, (const uint8_t*)bank, eb,
+                               (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8x, q8x_bytes, w.q8a,
+                               dbg_gu, inv, H, I, E, K, n_mfma);
+        if ((rc = launch_status("moe_layer_grouped/gate_up_mfma"))) return rc;
+    }
     if (dbg_act && hipMemcpyAsync(dbg_act, w.q8a, (size_t)P * nbj * Q8_BLK, hipMemcpyDeviceToDevice, s) != hipSuccess)
         return fail(FT_HIP_E_LAUNCH, "%s: debug copy failed", nm);
-    const size_t lds_dn = (size_t)NTD * nbj * 40;
-    if (nbj <= 24)
-        hipLaunchKernelGGL(k_grouped_down<6>, dim3(H / DU, gmax), dim3(GT), lds_dn, s, (const uint8_t*)bank, eb, gu_bytes,
-                           (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8a, w.ydn, H, I, E);
-    else
-        hipLaunchKernelGGL(k_grouped_down<8>, dim3(H / DU, gmax), dim3(GT), lds_dn, s, (const uint8_t*)bank, eb, gu_bytes,
-                           (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8a, w.ydn, H, I, E);
-    if ((rc = launch_status("moe_layer_grouped/down"))) return rc;
+    if (dot4) {
+        const size_t lds_dn = (size_t)NTD * nbj * 40;
+        if (nbj <= 24)
+            hipLaunchKernelGGL(k_grouped_down<6>, dim3(H / DU, gmax), dim3(GT), lds_dn, s, (const uint8_t*)bank, eb,
+                               gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8a, w.ydn,
+                               H, I, E, n_mfma);
+        else
+            hipLaunchKernelGGL(k_grouped_down<8>, dim3(H / DU, gmax), dim3(GT), lds_dn, s, (const uint8_t*)bank, eb,
+                               gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8a, w.ydn,
+                               H, I, E, n_mfma);
+        if ((rc = launch_status("moe_layer_grouped/down"))) return rc;
+    }
+    if (mfma) {
+        if (nbj <= 32) {  // one K slice: 8 tiles of 16 rows per workgroup
+            const size_t lds_md = (size_t)GW * nbj * 32 + sizeof(float) * GW * 16 * MT;
+            hipLaunchKernelGGL((k_mfma_down<1, 32>), dim3(H / (16 * GW), gbig), dim3(GT), lds_md, s,
+                               (const uint8_t*)bank, eb, gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist,
+                               (const uint8_t*)w.q8a, q8a_bytes, w.ydn, H, I, E, n_mfma);
+        } else {  // long rows: one tile per workgroup, 8 K slices of up to 64 blocks
+            const size_t lds_md = (size_t)nbj * 32 + sizeof(float) * GW * 16 * MT;
+            hipLaunchKernelGGL((k_mfma_down<GW, 64>), dim3(H / 16, gbig), dim3(GT), lds_md, s, (const uint8_t*)bank,
+                               eb, gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8a,
+                               q8a_bytes, w.ydn, H, I, E, n_mfma);
+        }
+        if ((rc = launch_status("moe_layer_grouped/down_mfma"))) return rc;
+    }
     hipLaunchKernelGGL(k_grouped_combine, dim3((H + 255) / 256, (unsigned)n_seqs), dim3(256), 0, s, (const float*)w.ydn,
                        (const float*)wts, x, x_out, H, K);
     return launch_status("moe_layer_grouped/combine");

@@ -256,7 +256,22 @@ __global__ __launch_bounds__(256) void k_topk_router(const float* logits, const 
         taken[i] = 0;
     }
     __syncthreads();
-    for (int j = 0; j < k; ++j) {
+    if (E <= 256) {
+        // one thread per logit: its rank is the number of logits ahead of it
+        // in the order above (a total order: ranks are distinct); ranks < k
+        // are the chosen, in rank order
+        if (t < E) {
+            const float v = sv[t];
+            int rank = 0;
+            for (int i = 0; i < E; ++i) rank += topk_better(sv[i], i, v, t, E) ? 1 : 0;
+            if (rank < k) {
+                selv[rank] = v;
+                seli[rank] = t;
+            }
+        }
+        __syncthreads();
+    }
+    for (int j = 0; E > 256 && j < k; ++j) {
         float bv = 0.0f;
         int bi = E;
         for (int i = t; i < E; i += 256)

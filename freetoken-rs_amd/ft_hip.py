@@ -55,6 +55,7 @@ SIGNATURES = {
     "ft_hip_fused_set_spin_limit": (_I, [_P, _I]),
     "ft_hip_fused_set_prefetch": (_I, [_P, _I]),
     "ft_hip_set_input_norm": (_I, [_P, _I]),
+    "ft_hip_set_grouped_mfma_min": (_I, [_P, _I]),
     "ft_hip_fused_workspace_init": (_I, [_P, _P, _P, _SZ]),
     "ft_hip_pack_experts_fused": (_I, [_P, _P, _P, _I, _U64, _P, _I64, _I64, _I64]),
     "ft_hip_pack_router_fused": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
@@ -260,6 +261,10 @@ class Q4Gemv:
         """1: the layer entry points run on rmsnorm(x) (logits and gate|up sums times
         1/sqrt(mean(x*x) + 1e-6)); 0 (default): on x as given."""
         check(lib().ft_hip_set_input_norm(self._ctx, int(on)))
+
+    def set_grouped_mfma_min(self, n_tokens):
+        """moe_layer_grouped: experts with >= n_tokens tokens take the MFMA kernels (default 16)."""
+        check(lib().ft_hip_set_grouped_mfma_min(self._ctx, int(n_tokens)))
 
     def fused_workspace_init(self, ws, stream=None):
         check(lib().ft_hip_fused_workspace_init(self._ctx, _stream(stream), _ptr(ws), ws.numel() * ws.element_size()))

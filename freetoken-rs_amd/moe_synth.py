@@ -155,7 +155,9 @@ class FusedStack:
     kernel (ft_hip_moe_stack_fused): one launch runs all layers of one token.
     The packed banks also serve the grouped batched path (GroupedStack)."""
 
-    def __init__(self, model):
+    def __init__(self, model, workspace=True):
+        """workspace=False: the packed banks and routers only (for the grouped
+        path on shapes the fused kernel does not take)."""
         g, s = model.g, model.shape
         H, I, E, K = s.hidden, s.inter, s.n_experts, s.top_k
         self.m, self.g = model, g
@@ -164,8 +166,10 @@ class FusedStack:
         g.pack_experts_fused(model.banks, model.layout, model.expert_bytes, self.banks, model.L * E, H, I)
         self.routers = torch.empty_like(model.routers)
         g.pack_router_fused(model.routers, self.routers, model.L, E, H)
-        self.ws = torch.empty(g.fused_workspace_bytes(H, I, E, K), dtype=torch.uint8, device=model.device)
-        g.fused_workspace_init(self.ws)
+        self.ws = None
+        if workspace:
+            self.ws = torch.empty(g.fused_workspace_bytes(H, I, E, K), dtype=torch.uint8, device=model.device)
+            g.fused_workspace_init(self.ws)
 
     def n_workgroups(self):
         s = self.m.shape

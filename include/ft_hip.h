@@ -187,7 +187,7 @@ int ft_hip_moe_layer(ft_hip_ctx* ctx, void* stream, const float* x, float* x_out
  * (slot order) are bit-identical; f32 GEMV sums may differ in order.
  * dbg_gu [n_seqs*top_k][2I] f32 and dbg_act [n_seqs*top_k][I/32][40] (NULL
  * in normal use) receive the gate|up sums and act q8 blocks per pair.
- * Shapes: hidden 2816 or 4096, inter a multiple of 32 up to 1024,
+ * Shapes: hidden 2816 or 4096, inter a multiple of 32 up to 16384,
  * n_seqs*top_k <= 4096. */
 size_t ft_hip_moe_layer_grouped_workspace_bytes(int64_t n_seqs, int64_t hidden, int64_t inter,
                                                 int64_t n_experts, int64_t top_k);
@@ -196,6 +196,16 @@ int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const float* x, floa
                              const float* router_w, const float* router_bias, const float* expert_scale,
                              const void* bank, int32_t* ids, float* wts, void* workspace,
                              size_t workspace_bytes, float* dbg_gu, void* dbg_act);
+
+/* ft_hip_moe_layer_grouped: experts routed at least n_tokens tokens of the
+ * batch take the int8 MFMA tile kernels (16 rows x 16 tokens per
+ * v_mfma_i32_16x16x32_i8, one q4_0 block per instruction), the others the
+ * v_dot4 kernels; results agree to f32 summation order (q8 quants, int32
+ * block dots, routing and GELU q8 are the same). Default 16; 1 = MFMA for
+ * every expert. Rows longer than 1024 weights (inter > 1024) always take the
+ * MFMA kernels. No reference counterpart (the reference runs one GEMV per
+ * (token, expert) pair, ft-model/src/lib.rs:1507-1606). */
+int ft_hip_set_grouped_mfma_min(ft_hip_ctx* ctx, int n_tokens);
 
 /* Input RMS norm of the layer entry points (ft_hip_moe_layer,
  * ft_hip_moe_layer_grouped, ft_hip_moe_stack_fused); off (0) after create.

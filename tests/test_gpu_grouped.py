@@ -9,7 +9,10 @@ and layer outputs within max|d| <= 1e-3 * ||ref||_2.
 The ungrouped launch-by-launch layer (one GEMV per pair, as the reference's
 batched path, ft-model/src/lib.rs:1507-1606) must pick the same experts with
 the same weights. With the input RMS norm on, its scale enters the logits
-and the gate|up sums; the same checks hold.
+and the gate|up sums; the same checks hold. Experts with >= 16 tokens (the
+default) take the int8 MFMA tile kernels, the others the dot4 kernels; each
+case also runs with every expert forced onto one path (mfma_min 1 or 10**6),
+and the large-expert shape (inter 14336) always takes the MFMA kernels.
 """
 import numpy as np
 import pytest
@@ -47,8 +50,10 @@ def _banks(m, layer, ids):
     return gu, dn
 
 
-@pytest.mark.parametrize("B,zipf,norm", [(16, False, False), (64, False, False), (64, True, False), (16, True, True)])
-def test_grouped_layer_matches_oracle(gemv, orc, gstack, B, zipf, norm):
+@pytest.mark.parametrize("B,zipf,norm,mfma_min", [(16, False, False, 16), (64, False, False, 16), (64, True, False, 16),
+                                                  (16, True, True, 16), (16, False, False, 1), (64, True, True, 1),
+                                                  (64, True, False, 10**6)])
+def test_grouped_layer_matches_oracle(gemv, orc, gstack, B, zipf, norm, mfma_min):
     m = gstack.m
     s = m.shape
     H, I, E, K = s.hidden, s.inter, s.n_experts, s.top_k
@@ -65,6 +70,7 @@ def test_grouped_layer_matches_oracle(gemv, orc, gstack, B, zipf, norm):
         dact = torch.zeros((B * K, I // 32, 40), dtype=torch.uint8, device=DEV)
         layer = 1
         gemv.set_input_norm(norm)
+        gemv.set_grouped_mfma_min(mfma_min)
         gs.layer(layer, x, xo, ids, wts, dgu, dact)
         X, XO, IDS, WTS = host(x), host(xo), host(ids).reshape(B, K), host(wts).reshape(B, K)
         GU, ACT = host(dgu).reshape(B, K, 2 * I), host(dact).reshape(B, K, I // 32, 40)
@@ -117,6 +123,7 @@ def test_grouped_layer_matches_oracle(gemv, orc, gstack, B, zipf, norm):
     finally:
         m.bias = saved
         gemv.set_input_norm(0)
+        gemv.set_grouped_mfma_min(16)
 
 
 def test_grouped_repeatable_and_empty(gemv, gstack):
@@ -132,3 +139,43 @@ def test_grouped_repeatable_and_empty(gemv, gstack):
     s = m.shape
     gemv.moe_layer_grouped(x, a, 0, s.hidden, s.inter, s.n_experts, s.top_k, m.routers[0], None, None,
                            gs.bank(0), gs.ids[0], gs.wts[0], gs.ws)
+
+
+@pytest.mark.parametrize("norm", [False, True])
+def test_grouped_large_expert_mfma(gemv, orc, norm):
+    """Config 5's shape (H 4096, 8 experts of I 14336, top-2), 12 tokens in
+    one grouped layer (MFMA kernels, K-split down rows): per token routing
+    bit-exact, act q8 bit-exact from the kernel's own gate|up sums, gate|up
+    sums and outputs within the north-star tolerance."""
+    m = moe_synth.SyntheticMoE(gemv, moe_synth.LARGE, n_layers=1)
+    st = moe_synth.FusedStack(m, workspace=False)
+    s = m.shape
+    H, I, E, K, B = s.hidden, s.inter, s.n_experts, s.top_k, 12
+    gs = moe_synth.GroupedStack(st, B)
+    x = _hidden(m, B, first=40)
+    xo = torch.zeros_like(x)
+    ids = torch.zeros(B * K, dtype=torch.int32, device=DEV)
+    wts = torch.zeros(B * K, dtype=torch.float32, device=DEV)
+    dgu = torch.zeros((B * K, 2 * I), dtype=torch.float32, device=DEV)
+    dact = torch.zeros((B * K, I // 32, 40), dtype=torch.uint8, device=DEV)
+    gemv.set_input_norm(norm)
+    try:
+        gs.layer(0, x, xo, ids, wts, dgu, dact)
+    finally:
+        gemv.set_input_norm(0)
+    X, XO, IDS, WTS = host(x), host(xo), host(ids).reshape(B, K), host(wts).reshape(B, K)
+    GU, ACT = host(dgu).reshape(B, K, 2 * I), host(dact).reshape(B, K, I // 32, 40)
+    W_r = host(m.routers[0])
+    gub, dnb = _banks(m, 0, IDS.ravel())
+    for t in range(B):
+        r = orc.moe_layer(X[t], W_r, gub, dnb, H, I, K, layout=m.layout, threads=8, input_norm=norm)
+        assert np.array_equal(IDS[t], r["ids"]), t
+        assert np.array_equal(WTS[t].view(np.uint32), r["wts"].view(np.uint32)), t
+        for k in range(K):
+            assert np.max(np.abs(GU[t, k] - r["y_gu"][k])) <= 1e-3 * np.linalg.norm(r["y_gu"][k]), (t, k)
+            _, ad, aq = orc.gelu_mul_q8(GU[t, k], I, orc.GELU_PORTABLE)
+            blk = ACT[t, k]
+            assert np.array_equal(blk[:, 0:4].copy().view(np.float32)[:, 0].view(np.uint32), ad.view(np.uint32))
+            assert np.array_equal(blk[:, 8:40].copy().view(np.int8).ravel(), aq)
+        dref = r["x_out"] - X[t]
+        assert np.max(np.abs((XO[t] - X[t]) - dref)) <= 1e-3 * np.linalg.norm(dref), t
