@@ -9,8 +9,9 @@
 // an FMA, so neither may this file, except where the Rust source itself calls
 // an FMA intrinsic (_mm256_fmadd_ps in dot_q4_q8_avx2).
 //
-// Two functions have no counterpart in the reference and are definitions of
-// this build, shared bit-for-bit with the GPU kernels:
+// Three functions have no counterpart in the reference and are definitions of
+// this build, shared bit-for-bit with the GPU kernels (the input RMS norm,
+// orc_rms_inv, is the third; see its comment):
 //   * orc_router_logits: the reference computes router logits only on its GPU
 //     (ft-cuda/src/q4.cu:1153-1174) in an order tied to its launch shape; this
 //     build defines one order (the "R-order", below) that CPU and GPU follow.
