@@ -627,11 +627,17 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
     const int64_t gu_bytes = 2LL * I * nb * 18;
     int rc;
     const float* inv = ctx->input_norm ? w.inv : nullptr;
-    if (inv && (rc = ft::launch_rms_inv(stream, x, w.inv, hidden, n_seqs))) return rc;
-    if ((rc = ft::launch_router_logits(stream, router_w, x, router_bias, inv, w.logits, hidden, n_experts, n_seqs)))
-        return rc;
+    if (n_experts * 16 >= hidden / 32) {  // logits, norm scale and q8(x) in one launch
+        if ((rc = ft::launch_route_prep(stream, router_w, x, router_bias, ctx->input_norm, w.inv, w.q8x, w.logits,
+                                        hidden, n_experts, n_seqs)))
+            return rc;
+    } else {
+        if (inv && (rc = ft::launch_rms_inv(stream, x, w.inv, hidden, n_seqs))) return rc;
+        if ((rc = ft::launch_router_logits(stream, router_w, x, router_bias, inv, w.logits, hidden, n_experts, n_seqs)))
+            return rc;
+        if ((rc = ft_hip_quantize_q8(ctx, stream, x, hidden, w.q8x, hidden, n_seqs))) return rc;
+    }
     if ((rc = ft_hip_topk_router(ctx, stream, w.logits, expert_scale, ids, wts, n_experts, top_k, n_seqs))) return rc;
-    if ((rc = ft_hip_quantize_q8(ctx, stream, x, hidden, w.q8x, hidden, n_seqs))) return rc;
     // groups of >= n_mfma tokens take the MFMA tile kernels, the others the
     // dot4 kernels; rows longer than 32 blocks (I > 1024) only the former
     const int n_mfma = nbj > 32 ? 1 : std::max(1, ctx->grouped_mfma_min);

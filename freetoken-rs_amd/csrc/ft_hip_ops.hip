@@ -64,10 +64,25 @@ __host__ __device__ __forceinline__ int64_t row_bytes_of(int layout, int k) {
 }
 
 // Stage an entry's q8 activation row (nb blocks of 40 B) into LDS.
+// The entry's q8 row into LDS; a thread issues up to 16 loads before its
+// first store, so a long row costs a few load latencies, not one per word.
 __device__ __forceinline__ void stage_q8(const GemvArgs& a, int e, int* lds) {
-    const int nb = a.k >> 5;
+    const int n = (a.k >> 5) * 10;
     const int* src = reinterpret_cast<const int*>(a.q8 + (int64_t)entry_xrow(a, e) * a.q8_stride_blocks * Q8_BLK);
-    for (int i = threadIdx.x; i < nb * 10; i += blockDim.x) lds[i] = src[i];
+    const int t = threadIdx.x, nt = blockDim.x;
+    for (int base = 0; base < n; base += 16 * nt) {
+        int v[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int i = base + r * nt + t;
+            v[r] = i < n ? src[i] : 0;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int i = base + r * nt + t;
+            if (i < n) lds[i] = v[r];
+        }
+    }
     __syncthreads();
 }
 
@@ -88,7 +103,23 @@ __global__ __launch_bounds__(256) void k_gemv_q4_grouped(GemvArgs a) {
     float acc = 0.0f;
     if (row < a.n_rows) {
         const uint8_t* wr = entry_base(a, e) + (int64_t)row * row_bytes_of(LAYOUT, a.k);
-        for (int b = sub; b < nb; b += 8) {
+        // four blocks per step, their loads issued together (long rows are
+        // otherwise one load latency per block)
+        int b = sub;
+        for (; b + 24 < nb; b += 32) {
+            float d4[4];
+            uint4 q[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) load_block<LAYOUT>(wr, b + 8 * u, qs_off, d4[u], q[u]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int* xb = lds + (b + 8 * u) * 10;
+                const float d8 = __int_as_float(xb[0]);
+                const int diff = block_dot(q[u], xb + 2, xb[1]);
+                acc = fmaf((float)diff, d4[u] * d8, acc);
+            }
+        }
+        for (; b < nb; b += 8) {
             float d4;
             uint4 q;
             load_block<LAYOUT>(wr, b, qs_off, d4, q);
@@ -215,6 +246,39 @@ __global__ __launch_bounds__(64) void k_router_logits(const float* W, const floa
     }
 }
 
+// The head of a layer in one launch (grid (n_rows, n_seqs), one wavefront per
+// logit): router logits as k_router_logits, with the input RMS norm's scale
+// computed by each workgroup for its seq (the same R-order self-dot as
+// k_rms_inv, so the same bits) when norm is set; workgroup (e, s) with e <
+// ceil(nb/16) also quantizes blocks 16e..16e+15 of x_s to q8 (the
+// arithmetic of k_quantize_q8) and e == 0 stores inv[s].
+__global__ __launch_bounds__(64) void k_route_prep(const float* W, const float* x, const float* bias, int norm,
+                                                   float* inv, uint8_t* q8, float* y, int dim, int n_rows) {
+    extern __shared__ float P[];
+    __shared__ float G[8];
+    __shared__ float irs;
+    const int e = blockIdx.x, s = blockIdx.y, l = threadIdx.x;
+    const float* xs = x + (int64_t)s * dim;
+    if (norm) {
+        const float ss = rorder_dot(xs, xs, dim, P, G);
+        if (l == 0) irs = 1.0f / sqrtf(ss / (float)dim + 1e-6f);  // correctly rounded (HIP default)
+        __syncthreads();  // irs set; P and G free for the next dot
+    }
+    float t = rorder_dot(W + (int64_t)e * dim, xs, dim, P, G);
+    const float ir = norm ? irs : 1.0f;
+    if (l == 0) {
+        if (norm) t = t * ir;
+        if (bias) t = t + bias[e];
+        y[(int64_t)s * n_rows + e] = t;
+        if (norm && e == 0) inv[s] = ir;
+    }
+    const int nb = dim >> 5, b = e * 16 + (l >> 2);
+    if (e * 16 < nb) {  // uniform per workgroup; the quads of blocks beyond nb idle
+        if (b < nb)
+            quantize_block_quad(xs + 32 * b, l & 3, reinterpret_cast<uint32_t*>(q8 + ((int64_t)s * nb + b) * Q8_BLK));
+    }
+}
+
 // Scale of the input RMS norm per seq: inv[s] = 1 / sqrt(ss / dim + 1e-6),
 // ss = x_s.x_s in the R-order, each op rounded once. Grid n_seqs.
 __global__ __launch_bounds__(64) void k_rms_inv(const float* x, float* inv, int dim) {
@@ -296,20 +360,18 @@ __global__ __launch_bounds__(256) void k_topk_router(const float* logits, const 
         }
         __syncthreads();
     }
-    if (t == 0) {
-        const float mx = selv[0];
-        float ex[32];
+    // softmax over the chosen: thread j < k computes exp(l_j - l_max), the
+    // sum runs in rank order from 0.0f (the same bits as one thread doing all)
+    __shared__ float exv[32];
+    if (t < k) exv[t] = expf_portable(selv[t] - selv[0]);
+    __syncthreads();
+    if (t < k) {
         float denom = 0.0f;
-        for (int j = 0; j < k; ++j) {
-            ex[j] = expf_portable(selv[j] - mx);
-            denom = denom + ex[j];
-        }
-        for (int j = 0; j < k; ++j) {
-            float w = ex[j] / denom;
-            if (escale) w = w * escale[seli[j]];
-            ids[(int64_t)s * k + j] = seli[j];
-            wts[(int64_t)s * k + j] = w;
-        }
+        for (int j = 0; j < k; ++j) denom = denom + exv[j];
+        float w = exv[t] / denom;
+        if (escale) w = w * escale[seli[t]];
+        ids[(int64_t)s * k + t] = seli[t];
+        wts[(int64_t)s * k + t] = w;
     }
 }
 
@@ -557,6 +619,17 @@ int launch_router_logits(void* stream, const float* w, const float* x, const flo
     return launch_status("router_logits");
 }
 
+int launch_route_prep(void* stream, const float* w, const float* x, const float* bias, int norm, float* inv,
+                      void* q8, float* y, int64_t dim, int64_t n_rows, int64_t n_seqs) {
+    if (n_rows == 0 || n_seqs == 0) return FT_HIP_OK;
+    // every q8 block needs a workgroup: rows >= ceil(blocks / 16)
+    if (n_rows * 16 < dim / 32) return fail(FT_HIP_E_SHAPE, "route_prep: %lld rows cannot quantize %lld blocks",
+                                            (long long)n_rows, (long long)(dim / 32));
+    hipLaunchKernelGGL(k_route_prep, dim3((unsigned)n_rows, (unsigned)n_seqs), dim3(64), (size_t)(dim / 16) * 4,
+                       S(stream), w, x, bias, norm, inv, (uint8_t*)q8, y, (int)dim, (int)n_rows);
+    return launch_status("route_prep");
+}
+
 int launch_rms_inv(void* stream, const float* x, float* inv, int64_t dim, int64_t n_seqs) {
     if (n_seqs == 0) return FT_HIP_OK;
     hipLaunchKernelGGL(k_rms_inv, dim3((unsigned)n_seqs), dim3(64), (size_t)(dim / 16) * 4, S(stream), x, inv,
@@ -684,11 +757,17 @@ extern "C" int ft_hip_moe_layer(ft_hip_ctx* ctx, void* stream, const float* x, f
     if (n_seqs == 0) return FT_HIP_OK;
     int rc;
     const float* inv = ctx->input_norm ? w.inv : nullptr;
-    if (inv && (rc = ft::launch_rms_inv(stream, x, w.inv, hidden, n_seqs))) return rc;
-    if ((rc = ft::launch_router_logits(stream, router_w, x, router_bias, inv, w.logits, hidden, n_experts, n_seqs)))
-        return rc;
+    if (n_experts * 16 >= hidden / 32) {  // logits, norm scale and q8(x) in one launch
+        if ((rc = ft::launch_route_prep(stream, router_w, x, router_bias, ctx->input_norm, w.inv, w.q8x, w.logits,
+                                        hidden, n_experts, n_seqs)))
+            return rc;
+    } else {
+        if (inv && (rc = ft::launch_rms_inv(stream, x, w.inv, hidden, n_seqs))) return rc;
+        if ((rc = ft::launch_router_logits(stream, router_w, x, router_bias, inv, w.logits, hidden, n_experts, n_seqs)))
+            return rc;
+        if ((rc = ft_hip_quantize_q8(ctx, stream, x, hidden, w.q8x, hidden, n_seqs))) return rc;
+    }
     if ((rc = ft_hip_topk_router(ctx, stream, w.logits, expert_scale, ids, wts, n_experts, top_k, n_seqs))) return rc;
-    if ((rc = ft_hip_quantize_q8(ctx, stream, x, hidden, w.q8x, hidden, n_seqs))) return rc;
     const int64_t n_pairs = n_seqs * top_k;
     GemvArgs a{};
     a.base = (const uint8_t*)bank;

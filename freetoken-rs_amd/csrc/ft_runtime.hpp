@@ -27,6 +27,10 @@ int launch_status(const char* what);
 // already checked by the caller).
 int launch_router_logits(void* stream, const float* w, const float* x, const float* bias, const float* in_scale,
                          float* y, int64_t dim, int64_t n_rows, int64_t n_seqs);
+// Router logits (+ the input norm's scale when norm) and q8(x) in one launch;
+// needs n_rows * 16 >= dim / 32.
+int launch_route_prep(void* stream, const float* w, const float* x, const float* bias, int norm, float* inv,
+                      void* q8, float* y, int64_t dim, int64_t n_rows, int64_t n_seqs);
 // Input RMS norm scale per seq: inv[s] = 1 / sqrt(R-order(x_s . x_s) / dim + 1e-6).
 int launch_rms_inv(void* stream, const float* x, float* inv, int64_t dim, int64_t n_seqs);
 }  // namespace ft
