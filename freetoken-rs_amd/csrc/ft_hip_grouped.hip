@@ -369,7 +369,7 @@ __device__ __forceinline__ void scales4(const uint16_t* p, float (&sc)[4]) {
 // then, as k_grouped_gu, the input-norm scale, GELU*up and the q8 of act
 // block j per token.
 template <int BPW>
-__global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* bank, int64_t expert_bytes, const int32_t* meta,
+__global__ __launch_bounds__(GT, 2) __attribute__((amdgpu_waves_per_eu(4))) void k_mfma_gu(const uint8_t* bank, int64_t expert_bytes, const int32_t* meta,
                                                    const int32_t* plist, const uint8_t* q8x, uint32_t q8x_bytes,
                                                    uint8_t* q8a, float* dbg_gu, const float* in_scale, int H, int I,
                                                    int E, int K, int n_min) {
@@ -401,7 +401,7 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* bank, int64_t 
         const uint32_t vd = (uint32_t)((p / K) * nb + b0) * Q8_BLK, vq = vd + 8 + 4 * lg;
         // blocks in NBB-block batches, the next batch's loads issued before
         // the current batch's MFMAs (two register buffers)
-        constexpr int NBB = BPW > 12 ? 4 : BPW, NBATCH = (BPW + NBB - 1) / NBB;
+        constexpr int NBB = 1, NBATCH = (BPW + NBB - 1) / NBB;
         uint32_t aw[2][NBB][4];
         ActOp av[2][NBB];
         auto load = [&](int k, int buf) __attribute__((always_inline)) {
@@ -479,57 +479,64 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* bank, int64_t 
 }
 
 // Down rows of active expert g for its tokens, 16 at a time. The workgroup
-// takes GW/KS 16-row down tiles; wave w works on tile u*(GW/KS) + w/KS, K
+// takes GW/KS groups of RT consecutive 16-row down tiles; wave w works on the
+// RT tiles of group w/KS (they share each block's activation operand), K
 // slice w%KS (blocks [s*BW, s*BW+BW) below nbj); the KS slice partials of a
 // (row, token) are summed in slice order into y[pair][row].
-template <int KS, int BW>
-__global__ __launch_bounds__(GT, 1) void k_mfma_down(const uint8_t* bank, int64_t expert_bytes, int64_t gu_bytes,
+template <int KS, int BW, int RT>
+__global__ __launch_bounds__(GT, 2) void k_mfma_down(const uint8_t* bank, int64_t expert_bytes, int64_t gu_bytes,
                                                      const int32_t* meta, const int32_t* plist, const uint8_t* q8a,
                                                      uint32_t q8a_bytes, float* ydn, int H, int I, int E, int n_min) {
     extern __shared__ __align__(16) uint8_t lds[];
-    constexpr int TPW = GW / KS;  // tiles per workgroup
+    constexpr int TPW = GW / KS;   // tile groups per workgroup
+    constexpr int TW = TPW * RT;   // tiles per workgroup
     const int nbj = I >> 5, dn_tile = nbj * 288;
     const int u = blockIdx.x, g = blockIdx.y;
     if (g >= meta[1 + 3 * E]) return;  // groups of >= n_min tokens come first
     const int e = meta[1 + g], s0 = meta[1 + E + g], n = meta[1 + 2 * E + g];
     if (n < n_min) return;
-    // LDS: the tiles' scales [TPW][nbj][16] f16; slice partials [GW][16][MT]
+    // LDS: the tiles' scales [TW][nbj][16] f16; slice partials [GW][RT][16][MT]
     uint16_t* scl = reinterpret_cast<uint16_t*>(lds);
-    float* red = reinterpret_cast<float*>(lds + TPW * nbj * 32);
+    float* red = reinterpret_cast<float*>(lds + TW * nbj * 32);
     const int t = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(t >> 6), li = t & 15, lg = (t >> 4) & 3;
     const int tl = wave / KS, sl = wave % KS, bs = sl * BW;
-    const int tile = u * TPW + tl;
-    const uint8_t* Dt = bank + (int64_t)e * expert_bytes + gu_bytes + (int64_t)tile * dn_tile;
-    const uint16_t* st = scl + tl * nbj * 16;
-    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(Dt + nbj * 32, (uint32_t)nbj * 256);  // the tile's qs
+    const int tile0 = (u * TPW + tl) * RT;  // this wave's first tile
+    const uint8_t* D0 = bank + (int64_t)e * expert_bytes + gu_bytes;  // the expert's down tiles
+    const uint16_t* st = scl + tl * RT * nbj * 16;
+    // the wave's RT tiles: qs of tile tile0+m at m*dn_tile + nbj*32 from D0 + tile0*dn_tile
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(D0 + (int64_t)tile0 * dn_tile, (uint32_t)(RT * dn_tile));
     const __amdgpu_buffer_rsrc_t ra = buf_rsrc(q8a, q8a_bytes);
-    const uint32_t vw = li * 16 + 4 * lg;
+    const uint32_t vw = nbj * 32 + li * 16 + 4 * lg;
     for (int c0 = 0; c0 < n; c0 += MT) {
         const int nt = min(MT, n - c0);
         const int p = plist[s0 + c0 + min(li, nt - 1)];
         const uint32_t vd = (uint32_t)p * nbj * Q8_BLK, vq = vd + 8 + 4 * lg;
         // blocks in NBB-block batches, the next batch's loads issued before
         // the current batch's MFMAs (two register buffers)
-        constexpr int NBB = BW > 32 ? 16 : BW, NBATCH = BW / NBB;
-        uint32_t aw[2][NBB];
+        constexpr int NBB = 4, NBATCH = BW / NBB;
+        uint32_t aw[2][NBB][RT];
         ActOp av[2][NBB];
         auto load = [&](int k, int buf) __attribute__((always_inline)) {
 #pragma unroll
             for (int b = 0; b < NBB; ++b) {
                 const int bb = min(bs + k * NBB + b, nbj - 1);
-                aw[buf][b] = buf_ld(rw, vw, bb * 256);
+#pragma unroll
+                for (int m = 0; m < RT; ++m) aw[buf][b][m] = buf_ld(rw, vw, m * dn_tile + bb * 256);
                 av[buf][b] = act_op(ra, vq, vd, bb * Q8_BLK, li < nt);
             }
         };
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        float acc[RT][4];
+#pragma unroll
+        for (int m = 0; m < RT; ++m)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[m][v] = 0.0f;
         load(0, 0);
         if (c0 == 0) {  // the tiles' scales to LDS, with the first batch in flight
             stage<8>(
-                TPW * nbj * 8,
+                TW * nbj * 8,
                 [&](int i) {
                     const int k = i / (nbj * 8), r = i - k * nbj * 8;
-                    return reinterpret_cast<const uint32_t*>(bank + (int64_t)e * expert_bytes + gu_bytes +
-                                                             (int64_t)(u * TPW + k) * dn_tile)[r];
+                    return reinterpret_cast<const uint32_t*>(D0 + (int64_t)(u * TW + k) * dn_tile)[r];
                 },
                 [&](int i, uint32_t v) { reinterpret_cast<uint32_t*>(scl)[i] = v; });
             __syncthreads();
@@ -543,30 +550,39 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_down(const uint8_t* bank, int64_
             for (int b = 0; b < NBB; ++b) {
                 if (bs + k * NBB + b < nbj) {  // uniform
                     const ActOp a = av[k & 1][b];
-                    const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib_op(aw[k & 1][b]), a.b, c_init(a.qsum), 0, 0, 0);
-                    float sc[4];
-                    scales4(st + (bs + k * NBB + b) * 16 + 4 * lg, sc);
+                    const v4i c = c_init(a.qsum);
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) acc[v] = fmaf((float)d[v], sc[v] * a.d, acc[v]);
+                    for (int m = 0; m < RT; ++m) {
+                        const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib_op(aw[k & 1][b][m]), a.b, c, 0, 0, 0);
+                        float sc[4];
+                        scales4(st + (m * nbj + bs + k * NBB + b) * 16 + 4 * lg, sc);
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) acc[m][v] = fmaf((float)d[v], sc[v] * a.d, acc[m][v]);
+                    }
                 }
-                __builtin_amdgcn_sched_barrier(0);  // one block's MFMA result live at a time
+                __builtin_amdgcn_sched_barrier(0);  // one block's MFMA results live at a time
             }
         }
         if (KS == 1) {
             if (li < nt) {
 #pragma unroll
-                for (int v = 0; v < 4; ++v) ydn[(int64_t)p * H + tile * 16 + 4 * lg + v] = acc[v];
+                for (int m = 0; m < RT; ++m)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) ydn[(int64_t)p * H + (tile0 + m) * 16 + 4 * lg + v] = acc[m][v];
             }
         } else {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) red[(wave * 16 + 4 * lg + v) * MT + li] = acc[v];
+            for (int m = 0; m < RT; ++m)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) red[((wave * RT + m) * 16 + 4 * lg + v) * MT + li] = acc[m][v];
             __syncthreads();
-            for (int i = t; i < TPW * 16 * nt; i += GT) {  // (tile, row, token) sums over the slices in order
+            for (int i = t; i < TW * 16 * nt; i += GT) {  // (tile, row, token) sums over the slices in order
                 const int k = i / (16 * nt), r = (i / nt) % 16, tt = i % nt;
+                const int kg = k / RT, m = k % RT;
                 float sv = 0.0f;
 #pragma unroll
-                for (int q = 0; q < KS; ++q) sv = sv + red[((k * KS + q) * 16 + r) * MT + tt];
-                ydn[(int64_t)plist[s0 + c0 + tt] * H + (u * TPW + k) * 16 + r] = sv;
+                for (int q = 0; q < KS; ++q) sv = sv + red[(((kg * KS + q) * RT + m) * 16 + r) * MT + tt];
+                ydn[(int64_t)plist[s0 + c0 + tt] * H + (u * TW + k) * 16 + r] = sv;
             }
             __syncthreads();
         }
@@ -689,12 +705,14 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
     if (mfma) {
         if (nbj <= 32) {  // one K slice: 8 tiles of 16 rows per workgroup
             const size_t lds_md = (size_t)GW * nbj * 32 + sizeof(float) * GW * 16 * MT;
-            hipLaunchKernelGGL((k_mfma_down<1, 32>), dim3(H / (16 * GW), gbig), dim3(GT), lds_md, s,
+            hipLaunchKernelGGL((k_mfma_down<1, 32, 1>), dim3(H / (16 * GW), gbig), dim3(GT), lds_md, s,
                                (const uint8_t*)bank, eb, gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist,
                                (const uint8_t*)w.q8a, q8a_bytes, w.ydn, H, I, E, n_mfma);
-        } else {  // long rows: one tile per workgroup, 8 K slices of up to 64 blocks
-            const size_t lds_md = (size_t)nbj * 32 + sizeof(float) * GW * 16 * MT;
-            hipLaunchKernelGGL((k_mfma_down<GW, 64>), dim3(H / 16, gbig), dim3(GT), lds_md, s, (const uint8_t*)bank,
+        } else {  // long rows: DRT tiles per workgroup, 8 K slices of up to 64 blocks
+            constexpr int DRT = 4;
+            const size_t lds_md = (size_t)DRT * nbj * 32 + sizeof(float) * GW * DRT * 16 * MT;
+            hipLaunchKernelGGL((k_mfma_down<GW, 64, DRT>), dim3(H / (16 * DRT), gbig), dim3(GT), lds_md, s,
+                               (const uint8_t*)bank,
                                eb, gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8a,
                                q8a_bytes, w.ydn, H, I, E, n_mfma);
         }
