@@ -20,6 +20,7 @@
 #include "ft_runtime.hpp"
 
 #include <algorithm>
+#include <limits>
 
 using namespace ft;
 
@@ -655,13 +656,17 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
     }
     if ((rc = ft_hip_topk_router(ctx, stream, w.logits, expert_scale, ids, wts, n_experts, top_k, n_seqs))) return rc;
     // groups of >= n_mfma tokens take the MFMA tile kernels, the others the
-    // dot4 kernels; rows longer than 32 blocks (I > 1024) only the former
-    const int n_mfma = nbj > 32 ? 1 : std::max(1, ctx->grouped_mfma_min);
+    // dot4 kernels; rows longer than 32 blocks (I > 1024) only the former.
+    // Automatic (0): every group on one family, MFMA from 2 pairs per expert
+    // on (measured: one family's launches beat a split of both)
+    int n_mfma = ctx->grouped_mfma_min;
+    if (n_mfma <= 0) n_mfma = (int64_t)P >= 2 * n_experts ? 1 : std::numeric_limits<int>::max();
+    if (nbj > 32) n_mfma = 1;
     hipLaunchKernelGGL(k_group_pairs, dim3(1), dim3(1024), 0, s, (const int32_t*)ids, P, E, n_mfma, w.meta, w.plist,
                        w.ppos);
     if ((rc = launch_status("moe_layer_grouped/group"))) return rc;
     const int gmax = std::min(E, P);
-    const int gbig = std::min(gmax, P / n_mfma);  // at most this many groups of >= n_mfma tokens
+    const int gbig = std::min(gmax, n_mfma > P ? 0 : P / n_mfma);  // at most this many groups of >= n_mfma tokens
     const bool dot4 = n_mfma > 1, mfma = n_seqs >= n_mfma;
     const uint32_t q8x_bytes = (uint32_t)(n_seqs * nb * Q8_BLK), q8a_bytes = (uint32_t)((int64_t)P * nbj * Q8_BLK);
     if (dot4) {
@@ -703,9 +708,9 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
         if ((rc = launch_status("moe_layer_grouped/down"))) return rc;
     }
     if (mfma) {
-        if (nbj <= 32) {  // one K slice: 8 tiles of 16 rows per workgroup
-            const size_t lds_md = (size_t)GW * nbj * 32 + sizeof(float) * GW * 16 * MT;
-            hipLaunchKernelGGL((k_mfma_down<1, 32, 1>), dim3(H / (16 * GW), gbig), dim3(GT), lds_md, s,
+        if (nbj <= 32) {  // one K slice: 8 waves x 2 tiles of 16 rows per workgroup
+            const size_t lds_md = (size_t)GW * 2 * nbj * 32 + sizeof(float) * GW * 2 * 16 * MT;
+            hipLaunchKernelGGL((k_mfma_down<1, 32, 2>), dim3(H / (16 * GW * 2), gbig), dim3(GT), lds_md, s,
                                (const uint8_t*)bank, eb, gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist,
                                (const uint8_t*)w.q8a, q8a_bytes, w.ydn, H, I, E, n_mfma);
         } else {  // long rows: DRT tiles per workgroup, 8 K slices of up to 64 blocks

@@ -56,7 +56,7 @@ extern "C" int ft_hip_create(int device, ft_hip_ctx** out) {
     c->num_xcds = 8;  // MI355X: 8 XCDs of 32 CUs
     c->fused_spin_limit = 1 << 21;
     c->fused_prefetch = 1;
-    c->grouped_mfma_min = 16;
+    c->grouped_mfma_min = 0;  // automatic
     std::snprintf(c->arch, sizeof c->arch, "%s", p.gcnArchName);
     *out = c;
     return FT_HIP_OK;
@@ -73,7 +73,7 @@ extern "C" int ft_hip_set_input_norm(ft_hip_ctx* ctx, int on) {
 extern "C" int ft_hip_set_grouped_mfma_min(ft_hip_ctx* ctx, int n_tokens) {
     clear_error();
     if (!ctx) return fail(FT_HIP_E_INVALID, "set_grouped_mfma_min: null ctx");
-    if (n_tokens < 1) return fail(FT_HIP_E_SHAPE, "set_grouped_mfma_min: n_tokens=%d < 1", n_tokens);
+    if (n_tokens < 0) return fail(FT_HIP_E_SHAPE, "set_grouped_mfma_min: n_tokens=%d < 0", n_tokens);
     ctx->grouped_mfma_min = n_tokens;
     return FT_HIP_OK;
 }

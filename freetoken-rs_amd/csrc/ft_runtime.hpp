@@ -13,7 +13,7 @@ struct ft_hip_ctx {
     int fused_spin_limit;  // polls before a fused-kernel wait gives up
     int fused_prefetch;    // fused kernel: stream predicted experts ahead (1) or not (0)
     int input_norm;        // layer entry points run on rmsnorm(x) (1) or x (0)
-    int grouped_mfma_min;  // grouped layer: experts with at least this many tokens take the MFMA kernels
+    int grouped_mfma_min;  // grouped layer: experts with at least this many tokens take the MFMA kernels (0: auto)
     char arch[64];
 };
 

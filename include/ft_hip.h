@@ -201,10 +201,12 @@ int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const float* x, floa
  * batch take the int8 MFMA tile kernels (16 rows x 16 tokens per
  * v_mfma_i32_16x16x32_i8, one q4_0 block per instruction), the others the
  * v_dot4 kernels; results agree to f32 summation order (q8 quants, int32
- * block dots, routing and GELU q8 are the same). Default 16; 1 = MFMA for
- * every expert. Rows longer than 1024 weights (inter > 1024) always take the
- * MFMA kernels. No reference counterpart (the reference runs one GEMV per
- * (token, expert) pair, ft-model/src/lib.rs:1507-1606). */
+ * block dots, routing and GELU q8 are the same). 0 (the default) = automatic:
+ * every expert on the MFMA kernels when the batch has at least 2 (token,
+ * expert) pairs per expert, else every expert on the dot4 kernels; 1 = MFMA
+ * for every expert. Rows longer than 1024 weights (inter > 1024) always take
+ * the MFMA kernels. No reference counterpart (the reference runs one GEMV
+ * per (token, expert) pair, ft-model/src/lib.rs:1507-1606). */
 int ft_hip_set_grouped_mfma_min(ft_hip_ctx* ctx, int n_tokens);
 
 /* Input RMS norm of the layer entry points (ft_hip_moe_layer,
