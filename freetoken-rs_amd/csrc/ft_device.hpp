@@ -203,6 +203,17 @@ __device__ __forceinline__ void quantize_block_quad(const float* v, int part, ui
     }
 }
 
+// Router order as one unsigned compare: a larger key sorts first. Monotone
+// float bits (larger logit first), then the complemented index (lower index
+// first on equal values; -0 and +0 are equal); NaN below every number.
+__device__ __forceinline__ uint64_t rank_key(float v, int i) {
+    v = v + 0.0f;  // -0 -> +0: equal values tie on the index
+    const uint32_t b = __float_as_uint(v);
+    uint32_t mo = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    mo = v == v ? mo : 0u;  // NaN below -inf
+    return ((uint64_t)mo << 32) | (0xFFFFFFFFu - (uint32_t)i);
+}
+
 // ---------------------------------------------------------------------------
 // Portable exp / tanh: only IEEE basic operations (fma, floor, ldexp, +, -, /)
 // in a fixed order, so the host oracle computes the same bits. Cody-Waite

@@ -264,13 +264,7 @@ __device__ __forceinline__ void stamp(const FusedParams& P, int l, int ev) {
 // exp(l - l_max), summed in rank order. Each logit carries a 64-bit key
 // (monotone float bits, then the complemented index) so that "sorts before"
 // is one unsigned compare; four threads share one logit's E comparisons.
-__device__ __forceinline__ uint64_t rank_key(float v, int i) {
-    v = v + 0.0f;  // -0 -> +0: equal values tie on the index
-    const uint32_t b = __float_as_uint(v);
-    uint32_t mo = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    mo = v == v ? mo : 0u;  // NaN below -inf
-    return ((uint64_t)mo << 32) | (0xFFFFFFFFu - (uint32_t)i);
-}
+// (rank_key: ft_device.hpp)
 
 // Scale of the input RMS norm from the 8 groups' sums of squares (R-order,
 // like a router row with W = x): ss = the group sums in order from 0.0f,

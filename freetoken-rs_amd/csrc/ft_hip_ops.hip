@@ -322,12 +322,23 @@ __global__ __launch_bounds__(256) void k_topk_router(const float* logits, const 
     __syncthreads();
     if (E <= 256) {
         // one thread per logit: its rank is the number of logits ahead of it
-        // in the order above (a total order: ranks are distinct); ranks < k
-        // are the chosen, in rank order
+        // in the order above, counted with the branch-free keys of rank_key
+        // (a total order: ranks are distinct); ranks < k are the chosen, in
+        // rank order
+        __shared__ uint64_t key[256];
+        if (t < E) key[t] = rank_key(sv[t], t);
+        __syncthreads();
         if (t < E) {
             const float v = sv[t];
+            const uint64_t kt = key[t];
             int rank = 0;
-            for (int i = 0; i < E; ++i) rank += topk_better(sv[i], i, v, t, E) ? 1 : 0;
+            for (int i0 = 0; i0 < E; i0 += 16) {  // 16 keys per step, their LDS reads issued together
+                uint64_t c[16];
+#pragma unroll
+                for (int q = 0; q < 16; ++q) c[q] = key[min(i0 + q, E - 1)];
+#pragma unroll
+                for (int q = 0; q < 16; ++q) rank += (i0 + q < E && c[q] > kt) ? 1 : 0;
+            }
             if (rank < k) {
                 selv[rank] = v;
                 seli[rank] = t;
