@@ -126,16 +126,17 @@ class GraphRunner:
 
 
 def time_dominant_kernel(g, model, reps=3):
-    """Average duration of the gate|up grouped GEMV (the kernel moving 2/3 of
-    the bytes) with HIP events on the stream it runs on, rotating over all
-    layers so that no layer's bank is cache-resident."""
+    """Average duration of the layer's gate|up launch (k_gemv_gu_act: the
+    grouped gate|up GEMV with GELU*up and q8, moving 2/3 of the bytes) with
+    HIP events on the stream it runs on, rotating over all layers so that no
+    layer's bank is cache-resident."""
     import torch
     s = model.shape
     H, I, E, k = s.hidden, s.inter, s.n_experts, s.top_k
     stream = torch.cuda.Stream()
     ids = torch.arange(0, E, E // k, dtype=torch.int32, device=model.device)[:k].contiguous()
     q8x = torch.zeros(H // 32 * 40, dtype=torch.uint8, device=model.device)
-    ygu = torch.zeros(k * 2 * I, dtype=torch.float32, device=model.device)
+    q8a = torch.zeros(k * (I // 32) * 40, dtype=torch.uint8, device=model.device)
     x = model.hidden(0)
     with torch.cuda.stream(stream):
         g.quantize_q8(x, 0, q8x, H, 1, stream=stream)
@@ -143,8 +144,7 @@ def time_dominant_kernel(g, model, reps=3):
 
         def launch(l):
             bank = model.banks[l * E * eb:(l + 1) * E * eb]
-            g.gemv_grouped_slots(bank, eb, 0, ids, None, k, q8x, 0, ygu, 2 * I, 2 * I, H, model.layout,
-                                 stream=stream)
+            g.gemv_gate_up_act(bank, eb, ids, k, k, q8x, H, I, q8a, layout=model.layout, stream=stream)
 
         for l in range(model.L):
             launch(l)
@@ -328,7 +328,7 @@ def main():
         k_name = f"k_moe_stack_fused (whole {model.L}-layer section, one launch per token)"
     elif B == 1:
         k_us, k_bytes = time_dominant_kernel(g, model)
-        k_name = f"k_gemv_q4_grouped (gate|up, {k} experts)"
+        k_name = f"k_gemv_gu_act (gate|up GEMV + GELU*up q8, {k} experts)"
     else:  # the step's graph as a whole: its expert bytes over the step time
         k_us, k_bytes = us_step, step_bytes
         k_name = f"whole step ({model.L} {path} layers of {B} tokens in one HIP graph; not a single kernel)"

@@ -65,7 +65,6 @@ constexpr int MAX_E = 128;      // group partials use four threads per expert
 constexpr int NGROUP = 8;       // R-order groups, one group unit each
 constexpr int DN_ROWS = 16;     // rows per router chunk and per down tile
 constexpr int DN_UNIT = DN_ROWS * FT_WAVES;  // rows per down unit: one tile per wave
-constexpr int WAIT_U = 8;       // tagged words per thread per wait (n <= 4096)
 constexpr int POLL_SLEEP = 1;   // s_sleep units (64 clocks) between polls
 constexpr int NREP = 1;         // replicas of the group broadcast
 constexpr int CTL_EPOCH = 0;    // control words (u32 indices)

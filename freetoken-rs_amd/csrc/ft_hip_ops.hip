@@ -10,6 +10,12 @@
 
 using namespace ft;
 
+// lanes per row of the gate|up launch with the activation (k_gemv_gu_act):
+// 4 lanes take 256-thread workgroups, so that a long layer's block-pairs
+// (I/32 per pair) all run at once; measured faster than 8 on the
+// large-expert shape
+constexpr int GU_LANES = 4;
+
 // ---------------------------------------------------------------------------
 // Weight addressing shared by the grouped GEMV and the block-dot dump.
 // ---------------------------------------------------------------------------
@@ -63,12 +69,9 @@ __host__ __device__ __forceinline__ int64_t row_bytes_of(int layout, int k) {
     return (int64_t)nb * 18;
 }
 
-// Stage an entry's q8 activation row (nb blocks of 40 B) into LDS.
-// The entry's q8 row into LDS; a thread issues up to 16 loads before its
-// first store, so a long row costs a few load latencies, not one per word.
-__device__ __forceinline__ void stage_q8(const GemvArgs& a, int e, int* lds) {
-    const int n = (a.k >> 5) * 10;
-    const int* src = reinterpret_cast<const int*>(a.q8 + (int64_t)entry_xrow(a, e) * a.q8_stride_blocks * Q8_BLK);
+// n words from src into LDS; a thread issues up to 16 loads before its first
+// store, so a long row costs a few load latencies, not one per word.
+__device__ __forceinline__ void stage_words(const int* src, int n, int* lds) {
     const int t = threadIdx.x, nt = blockDim.x;
     for (int base = 0; base < n; base += 16 * nt) {
         int v[16];
@@ -86,6 +89,104 @@ __device__ __forceinline__ void stage_q8(const GemvArgs& a, int e, int* lds) {
     __syncthreads();
 }
 
+// An entry's q8 activation row (nb blocks of 40 B) into LDS.
+__device__ __forceinline__ void stage_q8(const GemvArgs& a, int e, int* lds) {
+    stage_words(reinterpret_cast<const int*>(a.q8 + (int64_t)entry_xrow(a, e) * a.q8_stride_blocks * Q8_BLK),
+                (a.k >> 5) * 10, lds);
+}
+
+// Top-k of E <= 256 logits sv (LDS) in the router's order (larger first,
+// then lower index, NaN last), by a workgroup of at least E threads: one
+// thread per logit, its rank the number of logits ahead of it, counted with
+// the branch-free keys of rank_key (a total order: ranks are distinct); ranks
+// < k go to selv/seli in rank order.
+// Barriers inside; the caller reads selv/seli after it returns.
+__device__ __forceinline__ void topk_rank_select(const float* sv, int E, int k, uint64_t* key, float* selv,
+                                                 int* seli) {
+    const int t = threadIdx.x;
+    if (t < E) key[t] = rank_key(sv[t], t);
+    __syncthreads();
+    if (t < E) {
+        const float v = sv[t];
+        const uint64_t kt = key[t];
+        int rank = 0;
+        for (int i0 = 0; i0 < E; i0 += 16) {  // 16 keys per step, their LDS reads issued together
+            uint64_t c[16];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) c[q] = key[min(i0 + q, E - 1)];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) rank += (i0 + q < E && c[q] > kt) ? 1 : 0;
+        }
+        if (rank < k) {
+            selv[rank] = v;
+            seli[rank] = t;
+        }
+    }
+    __syncthreads();
+}
+
+// Softmax over the chosen (rank order): thread j < k computes
+// exp(l_j - l_max); the sum runs in rank order from 0.0f (the same bits as
+// one thread doing all); returns thread j's weight (times escale of its
+// expert when given). One barrier inside.
+__device__ __forceinline__ float topk_softmax(const float* selv, const int* seli, int k, const float* escale,
+                                              float* exv) {
+    const int t = threadIdx.x;
+    if (t < k) exv[t] = expf_portable(selv[t] - selv[0]);
+    __syncthreads();
+    float w = 0.0f;
+    if (t < k) {
+        float denom = 0.0f;
+        for (int j = 0; j < k; ++j) denom = denom + exv[j];
+        w = exv[t] / denom;
+        if (escale) w = w * escale[seli[t]];
+    }
+    return w;
+}
+
+// One row's share of a lane: lane `sub` of the row's LPR takes blocks sub,
+// sub+LPR, ..., an fma chain in block order (four blocks' loads issued
+// together: long rows are otherwise one load latency per block). The caller
+// sums the LPR lanes by xor 1, 2, 4 (, 8).
+template <int LAYOUT, int LPR = 8>
+__device__ __forceinline__ float gemv_row_part(const uint8_t* wr, int sub, int nb, const int* lds) {
+    const int qs_off = (nb * 2 + 15) / 16 * 16;
+    float acc = 0.0f;
+    int b = sub;
+    for (; b + 3 * LPR < nb; b += 4 * LPR) {
+        float d4[4];
+        uint4 q[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) load_block<LAYOUT>(wr, b + LPR * u, qs_off, d4[u], q[u]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int* xb = lds + (b + LPR * u) * 10;
+            const float d8 = __int_as_float(xb[0]);
+            const int diff = block_dot(q[u], xb + 2, xb[1]);
+            acc = fmaf((float)diff, d4[u] * d8, acc);
+        }
+    }
+    for (; b < nb; b += LPR) {
+        float d4;
+        uint4 q;
+        load_block<LAYOUT>(wr, b, qs_off, d4, q);
+        const int* xb = lds + b * 10;
+        const float d8 = __int_as_float(xb[0]);
+        const int diff = block_dot(q, xb + 2, xb[1]);
+        acc = fmaf((float)diff, d4 * d8, acc);
+    }
+    return acc;
+}
+
+template <int LPR = 8>
+__device__ __forceinline__ float sum_row_lanes(float acc) {
+    acc += __shfl_xor(acc, 1);
+    acc += __shfl_xor(acc, 2);
+    if (LPR >= 8) acc += __shfl_xor(acc, 4);
+    if (LPR == 16) acc += __shfl_xor(acc, 8);
+    return acc;
+}
+
 // Grouped GEMV (replaces gemv_q4r_grouped_ptr/_idx, q4.cu:1497-1567, and the
 // v3 q4_0 variants, q4.cu:360-491, :1189-1241). A 256-thread workgroup owns 32
 // rows of one entry: 8 lanes per row, lane s takes blocks s, s+8, ...; the
@@ -99,40 +200,115 @@ __global__ __launch_bounds__(256) void k_gemv_q4_grouped(GemvArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row = (blockIdx.x * 4 + wave) * 8 + (lane >> 3);
     const int sub = lane & 7;
-    const int qs_off = (nb * 2 + 15) / 16 * 16;
     float acc = 0.0f;
-    if (row < a.n_rows) {
-        const uint8_t* wr = entry_base(a, e) + (int64_t)row * row_bytes_of(LAYOUT, a.k);
-        // four blocks per step, their loads issued together (long rows are
-        // otherwise one load latency per block)
-        int b = sub;
-        for (; b + 24 < nb; b += 32) {
-            float d4[4];
-            uint4 q[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) load_block<LAYOUT>(wr, b + 8 * u, qs_off, d4[u], q[u]);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int* xb = lds + (b + 8 * u) * 10;
-                const float d8 = __int_as_float(xb[0]);
-                const int diff = block_dot(q[u], xb + 2, xb[1]);
-                acc = fmaf((float)diff, d4[u] * d8, acc);
-            }
-        }
-        for (; b < nb; b += 8) {
-            float d4;
-            uint4 q;
-            load_block<LAYOUT>(wr, b, qs_off, d4, q);
-            const int* xb = lds + b * 10;
-            const float d8 = __int_as_float(xb[0]);
-            const int diff = block_dot(q, xb + 2, xb[1]);
-            acc = fmaf((float)diff, d4 * d8, acc);
-        }
-    }
-    acc += __shfl_xor(acc, 1);
-    acc += __shfl_xor(acc, 2);
-    acc += __shfl_xor(acc, 4);
+    if (row < a.n_rows)
+        acc = gemv_row_part<LAYOUT>(entry_base(a, e) + (int64_t)row * row_bytes_of(LAYOUT, a.k), sub, nb, lds);
+    acc = sum_row_lanes(acc);
     if (row < a.n_rows && sub == 0) a.y[(int64_t)e * a.y_stride + row] = acc;
+}
+
+// Gate|up GEMV of one pair with GELU(gate)*up and its q8 block in the same
+// launch (replaces gemv_q4r_grouped + gelu_mul_quantize_q8, q4.cu). A
+// workgroup of 64*LPR threads owns gate rows 32j..32j+31 (the first LPR/2
+// waves) and up rows I+32j.. (the others) of pair blockIdx.y, LPR lanes per
+// row (gemv_row_part), and writes q8 block j of the pair's activation with
+// k_gelu_mul_q8's arithmetic. LPR 8 gives k_gemv_q4_grouped's sums (and so
+// the bits of the two launches); LPR 4 sums each row in 4 lane chains.
+// Grid (I/32, n_pairs).
+//
+// TOPK: the routing of the pair's seq (top-div of the E <= 256 logits and
+// their softmax, the arithmetic of k_topk_router) is computed by every
+// workgroup from the logits, the expert of pair blockIdx.y taken from it, and
+// ids/wts written by the seq's workgroup (0, s*div); without TOPK the pair's
+// expert is a.slots[pair].
+template <int LAYOUT, bool TOPK, int LPR = 8>
+__global__ __launch_bounds__(64 * LPR, 24 / LPR) void k_gemv_gu_act(GemvArgs a, int inter, uint8_t* q8a,
+                                                                  const float* in_scale, int div, const float* logits,
+                                                                  const float* escale, int32_t* ids, float* wts,
+                                                                  int E) {
+    extern __shared__ int lds[];
+    __shared__ float gs[64];
+    const int e = blockIdx.y, t = threadIdx.x;
+    __shared__ float sv[TOPK ? 256 : 1], selv[TOPK ? 32 : 1];
+    __shared__ int seli[TOPK ? 32 : 1];
+    __shared__ uint64_t key[TOPK ? 256 : 1];
+    __shared__ float exv[TOPK ? 32 : 1];
+    const int s = e / div;
+    if (TOPK && t < E) sv[t] = logits[(int64_t)s * E + t];
+    stage_q8(a, e, lds);  // its barrier also covers sv
+    int slot;
+    if constexpr (TOPK) {
+        topk_rank_select(sv, E, div, key, selv, seli);
+        const float w = topk_softmax(selv, seli, div, escale, exv);
+        if (blockIdx.x == 0 && e == s * div && t < div) {
+            ids[(int64_t)s * div + t] = seli[t];
+            wts[(int64_t)s * div + t] = w;
+        }
+        slot = seli[e - s * div];
+    } else {
+        slot = a.slots[e];
+    }
+    const uint8_t* eb = a.base + (uint64_t)slot * a.expert_bytes + a.bank_off;
+    const int nb = a.k >> 5;
+    // waves 0..LPR/2-1: gate rows, the others up rows, 64/LPR rows per wave
+    const int lane = t & 63, wave = t >> 6;
+    const bool up = wave >= LPR / 2;
+    const int rl = (wave - (up ? LPR / 2 : 0)) * (64 / LPR) + lane / LPR, sub = lane % LPR;
+    const int row = (up ? inter : 0) + (int)blockIdx.x * 32 + rl;
+    float acc = gemv_row_part<LAYOUT, LPR>(eb + (int64_t)row * row_bytes_of(LAYOUT, a.k), sub, nb, lds);
+    acc = sum_row_lanes<LPR>(acc);
+    if (sub == 0) gs[(up ? 32 : 0) + rl] = acc;
+    __syncthreads();
+    if (threadIdx.x < 64) {  // both half-waves compute block j; the first stores it
+        const int l = threadIdx.x & 31;
+        float gate = gs[l], up = gs[32 + l];
+        if (in_scale) {
+            const float sc = in_scale[e / div];
+            gate = gate * sc;
+            up = up * sc;
+        }
+        const float v = gelu_tanh(gate) * up;
+        const Q8Lane r = q8_quantize_half(v);
+        if (threadIdx.x < 32) q8_store_half(q8a + ((int64_t)e * (inter >> 5) + blockIdx.x) * Q8_BLK, l, r);
+    }
+}
+
+// Down GEMV of the k pairs of one seq with the residual combine of
+// k_combine_residual in the same launch: a workgroup owns rows R*j..R*j+R-1
+// (R = (256/LPR)/k) of all k pairs of seq s (the k q8 activation rows,
+// contiguous, staged together) and computes out = x + ((0 + w0*y0) + w1*y1
+// + ...) for them, pairs in order. LPR lanes per row: 8 is
+// k_gemv_q4_grouped's arithmetic; 16 (long rows) sums each row's blocks in
+// 16 lane chains instead, twice the workgroups. Grid (ceil(H/R), n_seqs).
+template <int LAYOUT, int LPR>
+__global__ __launch_bounds__(256) void k_gemv_down_combine(GemvArgs a, const float* wts, const float* x, float* out,
+                                                           int k) {
+    extern __shared__ int lds[];
+    constexpr int NE = 256 / LPR;  // row entries per workgroup
+    __shared__ float ys[NE];
+    const int s = blockIdx.y, R = NE / k;
+    const int nb = a.k >> 5;
+    stage_words(reinterpret_cast<const int*>(a.q8 + (int64_t)s * k * a.q8_stride_blocks * Q8_BLK), k * nb * 10, lds);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int re = wave * (64 / LPR) + lane / LPR, sub = lane % LPR;  // row entry: pair kk, local row rl
+    const int kk = re / R, rl = re - kk * R;
+    const int row = (int)blockIdx.x * R + rl;
+    float acc = 0.0f;
+    if (row < a.n_rows)
+        acc = gemv_row_part<LAYOUT, LPR>(entry_base(a, s * k + kk) + (int64_t)row * row_bytes_of(LAYOUT, a.k), sub,
+                                         nb, lds + kk * nb * 10);
+    acc = sum_row_lanes<LPR>(acc);
+    if (sub == 0) ys[re] = acc;
+    __syncthreads();
+    const int i = (int)blockIdx.x * R + (int)threadIdx.x;
+    if ((int)threadIdx.x < R && i < a.n_rows) {
+        float h = 0.0f;
+        for (int q = 0; q < k; ++q) {
+            const float part = ys[q * R + threadIdx.x] * wts[(int64_t)s * k + q];
+            h = h + part;
+        }
+        out[(int64_t)s * a.n_rows + i] = x[(int64_t)s * a.n_rows + i] + h;
+    }
 }
 
 // Block-dot dump: the same addressing and block_dot() as k_gemv_q4_grouped.
@@ -196,6 +372,22 @@ __global__ __launch_bounds__(256) void k_gelu_mul_q8(const float* gu, uint8_t* q
     if (ok) q8_store_half(q8 + (e * nb + b) * Q8_BLK, l, r);
 }
 
+// s = ((0 + p[0]) + p[1]) + ... + p[n-1] (each add rounded, in order), with
+// the LDS reads issued eight at a time ahead of their adds
+__device__ __forceinline__ float group_sum(const float* p, int n) {
+    float s = 0.0f;
+    int c = 0;
+    for (; c + 8 <= n; c += 8) {
+        float v[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = p[c + q];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) s = s + v[q];
+    }
+    for (; c < n; ++c) s = s + p[c];
+    return s;
+}
+
 // R-order dot w.xs of one wavefront (the value is returned in lane 0):
 // lane c computes chunk partials P_c (16-element fma chains), lanes 0..7 sum
 // their group's chunks in order, lane 0 sums the 8 groups in order.
@@ -218,11 +410,7 @@ __device__ __forceinline__ float rorder_dot(const float* w, const float* xs, int
     }
     __syncthreads();
     const int C = dim >> 7;
-    if (l < 8) {
-        float gs = 0.0f;
-        for (int c = l * C; c < (l + 1) * C; ++c) gs = gs + P[c];
-        G[l] = gs;
-    }
+    if (l < 8) G[l] = group_sum(P + l * C, C);
     __syncthreads();
     float t = 0.0f;
     if (l == 0)
@@ -254,17 +442,48 @@ __global__ __launch_bounds__(64) void k_router_logits(const float* W, const floa
 // arithmetic of k_quantize_q8) and e == 0 stores inv[s].
 __global__ __launch_bounds__(64) void k_route_prep(const float* W, const float* x, const float* bias, int norm,
                                                    float* inv, uint8_t* q8, float* y, int dim, int n_rows) {
-    extern __shared__ float P[];
-    __shared__ float G[8];
+    extern __shared__ float P[];  // 2 * dim/16 chunk partials
+    __shared__ float G[8], G2[16];
     __shared__ float irs;
     const int e = blockIdx.x, s = blockIdx.y, l = threadIdx.x;
     const float* xs = x + (int64_t)s * dim;
-    if (norm) {
-        const float ss = rorder_dot(xs, xs, dim, P, G);
-        if (l == 0) irs = 1.0f / sqrtf(ss / (float)dim + 1e-6f);  // correctly rounded (HIP default)
-        __syncthreads();  // irs set; P and G free for the next dot
+    float t;
+    if (norm) {  // both R-order dots in one pass: x.x (P) and w.x (Q), each in its own order
+        const float* w = W + (int64_t)e * dim;
+        float* Q = P + (dim >> 4);
+        for (int c = l; c < (dim >> 4); c += 64) {
+            const float4* w4 = reinterpret_cast<const float4*>(w + 16 * c);
+            const float4* x4 = reinterpret_cast<const float4*>(xs + 16 * c);
+            float p = 0.0f, q = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float4 a = w4[k], b = x4[k];
+                p = fmaf(b.x, b.x, p);
+                p = fmaf(b.y, b.y, p);
+                p = fmaf(b.z, b.z, p);
+                p = fmaf(b.w, b.w, p);
+                q = fmaf(a.x, b.x, q);
+                q = fmaf(a.y, b.y, q);
+                q = fmaf(a.z, b.z, q);
+                q = fmaf(a.w, b.w, q);
+            }
+            P[c] = p;
+            Q[c] = q;
+        }
+        __syncthreads();
+        const int C = dim >> 7;
+        if (l < 16) G2[l] = group_sum((l < 8 ? P : Q) + (l & 7) * C, C);
+        __syncthreads();
+        t = 0.0f;
+        if (l == 0) {
+            float ss = 0.0f;
+            for (int g = 0; g < 8; ++g) ss = ss + G2[g];
+            for (int g = 0; g < 8; ++g) t = t + G2[8 + g];
+            irs = 1.0f / sqrtf(ss / (float)dim + 1e-6f);  // correctly rounded (HIP default)
+        }
+    } else {
+        t = rorder_dot(W + (int64_t)e * dim, xs, dim, P, G);
     }
-    float t = rorder_dot(W + (int64_t)e * dim, xs, dim, P, G);
     const float ir = norm ? irs : 1.0f;
     if (l == 0) {
         if (norm) t = t * ir;
@@ -321,30 +540,8 @@ __global__ __launch_bounds__(256) void k_topk_router(const float* logits, const 
     }
     __syncthreads();
     if (E <= 256) {
-        // one thread per logit: its rank is the number of logits ahead of it
-        // in the order above, counted with the branch-free keys of rank_key
-        // (a total order: ranks are distinct); ranks < k are the chosen, in
-        // rank order
         __shared__ uint64_t key[256];
-        if (t < E) key[t] = rank_key(sv[t], t);
-        __syncthreads();
-        if (t < E) {
-            const float v = sv[t];
-            const uint64_t kt = key[t];
-            int rank = 0;
-            for (int i0 = 0; i0 < E; i0 += 16) {  // 16 keys per step, their LDS reads issued together
-                uint64_t c[16];
-#pragma unroll
-                for (int q = 0; q < 16; ++q) c[q] = key[min(i0 + q, E - 1)];
-#pragma unroll
-                for (int q = 0; q < 16; ++q) rank += (i0 + q < E && c[q] > kt) ? 1 : 0;
-            }
-            if (rank < k) {
-                selv[rank] = v;
-                seli[rank] = t;
-            }
-        }
-        __syncthreads();
+        topk_rank_select(sv, E, k, key, selv, seli);
     }
     for (int j = 0; E > 256 && j < k; ++j) {
         float bv = 0.0f;
@@ -371,16 +568,9 @@ __global__ __launch_bounds__(256) void k_topk_router(const float* logits, const 
         }
         __syncthreads();
     }
-    // softmax over the chosen: thread j < k computes exp(l_j - l_max), the
-    // sum runs in rank order from 0.0f (the same bits as one thread doing all)
     __shared__ float exv[32];
-    if (t < k) exv[t] = expf_portable(selv[t] - selv[0]);
-    __syncthreads();
+    const float w = topk_softmax(selv, seli, k, escale, exv);
     if (t < k) {
-        float denom = 0.0f;
-        for (int j = 0; j < k; ++j) denom = denom + exv[j];
-        float w = exv[t] / denom;
-        if (escale) w = w * escale[seli[t]];
         ids[(int64_t)s * k + t] = seli[t];
         wts[(int64_t)s * k + t] = w;
     }
@@ -636,7 +826,7 @@ int launch_route_prep(void* stream, const float* w, const float* x, const float*
     // every q8 block needs a workgroup: rows >= ceil(blocks / 16)
     if (n_rows * 16 < dim / 32) return fail(FT_HIP_E_SHAPE, "route_prep: %lld rows cannot quantize %lld blocks",
                                             (long long)n_rows, (long long)(dim / 32));
-    hipLaunchKernelGGL(k_route_prep, dim3((unsigned)n_rows, (unsigned)n_seqs), dim3(64), (size_t)(dim / 16) * 4,
+    hipLaunchKernelGGL(k_route_prep, dim3((unsigned)n_rows, (unsigned)n_seqs), dim3(64), (size_t)(dim / 16) * 8,
                        S(stream), w, x, bias, norm, inv, (uint8_t*)q8, y, (int)dim, (int)n_rows);
     return launch_status("route_prep");
 }
@@ -648,6 +838,41 @@ int launch_rms_inv(void* stream, const float* x, float* inv, int64_t dim, int64_
     return launch_status("rms_inv");
 }
 }  // namespace ft
+
+extern "C" int ft_hip_gemv_gate_up_act(ft_hip_ctx* ctx, void* stream, const void* base, uint64_t expert_bytes,
+                                       const int32_t* slots, int64_t n_pairs, int64_t x_div, const void* q8x,
+                                       int64_t hidden, int64_t inter, int layout, const float* in_scale,
+                                       void* q8_act) {
+    clear_error();
+    const char* nm = "gemv_gate_up_act";
+    if (hidden <= 0 || hidden % 32 || hidden > 32 * 4096)
+        return fail(FT_HIP_E_SHAPE, "%s: hidden=%lld must be a positive multiple of 32 up to 131072", nm, (long long)hidden);
+    if (inter <= 0 || inter % 32) return fail(FT_HIP_E_SHAPE, "%s: inter=%lld must be a positive multiple of 32", nm, (long long)inter);
+    if (n_pairs < 0 || n_pairs > 65535 || x_div <= 0) return fail(FT_HIP_E_SHAPE, "%s: n_pairs or x_div out of range", nm);
+    if (int rc = check_layout(layout)) return rc;
+    if (layout == FT_LAYOUT_Q4R && ((reinterpret_cast<uintptr_t>(base) | expert_bytes) & 15))
+        return fail(FT_HIP_E_SHAPE, "%s: q4r banks need 16-byte aligned base and expert_bytes", nm);
+    if ((int64_t)expert_bytes < 2 * inter * row_bytes_of(layout, (int)hidden))
+        return fail(FT_HIP_E_SHAPE, "%s: expert_bytes too small for the gate|up rows", nm);
+    if (!ctx || !base || !slots || !q8x || !q8_act) return fail(FT_HIP_E_INVALID, "%s: null argument", nm);
+    if (n_pairs == 0) return FT_HIP_OK;
+    GemvArgs a{};
+    a.base = (const uint8_t*)base;
+    a.expert_bytes = expert_bytes;
+    a.slots = slots;
+    a.x_div = (int)x_div;
+    a.q8 = (const uint8_t*)q8x;
+    a.q8_stride_blocks = hidden / 32;
+    a.n_rows = (int)(2 * inter);
+    a.k = (int)hidden;
+    auto kern = layout == FT_LAYOUT_Q4R ? k_gemv_gu_act<FT_LAYOUT_Q4R, false, GU_LANES>
+                                        : k_gemv_gu_act<FT_LAYOUT_Q4_0, false, GU_LANES>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)(inter / 32), (unsigned)n_pairs), dim3(64 * GU_LANES),
+                       (size_t)(hidden / 32) * Q8_BLK,
+                       S(stream), a, (int)inter, (uint8_t*)q8_act, in_scale, (int)x_div, (const float*)nullptr,
+                       (const float*)nullptr, (int32_t*)nullptr, (float*)nullptr, 0);
+    return launch_status(nm);
+}
 
 extern "C" int ft_hip_topk_router(ft_hip_ctx* ctx, void* stream, const float* logits, const float* expert_scale,
                                   int32_t* ids, float* wts, int64_t e_count, int64_t k, int64_t n_seqs) {
@@ -718,7 +943,6 @@ extern "C" int ft_hip_gen_q4_rows(ft_hip_ctx* ctx, void* stream, uint64_t key, i
 struct LayerWs {
     float* logits;
     uint8_t* q8x;
-    float* ygu;
     uint8_t* q8a;
     float* ydn;
     float* inv;         // [B] input RMS norm scales
@@ -732,7 +956,6 @@ static LayerWs layer_ws(void* base, int64_t B, int64_t H, int64_t I, int64_t E, 
     uint8_t* p = (uint8_t*)base;
     w.logits = (float*)(p + off); off += up(sizeof(float) * B * E);
     w.q8x = p + off; off += up((size_t)B * (H / 32) * Q8_BLK);
-    w.ygu = (float*)(p + off); off += up(sizeof(float) * B * K * 2 * I);
     w.q8a = p + off; off += up((size_t)B * K * (I / 32) * Q8_BLK);
     w.ydn = (float*)(p + off); off += up(sizeof(float) * B * K * H);
     w.inv = (float*)(p + off); off += up(sizeof(float) * B);
@@ -765,6 +988,9 @@ extern "C" int ft_hip_moe_layer(ft_hip_ctx* ctx, void* stream, const float* x, f
     const LayerWs w = layer_ws(workspace, n_seqs, hidden, inter, n_experts, top_k);
     if (workspace_bytes < w.bytes) return fail(FT_HIP_E_SHAPE, "%s: workspace_bytes=%zu < %zu", nm, workspace_bytes, w.bytes);
     if (!ctx || !x || !x_out || !router_w || !bank || !ids || !wts || !workspace) return fail(FT_HIP_E_INVALID, "%s: null argument", nm);
+    if (hidden > 32 * 4096 || inter > 32 * 4096) return fail(FT_HIP_E_SHAPE, "%s: rows longer than 131072", nm);
+    if (layout == FT_LAYOUT_Q4R && ((reinterpret_cast<uintptr_t>(bank) | expert_bytes | (uint64_t)gu_bytes) & 15))
+        return fail(FT_HIP_E_SHAPE, "%s: q4r banks need 16-byte aligned base and expert_bytes", nm);
     if (n_seqs == 0) return FT_HIP_OK;
     int rc;
     const float* inv = ctx->input_norm ? w.inv : nullptr;
@@ -778,7 +1004,10 @@ extern "C" int ft_hip_moe_layer(ft_hip_ctx* ctx, void* stream, const float* x, f
             return rc;
         if ((rc = ft_hip_quantize_q8(ctx, stream, x, hidden, w.q8x, hidden, n_seqs))) return rc;
     }
-    if ((rc = ft_hip_topk_router(ctx, stream, w.logits, expert_scale, ids, wts, n_experts, top_k, n_seqs))) return rc;
+    // top-k in the gate|up launch when the logits fit one thread each
+    const bool topk_in = n_experts <= 256;
+    if (!topk_in && (rc = ft_hip_topk_router(ctx, stream, w.logits, expert_scale, ids, wts, n_experts, top_k, n_seqs)))
+        return rc;
     const int64_t n_pairs = n_seqs * top_k;
     GemvArgs a{};
     a.base = (const uint8_t*)bank;
@@ -789,18 +1018,42 @@ extern "C" int ft_hip_moe_layer(ft_hip_ctx* ctx, void* stream, const float* x, f
     a.x_div = (int)top_k;  // pair p reads token p / top_k
     a.q8 = w.q8x;
     a.q8_stride_blocks = hidden / 32;
-    a.y = w.ygu;
-    a.y_stride = 2 * inter;
-    if ((rc = gemv_common(ctx, stream, a, n_pairs, 2 * inter, hidden, layout, false, "moe_layer/gate_up"))) return rc;
-    hipLaunchKernelGGL(k_gelu_mul_q8, dim3((unsigned)((n_pairs * inter + 255) / 256)), dim3(256), 0, S(stream),
-                       (const float*)w.ygu, w.q8a, (int)inter, n_pairs, inv, (int)top_k);
-    if ((rc = launch_status("moe_layer/gelu_mul_q8"))) return rc;
+    // gate|up with GELU*up and q8 (one launch), then down with the combine
+    // (one launch when the k activation rows of a seq fit in LDS together)
+    a.n_rows = (int)(2 * inter);
+    a.k = (int)hidden;
+    const dim3 g_gu((unsigned)(inter / 32), (unsigned)n_pairs);
+    const size_t l_gu = (size_t)(hidden / 32) * Q8_BLK;
+    {
+        auto kern = layout == FT_LAYOUT_Q4R
+                        ? (topk_in ? k_gemv_gu_act<FT_LAYOUT_Q4R, true, GU_LANES>
+                                   : k_gemv_gu_act<FT_LAYOUT_Q4R, false, GU_LANES>)
+                        : (topk_in ? k_gemv_gu_act<FT_LAYOUT_Q4_0, true, GU_LANES>
+                                   : k_gemv_gu_act<FT_LAYOUT_Q4_0, false, GU_LANES>);
+        hipLaunchKernelGGL(kern, g_gu, dim3(64 * GU_LANES), l_gu, S(stream), a, (int)inter, w.q8a, inv, (int)top_k,
+                           (const float*)w.logits, expert_scale, ids, wts, (int)n_experts);
+    }
+    if ((rc = launch_status("moe_layer/gate_up_act"))) return rc;
     a.bank_off = (uint64_t)gu_bytes;
     a.x_div = 1;
     a.q8 = w.q8a;
     a.q8_stride_blocks = inter / 32;
     a.y = w.ydn;
     a.y_stride = hidden;
+    const size_t l_dn = (size_t)top_k * (inter / 32) * Q8_BLK;
+    if (32 % top_k == 0 && l_dn <= 64 * 1024) {
+        a.n_rows = (int)hidden;
+        a.k = (int)inter;
+        // 16 lanes per row for long rows (at least 256 blocks) when k divides 16
+        const bool l16 = inter / 32 >= 256 && 16 % top_k == 0;
+        const int R = (int)((l16 ? 16 : 32) / top_k);
+        const dim3 g_dn((unsigned)((hidden + R - 1) / R), (unsigned)n_seqs);
+        auto kern = layout == FT_LAYOUT_Q4R
+                        ? (l16 ? k_gemv_down_combine<FT_LAYOUT_Q4R, 16> : k_gemv_down_combine<FT_LAYOUT_Q4R, 8>)
+                        : (l16 ? k_gemv_down_combine<FT_LAYOUT_Q4_0, 16> : k_gemv_down_combine<FT_LAYOUT_Q4_0, 8>);
+        hipLaunchKernelGGL(kern, g_dn, dim3(256), l_dn, S(stream), a, (const float*)wts, x, x_out, (int)top_k);
+        return launch_status("moe_layer/down_combine");
+    }
     if ((rc = gemv_common(ctx, stream, a, n_pairs, hidden, inter, layout, false, "moe_layer/down"))) return rc;
     hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)((hidden + 255) / 256), (unsigned)n_seqs), dim3(256), 0,
                        S(stream), w.ydn, wts, x, x_out, (int)hidden, (int)top_k);

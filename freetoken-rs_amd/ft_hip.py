@@ -37,6 +37,7 @@ SIGNATURES = {
                                           _I64, _I]),
     "ft_hip_q4q8_block_dots": (_I, [_P, _P, _P, _U64, _U64, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _I]),
     "ft_hip_gelu_mul_q8": (_I, [_P, _P, _P, _P, _I64, _I64]),
+    "ft_hip_gemv_gate_up_act": (_I, [_P, _P, _P, _U64, _P, _I64, _I64, _P, _I64, _I64, _I, _P, _P]),
     "ft_hip_router_logits": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64]),
     "ft_hip_topk_router": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64]),
     "ft_hip_reduce_pairs_weighted": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64]),
@@ -185,6 +186,13 @@ class Q4Gemv:
     # -- ft-cuda/src/lib.rs:354-374 --
     def gelu_mul_q8(self, gu, q8, inter, n, stream=None):
         check(lib().ft_hip_gelu_mul_q8(self._ctx, _stream(stream), _ptr(gu), _ptr(q8), inter, n))
+
+    # -- ft-model/src/lib.rs:1584-1593 (gate|up GEMV then gelu_mul_q8), one launch --
+    def gemv_gate_up_act(self, bank, expert_bytes, slots, n_pairs, x_div, q8x, hidden, inter, q8_act,
+                         layout=LAYOUT_Q4R, in_scale=None, stream=None):
+        check(lib().ft_hip_gemv_gate_up_act(self._ctx, _stream(stream), _ptr(bank), expert_bytes, _ptr(slots),
+                                            n_pairs, x_div, _ptr(q8x), hidden, inter, layout, _ptr(in_scale),
+                                            _ptr(q8_act)))
 
     # -- ft-cuda/src/lib.rs:674-694 --
     def gemv_f32_rows_dev(self, w, x, y, dim, n_rows, n_seqs, bias=None, stream=None):

@@ -116,6 +116,21 @@ int ft_hip_q4q8_block_dots(ft_hip_ctx* ctx, void* stream, const void* base,
 int ft_hip_gelu_mul_q8(ft_hip_ctx* ctx, void* stream, const float* gu, void* q8, int64_t inter,
                        int64_t n);
 
+/* Gate|up GEMV and the activation in one launch: replaces gemv_q4r_ptr over
+ * the gate|up rows followed by gelu_mul_q8 (ft-model/src/lib.rs:1584-1593;
+ * ft-cuda/src/lib.rs:354-374). Pair p runs expert slots[p] (gate|up rows
+ * [2I x H] at base + slots[p]*expert_bytes, in `layout`) against q8 row
+ * p / x_div of q8x ([*, H/32] blocks); the gate and up sums are multiplied by
+ * in_scale[p / x_div] when in_scale is not NULL (the input RMS norm).
+ * q8_act: [n_pairs, I/32] blocks of gelu_tanh(gate) * up, the arithmetic of
+ * ft_hip_gelu_mul_q8; the f32 gate and up sums run in 4 lane chains per row
+ * (lane s: blocks s, s+4, ...; ft_hip_gemv_q4_grouped_slots uses 8), so
+ * they may differ from that GEMV's in the last bits. */
+int ft_hip_gemv_gate_up_act(ft_hip_ctx* ctx, void* stream, const void* base, uint64_t expert_bytes,
+                            const int32_t* slots, int64_t n_pairs, int64_t x_div, const void* q8x,
+                            int64_t hidden, int64_t inter, int layout, const float* in_scale,
+                            void* q8_act);
+
 /* Replaces gemv_f32_rows_dev (ft-cuda/src/lib.rs:674-694): router logits
  * y[s][e] = sum_i W[e][i] * x[s][i] in this library's R-order (chunks of 16
  * elements by fma, 8 groups of dim/128 chunks, summed in order), plus bias[e]
@@ -161,6 +176,10 @@ int ft_hip_gen_q4_rows(ft_hip_ctx* ctx, void* stream, uint64_t key, int64_t row0
  * ft-model/src/lib.rs:1406-1476 with host routing replaced by device routing):
  *   logits = router(W_r, x) (+bias) -> top-k/softmax -> q8(x) -> grouped
  *   gate|up GEMV -> gelu*up -> q8 -> grouped down GEMV -> x_out = x + combine.
+ * Three launches: logits with q8(x); gate|up with the top-k (n_experts <= 256)
+ * and the activation; down with the combine (top_k dividing 32 and the k
+ * activation rows of a token within 64 KB). Other shapes add a top-k launch
+ * or a separate combine launch; the results are the same bits either way.
  * Expert e of this layer: gate|up rows [2I x H] at bank + e*expert_bytes,
  * down rows [H x I] right after them (gu_bytes = 2I * row_bytes(H)), both in
  * `layout`. x_out may equal x. workspace: device scratch of

@@ -359,6 +359,70 @@ def test_moe_layer_batched_two_layers(gemv, orc, gemma_layers):
         x = xo
 
 
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("scaled", [False, True])
+def test_gemv_gate_up_act_matches_two_launches(gemv, layout, scaled):
+    """ft_hip_gemv_gate_up_act against the grouped gate|up GEMV followed by
+    gelu_mul_q8 (on the sums times the scale, in f32), for 5 pairs over 2 q8
+    rows (x_div 3) of a small bank in both layouts. The two sum each row in a
+    different lane order, so the activations agree to the north-star
+    tolerance (max-abs 1e-3 of the L2 norm) and nearly every quant is equal."""
+    shape = moe_synth.Shape("small", 384, 160, 24, 3, 1, 9)
+    m = moe_synth.SyntheticMoE(gemv, shape, n_layers=1, layout=layout)
+    H, I, n = shape.hidden, shape.inter, 5
+    x = torch.stack([m.hidden(t) for t in range(2)])
+    q8x = torch.zeros(2 * (H // 32) * 40, dtype=torch.uint8, device=DEV)
+    gemv.quantize_q8(x, H, q8x, H, 2)
+    slots = torch.tensor([3, 17, 3, 0, 23], dtype=torch.int32, device=DEV)
+    sc = torch.tensor([0.75, 1.3125], dtype=torch.float32, device=DEV)
+    bank = m.banks[:shape.n_experts * m.expert_bytes]
+    out = torch.zeros(n * (I // 32) * 40, dtype=torch.uint8, device=DEV)
+    gemv.gemv_gate_up_act(bank, m.expert_bytes, slots, n, 3, q8x, H, I, out, layout=layout,
+                          in_scale=sc if scaled else None)
+    xi = torch.tensor([p // 3 for p in range(n)], dtype=torch.int32, device=DEV)
+    ygu = torch.zeros(n * 2 * I, dtype=torch.float32, device=DEV)
+    gemv.gemv_grouped_slots(bank, m.expert_bytes, 0, slots, xi, n, q8x, H // 32, ygu, 2 * I, 2 * I, H, layout)
+    if scaled:
+        ygu = (ygu.view(n, 2 * I) * sc[xi.long()].view(n, 1)).contiguous()
+    ref = torch.zeros_like(out)
+    gemv.gelu_mul_q8(ygu, ref, I, n)
+    d, _, qs = q8_split(host(out), n, I // 32)
+    d_r, _, qs_r = q8_split(host(ref), n, I // 32)
+    a_out = (d[:, :, None] * qs.reshape(n, I // 32, 32)).ravel()
+    a_ref = (d_r[:, :, None] * qs_r.reshape(n, I // 32, 32)).ravel()
+    assert np.max(np.abs(a_out - a_ref)) <= 1e-3 * np.linalg.norm(a_ref)
+    assert np.mean(qs == qs_r) >= 0.99
+
+
+@pytest.mark.parametrize("layout,top_k,n_experts,hidden,inter",
+                         [(0, 2, 24, 384, 160), (1, 4, 24, 384, 160), (0, 3, 24, 384, 160), (1, 6, 24, 384, 160),
+                          (1, 4, 300, 384, 160), (0, 2, 8, 128, 8192), (1, 8, 16, 256, 8192)])
+def test_moe_layer_small_shapes(gemv, orc, layout, top_k, n_experts, hidden, inter):
+    """Small layers in both weight layouts, 3 tokens: top-k 2, 4 and 8 take the
+    down launch that combines the k pairs of a token in one workgroup (16 lanes
+    per row for rows of 256+ blocks and k dividing 16, else 8), 3 and 6 (not
+    dividing 32) the separate down and combine launches; up to 256 experts
+    are routed inside the gate|up launch, 300 by the separate top-k launch.
+    Ids and weights exact against the oracle, outputs within tolerance."""
+    shape = moe_synth.Shape("small", hidden, inter, n_experts, top_k, 1, 9)
+    m = moe_synth.SyntheticMoE(gemv, shape, n_layers=1, layout=layout)
+    H, I, k, B = shape.hidden, shape.inter, top_k, 3
+    x = torch.stack([m.hidden(t) for t in range(B)])
+    ws = m.workspace(B)
+    ids = torch.zeros(B * k, dtype=torch.int32, device=DEV)
+    wts = torch.zeros(B * k, dtype=torch.float32, device=DEV)
+    xo = torch.zeros_like(x)
+    m.layer(0, x, xo, ids, wts, ws, n_seqs=B)
+    xin, ids_h, wts_h, xo_h = host(x), host(ids).reshape(B, k), host(wts).reshape(B, k), host(xo)
+    Wr = host(m.routers[0])
+    gu_b, dn_b = _oracle_banks(m, 0, sorted(set(ids_h.ravel().tolist())))
+    for t in range(B):
+        ref = orc.moe_layer(xin[t], Wr, gu_b, dn_b, H, I, k, layout=layout)
+        assert np.array_equal(ids_h[t], ref["ids"]) and np.array_equal(wts_h[t], ref["wts"]), t
+        d_ref = ref["x_out"] - xin[t]
+        assert np.max(np.abs((xo_h[t] - xin[t]) - d_ref)) <= 1e-3 * np.linalg.norm(d_ref), t
+
+
 @pytest.mark.parametrize("norm", [False, True])
 def test_moe_layer_large_expert(gemv, orc, norm):
     """Config 5's shape (H 4096, 8 experts of I 14336, top-2): one layer, 3 tokens
