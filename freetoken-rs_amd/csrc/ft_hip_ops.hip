@@ -183,7 +183,7 @@ __device__ __forceinline__ float sum_row_lanes(float acc) {
     acc += __shfl_xor(acc, 1);
     acc += __shfl_xor(acc, 2);
     if (LPR >= 8) acc += __shfl_xor(acc, 4);
-    if (LPR == 16) acc += __shfl_xor(acc, 8);
+    if (LPR >= 16) acc += __shfl_xor(acc, 8);
     return acc;
 }
 
@@ -388,13 +388,13 @@ __device__ __forceinline__ float group_sum(const float* p, int n) {
     return s;
 }
 
-// R-order dot w.xs of one wavefront (the value is returned in lane 0):
-// lane c computes chunk partials P_c (16-element fma chains), lanes 0..7 sum
-// their group's chunks in order, lane 0 sums the 8 groups in order.
+// R-order dot w.xs of one workgroup (the value is returned in thread 0):
+// thread c computes chunk partials P_c (16-element fma chains), threads 0..7
+// sum their group's chunks in order, thread 0 sums the 8 groups in order.
 __device__ __forceinline__ float rorder_dot(const float* w, const float* xs, int dim, float* P, float* G) {
     const int l = threadIdx.x;
     const int nch = dim >> 4;
-    for (int c = l; c < nch; c += 64) {
+    for (int c = l; c < nch; c += blockDim.x) {
         const float4* w4 = reinterpret_cast<const float4*>(w + 16 * c);
         const float4* x4 = reinterpret_cast<const float4*>(xs + 16 * c);
         float p = 0.0f;
@@ -420,8 +420,8 @@ __device__ __forceinline__ float rorder_dot(const float* w, const float* xs, int
 
 // Router logits in the R-order (replaces gemv_f32_rows, q4.cu:1153-1174),
 // times in_scale[s] (input RMS norm) when given, then + bias.
-// Grid (n_rows, n_seqs), one wavefront per logit.
-__global__ __launch_bounds__(64) void k_router_logits(const float* W, const float* x, const float* bias,
+// Grid (n_rows, n_seqs), one 256-thread workgroup per logit.
+__global__ __launch_bounds__(256) void k_router_logits(const float* W, const float* x, const float* bias,
                                                       const float* in_scale, float* y, int dim, int n_rows) {
     extern __shared__ float P[];  // dim/16 chunk partials
     __shared__ float G[8];
@@ -434,13 +434,13 @@ __global__ __launch_bounds__(64) void k_router_logits(const float* W, const floa
     }
 }
 
-// The head of a layer in one launch (grid (n_rows, n_seqs), one wavefront per
+// The head of a layer in one launch (grid (n_rows, n_seqs), one workgroup per
 // logit): router logits as k_router_logits, with the input RMS norm's scale
 // computed by each workgroup for its seq (the same R-order self-dot as
 // k_rms_inv, so the same bits) when norm is set; workgroup (e, s) with e <
 // ceil(nb/16) also quantizes blocks 16e..16e+15 of x_s to q8 (the
 // arithmetic of k_quantize_q8) and e == 0 stores inv[s].
-__global__ __launch_bounds__(64) void k_route_prep(const float* W, const float* x, const float* bias, int norm,
+__global__ __launch_bounds__(256) void k_route_prep(const float* W, const float* x, const float* bias, int norm,
                                                    float* inv, uint8_t* q8, float* y, int dim, int n_rows) {
     extern __shared__ float P[];  // 2 * dim/16 chunk partials
     __shared__ float G[8], G2[16];
@@ -451,7 +451,7 @@ __global__ __launch_bounds__(64) void k_route_prep(const float* W, const float* 
     if (norm) {  // both R-order dots in one pass: x.x (P) and w.x (Q), each in its own order
         const float* w = W + (int64_t)e * dim;
         float* Q = P + (dim >> 4);
-        for (int c = l; c < (dim >> 4); c += 64) {
+        for (int c = l; c < (dim >> 4); c += blockDim.x) {
             const float4* w4 = reinterpret_cast<const float4*>(w + 16 * c);
             const float4* x4 = reinterpret_cast<const float4*>(xs + 16 * c);
             float p = 0.0f, q = 0.0f;
@@ -493,14 +493,14 @@ __global__ __launch_bounds__(64) void k_route_prep(const float* W, const float* 
     }
     const int nb = dim >> 5, b = e * 16 + (l >> 2);
     if (e * 16 < nb) {  // uniform per workgroup; the quads of blocks beyond nb idle
-        if (b < nb)
+        if (l < 64 && b < nb)
             quantize_block_quad(xs + 32 * b, l & 3, reinterpret_cast<uint32_t*>(q8 + ((int64_t)s * nb + b) * Q8_BLK));
     }
 }
 
 // Scale of the input RMS norm per seq: inv[s] = 1 / sqrt(ss / dim + 1e-6),
 // ss = x_s.x_s in the R-order, each op rounded once. Grid n_seqs.
-__global__ __launch_bounds__(64) void k_rms_inv(const float* x, float* inv, int dim) {
+__global__ __launch_bounds__(256) void k_rms_inv(const float* x, float* inv, int dim) {
     extern __shared__ float P[];
     __shared__ float G[8];
     const int s = blockIdx.x;
@@ -815,7 +815,7 @@ namespace ft {
 int launch_router_logits(void* stream, const float* w, const float* x, const float* bias, const float* in_scale,
                          float* y, int64_t dim, int64_t n_rows, int64_t n_seqs) {
     if (n_rows == 0 || n_seqs == 0) return FT_HIP_OK;
-    hipLaunchKernelGGL(k_router_logits, dim3((unsigned)n_rows, (unsigned)n_seqs), dim3(64), (size_t)(dim / 16) * 4,
+    hipLaunchKernelGGL(k_router_logits, dim3((unsigned)n_rows, (unsigned)n_seqs), dim3(256), (size_t)(dim / 16) * 4,
                        S(stream), w, x, bias, in_scale, y, (int)dim, (int)n_rows);
     return launch_status("router_logits");
 }
@@ -826,14 +826,14 @@ int launch_route_prep(void* stream, const float* w, const float* x, const float*
     // every q8 block needs a workgroup: rows >= ceil(blocks / 16)
     if (n_rows * 16 < dim / 32) return fail(FT_HIP_E_SHAPE, "route_prep: %lld rows cannot quantize %lld blocks",
                                             (long long)n_rows, (long long)(dim / 32));
-    hipLaunchKernelGGL(k_route_prep, dim3((unsigned)n_rows, (unsigned)n_seqs), dim3(64), (size_t)(dim / 16) * 8,
+    hipLaunchKernelGGL(k_route_prep, dim3((unsigned)n_rows, (unsigned)n_seqs), dim3(256), (size_t)(dim / 16) * 8,
                        S(stream), w, x, bias, norm, inv, (uint8_t*)q8, y, (int)dim, (int)n_rows);
     return launch_status("route_prep");
 }
 
 int launch_rms_inv(void* stream, const float* x, float* inv, int64_t dim, int64_t n_seqs) {
     if (n_seqs == 0) return FT_HIP_OK;
-    hipLaunchKernelGGL(k_rms_inv, dim3((unsigned)n_seqs), dim3(64), (size_t)(dim / 16) * 4, S(stream), x, inv,
+    hipLaunchKernelGGL(k_rms_inv, dim3((unsigned)n_seqs), dim3(256), (size_t)(dim / 16) * 4, S(stream), x, inv,
                        (int)dim);
     return launch_status("rms_inv");
 }
