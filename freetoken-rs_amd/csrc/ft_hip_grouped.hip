@@ -142,7 +142,7 @@ __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t* ids, int P,
 // (input RMS norm, or null): a token's gate|up sums are first multiplied by
 // in_scale[token].
 template <int BPW>
-__global__ __launch_bounds__(GT, 1) void k_grouped_gu(const uint8_t* bank, int64_t expert_bytes, const int32_t* meta,
+__global__ __launch_bounds__(GT, 2) void k_grouped_gu(const uint8_t* bank, int64_t expert_bytes, const int32_t* meta,
                                                       const int32_t* plist, const uint8_t* q8x, uint8_t* q8a,
                                                       float* dbg_gu, const float* in_scale, int H, int I, int E,
                                                       int K, int n_mfma) {
@@ -170,26 +170,51 @@ __global__ __launch_bounds__(GT, 1) void k_grouped_gu(const uint8_t* bank, int64
 #pragma unroll
         for (int i = 0; i < BPW; ++i) sc[i] = *reinterpret_cast<const uint16_t*>(T + (b0 + i) * 128 + r * 2);
     }
+    __shared__ int ctok[NT];
     for (int c0 = 0; c0 < n; c0 += NT) {
         const int nt = min(NT, n - c0);
         __syncthreads();  // the previous chunk's LDS is consumed
-        stage<16>(  // x q8 of this chunk's tokens
-            nt * nb * 10,
-            [&](int i) {
-                const int tt = i / (nb * 10), rem = i - tt * nb * 10;
-                const int tok = plist[s0 + c0 + tt] / K;
-                return reinterpret_cast<const uint32_t*>(q8x + (int64_t)tok * nb * Q8_BLK)[rem];
-            },
-            [&](int i, uint32_t v) {
-                const int tt = i / (nb * 10), rem = i - tt * nb * 10, b = rem / 10, wd = rem - b * 10;
-                if (wd >= 2) reinterpret_cast<uint32_t*>(xq)[(tt * nb + b) * 8 + (wd - 2)] = v;
-                else reinterpret_cast<uint32_t*>(xp)[(tt * nb + b) * 2 + wd] = v;
-            });
+        if (t < nt) ctok[t] = plist[s0 + c0 + t] / K;
         __syncthreads();
-        for (int tt = 0; tt < nt; ++tt) {  // one token at a time: its BPW blocks' LDS reads in one batch
+        {  // x q8 of this chunk's tokens: every load issued before the first store
+            constexpr int W = 80 * BPW;  // q8 words per token (nb = 8 * BPW blocks of 10)
+            constexpr int MW = (W + GT - 1) / GT;
+            uint32_t v[NT][MW];
+#pragma unroll
+            for (int tt = 0; tt < NT; ++tt) {
+                const uint32_t* src =
+                    reinterpret_cast<const uint32_t*>(q8x + (int64_t)ctok[min(tt, nt - 1)] * nb * Q8_BLK);
+#pragma unroll
+                for (int m = 0; m < MW; ++m) {
+                    const int wi = t + m * GT;
+                    v[tt][m] = (tt < nt && wi < W) ? src[wi] : 0u;
+                }
+            }
+#pragma unroll
+            for (int tt = 0; tt < NT; ++tt) {
+#pragma unroll
+                for (int m = 0; m < MW; ++m) {
+                    const int wi = t + m * GT, b = wi / 10, wd = wi - b * 10;
+                    if (tt < nt && wi < W) {
+                        if (wd >= 2) reinterpret_cast<uint32_t*>(xq)[(tt * nb + b) * 8 + (wd - 2)] = v[tt][m];
+                        else reinterpret_cast<uint32_t*>(xp)[(tt * nb + b) * 2 + wd] = v[tt][m];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        for (int tt = 0; tt < nt; ++tt) {
+            // one token at a time, its blocks' LDS reads in batches of half
+            // the blocks. The weights pass through an opaque move per token:
+            // their nibble masks and f32 scales are not hoisted out of the
+            // token loop, where they would take ~100 more registers.
             float acc = 0.0f;
 #pragma unroll
+            for (int i = 0; i < BPW; ++i)
+                asm volatile("" : "+v"(qv[i].x), "+v"(qv[i].y), "+v"(qv[i].z), "+v"(qv[i].w), "+v"(sc[i]));
+#pragma unroll
             for (int i = 0; i < BPW; ++i) {
+                if (i % 4 == 0 && i > 0) __builtin_amdgcn_sched_barrier(0);
                 const int xb = tt * nb + b0 + i;
                 const int2 dq = xp[xb];
                 const int dot = block_dot_v(qv[i], xq[xb * 2], xq[xb * 2 + 1], dq.y);
