@@ -179,6 +179,10 @@ __global__ __launch_bounds__(GT, 2) void k_grouped_gu(const uint8_t* bank, int64
         {  // x q8 of this chunk's tokens: every load issued before the first store
             constexpr int W = 80 * BPW;  // q8 words per token (nb = 8 * BPW blocks of 10)
             constexpr int MW = (W + GT - 1) / GT;
+            // an opaque thread index: the LDS offsets below are not hoisted
+            // out of the chunk loop (they would stay live through the dots)
+            int tq = t;
+            asm volatile("" : "+v"(tq));
             uint32_t v[NT][MW];
 #pragma unroll
             for (int tt = 0; tt < NT; ++tt) {
@@ -186,7 +190,7 @@ __global__ __launch_bounds__(GT, 2) void k_grouped_gu(const uint8_t* bank, int64
                     reinterpret_cast<const uint32_t*>(q8x + (int64_t)ctok[min(tt, nt - 1)] * nb * Q8_BLK);
 #pragma unroll
                 for (int m = 0; m < MW; ++m) {
-                    const int wi = t + m * GT;
+                    const int wi = tq + m * GT;
                     v[tt][m] = (tt < nt && wi < W) ? src[wi] : 0u;
                 }
             }
@@ -194,7 +198,7 @@ __global__ __launch_bounds__(GT, 2) void k_grouped_gu(const uint8_t* bank, int64
             for (int tt = 0; tt < NT; ++tt) {
 #pragma unroll
                 for (int m = 0; m < MW; ++m) {
-                    const int wi = t + m * GT, b = wi / 10, wd = wi - b * 10;
+                    const int wi = tq + m * GT, b = wi / 10, wd = wi - b * 10;
                     if (tt < nt && wi < W) {
                         if (wd >= 2) reinterpret_cast<uint32_t*>(xq)[(tt * nb + b) * 8 + (wd - 2)] = v[tt][m];
                         else reinterpret_cast<uint32_t*>(xp)[(tt * nb + b) * 2 + wd] = v[tt][m];
@@ -203,9 +207,10 @@ __global__ __launch_bounds__(GT, 2) void k_grouped_gu(const uint8_t* bank, int64
             }
         }
         __syncthreads();
+#pragma unroll 1
         for (int tt = 0; tt < nt; ++tt) {
-            // one token at a time, its blocks' LDS reads in batches of half
-            // the blocks. The weights pass through an opaque move per token:
+            // one token at a time (not unrolled), its blocks' LDS reads in
+            // batches of four blocks. The weights pass through an opaque move per token:
             // their nibble masks and f32 scales are not hoisted out of the
             // token loop, where they would take ~100 more registers.
             float acc = 0.0f;
