@@ -61,7 +61,7 @@ def parse():
                          "shape at batch 1")
     ap.add_argument("--mfma-min", type=int, default=0,
                     help="grouped path: experts with at least this many tokens take the int8 MFMA kernels "
-                         "(0: automatic, every expert on MFMA from 2 pairs per expert on)")
+                         "(0: automatic, every expert on MFMA from 8 pairs per expert on)")
     ap.add_argument("--layers", type=int, default=0, help="0 = the config's layer count")
     ap.add_argument("--prefetch", type=int, choices=[0, 1], default=1,
                     help="fused path: stream the early-routed experts of the next layer ahead (1) or not (0)")

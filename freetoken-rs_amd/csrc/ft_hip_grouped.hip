@@ -687,10 +687,11 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
     if ((rc = ft_hip_topk_router(ctx, stream, w.logits, expert_scale, ids, wts, n_experts, top_k, n_seqs))) return rc;
     // groups of >= n_mfma tokens take the MFMA tile kernels, the others the
     // dot4 kernels; rows longer than 32 blocks (I > 1024) only the former.
-    // Automatic (0): every group on one family, MFMA from 2 pairs per expert
-    // on (measured: one family's launches beat a split of both)
+    // Automatic (0): every group on one family, MFMA from 8 pairs per expert
+    // on (measured on the Gemma shape: dot4 faster at 4 pairs per expert,
+    // MFMA at 8 and 16; one family's launches beat a split of both)
     int n_mfma = ctx->grouped_mfma_min;
-    if (n_mfma <= 0) n_mfma = (int64_t)P >= 2 * n_experts ? 1 : std::numeric_limits<int>::max();
+    if (n_mfma <= 0) n_mfma = (int64_t)P >= 8 * n_experts ? 1 : std::numeric_limits<int>::max();
     if (nbj > 32) n_mfma = 1;
     hipLaunchKernelGGL(k_group_pairs, dim3(1), dim3(1024), 0, s, (const int32_t*)ids, P, E, n_mfma, w.meta, w.plist,
                        w.ppos);

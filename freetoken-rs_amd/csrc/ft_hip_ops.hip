@@ -498,6 +498,76 @@ __global__ __launch_bounds__(256) void k_route_prep(const float* W, const float*
     }
 }
 
+// k_route_prep for 8 logits per workgroup (batched decode): workgroup
+// (eg, s) computes logits 8eg..8eg+7 of seq s, each in the R-order as
+// k_route_prep (the same bits), reading each chunk of x once for the 8 router
+// rows and the self-dot; and quantizes q8 blocks [eg*Q, eg*Q+Q) of x_s,
+// Q = ceil(nb / gridDim.x). e == 0's workgroup stores inv[s].
+// Grid (n_rows/8, n_seqs), 256 threads.
+__global__ __launch_bounds__(256) void k_route_prep8(const float* W, const float* x, const float* bias, int norm,
+                                                     float* inv, uint8_t* q8, float* y, int dim, int n_rows) {
+    extern __shared__ float P[];  // [9][dim/16] chunk partials: the 8 logits', then x.x
+    __shared__ float G[9][8], tot[9];
+    const int eg = blockIdx.x, s = blockIdx.y, l = threadIdx.x;
+    const int nch = dim >> 4;
+    const float* xs = x + (int64_t)s * dim;
+    const float* w0 = W + (int64_t)eg * 8 * dim;
+    for (int c = l; c < nch; c += blockDim.x) {
+        const float4* x4 = reinterpret_cast<const float4*>(xs + 16 * c);
+        float4 xv[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) xv[k] = x4[k];
+        float pe[8], ps = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float4* w4 = reinterpret_cast<const float4*>(w0 + (int64_t)j * dim + 16 * c);
+            float p = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float4 a = w4[k], b = xv[k];
+                p = fmaf(a.x, b.x, p);
+                p = fmaf(a.y, b.y, p);
+                p = fmaf(a.z, b.z, p);
+                p = fmaf(a.w, b.w, p);
+            }
+            pe[j] = p;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 b = xv[k];
+            ps = fmaf(b.x, b.x, ps);
+            ps = fmaf(b.y, b.y, ps);
+            ps = fmaf(b.z, b.z, ps);
+            ps = fmaf(b.w, b.w, ps);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) P[j * nch + c] = pe[j];
+        P[8 * nch + c] = ps;
+    }
+    __syncthreads();
+    const int C = dim >> 7;
+    if (l < 72) G[l >> 3][l & 7] = group_sum(P + (l >> 3) * nch + (l & 7) * C, C);
+    __syncthreads();
+    if (l < 9) {
+        float t = 0.0f;
+        for (int g = 0; g < 8; ++g) t = t + G[l][g];
+        tot[l] = t;
+    }
+    __syncthreads();
+    if (l < 8) {
+        const float ir = norm ? 1.0f / sqrtf(tot[8] / (float)dim + 1e-6f) : 1.0f;  // correctly rounded
+        const int e = eg * 8 + l;
+        float t = tot[l];
+        if (norm) t = t * ir;
+        if (bias) t = t + bias[e];
+        y[(int64_t)s * n_rows + e] = t;
+        if (norm && e == 0) inv[s] = ir;
+    }
+    const int nb = dim >> 5, Q = (nb + gridDim.x - 1) / gridDim.x, b = eg * Q + (l >> 2);
+    if ((l >> 2) < Q && b < nb)
+        quantize_block_quad(xs + 32 * b, l & 3, reinterpret_cast<uint32_t*>(q8 + ((int64_t)s * nb + b) * Q8_BLK));
+}
+
 // Scale of the input RMS norm per seq: inv[s] = 1 / sqrt(ss / dim + 1e-6),
 // ss = x_s.x_s in the R-order, each op rounded once. Grid n_seqs.
 __global__ __launch_bounds__(256) void k_rms_inv(const float* x, float* inv, int dim) {
@@ -826,6 +896,16 @@ int launch_route_prep(void* stream, const float* w, const float* x, const float*
     // every q8 block needs a workgroup: rows >= ceil(blocks / 16)
     if (n_rows * 16 < dim / 32) return fail(FT_HIP_E_SHAPE, "route_prep: %lld rows cannot quantize %lld blocks",
                                             (long long)n_rows, (long long)(dim / 32));
+    // larger batches: eight logits per workgroup (each chunk of x read once
+    // for them), when the rows split into eights that still cover the q8
+    // blocks at up to 64 per workgroup (measured: faster at 64 seqs, slower
+    // at 16, where the eighth as many workgroups no longer fill the chip)
+    if (n_seqs >= 32 && n_rows % 8 == 0 && (n_rows / 8) * 64 >= dim / 32) {
+        hipLaunchKernelGGL(k_route_prep8, dim3((unsigned)(n_rows / 8), (unsigned)n_seqs), dim3(256),
+                           (size_t)(dim / 16) * 9 * 4, S(stream), w, x, bias, norm, inv, (uint8_t*)q8, y, (int)dim,
+                           (int)n_rows);
+        return launch_status("route_prep8");
+    }
     hipLaunchKernelGGL(k_route_prep, dim3((unsigned)n_rows, (unsigned)n_seqs), dim3(256), (size_t)(dim / 16) * 8,
                        S(stream), w, x, bias, norm, inv, (uint8_t*)q8, y, (int)dim, (int)n_rows);
     return launch_status("route_prep");

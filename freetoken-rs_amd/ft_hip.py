@@ -272,7 +272,7 @@ class Q4Gemv:
 
     def set_grouped_mfma_min(self, n_tokens):
         """moe_layer_grouped: experts with >= n_tokens tokens take the MFMA kernels (0, the default:
-        all MFMA from 2 pairs per expert on, else all dot4)."""
+        all MFMA from 8 pairs per expert on, else all dot4)."""
         check(lib().ft_hip_set_grouped_mfma_min(self._ctx, int(n_tokens)))
 
     def fused_workspace_init(self, ws, stream=None):

@@ -221,7 +221,7 @@ int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const float* x, floa
  * v_mfma_i32_16x16x32_i8, one q4_0 block per instruction), the others the
  * v_dot4 kernels; results agree to f32 summation order (q8 quants, int32
  * block dots, routing and GELU q8 are the same). 0 (the default) = automatic:
- * every expert on the MFMA kernels when the batch has at least 2 (token,
+ * every expert on the MFMA kernels when the batch has at least 8 (token,
  * expert) pairs per expert, else every expert on the dot4 kernels; 1 = MFMA
  * for every expert. Rows longer than 1024 weights (inter > 1024) always take
  * the MFMA kernels. No reference counterpart (the reference runs one GEMV
