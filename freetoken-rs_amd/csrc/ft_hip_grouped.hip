@@ -90,17 +90,76 @@ __device__ __forceinline__ void stage(int n, Ld ld, St st) {
 // Groups are numbered with the experts of >= n_mfma tokens first (meta[1 +
 // 3E] of them, for the MFMA kernels), then the others (for the dot4
 // kernels), each in expert order.
+//
+// TOPK (E <= 32 as launched): the routing itself first, from the logits (the
+// arithmetic of k_topk_router, so the same ids and weights): 1024/E tokens
+// per round, one thread per logit ranking it by rank_key among its token's
+// E, then the softmax over each token's K in rank order; ids/wts written to
+// ids_out/wts_out and kept in LDS for the grouping.
+template <bool TOPK>
 __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t* ids, int P, int E, int n_mfma, int32_t* meta,
-                                                      int32_t* plist, int32_t* ppos) {
+                                                      int32_t* plist, int32_t* ppos, const float* logits,
+                                                      const float* escale, int32_t* ids_out, float* wts_out, int K) {
     __shared__ int cnt[1024];
     __shared__ int scan[1024];
     __shared__ int act[1024];
     __shared__ int big[1024];
+    __shared__ int sid[TOPK ? MAX_PAIRS : 1];
+    __shared__ uint64_t key[TOPK ? 1024 : 1];
+    __shared__ float sv[TOPK ? 1024 : 1], selv[TOPK ? 1024 : 1], exv[TOPK ? 1024 : 1];
+    __shared__ int seli[TOPK ? 1024 : 1];
     const int t = threadIdx.x;
+    if constexpr (TOPK) {
+        const int B = P / K, TPR = 1024 / E;  // tokens per round
+        const int slot = t / E, e = t - slot * E;
+        const int ss = t / K, rr = t - ss * K;  // softmax: token slot ss, rank rr
+        for (int r0 = 0; r0 < B; r0 += TPR) {
+            const bool on = slot < TPR && r0 + slot < B;
+            if (on) {
+                const float v = logits[(int64_t)(r0 + slot) * E + e];
+                sv[t] = v;
+                key[t] = rank_key(v, e);
+            }
+            __syncthreads();
+            if (on) {
+                const uint64_t kt = key[t];
+                const uint64_t* kr = key + slot * E;
+                int rank = 0;
+                for (int i0 = 0; i0 < E; i0 += 16) {  // 16 keys per step, their LDS reads issued together
+                    uint64_t c[16];
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) c[q] = kr[min(i0 + q, E - 1)];
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) rank += (i0 + q < E && c[q] > kt) ? 1 : 0;
+                }
+                if (rank < K) {
+                    selv[slot * K + rank] = sv[t];
+                    seli[slot * K + rank] = e;
+                }
+            }
+            __syncthreads();
+            const bool on2 = ss < TPR && r0 + ss < B;
+            if (on2) exv[t] = expf_portable(selv[t] - selv[ss * K]);
+            __syncthreads();
+            if (on2) {
+                float denom = 0.0f;
+                for (int j = 0; j < K; ++j) denom = denom + exv[ss * K + j];
+                float w = exv[t] / denom;
+                const int id = seli[t];
+                if (escale) w = w * escale[id];
+                const int p = (r0 + ss) * K + rr;
+                ids_out[p] = id;
+                wts_out[p] = w;
+                sid[p] = id;
+            }
+            __syncthreads();
+        }
+    }
+    auto pid = [&](int p) { return TOPK ? sid[p] : ids[p]; };
     for (int e = t; e < E; e += 1024) cnt[e] = 0;
     __syncthreads();
     for (int p = t; p < P; p += 1024) {
-        const int e = min(max(ids[p], 0), E - 1);
+        const int e = min(max(pid(p), 0), E - 1);
         ppos[p] = atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
@@ -132,7 +191,7 @@ __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t* ids, int P,
     }
     __syncthreads();
     for (int p = t; p < P; p += 1024) {
-        const int e = min(max(ids[p], 0), E - 1);
+        const int e = min(max(pid(p), 0), E - 1);
         plist[scan[e] - cnt[e] + ppos[p]] = p;
     }
 }
@@ -684,7 +743,13 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
             return rc;
         if ((rc = ft_hip_quantize_q8(ctx, stream, x, hidden, w.q8x, hidden, n_seqs))) return rc;
     }
-    if ((rc = ft_hip_topk_router(ctx, stream, w.logits, expert_scale, ids, wts, n_experts, top_k, n_seqs))) return rc;
+    // the routing inside the grouping launch for few experts (up to 32, in up
+    // to 4 rounds of 1024/E tokens), else its own launch: one workgroup
+    // ranking 128 logits per token is LDS-bound (batch 16 of the Gemma
+    // shape: 188.4 vs 172.6 us/token); at 8 experts it saves the launch
+    const bool topk_in = E <= 32 && n_seqs <= 4 * (1024 / E);
+    if (!topk_in && (rc = ft_hip_topk_router(ctx, stream, w.logits, expert_scale, ids, wts, n_experts, top_k, n_seqs)))
+        return rc;
     // groups of >= n_mfma tokens take the MFMA tile kernels, the others the
     // dot4 kernels; rows longer than 32 blocks (I > 1024) only the former.
     // Automatic (0): every group on one family, MFMA from 8 pairs per expert
@@ -693,8 +758,9 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
     int n_mfma = ctx->grouped_mfma_min;
     if (n_mfma <= 0) n_mfma = (int64_t)P >= 8 * n_experts ? 1 : std::numeric_limits<int>::max();
     if (nbj > 32) n_mfma = 1;
-    hipLaunchKernelGGL(k_group_pairs, dim3(1), dim3(1024), 0, s, (const int32_t*)ids, P, E, n_mfma, w.meta, w.plist,
-                       w.ppos);
+    hipLaunchKernelGGL(topk_in ? k_group_pairs<true> : k_group_pairs<false>, dim3(1), dim3(1024), 0, s,
+                       (const int32_t*)ids, P, E, n_mfma, w.meta, w.plist, w.ppos, (const float*)w.logits, expert_scale,
+                       ids, wts, K);
     if ((rc = launch_status("moe_layer_grouped/group"))) return rc;
     const int gmax = std::min(E, P);
     const int gbig = std::min(gmax, n_mfma > P ? 0 : P / n_mfma);  // at most this many groups of >= n_mfma tokens
