@@ -69,19 +69,20 @@ __host__ __device__ __forceinline__ int64_t row_bytes_of(int layout, int k) {
     return (int64_t)nb * 18;
 }
 
-// n words from src into LDS; a thread issues up to 16 loads before its first
+// n words from src into LDS; a thread issues up to R loads before its first
 // store, so a long row costs a few load latencies, not one per word.
+template <int R = 16>
 __device__ __forceinline__ void stage_words(const int* src, int n, int* lds) {
     const int t = threadIdx.x, nt = blockDim.x;
-    for (int base = 0; base < n; base += 16 * nt) {
-        int v[16];
+    for (int base = 0; base < n; base += R * nt) {
+        int v[R];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
+        for (int r = 0; r < R; ++r) {
             const int i = base + r * nt + t;
             v[r] = i < n ? src[i] : 0;
         }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
+        for (int r = 0; r < R; ++r) {
             const int i = base + r * nt + t;
             if (i < n) lds[i] = v[r];
         }
@@ -288,7 +289,10 @@ __global__ __launch_bounds__(256) void k_gemv_down_combine(GemvArgs a, const flo
     __shared__ float ys[NE];
     const int s = blockIdx.y, R = NE / k;
     const int nb = a.k >> 5;
-    stage_words(reinterpret_cast<const int*>(a.q8 + (int64_t)s * k * a.q8_stride_blocks * Q8_BLK), k * nb * 10, lds);
+    // up to 40 loads per thread in one batch: the k rows (36 words per thread
+    // for two rows of 448 blocks) arrive in one load latency
+    stage_words<40>(reinterpret_cast<const int*>(a.q8 + (int64_t)s * k * a.q8_stride_blocks * Q8_BLK), k * nb * 10,
+                    lds);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int re = wave * (64 / LPR) + lane / LPR, sub = lane % LPR;  // row entry: pair kk, local row rl
     const int kk = re / R, rl = re - kk * R;
