@@ -240,10 +240,12 @@ __global__ __launch_bounds__(64 * LPR, 24 / LPR) void k_gemv_gu_act(GemvArgs a, 
     int slot;
     if constexpr (TOPK) {
         topk_rank_select(sv, E, div, key, selv, seli);
-        const float w = topk_softmax(selv, seli, div, escale, exv);
-        if (blockIdx.x == 0 && e == s * div && t < div) {
-            ids[(int64_t)s * div + t] = seli[t];
-            wts[(int64_t)s * div + t] = w;
+        if (blockIdx.x == 0 && e == s * div) {  // the seq's writer (uniform per workgroup): the weights too
+            const float w = topk_softmax(selv, seli, div, escale, exv);
+            if (t < div) {
+                ids[(int64_t)s * div + t] = seli[t];
+                wts[(int64_t)s * div + t] = w;
+            }
         }
         slot = seli[e - s * div];
     } else {
