@@ -163,22 +163,37 @@ __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t* ids, int P,
         ppos[p] = atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
-    // exclusive prefix sums of counts and of "active" flags (E <= 1024)
+    // inclusive prefix sums of counts and of "active" / "big" flags (E <=
+    // 1024): within each wavefront by shuffles, then each thread adds the
+    // totals of the wavefronts before its own (integer sums: exact in any order)
     const int c = t < E ? cnt[t] : 0;
-    scan[t] = c;
-    act[t] = c > 0;
-    big[t] = c > 0 && c >= n_mfma;
-    __syncthreads();
-    for (int d = 1; d < 1024; d <<= 1) {
-        const int a = t >= d ? scan[t - d] : 0;
-        const int b = t >= d ? act[t - d] : 0;
-        const int f = t >= d ? big[t - d] : 0;
-        __syncthreads();
-        scan[t] += a;
-        act[t] += b;
-        big[t] += f;
-        __syncthreads();
+    int vc = c, va = c > 0, vf = c > 0 && c >= n_mfma;
+    const int lane = t & 63, wv = t >> 6;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int nc = __shfl_up(vc, d), na = __shfl_up(va, d), nf = __shfl_up(vf, d);
+        if (lane >= d) {
+            vc += nc;
+            va += na;
+            vf += nf;
+        }
     }
+    __shared__ int wtot[3][16];
+    if (lane == 63) {
+        wtot[0][wv] = vc;
+        wtot[1][wv] = va;
+        wtot[2][wv] = vf;
+    }
+    __syncthreads();
+    for (int q = 0; q < wv; ++q) {
+        vc += wtot[0][q];
+        va += wtot[1][q];
+        vf += wtot[2][q];
+    }
+    scan[t] = vc;
+    act[t] = va;
+    big[t] = vf;
+    __syncthreads();
     if (t < E && c > 0) {
         const int g = c >= n_mfma ? big[t] - 1 : big[1023] + (act[t] - big[t]) - 1;
         meta[1 + g] = t;                 // gexp
