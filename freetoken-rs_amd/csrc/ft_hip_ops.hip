@@ -504,28 +504,29 @@ __global__ __launch_bounds__(256) void k_route_prep(const float* W, const float*
     }
 }
 
-// k_route_prep for 8 logits per workgroup (batched decode): workgroup
-// (eg, s) computes logits 8eg..8eg+7 of seq s, each in the R-order as
-// k_route_prep (the same bits), reading each chunk of x once for the 8 router
-// rows and the self-dot; and quantizes q8 blocks [eg*Q, eg*Q+Q) of x_s,
-// Q = ceil(nb / gridDim.x). e == 0's workgroup stores inv[s].
-// Grid (n_rows/8, n_seqs), 256 threads.
-__global__ __launch_bounds__(256) void k_route_prep8(const float* W, const float* x, const float* bias, int norm,
-                                                     float* inv, uint8_t* q8, float* y, int dim, int n_rows) {
-    extern __shared__ float P[];  // [9][dim/16] chunk partials: the 8 logits', then x.x
-    __shared__ float G[9][8], tot[9];
+// k_route_prep for EG logits per workgroup (batched decode): workgroup
+// (eg, s) computes logits EG*eg..EG*eg+EG-1 of seq s, each in the R-order as
+// k_route_prep (the same bits), reading each chunk of x once for the EG
+// router rows and the self-dot; and quantizes q8 blocks [eg*Q, eg*Q+Q) of
+// x_s, Q = ceil(nb / gridDim.x). e == 0's workgroup stores inv[s].
+// Grid (n_rows/EG, n_seqs), 256 threads.
+template <int EG>
+__global__ __launch_bounds__(256) void k_route_prep_n(const float* W, const float* x, const float* bias, int norm,
+                                                      float* inv, uint8_t* q8, float* y, int dim, int n_rows) {
+    extern __shared__ float P[];  // [EG+1][dim/16] chunk partials: the EG logits', then x.x
+    __shared__ float G[EG + 1][8], tot[EG + 1];
     const int eg = blockIdx.x, s = blockIdx.y, l = threadIdx.x;
     const int nch = dim >> 4;
     const float* xs = x + (int64_t)s * dim;
-    const float* w0 = W + (int64_t)eg * 8 * dim;
+    const float* w0 = W + (int64_t)eg * EG * dim;
     for (int c = l; c < nch; c += blockDim.x) {
         const float4* x4 = reinterpret_cast<const float4*>(xs + 16 * c);
         float4 xv[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) xv[k] = x4[k];
-        float pe[8], ps = 0.0f;
+        float pe[EG], ps = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < EG; ++j) {
             const float4* w4 = reinterpret_cast<const float4*>(w0 + (int64_t)j * dim + 16 * c);
             float p = 0.0f;
 #pragma unroll
@@ -547,22 +548,22 @@ __global__ __launch_bounds__(256) void k_route_prep8(const float* W, const float
             ps = fmaf(b.w, b.w, ps);
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) P[j * nch + c] = pe[j];
-        P[8 * nch + c] = ps;
+        for (int j = 0; j < EG; ++j) P[j * nch + c] = pe[j];
+        P[EG * nch + c] = ps;
     }
     __syncthreads();
     const int C = dim >> 7;
-    if (l < 72) G[l >> 3][l & 7] = group_sum(P + (l >> 3) * nch + (l & 7) * C, C);
+    if (l < 8 * (EG + 1)) G[l >> 3][l & 7] = group_sum(P + (l >> 3) * nch + (l & 7) * C, C);
     __syncthreads();
-    if (l < 9) {
+    if (l < EG + 1) {
         float t = 0.0f;
         for (int g = 0; g < 8; ++g) t = t + G[l][g];
         tot[l] = t;
     }
     __syncthreads();
-    if (l < 8) {
-        const float ir = norm ? 1.0f / sqrtf(tot[8] / (float)dim + 1e-6f) : 1.0f;  // correctly rounded
-        const int e = eg * 8 + l;
+    if (l < EG) {
+        const float ir = norm ? 1.0f / sqrtf(tot[EG] / (float)dim + 1e-6f) : 1.0f;  // correctly rounded
+        const int e = eg * EG + l;
         float t = tot[l];
         if (norm) t = t * ir;
         if (bias) t = t + bias[e];
@@ -902,15 +903,15 @@ int launch_route_prep(void* stream, const float* w, const float* x, const float*
     // every q8 block needs a workgroup: rows >= ceil(blocks / 16)
     if (n_rows * 16 < dim / 32) return fail(FT_HIP_E_SHAPE, "route_prep: %lld rows cannot quantize %lld blocks",
                                             (long long)n_rows, (long long)(dim / 32));
-    // larger batches: eight logits per workgroup (each chunk of x read once
-    // for them), when the rows split into eights that still cover the q8
-    // blocks at up to 64 per workgroup (measured: faster at 64 seqs, slower
-    // at 16, where the eighth as many workgroups no longer fill the chip)
-    if (n_seqs >= 32 && n_rows % 8 == 0 && (n_rows / 8) * 64 >= dim / 32) {
-        hipLaunchKernelGGL(k_route_prep8, dim3((unsigned)(n_rows / 8), (unsigned)n_seqs), dim3(256),
-                           (size_t)(dim / 16) * 9 * 4, S(stream), w, x, bias, norm, inv, (uint8_t*)q8, y, (int)dim,
-                           (int)n_rows);
-        return launch_status("route_prep8");
+    // batches: EG logits per workgroup (each chunk of x read once for them),
+    // when the rows split into groups that still cover the q8 blocks at up to
+    // 64 per workgroup: 8 from 32 seqs (measured faster at 64), 4 from 16
+    const int eg = n_seqs >= 32 ? 8 : (n_seqs >= 16 ? 4 : 1);
+    if (eg > 1 && n_rows % eg == 0 && (n_rows / eg) * 64 >= dim / 32) {
+        hipLaunchKernelGGL(eg == 8 ? k_route_prep_n<8> : k_route_prep_n<4>, dim3((unsigned)(n_rows / eg),
+                           (unsigned)n_seqs), dim3(256), (size_t)(dim / 16) * (eg + 1) * 4, S(stream), w, x, bias,
+                           norm, inv, (uint8_t*)q8, y, (int)dim, (int)n_rows);
+        return launch_status("route_prep_n");
     }
     hipLaunchKernelGGL(k_route_prep, dim3((unsigned)n_rows, (unsigned)n_seqs), dim3(256), (size_t)(dim / 16) * 8,
                        S(stream), w, x, bias, norm, inv, (uint8_t*)q8, y, (int)dim, (int)n_rows);
