@@ -193,7 +193,7 @@ def cpu_baseline(model, hidden, seconds, threads, input_norm):
             b = None if bias is None else bias[l].ctypes.data_as(P)
             rc = L.orc_moe_layer(x.ctypes.data_as(P), H, I, E, k, routers[l].ctypes.data_as(P), b, None,
                                  ctypes.cast(gu_ptrs[l], P), ctypes.cast(dn_ptrs[l], P), model.layout, threads,
-                                 orc.GELU_LIBM, int(input_norm), x_out.ctypes.data_as(P), None, None, None, None, None, None,
+                                 int(input_norm), x_out.ctypes.data_as(P), None, None, None, None, None, None,
                                  None, None)
             assert rc == 0
             x, x_out = x_out, x

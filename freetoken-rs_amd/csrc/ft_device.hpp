@@ -1,6 +1,6 @@
 // ft_device.hpp -- device-side building blocks shared by every kernel of the
 // library: the q8 block format, the per-block integer dot, q8 quantisation,
-// the q4_0 block quantiser, the portable exp/tanh, and the seeded generator.
+// the q4_0 block quantiser, GELU and exp (libm-exact), and the seeded generator.
 //
 // The translation units that include this file are compiled with
 // -ffp-contract=off, so a*b+c stays two roundings unless fmaf()/fma() is
@@ -10,6 +10,8 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "ft_libm.hpp"
 
 namespace ft {
 
@@ -72,6 +74,13 @@ __device__ __forceinline__ int block_dot_v(const uint4 w, const uint4 lo, const 
 // half of a wavefront (ft-core/src/q4_0.rs:62-78): d = amax/127 (IEEE
 // division), inv = 1/d, q = clamp(round_half_away(v*inv), -127, 127).
 // ---------------------------------------------------------------------------
+// clamp(r, -127, 127) as i8 in Rust: a NaN product (inf*0 in a block that
+// holds inf, 0*inf when amax/127 is subnormal, a NaN input) becomes 0, where
+// fminf/fmaxf alone would return -127.
+__device__ __forceinline__ float q8_clamp(float r) {
+    return r == r ? fminf(127.0f, fmaxf(-127.0f, r)) : 0.0f;
+}
+
 struct Q8Lane {
     float d;
     int q;
@@ -85,7 +94,7 @@ __device__ __forceinline__ Q8Lane q8_quantize_half(float v) {
     float d = a > 0.0f ? a / 127.0f : 0.0f;
     float inv = d > 0.0f ? 1.0f / d : 0.0f;
     float r = roundf(v * inv);
-    r = fminf(127.0f, fmaxf(-127.0f, r));
+    r = q8_clamp(r);
     int q = (int)r;
     int s = q;
 #pragma unroll
@@ -158,7 +167,7 @@ __device__ __forceinline__ uint32_t q8_quantize_lanes32(float v, float* d_out, i
     const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
     const float inv = d > 0.0f ? 1.0f / d : 0.0f;
     float r = roundf(v * inv);
-    r = fminf(127.0f, fmaxf(-127.0f, r));
+    r = q8_clamp(r);
     const int q = (int)r;
     *d_out = d;
     *qsum_out = half_sum32(q);
@@ -187,7 +196,7 @@ __device__ __forceinline__ void quantize_block_quad(const float* v, int part, ui
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         float r = roundf(x[i] * inv);
-        r = fminf(127.0f, fmaxf(-127.0f, r));
+        r = q8_clamp(r);
         const int q = (int)r;
         qsum += q;
         const uint32_t byte = (uint32_t)(uint8_t)(int8_t)q << (8 * (i & 3));
@@ -215,94 +224,30 @@ __device__ __forceinline__ uint64_t rank_key(float v, int i) {
 }
 
 // ---------------------------------------------------------------------------
-// Portable exp / tanh: only IEEE basic operations (fma, floor, ldexp, +, -, /)
-// in a fixed order, so the host oracle computes the same bits. Cody-Waite
-// reduction x = n*ln2 + r with a two-part ln2, degree-13 Taylor polynomial of
-// e^r by Horner with fma (Cody & Waite, Software Manual for the Elementary
-// Functions, 1980).
+// GELU and the softmax exp with the bits of the libm calls ft-core makes
+// (f32::tanh, ft-model/src/lib.rs:436; f32::exp, :1495): restatements of
+// glibc's tanhf / expf, swept against the host libm over every f32 input.
 // ---------------------------------------------------------------------------
-// Coefficients: [0] INV_LN2, [1] LN2_HI, [2] LN2_LO, [3..16] Taylor
-// coefficients of e^r from 1/13! down to 1 (Horner order).
-struct ExpTable {
-    double k[17];
-};
-
-__host__ __device__ constexpr ExpTable exp_table() {
-    return ExpTable{{1.44269504088896338700e+00, 6.93147180369123816490e-01, 1.90821492927058770002e-10,
-                     1.6059043836821614599e-10, 2.0876756987868098979e-09, 2.5052108385441718775e-08,
-                     2.7557319223985890653e-07, 2.7557319223985890653e-06, 2.4801587301587301566e-05,
-                     1.9841269841269841253e-04, 1.3888888888888888889e-03, 8.3333333333333332177e-03,
-                     4.1666666666666664354e-02, 1.6666666666666665741e-01, 5.0000000000000000000e-01, 1.0, 1.0}};
-}
-
-// T: anything indexable by [0..16] holding exp_table(): the constexpr table
-// itself, or a copy in LDS (a persistent kernel reads it from there so the
-// compiler does not keep 17 f64 constants live in registers across its loop).
+// expf for the routing weights. T: anything indexable by 0..31 holding
+// libm::exp2_table() (libm::Exp2TableRef reads the constant table; a
+// persistent kernel passes a copy in LDS so the lookup does not wait behind
+// its own weight loads).
 template <typename T>
-__device__ __forceinline__ double exp_portable_t(double x, const T& k) {
-    if (x > 700.0) return __builtin_huge_val();
-    if (x < -740.0) return 0.0;
-    double n = floor(fma(x, k[0], 0.5));
-    double r = fma(-n, k[1], x);
-    r = fma(-n, k[2], r);
-    double p = k[3];
-#pragma unroll
-    for (int i = 4; i < 17; ++i) p = fma(p, r, k[i]);
-    return ldexp(p, (int)n);
-}
+__device__ __forceinline__ float expf_libm_t(float x, const T& tab) { return libm::expf_glibc_t(x, tab); }
 
-struct ExpConst {
-    __device__ __forceinline__ double operator[](int i) const { return exp_table().k[i]; }
-};
+__device__ __forceinline__ float expf_libm(float x) { return libm::expf_glibc(x); }
 
-// The same constants, each materialised in scalar registers at its use (an
-// opaque move the compiler cannot hoist): inside a long persistent loop this
-// keeps them out of the vector registers, where hoisted copies would be
-// spilled and reloaded.
-struct ExpConstS {
-    __device__ __forceinline__ double operator[](int i) const {
-        double v = exp_table().k[i];
-        asm volatile("" : "+s"(v));
-        return v;
-    }
-};
-
-__device__ __forceinline__ double exp_portable(double x) { return exp_portable_t(x, ExpConst{}); }
-
-template <typename T>
-__device__ __forceinline__ float tanh_portable_t(float z, const T& k) {
-    double a = fabs((double)z);
-    double t;
-    if (a >= 9.5) t = 1.0;
-    else if (a < 0x1p-13) t = a;
-    else {
-        double e = exp_portable_t(2.0 * a, k);
-        t = 1.0 - 2.0 / (e + 1.0);
-    }
-    float tf = (float)t;
-    return signbit(z) ? -tf : tf;
-}
-
-__device__ __forceinline__ float tanh_portable(float z) { return tanh_portable_t(z, ExpConst{}); }
-
-template <typename T>
-__device__ __forceinline__ float expf_portable_t(float x, const T& k) { return (float)exp_portable_t((double)x, k); }
-
-__device__ __forceinline__ float expf_portable(float x) { return expf_portable_t(x, ExpConst{}); }
-
-// gelu_tanh (ft-model/src/lib.rs:435-437), left to right, no contraction.
-template <typename T>
-__device__ __forceinline__ float gelu_tanh_t(float g, const T& k) {
+// gelu_tanh (ft-model/src/lib.rs:435-437), left to right, no contraction:
+// 0.5*g*(1 + tanh(0.7978845608*(g + 0.044715*g*g*g))).
+__device__ __forceinline__ float gelu_tanh(float g) {
     float c = 0.044715f * g;
     c = c * g;
     c = c * g;
-    float inner = g + c;
-    float t = tanh_portable_t(0.7978845608f * inner, k);
-    float h = 0.5f * g;
+    const float inner = g + c;
+    const float t = libm::tanhf_glibc(0.7978845608f * inner);
+    const float h = 0.5f * g;
     return h * (1.0f + t);
 }
-
-__device__ __forceinline__ float gelu_tanh(float g) { return gelu_tanh_t(g, ExpConst{}); }
 
 // ---------------------------------------------------------------------------
 // Seeded generator (same definition as the host oracle): value i of a tensor

@@ -96,6 +96,8 @@ struct FusedParams {
     uint8_t* dbg_act;           // [L][K][I/32][40] or null
     float* dbg_x;               // [L+1][H] or null
     uint64_t* trace;            // [grid][L+1][TRACE_SLOTS] wall-clock stamps or null
+    int32_t* rec_gu;            // [L][K][2I][H/32] gate|up block dots (debug build, tests) or null
+    int32_t* rec_dn;            // [L][K][H][I/32] down block dots (debug build, tests) or null
     int64_t expert_bytes, gu_bytes;
     int H, I, E, K, L;
     int n_gu, n_dn, n_unit;     // K*I/32 gate|up units, K*H/128 down units, max of the two
@@ -118,9 +120,17 @@ struct alignas(16) Misc {       // placed 16-byte aligned
     int pown[MAX_K];            // unit group that runs routed slot p
     int mlist[MAX_K];           // unit groups whose held expert was not routed (misses), ascending
     int mexp[MAX_K];            // the expert each of them runs instead
+    int mslot[MAX_K];           // and its routed slot
     int mcount;
     int abort_flag;
     float inv_r;                // the input RMS norm's scale of the current layer (1 without the norm)
+    uint64_t exp2[32];          // libm::exp2_table() for the routing weights' expf
+};
+
+// The expf table read from the copy in LDS.
+struct Exp2Lds {
+    const uint64_t* t;
+    __device__ __forceinline__ uint64_t operator[](uint64_t i) const { return t[i]; }
 };
 
 // Tagged words use system-scope (sc0 sc1) relaxed accesses: in a probe a
@@ -405,8 +415,10 @@ __device__ __forceinline__ void miss_list(Misc* m, int K, bool first) {
     const uint64_t mm = __ballot(mis);
     if (mis) {
         const int mi = __popcll(mm & ((1ull << t) - 1));
+        const int sl = unit_slot(m, K, t, first);
         m->mlist[mi] = t;
-        m->mexp[mi] = m->sel_i[unit_slot(m, K, t, first)];
+        m->mexp[mi] = m->sel_i[sl];
+        m->mslot[mi] = sl;
     }
     if (t == 0) m->mcount = __popcll(mm);
 }
@@ -421,7 +433,7 @@ __device__ __forceinline__ void route_weights(const FusedParams& P, Misc* m, int
     const float v0 = m->sel_v[0];
     const float vt = m->sel_v[min(t, K - 1)];
     const int it = m->sel_i[min(t, K - 1)];
-    const float ex = expf_portable_t(vt - v0, ExpConstS{});
+    const float ex = expf_libm_t(vt - v0, Exp2Lds{m->exp2});
     float denom = 0.0f;
 #pragma unroll
     for (int j = 0; j < MAX_K; ++j)  // in rank order, as the reference's iterator sum
@@ -551,6 +563,21 @@ __device__ __forceinline__ float ld_bias(const FusedParams& P, int layer) {
     return (P.bias && t < P.E) ? P.bias[(int64_t)layer * P.E + t] : 0.0f;
 }
 
+// Outputs of a launch that aborted (or ran on a poisoned workspace): group
+// unit g sets its H/8 rows of x_out to NaN, and group unit 0 sets every
+// routing record to id -1 / weight NaN, so a caller that does not poll
+// ft_hip_fused_status cannot take stale values for results.
+__device__ __forceinline__ void poison_outputs(const FusedParams& P, int g) {
+    const int HG = P.H / NGROUP;
+    const float qnan = __int_as_float(0x7fc00000);
+    for (int i = threadIdx.x; i < HG; i += FT_THREADS) P.x_out[(int64_t)g * HG + i] = qnan;
+    if (g == 0)
+        for (int i = threadIdx.x; i < P.L * P.K; i += FT_THREADS) {
+            if (P.ids_out) P.ids_out[i] = -1;
+            if (P.wts_out) P.wts_out[i] = qnan;
+        }
+}
+
 // BPW: gate|up blocks per wave, exactly H/32/8; DB: down blocks per thread,
 // ceil(I/32/4) (surplus blocks re-read a valid one and are masked); CPT:
 // router chunks per group-unit thread, ceil(H/128/4). Loads are
@@ -580,11 +607,15 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     const int H = P.H, I = P.I, E = P.E, K = P.K, L = P.L;
     const int nb = H >> 5, nbj = I >> 5, HG = H / NGROUP;
     if (t == 0) m->abort_flag = 0;
+    if (t < 32) m->exp2[t] = libm::exp2_table().t[t];
     __syncthreads();
     // A workspace whose abort word is set (an earlier launch gave up a wait)
     // is poisoned until ft_hip_fused_workspace_init: its epoch may not have
     // advanced, so stale tags could match. Do nothing; the status reports it.
-    if (ld_ctl(P.ctl + CTL_ABORT) != 0) return;
+    if (ld_ctl(P.ctl + CTL_ABORT) != 0) {
+        if (w >= P.n_unit && w < P.n_unit + NGROUP) poison_outputs(P, w - P.n_unit);
+        return;
+    }
     const uint32_t epoch = ld_ctl(P.ctl + CTL_EPOCH);
     auto tag_g = [&](int l) { return epoch + 4u * l + 1u; };
     auto tag_a = [&](int l) { return epoch + 4u * l + 2u; };
@@ -625,6 +656,9 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         const bool pu = w >= P.n_unit + NGROUP;
         const int g = w - P.n_unit - (pu ? NGROUP : 0), r0 = g * HG;
         const bool record = !pu && g == 0;  // group unit 0 writes ids/wts
+        auto fail = [&]() __attribute__((always_inline)) {  // a wait gave up: mark the outputs
+            if (!pu) poison_outputs(P, g);
+        };
         if (pu && (!pf || L < 2)) return;    // nothing to predict
         uint32_t* q8w = reinterpret_cast<uint32_t*>(gp + (C + 1) * E);
         float4 wv[CPT][4];
@@ -657,16 +691,18 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         if (pu) {
             group_publish<CPT, C, DBG>(P, g, wv, gx, gp, q8w, pp_buf(1), tag_g(1), -1, true);
             own_sums();
-            if (!wait_words<DBG, UW_G>(P, m, epoch, pp_buf(1), (NGROUP - 1) * ES, opidx, tag_g(1), gq, odst)) return;
+            if (!wait_words<DBG, UW_G>(P, m, epoch, pp_buf(1), (NGROUP - 1) * ES, opidx, tag_g(1), gq, odst)) { fail(); return; }
             route_rank(P, m, reinterpret_cast<const float*>(gq), bias_p, 1, nullptr);
-            if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * E, gidx_e, tag_g(0), gq, pdst)) return;
+            if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * E, gidx_e, tag_g(0), gq, pdst)) { fail(); return; }
             if (t < K) st_tag(pid_buf(1) + g * PID_STRIDE + t, tag_g(1), (uint32_t)m->pid[1][t]);
         } else {
             group_publish<CPT, C, DBG>(P, g, wv, gx, gp, q8w, gq_buf(0), tag_g(0), -1);
             stamp<DBG>(P, -1, 11);
             own_sums();
-            if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, (NGROUP - 1) * ES, oidx, tag_g(0), gq, odst))
+            if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, (NGROUP - 1) * ES, oidx, tag_g(0), gq, odst)) {
+                fail();
                 return;
+            }
         }
         stamp<DBG>(P, -1, 12);
         route_rank(P, m, reinterpret_cast<const float*>(gq), bias_n, -1, nullptr);
@@ -684,7 +720,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
             stamp<DBG>(P, l, 1);
             // y of every unit group for this group's rows, [u][HG] in LDS
             auto yidx = [=](int i) { return (int64_t)(i / HG) * H + r0 + i % HG; };
-            if (!wait_words<DBG, UW_Y>(P, m, epoch, y_buf(l), K * HG, yidx, tag_y(l), reinterpret_cast<uint32_t*>(gy), l, 26)) return;
+            if (!wait_words<DBG, UW_Y>(P, m, epoch, y_buf(l), K * HG, yidx, tag_y(l), reinterpret_cast<uint32_t*>(gy), l, 26)) { fail(); return; }
             stamp<DBG>(P, l, 8);
             // x_{l+1} = x_l + sum_p (y_p * w_p), pairs in routing order
             // (ft-model/src/lib.rs:1634-1646); slot p ran on unit group pown[p]
@@ -719,12 +755,16 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                 stamp<DBG>(P, l, 11);
                 own_sums();
                 if (!wait_words<DBG, UW_G>(P, m, epoch, pp_buf(l + 2), (NGROUP - 1) * ES, opidx, tag_g(l + 2), gq, odst, l,
-                                           24))
+                                           24)) {
+                    fail();
                     return;
+                }
                 route_rank(P, m, reinterpret_cast<const float*>(gq), bias_p, l & 1, nullptr);
                 if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * E, gidx_e, tag_g(l + 1), gq,
-                                           pdst))
+                                           pdst)) {
+                    fail();
                     return;
+                }
                 stamp<DBG>(P, l, 12);
                 if (t < K) st_tag(pid_buf(l + 2) + g * PID_STRIDE + t, tag_g(l + 2), (uint32_t)m->pid[l & 1][t]);
             } else {
@@ -732,13 +772,17 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                 stamp<DBG>(P, l, 11);
                 own_sums();
                 if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, (NGROUP - 1) * ES, oidx, tag_g(l + 1),
-                                           gq, odst, l, 24))
+                                           gq, odst, l, 24)) {
+                    fail();
                     return;
+                }
                 stamp<DBG>(P, l, 12);
                 // the prediction of layer l+1, for the slot -> unit group map
                 if (pf && !wait_words<DBG, 1>(P, m, epoch, pid_buf(l + 1) + prep * PID_STRIDE, K, ident, tag_g(l + 1),
-                                      reinterpret_cast<uint32_t*>(m->pid[(l + 1) & 1]), l, 27))
+                                      reinterpret_cast<uint32_t*>(m->pid[(l + 1) & 1]), l, 27)) {
+                    fail();
                     return;
+                }
             }
             route_rank(P, m, reinterpret_cast<const float*>(gq), bias_n, -1, pf ? m->pid[(l + 1) & 1] : nullptr);
             route_weights(P, m, l + 1, !pf, record);
@@ -844,7 +888,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     // helpers a missed unit loads its whole tile now; with helpers its down
     // tile is loaded after its slice is computed (a CU keeps ~40 KB of loads
     // in flight, and the down tile is needed only after the act hand-over).
-    int p = u, eid = 0, hug = 0;
+    int p = u, eid = 0, hug = 0, hslot = 0;  // hslot: the missed tile's slot (debug records only)
     bool own_miss = true, hm = false;
     auto decide = [&](int layer, bool first) __attribute__((always_inline)) {
         miss_list(m, K, first);
@@ -861,6 +905,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
             if (mi >= 0 && mi < mc) {
                 hm = true;
                 hug = m->mlist[mi];
+                if (DBG) hslot = m->mslot[mi];
                 load_gu(layer, min(max(m->mexp[mi], 0), E - 1), (u - hug) & (FT_WAVES - 1), hq, hs);
             }
         } else if (own_miss) {
@@ -903,7 +948,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                     dg[I + j * 32 + t] = su;
                 }
                 stamp<DBG>(P, l, 17);
-                const float a = gelu_tanh_t(sg, ExpConstS{}) * su;
+                const float a = gelu_tanh(sg) * su;
                 stamp<DBG>(P, l, 18);
                 float d;
                 int qsum;
@@ -921,7 +966,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
             };
             // one wave's partial for row r: the fma chain over the BPW blocks
             // s*BPW.. of the tile in (q, c) against q8(x)
-            auto wave_partial = [&](const uint4 (&q)[BPW], const uint32_t (&c)[BPW], int s)
+            auto wave_partial = [&](const uint4 (&q)[BPW], const uint32_t (&c)[BPW], int s, int slot)
                                     __attribute__((always_inline)) {
                 const int b0 = s * BPW;
                 float acc = 0.0f;
@@ -931,6 +976,10 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                     const int2 dq8 = xdp[b0 + i];
                     const int diff = block_dot_v(q[i], lo, hi, dq8.y);
                     acc = fmaf((float)diff, h2f((uint16_t)c[i]) * __int_as_float(dq8.x), acc);
+                    if (DBG && P.rec_gu) {  // test record: the block's int32 dot
+                        const int row = r < 32 ? j * 32 + r : I + j * 32 + (r - 32);
+                        P.rec_gu[(((int64_t)l * K + slot) * 2 * I + row) * nb + b0 + i] = diff;
+                    }
                 }
                 return acc;
             };
@@ -938,14 +987,14 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
             auto help = [&]() __attribute__((always_inline)) {
                 if (hm) {
                     const int sl = (u - hug) & (FT_WAVES - 1);
-                    const float a2 = wave_partial(hq, hs, sl);
+                    const float a2 = wave_partial(hq, hs, sl, hslot);
                     st_tag(P.hp_t + (((int64_t)hug * nbj + j) * FT_WAVES + sl) * 64 + r, tag_a(l), __float_as_uint(a2));
                     if (DBG && P.trace && r == 0 && wave == 1)  // slot 29: wave 1's slice published
                         P.trace[((int64_t)blockIdx.x * (P.L + 1) + (l + 1)) * TRACE_SLOTS + 29] = wall_clock64();
                 }
             };
             if (!(helpers && own_miss)) {
-                red[wave * 64 + r] = wave_partial(qv, sc, wave);
+                red[wave * 64 + r] = wave_partial(qv, sc, wave, p);
                 stamp<DBG>(P, l, 2);
                 __syncthreads();
                 if (t < 32) tail();
@@ -993,9 +1042,11 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
             float acc = 0.0f;
 #pragma unroll
             for (int k = 0; k < DB; ++k) {
-                const float v = (float)block_dot_v(dq[k], alo[k], ahi[k], ap[k].y) *
-                                (h2f((uint16_t)dsc[k]) * __int_as_float(ap[k].x));
+                const int dot = block_dot_v(dq[k], alo[k], ahi[k], ap[k].y);
+                const float v = (float)dot * (h2f((uint16_t)dsc[k]) * __int_as_float(ap[k].x));
                 acc = s4o + 4 * k < nbj ? acc + v : acc;
+                if (DBG && P.rec_dn && s4o + 4 * k < nbj)  // test record: the block's int32 dot
+                    P.rec_dn[(((int64_t)l * K + p) * H + j * DN_UNIT + wave * DN_ROWS + rr) * nbj + s4o + 4 * k] = dot;
             }
             acc += quad_xor1(acc);
             acc += quad_xor2(acc);
@@ -1305,6 +1356,8 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
     P.dbg_act = (uint8_t*)dbg_act;
     P.dbg_x = dbg_x;
     P.trace = dbg_trace;
+    P.rec_gu = ctx->rec_gu;
+    P.rec_dn = ctx->rec_dn;
     P.expert_bytes = ft_hip_fused_expert_bytes(hidden, inter);
     P.gu_bytes = 2 * inter * (hidden / 32) * 18;
     P.spin_limit = ctx->fused_spin_limit;
@@ -1314,7 +1367,7 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
     // the kernel keeps exactly H/256 gate|up blocks per wave in flight
     const bool db6 = inter / 32 <= 24;
     // debug records and the phase trace are compiled in only when asked for
-    const bool dbg = dbg_gu || dbg_act || dbg_x || dbg_trace;
+    const bool dbg = dbg_gu || dbg_act || dbg_x || dbg_trace || (ctx->rec_gu && ctx->rec_dn);
     const void* kern =
         hidden == 2816
             ? (db6 ? (dbg ? reinterpret_cast<const void*>(k_moe_stack_fused<11, 6, 6, true>)

@@ -139,7 +139,7 @@ __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t* ids, int P,
             }
             __syncthreads();
             const bool on2 = ss < TPR && r0 + ss < B;
-            if (on2) exv[t] = expf_portable(selv[t] - selv[ss * K]);
+            if (on2) exv[t] = expf_libm(selv[t] - selv[ss * K]);
             __syncthreads();
             if (on2) {
                 float denom = 0.0f;
@@ -215,11 +215,11 @@ __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t* ids, int P,
 // the q8 of act block j per token. BPW = H/32/8 blocks per wave. in_scale
 // (input RMS norm, or null): a token's gate|up sums are first multiplied by
 // in_scale[token].
-template <int BPW>
+template <int BPW, bool REC>
 __global__ __launch_bounds__(GT, 2) void k_grouped_gu(const uint8_t* bank, int64_t expert_bytes, const int32_t* meta,
                                                       const int32_t* plist, const uint8_t* q8x, uint8_t* q8a,
                                                       float* dbg_gu, const float* in_scale, int H, int I, int E,
-                                                      int K, int n_mfma) {
+                                                      int K, int n_mfma, int32_t* rec) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int nb = H >> 5, nbj = I >> 5;
     const int j = blockIdx.x, g = blockIdx.y + meta[1 + 3 * E];  // after the MFMA kernels' groups
@@ -298,6 +298,10 @@ __global__ __launch_bounds__(GT, 2) void k_grouped_gu(const uint8_t* bank, int64
                 const int2 dq = xp[xb];
                 const int dot = block_dot_v(qv[i], xq[xb * 2], xq[xb * 2 + 1], dq.y);
                 acc = fmaf((float)dot, h2f((uint16_t)sc[i]) * __int_as_float(dq.x), acc);
+                if constexpr (REC) {  // test record: the block's int32 dot
+                    const int row = r < 32 ? j * 32 + r : I + j * 32 + (r - 32);
+                    rec[((int64_t)plist[s0 + c0 + tt] * 2 * I + row) * nb + b0 + i] = dot;
+                }
             }
             red[(wave * NT + tt) * 64 + r] = acc;
         }
@@ -333,10 +337,10 @@ __global__ __launch_bounds__(GT, 2) void k_grouped_gu(const uint8_t* bank, int64
 
 // Down rows 128u..128u+127 of active expert g (one 16-row tile per wave;
 // thread (rr, s4) holds row rr's blocks s4, s4+4, ...) for all of its tokens.
-template <int DB>
+template <int DB, bool REC>
 __global__ __launch_bounds__(GT, 1) void k_grouped_down(const uint8_t* bank, int64_t expert_bytes, int64_t gu_bytes,
                                                         const int32_t* meta, const int32_t* plist, const uint8_t* q8a,
-                                                        float* ydn, int H, int I, int E, int n_mfma) {
+                                                        float* ydn, int H, int I, int E, int n_mfma, int32_t* rec) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int nbj = I >> 5;
     const int u = blockIdx.x, g = blockIdx.y + meta[1 + 3 * E];  // after the MFMA kernels' groups
@@ -385,9 +389,13 @@ __global__ __launch_bounds__(GT, 1) void k_grouped_down(const uint8_t* bank, int
                 const int b = s4 + 4 * k;
                 const int xb = tt * nbj + min(b, nbj - 1);
                 const int2 pq = ap[xb];
-                const float v = (float)block_dot_v(dq[k], aq[xb * 2], aq[xb * 2 + 1], pq.y) *
-                                (h2f((uint16_t)dsc[k]) * __int_as_float(pq.x));
+                const int dot = block_dot_v(dq[k], aq[xb * 2], aq[xb * 2 + 1], pq.y);
+                const float v = (float)dot * (h2f((uint16_t)dsc[k]) * __int_as_float(pq.x));
                 acc = b < nbj ? acc + v : acc;
+                if constexpr (REC) {  // test record: the block's int32 dot
+                    if (b < nbj)
+                        rec[((int64_t)plist[s0 + c0 + tt] * H + u * DU + wave * 16 + rr) * nbj + b] = dot;
+                }
             }
             acc += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(acc), 0xB1, 0xF, 0xF, false));
             acc += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(acc), 0x4E, 0xF, 0xF, false));
@@ -473,11 +481,11 @@ __device__ __forceinline__ void scales4(const uint16_t* p, float (&sc)[4]) {
 // LDS); the 8 wave partials of a (row, token) are summed in wave order;
 // then, as k_grouped_gu, the input-norm scale, GELU*up and the q8 of act
 // block j per token.
-template <int BPW>
+template <int BPW, bool REC>
 __global__ __launch_bounds__(GT, 2) __attribute__((amdgpu_waves_per_eu(4))) void k_mfma_gu(const uint8_t* bank, int64_t expert_bytes, const int32_t* meta,
                                                    const int32_t* plist, const uint8_t* q8x, uint32_t q8x_bytes,
                                                    uint8_t* q8a, float* dbg_gu, const float* in_scale, int H, int I,
-                                                   int E, int K, int n_min) {
+                                                   int E, int K, int n_min, int32_t* rec) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int nb = H >> 5, nbj = I >> 5;
     const int j = blockIdx.x, g = blockIdx.y;
@@ -542,6 +550,15 @@ __global__ __launch_bounds__(GT, 2) __attribute__((amdgpu_waves_per_eu(4))) void
 #pragma unroll
                     for (int m = 0; m < 4; ++m) {
                         const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib_op(aw[k & 1][b][m]), a.b, c, 0, 0, 0);
+                        if constexpr (REC) {  // test record: D = the (row, token) blocks' int32 dots
+                            if (li < nt)
+#pragma unroll
+                                for (int v = 0; v < 4; ++v) {
+                                    const int rr = 16 * m + 4 * lg + v;
+                                    const int row = rr < 32 ? j * 32 + rr : I + j * 32 + (rr - 32);
+                                    rec[((int64_t)p * 2 * I + row) * nb + b0 + k * NBB + b] = d[v];
+                                }
+                        }
                         float sc[4];
                         scales4(scl + (b0 + k * NBB + b) * 64 + 16 * m + 4 * lg, sc);
 #pragma unroll
@@ -588,10 +605,11 @@ __global__ __launch_bounds__(GT, 2) __attribute__((amdgpu_waves_per_eu(4))) void
 // RT tiles of group w/KS (they share each block's activation operand), K
 // slice w%KS (blocks [s*BW, s*BW+BW) below nbj); the KS slice partials of a
 // (row, token) are summed in slice order into y[pair][row].
-template <int KS, int BW, int RT>
+template <int KS, int BW, int RT, bool REC>
 __global__ __launch_bounds__(GT, 2) void k_mfma_down(const uint8_t* bank, int64_t expert_bytes, int64_t gu_bytes,
                                                      const int32_t* meta, const int32_t* plist, const uint8_t* q8a,
-                                                     uint32_t q8a_bytes, float* ydn, int H, int I, int E, int n_min) {
+                                                     uint32_t q8a_bytes, float* ydn, int H, int I, int E, int n_min,
+                                                     int32_t* rec) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int TPW = GW / KS;   // tile groups per workgroup
     constexpr int TW = TPW * RT;   // tiles per workgroup
@@ -659,6 +677,12 @@ __global__ __launch_bounds__(GT, 2) void k_mfma_down(const uint8_t* bank, int64_
 #pragma unroll
                     for (int m = 0; m < RT; ++m) {
                         const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib_op(aw[k & 1][b][m]), a.b, c, 0, 0, 0);
+                        if constexpr (REC) {  // test record: D = the (row, token) blocks' int32 dots
+                            if (li < nt)
+#pragma unroll
+                                for (int v = 0; v < 4; ++v)
+                                    rec[((int64_t)p * H + (tile0 + m) * 16 + 4 * lg + v) * nbj + bs + k * NBB + b] = d[v];
+                        }
                         float sc[4];
                         scales4(st + (m * nbj + bs + k * NBB + b) * 16 + 4 * lg, sc);
 #pragma unroll
@@ -781,57 +805,53 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
     const int gbig = std::min(gmax, n_mfma > P ? 0 : P / n_mfma);  // at most this many groups of >= n_mfma tokens
     const bool dot4 = n_mfma > 1, mfma = n_seqs >= n_mfma;
     const uint32_t q8x_bytes = (uint32_t)(n_seqs * nb * Q8_BLK), q8a_bytes = (uint32_t)((int64_t)P * nbj * Q8_BLK);
+    // a block-dot record (ft_hip_set_block_dot_record, tests only) selects
+    // the instantiations that store every int32 block dot
+    int32_t* rgu = ctx->rec_gu;
+    int32_t* rdn = ctx->rec_dn;
+    const bool rec = rgu && rdn;
     if (dot4) {
         const size_t lds_gu = (size_t)NT * nb * 40 + sizeof(float) * (GW * NT * 64 + NT * 64 + NT * 32) + 4 * NT * 10;
-        if (H == 2816)
-            hipLaunchKernelGGL(k_grouped_gu<11>, dim3(nbj, gmax), dim3(GT), lds_gu, s, (const uint8_t*)bank, eb,
-                               (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8x, w.q8a, dbg_gu, inv,
-                               H, I, E, K, n_mfma);
-        else
-            hipLaunchKernelGGL(k_grouped_gu<16>, dim3(nbj, gmax), dim3(GT), lds_gu, s, (const uint8_t*)bank, eb,
-                               (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8x, w.q8a, dbg_gu, inv,
-                               H, I, E, K, n_mfma);
+        auto kern = H == 2816 ? (rec ? k_grouped_gu<11, true> : k_grouped_gu<11, false>)
+                              : (rec ? k_grouped_gu<16, true> : k_grouped_gu<16, false>);
+        hipLaunchKernelGGL(kern, dim3(nbj, gmax), dim3(GT), lds_gu, s, (const uint8_t*)bank, eb, (const int32_t*)w.meta,
+                           (const int32_t*)w.plist, (const uint8_t*)w.q8x, w.q8a, dbg_gu, inv, H, I, E, K, n_mfma, rgu);
         if ((rc = launch_status("moe_layer_grouped/gate_up"))) return rc;
     }
     if (mfma) {
         const size_t lds_mg = (size_t)nb * 128 + sizeof(float) * (GW * 64 * MT + MT * 64 + MT * 32) + 4 * MT * 10;
-        if (H == 2816)
-            hipLaunchKernelGGL(k_mfma_gu<11>, dim3(nbj, gbig), dim3(GT), lds_mg, s, (const uint8_t*)bank, eb,
-                               (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8x, q8x_bytes, w.q8a,
-                               dbg_gu, inv, H, I, E, K, n_mfma);
-        else
-            hipLaunchKernelGGL(k_mfma_gu<16>, dim3(nbj, gbig), dim3(GT), lds_mg, s, (const uint8_t*)bank, eb,
-                               (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8x, q8x_bytes, w.q8a,
-                               dbg_gu, inv, H, I, E, K, n_mfma);
+        auto kern = H == 2816 ? (rec ? k_mfma_gu<11, true> : k_mfma_gu<11, false>)
+                              : (rec ? k_mfma_gu<16, true> : k_mfma_gu<16, false>);
+        hipLaunchKernelGGL(kern, dim3(nbj, gbig), dim3(GT), lds_mg, s, (const uint8_t*)bank, eb, (const int32_t*)w.meta,
+                           (const int32_t*)w.plist, (const uint8_t*)w.q8x, q8x_bytes, w.q8a, dbg_gu, inv, H, I, E, K,
+                           n_mfma, rgu);
         if ((rc = launch_status("moe_layer_grouped/gate_up_mfma"))) return rc;
     }
     if (dbg_act && hipMemcpyAsync(dbg_act, w.q8a, (size_t)P * nbj * Q8_BLK, hipMemcpyDeviceToDevice, s) != hipSuccess)
         return fail(FT_HIP_E_LAUNCH, "%s: debug copy failed", nm);
     if (dot4) {
         const size_t lds_dn = (size_t)NTD * nbj * 40;
-        if (nbj <= 24)
-            hipLaunchKernelGGL(k_grouped_down<6>, dim3(H / DU, gmax), dim3(GT), lds_dn, s, (const uint8_t*)bank, eb,
-                               gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8a, w.ydn,
-                               H, I, E, n_mfma);
-        else
-            hipLaunchKernelGGL(k_grouped_down<8>, dim3(H / DU, gmax), dim3(GT), lds_dn, s, (const uint8_t*)bank, eb,
-                               gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8a, w.ydn,
-                               H, I, E, n_mfma);
+        auto kern = nbj <= 24 ? (rec ? k_grouped_down<6, true> : k_grouped_down<6, false>)
+                              : (rec ? k_grouped_down<8, true> : k_grouped_down<8, false>);
+        hipLaunchKernelGGL(kern, dim3(H / DU, gmax), dim3(GT), lds_dn, s, (const uint8_t*)bank, eb, gu_bytes,
+                           (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8a, w.ydn, H, I, E,
+                           n_mfma, rdn);
         if ((rc = launch_status("moe_layer_grouped/down"))) return rc;
     }
     if (mfma) {
         if (nbj <= 32) {  // one K slice: 8 waves x 2 tiles of 16 rows per workgroup
             const size_t lds_md = (size_t)GW * 2 * nbj * 32 + sizeof(float) * GW * 2 * 16 * MT;
-            hipLaunchKernelGGL((k_mfma_down<1, 32, 2>), dim3(H / (16 * GW * 2), gbig), dim3(GT), lds_md, s,
-                               (const uint8_t*)bank, eb, gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist,
-                               (const uint8_t*)w.q8a, q8a_bytes, w.ydn, H, I, E, n_mfma);
+            auto kern = rec ? k_mfma_down<1, 32, 2, true> : k_mfma_down<1, 32, 2, false>;
+            hipLaunchKernelGGL(kern, dim3(H / (16 * GW * 2), gbig), dim3(GT), lds_md, s, (const uint8_t*)bank, eb,
+                               gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8a,
+                               q8a_bytes, w.ydn, H, I, E, n_mfma, rdn);
         } else {  // long rows: DRT tiles per workgroup, 8 K slices of up to 64 blocks
             constexpr int DRT = 4;
             const size_t lds_md = (size_t)DRT * nbj * 32 + sizeof(float) * GW * DRT * 16 * MT;
-            hipLaunchKernelGGL((k_mfma_down<GW, 64, DRT>), dim3(H / (16 * DRT), gbig), dim3(GT), lds_md, s,
-                               (const uint8_t*)bank,
-                               eb, gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8a,
-                               q8a_bytes, w.ydn, H, I, E, n_mfma);
+            auto kern = rec ? k_mfma_down<GW, 64, DRT, true> : k_mfma_down<GW, 64, DRT, false>;
+            hipLaunchKernelGGL(kern, dim3(H / (16 * DRT), gbig), dim3(GT), lds_md, s, (const uint8_t*)bank, eb,
+                               gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8a,
+                               q8a_bytes, w.ydn, H, I, E, n_mfma, rdn);
         }
         if ((rc = launch_status("moe_layer_grouped/down_mfma"))) return rc;
     }

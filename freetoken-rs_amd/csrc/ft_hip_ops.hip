@@ -133,7 +133,7 @@ __device__ __forceinline__ void topk_rank_select(const float* sv, int E, int k, 
 __device__ __forceinline__ float topk_softmax(const float* selv, const int* seli, int k, const float* escale,
                                               float* exv) {
     const int t = threadIdx.x;
-    if (t < k) exv[t] = expf_portable(selv[t] - selv[0]);
+    if (t < k) exv[t] = expf_libm(selv[t] - selv[0]);
     __syncthreads();
     float w = 0.0f;
     if (t < k) {

@@ -78,6 +78,16 @@ extern "C" int ft_hip_set_grouped_mfma_min(ft_hip_ctx* ctx, int n_tokens) {
     return FT_HIP_OK;
 }
 
+extern "C" int ft_hip_set_block_dot_record(ft_hip_ctx* ctx, int32_t* gu_dots, int32_t* dn_dots) {
+    clear_error();
+    if (!ctx) return fail(FT_HIP_E_INVALID, "set_block_dot_record: null ctx");
+    if ((gu_dots == nullptr) != (dn_dots == nullptr))
+        return fail(FT_HIP_E_INVALID, "set_block_dot_record: give both records or neither");
+    ctx->rec_gu = gu_dots;
+    ctx->rec_dn = dn_dots;
+    return FT_HIP_OK;
+}
+
 extern "C" int ft_hip_destroy(ft_hip_ctx* ctx) {
     clear_error();
     delete ctx;

@@ -14,6 +14,8 @@ struct ft_hip_ctx {
     int fused_prefetch;    // fused kernel: stream predicted experts ahead (1) or not (0)
     int input_norm;        // layer entry points run on rmsnorm(x) (1) or x (0)
     int grouped_mfma_min;  // grouped layer: experts with at least this many tokens take the MFMA kernels (0: auto)
+    int32_t* rec_gu;       // test record of gate|up block dots (ft_hip_set_block_dot_record), or null
+    int32_t* rec_dn;       // test record of down block dots, or null
     char arch[64];
 };
 

@@ -57,6 +57,7 @@ SIGNATURES = {
     "ft_hip_fused_set_prefetch": (_I, [_P, _I]),
     "ft_hip_set_input_norm": (_I, [_P, _I]),
     "ft_hip_set_grouped_mfma_min": (_I, [_P, _I]),
+    "ft_hip_set_block_dot_record": (_I, [_P, _P, _P]),
     "ft_hip_fused_workspace_init": (_I, [_P, _P, _P, _SZ]),
     "ft_hip_pack_experts_fused": (_I, [_P, _P, _P, _I, _U64, _P, _I64, _I64, _I64]),
     "ft_hip_pack_router_fused": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
@@ -269,6 +270,11 @@ class Q4Gemv:
         """1: the layer entry points run on rmsnorm(x) (logits and gate|up sums times
         1/sqrt(mean(x*x) + 1e-6)); 0 (default): on x as given."""
         check(lib().ft_hip_set_input_norm(self._ctx, int(on)))
+
+    def set_block_dot_record(self, gu_dots, dn_dots):
+        """Test hook: record every int32 block dot of the grouped / fused
+        kernels into two int32 tensors (None, None: off)."""
+        check(lib().ft_hip_set_block_dot_record(self._ctx, _ptr(gu_dots), _ptr(dn_dots)))
 
     def set_grouped_mfma_min(self, n_tokens):
         """moe_layer_grouped: experts with >= n_tokens tokens take the MFMA kernels (0, the default:

@@ -112,7 +112,8 @@ int ft_hip_q4q8_block_dots(ft_hip_ctx* ctx, void* stream, const void* base,
 /* Replaces gelu_mul_q8 (ft-cuda/src/lib.rs:354-374; kernel q4.cu:255-287):
  * act = gelu_tanh(gu[:, j]) * gu[:, inter + j] (ft-model/src/lib.rs:435-437),
  * then Q8Vec::quantize. gu: [n, 2*inter] f32, q8: [n, inter/32] blocks.
- * tanh is the library's portable tanh (IEEE basic ops only). */
+ * tanh returns the bits of glibc's tanhf, which Rust's f32::tanh calls on
+ * Linux (a restatement of its fdlibm algorithm in IEEE basic operations). */
 int ft_hip_gelu_mul_q8(ft_hip_ctx* ctx, void* stream, const float* gu, void* q8, int64_t inter,
                        int64_t n);
 
@@ -171,6 +172,19 @@ int ft_hip_gen_values(ft_hip_ctx* ctx, void* stream, uint64_t key, int64_t start
                       float scale, float* out);
 int ft_hip_gen_q4_rows(ft_hip_ctx* ctx, void* stream, uint64_t key, int64_t row0,
                        int64_t n_rows, int64_t k, float scale, void* out, int layout);
+
+/* Test hook (no reference counterpart): while set, ft_hip_moe_layer_grouped
+ * and ft_hip_moe_stack_fused run instantiations of their kernels that also
+ * store every per-block int32 dot sum_i (q4_i - 8) * q8_i their production
+ * inner loops compute (v_dot4 and int8 MFMA alike; the production
+ * instantiations are unchanged), into
+ *   grouped: gu_dots [n_seqs*top_k pairs][2*inter rows][hidden/32 blocks],
+ *            dn_dots [pairs][hidden rows][inter/32 blocks], pair p = s*top_k + k;
+ *   fused:   gu_dots [n_layers][top_k slots][2*inter][hidden/32],
+ *            dn_dots [n_layers][top_k][hidden][inter/32] (with the dbg_* record on).
+ * Rows are the expert's gate rows then up rows (gate|up) or its down rows.
+ * Both NULL (the state after create) turns it off; give both or neither. */
+int ft_hip_set_block_dot_record(ft_hip_ctx* ctx, int32_t* gu_dots, int32_t* dn_dots);
 
 /* One MoE expert-FFN layer for n_seqs tokens (the composition of
  * ft-model/src/lib.rs:1406-1476 with host routing replaced by device routing):

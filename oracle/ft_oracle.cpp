@@ -15,11 +15,12 @@
 //   * orc_router_logits: the reference computes router logits only on its GPU
 //     (ft-cuda/src/q4.cu:1153-1174) in an order tied to its launch shape; this
 //     build defines one order (the "R-order", below) that CPU and GPU follow.
-//   * the "portable" tanh/exp: Rust's f32::tanh/f32::exp call the platform
-//     libm (ft-model/src/lib.rs:436, :1495), whose last-bit behaviour no GPU
-//     library reproduces. The portable versions use only IEEE basic ops
-//     (+ - * / fma ldexp) in a fixed order, so host and device agree exactly.
-//     The libm versions are kept as the faithful restatement.
+//
+// GELU's tanh and the routing softmax's exp are the host libm's tanhf / expf,
+// the functions Rust's f32::tanh / f32::exp call on Linux (ft-model/src/
+// lib.rs:436, :1495). The kernels compute the same bits with a restatement of
+// glibc's algorithms (freetoken-rs_amd/csrc/ft_libm.hpp, swept against this
+// libm over every f32 input by tests/test_libm.py).
 
 #include <immintrin.h>
 #include <atomic>
@@ -94,6 +95,10 @@ void orc_dequantize_row(const uint8_t* row, int64_t k, float* out) {
 // ft-core/src/q4_0.rs:62-78 (Q8Vec::quantize): d = amax/127 in f32,
 // inv = 1/d, q = clamp(round_half_away(v*inv), -127, 127). Zero block: d=0,
 // q=0. The scale stays f32 (it is NOT ggml's fp16 block_q8_0 scale).
+// Non-finite values follow Rust: f32::max ignores NaN in the amax fold (as
+// fmax does); a NaN product (inf*0 when the block holds inf, so inv = 0;
+// 0*inf when amax/127 is subnormal, so inv = inf; NaN input) stays NaN
+// through round() and clamp(), and `as i8` maps NaN to 0.
 void orc_q8_quantize(const float* x, int64_t k, float* d, int8_t* qs) {
     for (int64_t b = 0; b < k / QK; ++b) {
         const float* xb = x + b * QK;
@@ -104,7 +109,7 @@ void orc_q8_quantize(const float* x, int64_t k, float* d, int8_t* qs) {
         d[b] = s;
         for (int i = 0; i < QK; ++i) {
             float r = std::round(xb[i] * inv);   // half away from zero
-            r = std::fmin(127.0f, std::fmax(-127.0f, r));
+            r = r == r ? std::fmin(127.0f, std::fmax(-127.0f, r)) : 0.0f;  // NaN as i8 = 0
             qs[b * QK + i] = (int8_t)r;
         }
     }
@@ -336,70 +341,20 @@ static inline float gelu_arg(float g) {
     return 0.7978845608f * inner;
 }
 
-float orc_gelu_tanh_libm(float g) {
+float orc_gelu_tanh(float g) {
     float t = tanhf(gelu_arg(g));
     float h = 0.5f * g;
     return h * (1.0f + t);
 }
 
-// Portable exp on doubles (Cody-Waite range reduction x = n*ln2 + r with a
-// two-part ln2, then a degree-13 Taylor polynomial of e^r, |r| <= ln2/2, by
-// Horner's rule with fused multiply-adds; Cody & Waite, "Software Manual for
-// the Elementary Functions", 1980). Relative error < 1e-15 on the range used
-// here; bit-identical on any IEEE-754 machine that honours fma and ldexp.
-static const double LN2_HI = 6.93147180369123816490e-01;  // 0x3FE62E42FEE00000
-static const double LN2_LO = 1.90821492927058770002e-10;  // 0x3DEA39EF35793C76
-static const double INV_LN2 = 1.44269504088896338700e+00;
-
-double orc_exp_portable(double x) {
-    if (x > 700.0) return INFINITY;
-    if (x < -740.0) return 0.0;
-    double n = std::floor(std::fma(x, INV_LN2, 0.5));
-    double r = std::fma(-n, LN2_HI, x);
-    r = std::fma(-n, LN2_LO, r);
-    // 1/j! for j = 13..0
-    static const double C[14] = {
-        1.6059043836821614599e-10, 2.0876756987868098979e-09, 2.5052108385441718775e-08,
-        2.7557319223985890653e-07, 2.7557319223985890653e-06, 2.4801587301587301566e-05,
-        1.9841269841269841253e-04, 1.3888888888888888889e-03, 8.3333333333333332177e-03,
-        4.1666666666666664354e-02, 1.6666666666666665741e-01, 5.0000000000000000000e-01,
-        1.0000000000000000000e+00, 1.0000000000000000000e+00};
-    double p = C[0];
-    for (int j = 1; j < 14; ++j) p = std::fma(p, r, C[j]);
-    return std::ldexp(p, (int)n);
-}
-
-// tanh(z) = sign(z) * (1 - 2 / (e^{2|z|} + 1)), rounded once to f32.
-float orc_tanh_portable(float z) {
-    double a = std::fabs((double)z);
-    double t;
-    if (a >= 9.5) t = 1.0;                  // tanh rounds to 1.0f beyond ~9.01
-    else if (a < 0x1p-13) t = a;            // tanh(a) rounds to a here
-    else {
-        double e = orc_exp_portable(2.0 * a);
-        t = 1.0 - 2.0 / (e + 1.0);
-    }
-    float tf = (float)t;
-    return std::signbit(z) ? -tf : tf;
-}
-
-float orc_expf_portable(float x) { return (float)orc_exp_portable((double)x); }
-
-float orc_gelu_tanh_portable(float g) {
-    float t = orc_tanh_portable(gelu_arg(g));
-    float h = 0.5f * g;
-    return h * (1.0f + t);
-}
-
 // act[j] = gelu_tanh(gate[j]) * up[j], gate = gu[0..inter), up = gu[inter..2inter)
-// (ft-model/src/lib.rs:1625-1628), then Q8Vec::quantize (:1632). mode 0 = libm
-// tanh (faithful), 1 = portable tanh (the GPU's).
-void orc_gelu_mul_q8(const float* gu, int64_t inter, int mode, float* act, float* d, int8_t* qs) {
+// (ft-model/src/lib.rs:1625-1628), then Q8Vec::quantize (:1632).
+void orc_gelu_mul_q8(const float* gu, int64_t inter, float* act, float* d, int8_t* qs) {
     std::vector<float> tmp;
     if (!act) { tmp.resize((size_t)inter); act = tmp.data(); }
     for (int64_t j = 0; j < inter; ++j) {
         float g = gu[j];
-        float ge = mode == 0 ? orc_gelu_tanh_libm(g) : orc_gelu_tanh_portable(g);
+        float ge = orc_gelu_tanh(g);
         act[j] = ge * gu[j + inter];
     }
     orc_q8_quantize(act, inter, d, qs);
@@ -456,9 +411,7 @@ float orc_rms_inv(const float* x, int H) {
 // ft-model/src/lib.rs:1487-1504: stable sort by descending logit (ties keep
 // the lower expert index first), take k, w_j = exp(l_j - l_max) / sum (sum in
 // top-k order from 0.0f), times per_expert_scale[e] (NULL = 1).
-// mode 0 = libm expf, 1 = portable exp.
-int orc_topk_softmax(const float* logits, int E, int k, const float* expert_scale, int mode,
-                     int32_t* ids, float* wts) {
+int orc_topk_softmax(const float* logits, int E, int k, const float* expert_scale, int32_t* ids, float* wts) {
     if (k > E || k <= 0) return -1;
     std::vector<int> order((size_t)E);
     for (int i = 0; i < E; ++i) order[(size_t)i] = i;
@@ -475,7 +428,7 @@ int orc_topk_softmax(const float* logits, int E, int k, const float* expert_scal
     float denom = 0.0f;
     for (int j = 0; j < k; ++j) {
         float dl = logits[order[(size_t)j]] - mx;
-        ex[(size_t)j] = mode == 0 ? expf(dl) : orc_expf_portable(dl);
+        ex[(size_t)j] = expf(dl);
         denom = denom + ex[(size_t)j];
     }
     for (int j = 0; j < k; ++j) {
@@ -520,7 +473,7 @@ void orc_combine(const float* y, const float* w, int n_pairs, int64_t H, const f
 int orc_moe_layer(const float* x, int H, int I, int E, int k,
                   const float* W_r, const float* bias, const float* expert_scale,
                   const uint8_t* const* gu, const uint8_t* const* dn, int layout,
-                  int threads, int gelu_mode, int input_norm,
+                  int threads, int input_norm,
                   float* x_out, float* logits, int32_t* ids, float* wts,
                   float* y_gu, float* act, float* act_d, int8_t* act_qs, float* y_dn) {
     if (H % 128 || I % 32 || k <= 0 || k > E) return -1;
@@ -532,7 +485,7 @@ int orc_moe_layer(const float* x, int H, int I, int E, int k,
         if (input_norm) lg[(size_t)e] = lg[(size_t)e] * inv_r;
         if (bias) lg[(size_t)e] = lg[(size_t)e] + bias[e];
     }
-    orc_topk_softmax(lg.data(), E, k, expert_scale, gelu_mode, id.data(), w.data());
+    orc_topk_softmax(lg.data(), E, k, expert_scale, id.data(), w.data());
     for (int j = 0; j < k; ++j)
         if (!gu[id[(size_t)j]] || !dn[id[(size_t)j]]) return -2;
     std::vector<float> xd((size_t)H / 32);
@@ -546,7 +499,7 @@ int orc_moe_layer(const float* x, int H, int I, int E, int k,
         orc_gemv_q8(gu[e], 2 * I, layout, xd.data(), xq.data(), H, yg, threads);
         if (input_norm)
             for (int r = 0; r < 2 * I; ++r) yg[r] = yg[r] * inv_r;
-        orc_gelu_mul_q8(yg, I, gelu_mode, av.data() + (size_t)p * I, ad.data() + (size_t)p * I / 32,
+        orc_gelu_mul_q8(yg, I, av.data() + (size_t)p * I, ad.data() + (size_t)p * I / 32,
                         aq.data() + (size_t)p * I);
         orc_gemv_q8(dn[e], H, layout, ad.data() + (size_t)p * I / 32, aq.data() + (size_t)p * I, I,
                     ydn.data() + (size_t)p * H, threads);

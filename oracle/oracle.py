@@ -59,16 +59,12 @@ def _declare(L):
         "orc_dot_q4r_q8_scalar": (f32, [P, P, P, i64]),
         "orc_dot_q4r_q8_avx2": (f32, [P, P, P, i64]),
         "orc_gemv_q8": (None, [P, i64, i32, P, P, i64, P, i32]),
-        "orc_gelu_tanh_libm": (f32, [f32]),
-        "orc_gelu_tanh_portable": (f32, [f32]),
-        "orc_tanh_portable": (f32, [f32]),
-        "orc_exp_portable": (f64, [f64]),
-        "orc_expf_portable": (f32, [f32]),
-        "orc_gelu_mul_q8": (None, [P, i64, i32, P, P, P]),
+        "orc_gelu_tanh": (f32, [f32]),
+        "orc_gelu_mul_q8": (None, [P, i64, P, P, P]),
         "orc_router_logits": (i32, [P, P, i32, i32, P, P]),
-        "orc_topk_softmax": (i32, [P, i32, i32, P, i32, P, P]),
+        "orc_topk_softmax": (i32, [P, i32, i32, P, P, P]),
         "orc_combine": (None, [P, P, i32, i64, P, P]),
-        "orc_moe_layer": (i32, [P, i32, i32, i32, i32, P, P, P, P, P, i32, i32, i32, i32,
+        "orc_moe_layer": (i32, [P, i32, i32, i32, i32, P, P, P, P, P, i32, i32, i32,
                                 P, P, P, P, P, P, P, P, P]),
         "orc_rms_inv": (f32, [P, i32]),
         "orc_tensor_key": (u64, [u64, u32, u32, u32, u32]),
@@ -193,16 +189,14 @@ def gemv(w, x, n_rows, layout=0, threads=1):
 
 # ---- expert activation, router, combine ----
 
-GELU_LIBM, GELU_PORTABLE = 0, 1
-
-
-def gelu_mul_q8(gu, inter, mode=GELU_PORTABLE):
-    """ft-model/src/lib.rs:435-437 and :1625-1632 -> (act f32 [I], d [I/32], qs [I])."""
+def gelu_mul_q8(gu, inter):
+    """ft-model/src/lib.rs:435-437 and :1625-1632 -> (act f32 [I], d [I/32], qs [I]);
+    tanh is the host libm's tanhf, as Rust's f32::tanh."""
     gu = _f32(gu).ravel()
     act = np.zeros(inter, np.float32)
     d = np.zeros(inter // QK, np.float32)
     qs = np.zeros(inter, np.int8)
-    lib().orc_gelu_mul_q8(_p(gu), inter, mode, _p(act), _p(d), _p(qs))
+    lib().orc_gelu_mul_q8(_p(gu), inter, _p(act), _p(d), _p(qs))
     return act, d, qs
 
 
@@ -219,13 +213,14 @@ def router_logits(W, x, bias=None):
     return out
 
 
-def topk_softmax(logits, k, expert_scale=None, mode=GELU_PORTABLE):
-    """ft-model/src/lib.rs:1487-1504 -> (ids i32 [k], wts f32 [k])."""
+def topk_softmax(logits, k, expert_scale=None):
+    """ft-model/src/lib.rs:1487-1504 -> (ids i32 [k], wts f32 [k]); exp is the
+    host libm's expf, as Rust's f32::exp."""
     lg = _f32(logits).ravel()
     ids = np.zeros(k, np.int32)
     wts = np.zeros(k, np.float32)
     es = None if expert_scale is None else _f32(expert_scale)
-    rc = lib().orc_topk_softmax(_p(lg), lg.size, k, _p(es), mode, _p(ids), _p(wts))
+    rc = lib().orc_topk_softmax(_p(lg), lg.size, k, _p(es), _p(ids), _p(wts))
     if rc:
         raise ValueError("bad k")
     return ids, wts
@@ -251,7 +246,7 @@ def rms_inv(x):
 
 
 def moe_layer(x, W_r, gu_banks, dn_banks, H, I, k, bias=None, expert_scale=None,
-              layout=0, threads=1, gelu_mode=GELU_PORTABLE, input_norm=False):
+              layout=0, threads=1, input_norm=False):
     """One MoE layer for one token (ft-model/src/lib.rs:1487-1504, :1609-1653).
     input_norm: run on rmsnorm(x) in the form of rms_inv (logits and gate|up
     sums scaled by it; q8 quants and int32 dots those of x).
@@ -285,7 +280,7 @@ def moe_layer(x, W_r, gu_banks, dn_banks, H, I, k, bias=None, expert_scale=None,
     rc = lib().orc_moe_layer(
         _p(x), H, I, E, k, _p(W_r), _p(b), _p(es),
         ctypes.cast(gu_ptrs, ctypes.c_void_p), ctypes.cast(dn_ptrs, ctypes.c_void_p),
-        layout, threads, gelu_mode, int(bool(input_norm)),
+        layout, threads, int(bool(input_norm)),
         _p(r["x_out"]), _p(r["logits"]), _p(r["ids"]), _p(r["wts"]), _p(r["y_gu"]),
         _p(r["act"]), _p(r["act_d"]), _p(r["act_qs"]), _p(r["y_dn"]))
     if rc == -2:

@@ -61,10 +61,10 @@ def main():
     out["dot_blocks"] = orc.block_dots(w, qs8, 2816)
     out["dot_y"] = orc.gemv_q8(wr, 8, d8, qs8, 2816, layout=1)
 
-    # a6: GELU*up -> q8 (portable tanh) from a 2 x 704 gate|up row
+    # a6: GELU*up -> q8 (libm tanhf, as ft-core) from a 2 x 704 gate|up row
     gu = orc.gen_values(orc.tensor_key(CFG, 0, 3, orc.T_HIDDEN), 0, 2 * 704, 2.0)
     out["gelu_gu"] = gu
-    act, ad, aqs = orc.gelu_mul_q8(gu, 704, orc.GELU_PORTABLE)
+    act, ad, aqs = orc.gelu_mul_q8(gu, 704)
     out["gelu_act"], out["gelu_d"], out["gelu_qs"] = act, ad, aqs
 
     # a7-a11: one whole layer (H 128, I 64, E 8, top-2), q4r banks [E][gate|up | down]
@@ -81,7 +81,7 @@ def main():
     out["layer_x"], out["layer_Wr"], out["layer_bank"] = xl, Wr, np.stack(bank)
     out["layer_bias"] = np.array([0.0, -1.5, 0.75, 0.0, 2.0, -0.25, 0.0, 1.0], np.float32)
     for tag, bias in (("layer_", None), ("layerb_", out["layer_bias"])):
-        r = orc.moe_layer(xl, Wr, gu_b, dn_b, H, I, K, bias=bias, layout=1, gelu_mode=orc.GELU_PORTABLE)
+        r = orc.moe_layer(xl, Wr, gu_b, dn_b, H, I, K, bias=bias, layout=1)
         for key in ("logits", "ids", "wts", "act_d", "act_qs", "x_out"):
             out[tag + key] = r[key]
 

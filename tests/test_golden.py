@@ -78,7 +78,7 @@ def test_block_dots_and_gemv_reproduce_golden(orc, gold):
 
 
 def test_gelu_q8_reproduces_golden(orc, gold):
-    act, d, qs = orc.gelu_mul_q8(gold["gelu_gu"], 704, orc.GELU_PORTABLE)
+    act, d, qs = orc.gelu_mul_q8(gold["gelu_gu"], 704)
     assert np.array_equal(bits(act), bits(gold["gelu_act"]))
     assert np.array_equal(bits(d), bits(gold["gelu_d"]))
     assert np.array_equal(qs, gold["gelu_qs"])
@@ -96,8 +96,7 @@ def test_layer_reproduces_golden(orc, gold, tag):
     gu = {e: bank[e, :gb] for e in range(E)}
     dn = {e: bank[e, gb:] for e in range(E)}
     bias = gold["layer_bias"] if tag == "layerb_" else None
-    r = orc.moe_layer(gold["layer_x"], gold["layer_Wr"], gu, dn, H, I, K, bias=bias, layout=1,
-                      gelu_mode=orc.GELU_PORTABLE)
+    r = orc.moe_layer(gold["layer_x"], gold["layer_Wr"], gu, dn, H, I, K, bias=bias, layout=1)
     for key in ("logits", "ids", "wts", "act_d", "act_qs", "x_out"):
         assert np.array_equal(bits(r[key]), bits(gold[tag + key])), key
     # logits in f64 agree; the chosen experts are the stable argsort's

@@ -311,27 +311,40 @@ def test_fused_rejects_bad_shapes(gemv, stack):
 def test_fused_abort_poisons_workspace_until_init(gemv, stack):
     """A wait that gives up (forced from the host with a spin limit of 0, so
     the first incomplete poll aborts; every workgroup still exits normally)
-    records the abort; the workspace then stays poisoned -- launches on it do
-    nothing -- until ft_hip_fused_workspace_init, after which results match a
-    clean run bit for bit."""
+    records the abort and marks the outputs: x_out all NaN, ids -1, weights
+    NaN. The workspace then stays poisoned -- later launches compute nothing
+    and mark their outputs the same way -- until ft_hip_fused_workspace_init,
+    after which results match a clean run bit for bit."""
     m = stack.m
+    K, L = m.shape.top_k, m.L
     x = m.hidden(7)
     ref = torch.zeros_like(x)
     stack.run(x, ref)
     stack.check()
+
+    def marked(o, ids, wts):
+        return (bool(torch.all(torch.isnan(o))) and bool(torch.all(ids == -1))
+                and bool(torch.all(torch.isnan(wts))))
+
     gemv.fused_set_spin_limit(0)
     try:
-        stack.run(x, torch.zeros_like(x))
+        o = torch.full_like(x, 7.0)
+        ids = torch.zeros(L * K, dtype=torch.int32, device=DEV)
+        wts = torch.zeros(L * K, dtype=torch.float32, device=DEV)
+        stack.run(x, o, ids, wts)
         torch.cuda.synchronize()
     finally:
         gemv.fused_set_spin_limit(1 << 21)
     with pytest.raises(ft_hip.FtHipError) as ei:
         stack.check()
     assert ei.value.code == ft_hip.E_TIMEOUT
+    assert marked(o, ids, wts)
     o = torch.full_like(x, 7.0)
-    stack.run(x, o)  # poisoned workspace: the launch does nothing
+    ids = torch.zeros(L * K, dtype=torch.int32, device=DEV)
+    wts = torch.zeros(L * K, dtype=torch.float32, device=DEV)
+    stack.run(x, o, ids, wts)  # poisoned workspace: nothing computed, outputs marked
     torch.cuda.synchronize()
-    assert bool(torch.all(o == 7.0))
+    assert marked(o, ids, wts)
     with pytest.raises(ft_hip.FtHipError):
         stack.check()
     stack.reset()
@@ -339,3 +352,33 @@ def test_fused_abort_poisons_workspace_until_init(gemv, stack):
     stack.run(x, o)
     stack.check()
     assert np.array_equal(host(o).view(np.uint32), host(ref).view(np.uint32))
+
+
+@pytest.mark.parametrize("which,norm", [("uniform", False), ("uniform", True), ("zipf", False), ("zipf", True)])
+def test_fused_plain_build_matches_debug_build(gemv, orc, stack, zstack, which, norm):
+    """The build bench.py times (no debug pointers: the <..., false>
+    instantiation) against the debug build whose stages the teacher-forced
+    tests check: x_out, ids and weights bit-identical on the same tokens; and
+    the plain run's per-layer routing equals the oracle's on the debug run's
+    layer inputs."""
+    st = stack if which == "uniform" else zstack
+    m = st.m
+    K, L = m.shape.top_k, m.L
+    for token in (30, 31, 32):
+        r = _run_debug(st, token, norm)
+        x = m.hidden(token)
+        o = torch.zeros_like(x)
+        ids = torch.zeros(L * K, dtype=torch.int32, device=DEV)
+        wts = torch.zeros(L * K, dtype=torch.float32, device=DEV)
+        with input_norm(gemv, norm):
+            st.run(x, o, ids, wts)
+        st.check()
+        o, ids, wts = host(o), host(ids).reshape(L, K), host(wts).reshape(L, K)
+        assert np.array_equal(o.view(np.uint32), r["out"].view(np.uint32)), token
+        assert np.array_equal(ids, r["ids"]), token
+        assert np.array_equal(wts.view(np.uint32), r["wts"].view(np.uint32)), token
+        for l in range(L):
+            bias = None if m.bias is None else host(m.bias[l])
+            ie, we = route(orc, host(m.routers[l]), r["xs"][l], bias, K, norm)
+            assert np.array_equal(ids[l], ie), (token, l)
+            assert np.array_equal(wts[l].view(np.uint32), we.view(np.uint32)), (token, l)

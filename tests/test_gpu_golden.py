@@ -1,6 +1,6 @@
 """The HIP path against the frozen vectors in tests/golden/moe_tiny.npz.
 
-Bit-exact: q8 quants, per-block int32 dots, GELU*up q8 (portable tanh),
+Bit-exact: q8 quants, per-block int32 dots, GELU*up q8 (libm tanhf),
 top-k ids and weights. f32 outputs: max|dy| <= 1e-3 * ||y_ref||_2 (the
 north-star tolerance), and the layer's residual output within 1e-5 of
 ||x_out - x||.

@@ -98,7 +98,7 @@ def test_grouped_layer_matches_oracle(gemv, orc, gstack, B, zipf, norm, mfma_min
             d8, q8 = orc.q8_quantize(X[t])
             for k in range(K):
                 e = int(IDS[t, k])
-                _, ad, aq = orc.gelu_mul_q8(GU[t, k], I, orc.GELU_PORTABLE)
+                _, ad, aq = orc.gelu_mul_q8(GU[t, k], I)
                 blk = ACT[t, k]
                 assert np.array_equal(blk[:, 0:4].copy().view(np.float32)[:, 0].view(np.uint32), ad.view(np.uint32))
                 assert np.array_equal(blk[:, 8:40].copy().view(np.int8).ravel(), aq)
@@ -106,7 +106,7 @@ def test_grouped_layer_matches_oracle(gemv, orc, gstack, B, zipf, norm, mfma_min
                 if norm:
                     ref = (ref * orc.rms_inv(X[t])).astype(np.float32)
                 assert np.max(np.abs(GU[t, k] - ref)) <= 1e-3 * np.linalg.norm(ref)
-            r = orc.moe_layer(X[t], W_r, gub, dnb, H, I, K, bias=bias, layout=m.layout, gelu_mode=orc.GELU_PORTABLE,
+            r = orc.moe_layer(X[t], W_r, gub, dnb, H, I, K, bias=bias, layout=m.layout,
                               input_norm=norm)
             assert np.array_equal(r["ids"], IDS[t])
             dref = r["x_out"] - X[t]
@@ -176,7 +176,7 @@ def test_grouped_large_expert_mfma(gemv, orc, norm):
         assert np.array_equal(WTS[t].view(np.uint32), r["wts"].view(np.uint32)), t
         for k in range(K):
             assert np.max(np.abs(GU[t, k] - r["y_gu"][k])) <= 1e-3 * np.linalg.norm(r["y_gu"][k]), (t, k)
-            _, ad, aq = orc.gelu_mul_q8(GU[t, k], I, orc.GELU_PORTABLE)
+            _, ad, aq = orc.gelu_mul_q8(GU[t, k], I)
             blk = ACT[t, k]
             assert np.array_equal(blk[:, 0:4].copy().view(np.float32)[:, 0].view(np.uint32), ad.view(np.uint32))
             assert np.array_equal(blk[:, 8:40].copy().view(np.int8).ravel(), aq)

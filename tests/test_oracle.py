@@ -13,6 +13,8 @@ import math
 import numpy as np
 import pytest
 
+from cases import nonfinite_q8_blocks
+
 
 def xorshift_row(n, seed, add_golden=True):
     """ft-core/src/q4_0.rs:166-177 (pseudo_row); add_golden=False gives the
@@ -161,6 +163,13 @@ def test_q8_rounds_half_away_from_zero(orc):
     assert list(qs[:12]) == [127, 3, -3, 1, -1, 127, -127, 2, -2, 0, -1, 3]
 
 
+def test_q8_nonfinite_blocks_follow_rust_semantics(orc):
+    x, de, qe = nonfinite_q8_blocks()
+    d, qs = orc.q8_quantize(x)
+    assert np.array_equal(d.view(np.uint32), de.view(np.uint32)), (d, de)
+    assert np.array_equal(qs, qe), (qs.reshape(-1, 32)[:, :6], qe.reshape(-1, 32)[:, :6])
+
+
 def test_q8_zero_block_and_error_bound(orc):
     x = np.concatenate([np.zeros(32, np.float32),
                         np.random.default_rng(3).standard_normal(32 * 200).astype(np.float32)])
@@ -252,65 +261,54 @@ def test_q4r_layout_and_bit_identity(orc, k):
 
 
 # ---------------------------------------------------------------------------
-# GELU, portable exp/tanh (ft-model/src/lib.rs:435-437)
+# GELU (ft-model/src/lib.rs:435-437) on the host libm's tanhf
 # ---------------------------------------------------------------------------
 
-def test_exp_portable_accuracy(orc):
-    xs = np.concatenate([np.linspace(-700, 700, 20001), np.linspace(-1, 1, 20001)])
+_LIBM = None
+
+
+def libm_f32(name):
+    """The host libm's f32 function `name` through ctypes (the function Rust's
+    f32 method calls on Linux), independent of the oracle library."""
+    global _LIBM
+    if _LIBM is None:
+        import ctypes
+        _LIBM = ctypes.CDLL("libm.so.6")
+    f = getattr(_LIBM, name)
+    import ctypes
+    f.restype, f.argtypes = ctypes.c_float, [ctypes.c_float]
+    return f
+
+
+def test_gelu_special_values_and_accuracy(orc):
     L = orc.lib()
-    for x in xs[::7]:
-        e = L.orc_exp_portable(float(x))
-        ref = math.exp(float(x))
-        assert abs(e - ref) <= 4e-16 * ref, x
-
-
-def test_tanh_portable_matches_correctly_rounded_tanh(orc):
-    """(float)tanh_f64(z) is correctly rounded except at near-ties; the portable
-    tanh must agree on (essentially) every f32 input of the GELU range."""
-    L = orc.lib()
-    rng = np.random.default_rng(7)
-    z = np.concatenate([rng.standard_normal(20000).astype(np.float32) * 3,
-                        np.linspace(-10, 10, 20001, dtype=np.float32),
-                        np.array([0.0, -0.0, 1e-30, -1e-30, 9.49, 9.5, -9.5, 1e-4], np.float32)])
-    bad = 0
-    for v in z:
-        got = np.float32(L.orc_tanh_portable(float(v)))
-        ref = np.float32(math.tanh(float(v)))
-        if got != ref:
-            bad += 1
-            assert abs(float(got) - math.tanh(float(v))) <= 1.0 * np.spacing(np.float32(abs(ref)) or 1e-45)
-    assert bad <= 2
-
-
-def test_gelu_special_values_and_libm_agreement(orc):
-    L = orc.lib()
-    assert L.orc_gelu_tanh_portable(0.0) == 0.0
-    assert L.orc_gelu_tanh_portable(10.0) == 10.0
-    g = L.orc_gelu_tanh_portable(-10.0)
+    assert L.orc_gelu_tanh(0.0) == 0.0
+    assert L.orc_gelu_tanh(10.0) == 10.0
+    g = L.orc_gelu_tanh(-10.0)
     assert g == 0.0 and math.copysign(1.0, g) == -1.0
     rng = np.random.default_rng(8)
-    diff = 0
     for g in rng.standard_normal(5000).astype(np.float32) * 2:
-        a = np.float32(L.orc_gelu_tanh_portable(float(g)))
-        b = np.float32(L.orc_gelu_tanh_libm(float(g)))
+        a = np.float32(L.orc_gelu_tanh(float(g)))
         ref = 0.5 * float(g) * (1 + math.tanh(0.7978845608 * (float(g) + 0.044715 * float(g) ** 3)))
         # 1 + t cancels for negative g: its f32 rounding (~6e-8 absolute) is scaled by 0.5*|g|
         assert abs(float(a) - ref) <= 4e-7 * abs(ref) + 1.2e-7 * abs(float(g))
-        diff += a != b
-        # glibc 2.35 tanhf is not correctly rounded: the modes differ in the last bits only
-        assert abs(float(a) - float(b)) <= 4e-7 * abs(ref) + 1.2e-7 * abs(float(g))
-    assert diff < 1000  # measured ~11% of inputs on glibc 2.35
 
 
 def test_gelu_mul_q8_composition(orc):
-    """act[j] = gelu(gu[j]) * gu[I + j] (gate rows first), then q8."""
+    """act[j] = gelu(gu[j]) * gu[I + j] (gate rows first), each f32 op of
+    ft-model/src/lib.rs:436 rounded in order with libm's tanhf, then q8."""
     I = 704
     rng = np.random.default_rng(9)
     gu = rng.standard_normal(2 * I).astype(np.float32)
     act, d, qs = orc.gelu_mul_q8(gu, I)
-    L = orc.lib()
-    expect = np.array([np.float32(L.orc_gelu_tanh_portable(float(gu[j]))) * gu[I + j] for j in range(I)],
-                      np.float32)
+    tanhf = libm_f32("tanhf")
+    f = np.float32
+    expect = np.empty(I, np.float32)
+    for j in range(I):
+        g = gu[j]
+        inner = g + ((f(0.044715) * g) * g) * g
+        t = f(tanhf(float(f(0.7978845608) * inner)))
+        expect[j] = ((f(0.5) * g) * (f(1.0) + t)) * gu[I + j]
     assert np.array_equal(act, expect)
     d2, q2 = orc.q8_quantize(expect)
     assert np.array_equal(d, d2) and np.array_equal(qs, q2)
