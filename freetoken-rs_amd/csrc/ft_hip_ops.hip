@@ -1056,13 +1056,31 @@ extern "C" size_t ft_hip_moe_layer_workspace_bytes(int64_t n_seqs, int64_t hidde
     return layer_ws(nullptr, n_seqs, hidden, inter, n_experts, top_k).bytes;
 }
 
-extern "C" int ft_hip_moe_layer(ft_hip_ctx* ctx, void* stream, const float* x, float* x_out, int64_t n_seqs,
-                                int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k,
-                                const float* router_w, const float* router_bias, const float* expert_scale,
-                                const void* bank, uint64_t expert_bytes, int layout, int32_t* ids, float* wts,
-                                void* workspace, size_t workspace_bytes) {
-    clear_error();
-    const char* nm = "moe_layer";
+// The scratch of ft_hip_moe_layer_noalloc: every call on a device shares
+// this array (its contents are whatever the last call left; the layer writes
+// every byte it reads first, so nothing needs clearing). Host code never
+// names it directly: the device address comes from hipGetSymbolAddress at
+// ft_hip_create (scratch_setup) and is kept in the context.
+static __device__ __align__(256) uint8_t scratch[FT_HIP_NOALLOC_SCRATCH_BYTES];
+
+namespace ft {
+int scratch_setup(ft_hip_ctx* ctx) {
+    // called by ft_hip_create with ctx->device current
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+        return fail(FT_HIP_E_DEVICE, "create: no address for the no-alloc scratch on device %d (%s)", ctx->device,
+                    hipGetErrorString(e));
+    ctx->noalloc_scratch = ptr;
+    return FT_HIP_OK;
+}
+}  // namespace ft
+
+static int moe_layer_impl(const char* nm, ft_hip_ctx* ctx, void* stream, const float* x, float* x_out,
+                          int64_t n_seqs, int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k,
+                          const float* router_w, const float* router_bias, const float* expert_scale,
+                          const void* bank, uint64_t expert_bytes, int layout, int32_t* ids, float* wts,
+                          void* workspace, size_t workspace_bytes) {
     if (hidden <= 0 || hidden % 128) return fail(FT_HIP_E_SHAPE, "%s: hidden=%lld must be a positive multiple of 128", nm, (long long)hidden);
     if (inter <= 0 || inter % 32) return fail(FT_HIP_E_SHAPE, "%s: inter=%lld must be a positive multiple of 32", nm, (long long)inter);
     if (n_experts <= 0 || n_experts > 1024) return fail(FT_HIP_E_SHAPE, "%s: n_experts not in [1, 1024]", nm);
@@ -1145,4 +1163,35 @@ extern "C" int ft_hip_moe_layer(ft_hip_ctx* ctx, void* stream, const float* x, f
     hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)((hidden + 255) / 256), (unsigned)n_seqs), dim3(256), 0,
                        S(stream), w.ydn, wts, x, x_out, (int)hidden, (int)top_k);
     return launch_status("moe_layer/combine");
+}
+
+extern "C" int ft_hip_moe_layer(ft_hip_ctx* ctx, void* stream, const float* x, float* x_out, int64_t n_seqs,
+                                int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k,
+                                const float* router_w, const float* router_bias, const float* expert_scale,
+                                const void* bank, uint64_t expert_bytes, int layout, int32_t* ids, float* wts,
+                                void* workspace, size_t workspace_bytes) {
+    clear_error();
+    return moe_layer_impl("moe_layer", ctx, stream, x, x_out, n_seqs, hidden, inter, n_experts, top_k, router_w,
+                          router_bias, expert_scale, bank, expert_bytes, layout, ids, wts, workspace, workspace_bytes);
+}
+
+extern "C" int ft_hip_moe_layer_noalloc(ft_hip_ctx* ctx, void* stream, const float* x, float* x_out,
+                                        int64_t n_seqs, int64_t hidden, int64_t inter, int64_t n_experts,
+                                        int64_t top_k, const float* router_w, const float* router_bias,
+                                        const float* expert_scale, const void* bank, uint64_t expert_bytes,
+                                        int layout, int32_t* ids, float* wts) {
+    clear_error();
+    const char* nm = "moe_layer_noalloc";
+    if (!ctx) return fail(FT_HIP_E_INVALID, "%s: null ctx", nm);
+    if (!ctx->noalloc_scratch) return fail(FT_HIP_E_DEVICE, "%s: the context has no scratch address", nm);
+    const size_t need = ft_hip_moe_layer_workspace_bytes(n_seqs, hidden, inter, n_experts, top_k);
+    if (need > (size_t)FT_HIP_NOALLOC_SCRATCH_BYTES)
+        return fail(FT_HIP_E_SHAPE,
+                    "%s: n_seqs=%lld hidden=%lld inter=%lld n_experts=%lld top_k=%lld needs %zu bytes of scratch; "
+                    "this entry point holds %d (use ft_hip_moe_layer with a workspace)",
+                    nm, (long long)n_seqs, (long long)hidden, (long long)inter, (long long)n_experts,
+                    (long long)top_k, need, FT_HIP_NOALLOC_SCRATCH_BYTES);
+    return moe_layer_impl(nm, ctx, stream, x, x_out, n_seqs, hidden, inter, n_experts, top_k, router_w, router_bias,
+                          expert_scale, bank, expert_bytes, layout, ids, wts, ctx->noalloc_scratch,
+                          (size_t)FT_HIP_NOALLOC_SCRATCH_BYTES);
 }

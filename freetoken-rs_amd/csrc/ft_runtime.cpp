@@ -58,6 +58,10 @@ extern "C" int ft_hip_create(int device, ft_hip_ctx** out) {
     c->fused_prefetch = 1;
     c->grouped_mfma_min = 0;  // automatic
     std::snprintf(c->arch, sizeof c->arch, "%s", p.gcnArchName);
+    if (int rc = ft::scratch_setup(c)) {  // once per context, with its device current
+        delete c;
+        return rc;
+    }
     *out = c;
     return FT_HIP_OK;
 }

@@ -16,6 +16,7 @@ struct ft_hip_ctx {
     int grouped_mfma_min;  // grouped layer: experts with at least this many tokens take the MFMA kernels (0: auto)
     int32_t* rec_gu;       // test record of gate|up block dots (ft_hip_set_block_dot_record), or null
     int32_t* rec_dn;       // test record of down block dots, or null
+    void* noalloc_scratch; // device address of this device's no-alloc scratch array (ft_hip_moe_layer_noalloc)
     char arch[64];
 };
 
@@ -33,6 +34,9 @@ int launch_router_logits(void* stream, const float* w, const float* x, const flo
 // needs n_rows * 16 >= dim / 32.
 int launch_route_prep(void* stream, const float* w, const float* x, const float* bias, int norm, float* inv,
                       void* q8, float* y, int64_t dim, int64_t n_rows, int64_t n_seqs);
+// Resolves the no-alloc scratch array's device address for ctx->device
+// (current) into ctx->noalloc_scratch (ft_hip_ops.hip, beside the array).
+int scratch_setup(ft_hip_ctx* ctx);
 // Input RMS norm scale per seq: inv[s] = 1 / sqrt(R-order(x_s . x_s) / dim + 1e-6).
 int launch_rms_inv(void* stream, const float* x, float* inv, int64_t dim, int64_t n_seqs);
 }  // namespace ft

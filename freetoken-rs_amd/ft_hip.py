@@ -16,6 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libfthip.so")
 
 OK, E_INVALID, E_SHAPE, E_DEVICE, E_LAUNCH, E_TIMEOUT = 0, -1, -2, -3, -4, -5
+NOALLOC_SCRATCH_BYTES = 8 << 20  # FT_HIP_NOALLOC_SCRATCH_BYTES
 Q8_BLK = 40
 LAYOUT_Q4_0, LAYOUT_Q4R = 0, 1
 
@@ -47,6 +48,8 @@ SIGNATURES = {
     "ft_hip_moe_layer_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "ft_hip_moe_layer": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _U64, _I, _P, _P,
                               _P, _SZ]),
+    "ft_hip_moe_layer_noalloc": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _U64, _I, _P,
+                                      _P]),
     "ft_hip_moe_layer_grouped_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "ft_hip_moe_layer_grouped": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P,
                                       _SZ, _P, _P]),
@@ -232,6 +235,14 @@ class Q4Gemv:
                                      n_experts, top_k, _ptr(router_w), _ptr(router_bias), _ptr(expert_scale),
                                      _ptr(bank), expert_bytes, layout, _ptr(ids), _ptr(wts), _ptr(workspace),
                                      workspace.numel() * workspace.element_size()))
+
+    def moe_layer_noalloc(self, x, x_out, n_seqs, hidden, inter, n_experts, top_k, router_w, router_bias,
+                          expert_scale, bank, expert_bytes, layout, ids, wts, stream=None):
+        """moe_layer on the library's own scratch (no workspace; allocates nothing)."""
+        check(lib().ft_hip_moe_layer_noalloc(self._ctx, _stream(stream), _ptr(x), _ptr(x_out), n_seqs, hidden,
+                                             inter, n_experts, top_k, _ptr(router_w), _ptr(router_bias),
+                                             _ptr(expert_scale), _ptr(bank), expert_bytes, layout, _ptr(ids),
+                                             _ptr(wts)))
 
     # -- grouped batched layer (ft-model/src/lib.rs:1507-1606) --
     @staticmethod

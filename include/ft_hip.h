@@ -208,6 +208,23 @@ int ft_hip_moe_layer(ft_hip_ctx* ctx, void* stream, const float* x, float* x_out
                      int layout, int32_t* ids, float* wts, void* workspace,
                      size_t workspace_bytes);
 
+/* ft_hip_moe_layer without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. Its
+ * scratch is a library-owned device array of FT_HIP_NOALLOC_SCRATCH_BYTES per
+ * GPU (resolved at ft_hip_create, held until the process ends); a shape whose
+ * ft_hip_moe_layer_workspace_bytes() exceeds that returns FT_HIP_E_SHAPE.
+ * The call itself allocates nothing. Every call on one GPU shares that
+ * array: calls that overlap on one GPU (other streams, other contexts, other
+ * host threads) race and must be serialised by the caller. Same kernels and
+ * results as ft_hip_moe_layer. */
+#define FT_HIP_NOALLOC_SCRATCH_BYTES (8 << 20)
+int ft_hip_moe_layer_noalloc(ft_hip_ctx* ctx, void* stream, const float* x, float* x_out,
+                             int64_t n_seqs, int64_t hidden, int64_t inter, int64_t n_experts,
+                             int64_t top_k, const float* router_w, const float* router_bias,
+                             const float* expert_scale, const void* bank, uint64_t expert_bytes,
+                             int layout, int32_t* ids, float* wts);
+
 /* One MoE layer for n_seqs decode tokens with the (token, expert) pairs
  * grouped by expert: replaces the batched pair section of
  * ft-model/src/lib.rs:1507-1606 (quantize_q8, gemv_q4r_ptr over every pair,
