@@ -53,8 +53,10 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--config", choices=list(CONFIGS), default="gemma30",
-                    help="gemma30 = the headline (cfg2); zipf = cfg3; batch16/batch64 = cfg4; large1/large32 = cfg5")
+    ap.add_argument("--config", choices=list(CONFIGS) + ["dense"], default="gemma30",
+                    help="gemma30 = the headline (cfg2); zipf = cfg3; batch16/batch64 = cfg4; large1/large32 = "
+                         "cfg5; dense = the dense q4r GEMVs around the expert section (qkv, o_proj, shared MLP, "
+                         "lm_head)")
     ap.add_argument("--path", choices=["auto", "fused", "grouped", "multikernel"], default="auto",
                     help="auto: fused whole-stack kernel at batch 1 of the Gemma shape, grouped layers (dot4 and "
                          "int8 MFMA kernels) for batched decode, launch-by-launch layers for the large-expert "
@@ -162,6 +164,85 @@ def time_dominant_kernel(g, model, reps=3):
     return us, nbytes
 
 
+def bench_dense(args, g):
+    """--config dense: the dense q4r GEMVs around Gemma's expert section
+    (moe_synth.DENSE) through ft_hip_gemv_q4_grouped_slots with one entry,
+    as the reference's gemv_q4r_idx with a dense index. Each GEMV rotates over
+    enough seeded weight copies (>= 1.5 GB) that no launch finds its matrix in
+    the 256 MB last-level cache; `args.steps` launches per GEMV are captured
+    in one HIP graph and timed with HIP events on the graph's stream. value =
+    30 x (qkv + o_proj + shared gate|up + shared down) + lm_head, the dense
+    GEMV time of one decoded token."""
+    import numpy as np
+    import torch
+    import ft_hip
+    import moe_synth
+    dev = "cuda:0"
+    order = ["qkv", "o_proj", "shared_gate_up", "shared_down", "lm_head"]
+    per = {}
+    stream = torch.cuda.Stream()
+    for name in order:
+        rows, k = moe_synth.DENSE[name]
+        rb = ft_hip.row_bytes(k, ft_hip.LAYOUT_Q4R)
+        mbytes = rows * rb
+        copies = max(2, -(-1_500_000_000 // mbytes))
+        W = moe_synth.dense_weights(g, name, copies=copies, device=dev)
+        x = torch.from_numpy(np.random.default_rng(rows + k).standard_normal(k).astype(np.float32)).to(dev)
+        q8 = torch.zeros(k // 32 * 40, dtype=torch.uint8, device=dev)
+        y = torch.zeros(rows, dtype=torch.float32, device=dev)
+        slots = torch.zeros(1, dtype=torch.int32, device=dev)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            g.quantize_q8(x, 0, q8, k, 1, stream=stream)
+
+            def launches(n):
+                for i in range(n):
+                    c = i % copies
+                    g.gemv_grouped_slots(W[c * mbytes:(c + 1) * mbytes], 0, 0, slots, None, 1, q8, 0, y, rows,
+                                         rows, k, stream=stream)
+
+            launches(args.warmup)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                launches(args.steps)
+            graph.replay()
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record(stream)
+            graph.replay()
+            ev1.record(stream)
+        torch.cuda.synchronize()
+        us = ev0.elapsed_time(ev1) * 1000.0 / args.steps
+        gbps = mbytes / (us * 1e-6) / 1e9
+        per[name] = {"rows": rows, "k": k, "bytes": mbytes, "us": round(us, 3), "GBps": round(gbps, 1),
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "copies": copies}
+        log(f"[dense] {name:15s} {rows:6d} x {k}: {mbytes / 1e6:7.2f} MB, {us:8.2f} us/launch, {gbps:6.0f} GB/s "
+            f"({gbps / HBM_PEAK_GBPS:.1%} of peak), {copies} rotating copies")
+        del W, graph
+        torch.cuda.empty_cache()
+    L = moe_synth.GEMMA.n_layers
+    layer = ["qkv", "o_proj", "shared_gate_up", "shared_down"]
+    tok_us = L * sum(per[n]["us"] for n in layer) + per["lm_head"]["us"]
+    tok_bytes = L * sum(per[n]["bytes"] for n in layer) + per["lm_head"]["bytes"]
+    dom = max(order, key=lambda n: per[n]["us"] * (L if n in layer else 1))
+    d = per[dom]
+    res = {
+        "metric": "dense q4r GEMV µs/token (30 x qkv, o_proj, shared MLP + lm_head) + achieved HBM GB/s",
+        "value": round(tok_us, 2), "unit": "us/token", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(tok_us / 1000.0, 5), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "q4r x q8 (int8 dot, f32 accumulate)",
+        "data": "synthetic (seeded N(0,0.02) q4r weights, N(0,1) input)",
+        "config": {"workload": "dense q4r GEMVs of the Gemma-4-26B-A4B-shaped decode step, batch 1",
+                   "name": "dense", "gemvs": per, "layers": L},
+        "achieved_GBps": round(tok_bytes / (tok_us * 1e-6) / 1e9, 1),
+        "hbm_frac": round(tok_bytes / (tok_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+        "roofline": {"bound": "hbm", "achieved": d["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": d["frac"], "traffic": None, "kernel": f"k_gemv_q4_grouped<q4r> ({dom})",
+                     "bytes_per_launch": d["bytes"], "us_per_launch": d["us"]},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(res), flush=True)
+
+
 def cpu_baseline(model, hidden, seconds, threads, input_norm):
     """The oracle's restatement of ft-core's AVX2 CPU path (row-parallel over
     `threads` host threads, as rayon's par_iter_mut) over the same section,
@@ -216,6 +297,9 @@ def main():
     import ft_hip
     import moe_synth
 
+    if args.config == "dense":
+        bench_dense(args, ft_hip.Q4Gemv(0))
+        return
     shape_name, B, zipf_s, cfg_id = CONFIGS[args.config]
     shape = getattr(moe_synth, shape_name)
     path = args.path

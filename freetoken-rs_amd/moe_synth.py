@@ -41,6 +41,30 @@ class Shape:
 GEMMA = Shape("gemma4-26b-a4b-moe", 2816, 704, 128, 8, 30, 1)
 LARGE = Shape("large-expert-h4096-i14336", 4096, 14336, 8, 2, 32, 5)
 
+# The dense q4r GEMVs around Gemma's expert section, (rows, k): qkv
+# (ft-model/src/lib.rs:1255-1265), o_proj (:1335-1345), the shared MLP's
+# gate|up and down (:1371-1396) and lm_head (:1675-1682). The reference reads
+# the widths from its GGUF; these take the row widths of its own q4r test
+# (ft-cuda/tests/q4r.rs: k in {2816, 2112, 704, 4096}): 16 query heads x 256
+# (4096 rows, o_proj k 4096), k and v of 2048 rows each, a shared-MLP width of
+# 2112, and Gemma's 262,144-token vocabulary.
+DENSE = {"qkv": (8192, 2816), "o_proj": (2816, 4096), "shared_gate_up": (4224, 2816),
+         "shared_down": (2816, 2112), "lm_head": (262144, 2816)}
+DENSE_CFG = 200  # generator config id of the dense weights
+
+
+def dense_weights(gemv, name, copies=1, device="cuda", sigma=0.02):
+    """`copies` seeded q4r matrices of DENSE[name] in one allocation (copy c
+    at c * rows * row_bytes), generated on the device."""
+    rows, k = DENSE[name]
+    rb = ft_hip.row_bytes(k, ft_hip.LAYOUT_Q4R)
+    w = torch.empty(copies * rows * rb, dtype=torch.uint8, device=device)
+    idx = sorted(DENSE).index(name)
+    for c in range(copies):
+        gemv.gen_q4_rows(tensor_key(DENSE_CFG, c, idx, T_GU), 0, rows, k, gen_scale(sigma),
+                         w[c * rows * rb:(c + 1) * rows * rb], ft_hip.LAYOUT_Q4R)
+    return w
+
 
 def _mix64(z):
     z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & MASK64

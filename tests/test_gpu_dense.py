@@ -1,0 +1,105 @@
+"""The dense q4r GEMVs around Gemma's expert section (qkv, o_proj, the shared
+MLP, lm_head; ft-model/src/lib.rs:1255-1265, :1335-1345, :1371-1396,
+:1675-1682) on the same kernel family, at the shapes of moe_synth.DENSE.
+
+The reference runs each as gemv_q4r_idx with a dense index (one "expert",
+ft-model/src/lib.rs:1259-1262); here ft_hip_gemv_q4_grouped_slots with
+slots = [0]. Per-(row, block) int32 dots bit-exact against the oracle's
+integer dots (ft-core/src/q4_0.rs:105-118); outputs within 1e-3 * ||y||_2
+and 1e-5 * sum|w*x| per row. The shared MLP runs gate|up -> GELU*up q8 ->
+down: the q8 activation bit-exact against the oracle's GELU*up q8 of the
+GPU's own gate|up sums, in two launches (gemv + gelu_mul_q8, as the reference)
+and in one (ft_hip_gemv_gate_up_act). lm_head is checked on a slice of its
+262,144 rows (the launch covers all of them).
+"""
+import numpy as np
+import pytest
+import torch
+
+import ft_hip
+import moe_synth
+from cases import q4r_to_q4_0
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def q8_dev(gemv, x):
+    k = x.numel()
+    q8 = torch.zeros(k // 32 * 40, dtype=torch.uint8, device=DEV)
+    gemv.quantize_q8(x, 0, q8, k, 1)
+    return q8
+
+
+def check_gemv(gemv, orc, W, rows, k, x, check_rows):
+    """y = W q8(x) through the grouped entry point with one entry; returns y."""
+    q8 = q8_dev(gemv, x)
+    slots = torch.zeros(1, dtype=torch.int32, device=DEV)
+    y = torch.zeros(rows, dtype=torch.float32, device=DEV)
+    gemv.gemv_grouped_slots(W, 0, 0, slots, None, 1, q8, 0, y, rows, rows, k)
+    nb = k // 32
+    dots = torch.zeros(check_rows * nb, dtype=torch.int32, device=DEV)
+    gemv.block_dots(W, 0, 0, slots, None, 1, q8, 0, dots, check_rows, k)
+    y, dots = host(y), host(dots).reshape(check_rows, nb)
+    raw = q4r_to_q4_0(host(W[:check_rows * ft_hip.row_bytes(k, ft_hip.LAYOUT_Q4R)]), check_rows, k)
+    d8, qs8 = orc.q8_quantize(host(x))
+    assert np.array_equal(dots, orc.block_dots(raw, qs8, k))
+    ref = orc.gemv_q8(raw, check_rows, d8, qs8, k, threads=8)
+    assert np.max(np.abs(y[:check_rows] - ref)) <= 1e-3 * np.linalg.norm(ref)
+    from test_oracle import unpack_q4
+    nib, d4 = unpack_q4(raw, k)
+    mag = np.abs((nib.astype(np.float64) - 8) * np.repeat(d4, 32, axis=1)) @ np.abs(
+        qs8.astype(np.float64) * np.repeat(d8, 32))
+    assert np.all(np.abs(y[:check_rows].astype(np.float64) - ref) <= 1e-5 * mag + 1e-30)
+    return y
+
+
+@pytest.mark.parametrize("name", ["qkv", "o_proj", "shared_gate_up", "shared_down", "lm_head"])
+def test_dense_gemv(gemv, orc, name):
+    rows, k = moe_synth.DENSE[name]
+    W = moe_synth.dense_weights(gemv, name)
+    x = torch.from_numpy(np.random.default_rng(rows + k).standard_normal(k).astype(np.float32)).to(DEV)
+    y = check_gemv(gemv, orc, W, rows, k, x, rows if rows <= 8192 else 2048)
+    assert np.all(np.isfinite(y))  # every row of the launch was written
+
+
+def test_shared_mlp_chain(gemv, orc):
+    """gate|up (4224 x 2816) -> GELU*up q8 (2112) -> down (2816 x 2112)."""
+    (gu_rows, H), (_, I) = moe_synth.DENSE["shared_gate_up"], moe_synth.DENSE["shared_down"]
+    assert gu_rows == 2 * I
+    Wgu = moe_synth.dense_weights(gemv, "shared_gate_up")
+    Wdn = moe_synth.dense_weights(gemv, "shared_down")
+    x = torch.from_numpy(np.random.default_rng(11).standard_normal(H).astype(np.float32)).to(DEV)
+    ygu = check_gemv(gemv, orc, Wgu, gu_rows, H, x, gu_rows)
+    # GELU*up q8 of the GPU's own gate|up sums: bit-exact (two launches, as the reference)
+    q8a = torch.zeros(I // 32 * 40, dtype=torch.uint8, device=DEV)
+    gemv.gelu_mul_q8(torch.from_numpy(ygu).to(DEV), q8a, I, 1)
+    blk = host(q8a).reshape(I // 32, 40)
+    _, ad, aq = orc.gelu_mul_q8(ygu, I)
+    assert np.array_equal(blk[:, :4].copy().view(np.float32)[:, 0].view(np.uint32), ad.view(np.uint32))
+    assert np.array_equal(blk[:, 8:].copy().view(np.int8).ravel(), aq)
+    # one launch: gate|up GEMV with GELU*up and q8 (ft_hip_gemv_gate_up_act). Its f32 gate|up sums
+    # run in another lane order than the GEMV above, so its q8 may differ from the two-launch one by
+    # the rounding of those sums only: per block d within 1e-5 relative and quants within 1
+    q8b = torch.zeros_like(q8a)
+    slots = torch.zeros(1, dtype=torch.int32, device=DEV)
+    gemv.gemv_gate_up_act(Wgu, Wgu.numel(), slots, 1, 1, q8_dev(gemv, x), H, I, q8b)
+    b1 = host(q8b).reshape(I // 32, 40)
+    d1 = b1[:, :4].copy().view(np.float32)[:, 0]
+    assert np.all(np.abs(d1 - ad) <= 1e-5 * np.abs(ad))
+    assert np.max(np.abs(b1[:, 8:].copy().view(np.int8).astype(int).ravel() - aq.astype(int))) <= 1
+    # down from the act q8, through the grouped GEMV: dots bit-exact, f32 within tolerance
+    nb = I // 32
+    y = torch.zeros(H, dtype=torch.float32, device=DEV)
+    gemv.gemv_grouped_slots(Wdn, 0, 0, slots, None, 1, q8a, 0, y, H, H, I)
+    dots = torch.zeros(H * nb, dtype=torch.int32, device=DEV)
+    gemv.block_dots(Wdn, 0, 0, slots, None, 1, q8a, 0, dots, H, I)
+    raw = q4r_to_q4_0(host(Wdn), H, I)
+    assert np.array_equal(host(dots).reshape(H, nb), orc.block_dots(raw, aq, I))
+    ref = orc.gemv_q8(raw, H, ad, aq, I, threads=8)
+    assert np.max(np.abs(host(y) - ref)) <= 1e-3 * np.linalg.norm(ref)
