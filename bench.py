@@ -53,10 +53,10 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--config", choices=list(CONFIGS) + ["dense"], default="gemma30",
+    ap.add_argument("--config", choices=list(CONFIGS) + ["dense", "hbm"], default="gemma30",
                     help="gemma30 = the headline (cfg2); zipf = cfg3; batch16/batch64 = cfg4; large1/large32 = "
                          "cfg5; dense = the dense q4r GEMVs around the expert section (qkv, o_proj, shared MLP, "
-                         "lm_head)")
+                         "lm_head); hbm = the achievable HBM read rate")
     ap.add_argument("--path", choices=["auto", "fused", "grouped", "multikernel"], default="auto",
                     help="auto: fused whole-stack kernel at batch 1 of the Gemma shape, grouped layers (dot4 and "
                          "int8 MFMA kernels) for batched decode, launch-by-launch layers for the large-expert "
@@ -64,6 +64,8 @@ def parse():
     ap.add_argument("--mfma-min", type=int, default=0,
                     help="grouped path: experts with at least this many tokens take the int8 MFMA kernels "
                          "(0: automatic, every expert on MFMA from 8 pairs per expert on)")
+    ap.add_argument("--gemv-lanes", type=int, choices=[0, 8, 16, 32, 64], default=0,
+                    help="dense config: lanes per row of the q4r GEMV launches (0: automatic)")
     ap.add_argument("--layers", type=int, default=0, help="0 = the config's layer count")
     ap.add_argument("--prefetch", type=int, choices=[0, 1], default=1,
                     help="fused path: stream the early-routed experts of the next layer ahead (1) or not (0)")
@@ -219,6 +221,26 @@ def bench_dense(args, g):
             f"({gbps / HBM_PEAK_GBPS:.1%} of peak), {copies} rotating copies")
         del W, graph
         torch.cuda.empty_cache()
+    # the floor of one launch in the graph: the same entry point on a 1 x 32 matrix
+    Wf = torch.empty(ft_hip.row_bytes(32, ft_hip.LAYOUT_Q4R), dtype=torch.uint8, device=dev)
+    g.gen_q4_rows(moe_synth.tensor_key(moe_synth.DENSE_CFG, 0, 0, 0), 0, 1, 32, moe_synth.gen_scale(0.02), Wf,
+                  ft_hip.LAYOUT_Q4R)
+    q8f = torch.zeros(40, dtype=torch.uint8, device=dev)
+    yf = torch.zeros(1, dtype=torch.float32, device=dev)
+    slots = torch.zeros(1, dtype=torch.int32, device=dev)
+    with torch.cuda.stream(stream):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for _ in range(args.steps):
+                g.gemv_grouped_slots(Wf, 0, 0, slots, None, 1, q8f, 0, yf, 1, 1, 32, stream=stream)
+        graph.replay()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record(stream)
+        graph.replay()
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    floor_us = ev0.elapsed_time(ev1) * 1000.0 / args.steps
+    log(f"[dense] launch floor (1 x 32 matrix): {floor_us:.2f} us/launch")
     L = moe_synth.GEMMA.n_layers
     layer = ["qkv", "o_proj", "shared_gate_up", "shared_down"]
     tok_us = L * sum(per[n]["us"] for n in layer) + per["lm_head"]["us"]
@@ -232,12 +254,55 @@ def bench_dense(args, g):
         "vs_baseline": None, "dtype": "q4r x q8 (int8 dot, f32 accumulate)",
         "data": "synthetic (seeded N(0,0.02) q4r weights, N(0,1) input)",
         "config": {"workload": "dense q4r GEMVs of the Gemma-4-26B-A4B-shaped decode step, batch 1",
-                   "name": "dense", "gemvs": per, "layers": L},
+                   "name": "dense", "gemvs": per, "layers": L, "gemv_lanes": args.gemv_lanes or "auto",
+                   "launch_floor_us": round(floor_us, 3)},
         "achieved_GBps": round(tok_bytes / (tok_us * 1e-6) / 1e9, 1),
         "hbm_frac": round(tok_bytes / (tok_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
         "roofline": {"bound": "hbm", "achieved": d["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": d["frac"], "traffic": None, "kernel": f"k_gemv_q4_grouped<q4r> ({dom})",
+                     "frac": d["frac"], "traffic": None, "kernel": f"q4r GEMV launch ({dom})",
                      "bytes_per_launch": d["bytes"], "us_per_launch": d["us"]},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(res), flush=True)
+
+
+def bench_hbm(args, g):
+    """--config hbm: the achievable HBM read rate. ft_hip_stream_read over
+    one 8 GiB buffer (32x the 256 MB last-level cache), `args.steps` reads
+    per grid size, timed with HIP events on the launch stream; value = the
+    best grid's GB/s."""
+    import torch
+    dev = "cuda:0"
+    nbytes = 8 << 30
+    buf = torch.ones(nbytes // 4, dtype=torch.int32, device=dev)
+    out = torch.zeros(65536, dtype=torch.int32, device=dev)
+    stream = torch.cuda.Stream()
+    rates = {}
+    with torch.cuda.stream(stream):
+        for nwg in (1024, 2048, 4096, 8192, 16384, 32768, 65536):
+            for _ in range(max(1, args.warmup // 8)):
+                g.stream_read(buf, out, nwg, stream=stream)
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record(stream)
+            for _ in range(args.steps):
+                g.stream_read(buf, out, nwg, stream=stream)
+            ev1.record(stream)
+            torch.cuda.synchronize()
+            us = ev0.elapsed_time(ev1) * 1000.0 / args.steps
+            rates[nwg] = {"us": round(us, 1), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+            log(f"[hbm] {nwg:5d} workgroups: {us:9.1f} us per 8 GiB read, {rates[nwg]['GBps']:.0f} GB/s")
+    best = max(rates, key=lambda n: rates[n]["GBps"])
+    gbps = rates[best]["GBps"]
+    res = {
+        "metric": "achievable HBM read GB/s (one read of an 8 GiB buffer)", "value": gbps, "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(rates[best]["us"] / 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
+        "data": "synthetic (constant buffer)",
+        "config": {"workload": "read-only stream over 8 GiB of device memory", "name": "hbm", "bytes": nbytes,
+                   "workgroups": best, "by_workgroups": rates},
+        "roofline": {"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "k_stream_read",
+                     "bytes_per_launch": nbytes, "us_per_launch": rates[best]["us"]},
         "cpu_baseline": None,
     }
     print(json.dumps(res), flush=True)
@@ -297,8 +362,13 @@ def main():
     import ft_hip
     import moe_synth
 
+    if args.config == "hbm":
+        bench_hbm(args, ft_hip.Q4Gemv(0))
+        return
     if args.config == "dense":
-        bench_dense(args, ft_hip.Q4Gemv(0))
+        g = ft_hip.Q4Gemv(0)
+        g.set_gemv_lanes(args.gemv_lanes)
+        bench_dense(args, g)
         return
     shape_name, B, zipf_s, cfg_id = CONFIGS[args.config]
     shape = getattr(moe_synth, shape_name)

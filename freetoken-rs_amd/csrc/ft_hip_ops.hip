@@ -149,8 +149,9 @@ __device__ __forceinline__ float topk_softmax(const float* selv, const int* seli
 // sub+LPR, ..., an fma chain in block order (four blocks' loads issued
 // together: long rows are otherwise one load latency per block). The caller
 // sums the LPR lanes by xor 1, 2, 4 (, 8).
-template <int LAYOUT, int LPR = 8>
-__device__ __forceinline__ float gemv_row_part(const uint8_t* wr, int sub, int nb, const int* lds) {
+template <int LAYOUT, int LPR = 8, bool REC = false>
+__device__ __forceinline__ float gemv_row_part(const uint8_t* wr, int sub, int nb, const int* lds,
+                                               int32_t* rec = nullptr) {
     const int qs_off = (nb * 2 + 15) / 16 * 16;
     float acc = 0.0f;
     int b = sub;
@@ -164,6 +165,7 @@ __device__ __forceinline__ float gemv_row_part(const uint8_t* wr, int sub, int n
             const int* xb = lds + (b + LPR * u) * 10;
             const float d8 = __int_as_float(xb[0]);
             const int diff = block_dot(q[u], xb + 2, xb[1]);
+            if constexpr (REC) rec[b + LPR * u] = diff;
             acc = fmaf((float)diff, d4[u] * d8, acc);
         }
     }
@@ -174,6 +176,7 @@ __device__ __forceinline__ float gemv_row_part(const uint8_t* wr, int sub, int n
         const int* xb = lds + b * 10;
         const float d8 = __int_as_float(xb[0]);
         const int diff = block_dot(q, xb + 2, xb[1]);
+        if constexpr (REC) rec[b] = diff;
         acc = fmaf((float)diff, d4 * d8, acc);
     }
     return acc;
@@ -191,8 +194,9 @@ __device__ __forceinline__ float sum_row_lanes(float acc) {
 // Grouped GEMV (replaces gemv_q4r_grouped_ptr/_idx, q4.cu:1497-1567, and the
 // v3 q4_0 variants, q4.cu:360-491, :1189-1241). A 256-thread workgroup owns 32
 // rows of one entry: 8 lanes per row, lane s takes blocks s, s+8, ...; the
-// activation sits in LDS. Grid: (ceil(n_rows/32), n_entries).
-template <int LAYOUT>
+// activation sits in LDS. REC: every block's int32 dot is also stored to
+// a.dots[e][row][block] (test record). Grid: (ceil(n_rows/32), n_entries).
+template <int LAYOUT, bool REC>
 __global__ __launch_bounds__(256) void k_gemv_q4_grouped(GemvArgs a) {
     extern __shared__ int lds[];
     const int e = blockIdx.y;
@@ -203,9 +207,63 @@ __global__ __launch_bounds__(256) void k_gemv_q4_grouped(GemvArgs a) {
     const int sub = lane & 7;
     float acc = 0.0f;
     if (row < a.n_rows)
-        acc = gemv_row_part<LAYOUT>(entry_base(a, e) + (int64_t)row * row_bytes_of(LAYOUT, a.k), sub, nb, lds);
+        acc = gemv_row_part<LAYOUT, 8, REC>(entry_base(a, e) + (int64_t)row * row_bytes_of(LAYOUT, a.k), sub, nb,
+                                            lds, REC ? a.dots + ((int64_t)e * a.n_rows + row) * nb : nullptr);
     acc = sum_row_lanes(acc);
     if (row < a.n_rows && sub == 0) a.y[(int64_t)e * a.y_stride + row] = acc;
+}
+
+// Short-launch GEMV for q4r matrices whose k_gemv_q4_grouped grid would
+// leave most CUs with one workgroup or none (the dense projections of a
+// decode step: a few MB each, so the launch is one HBM latency long, not a
+// bandwidth-long stream). LPR lanes per row (16, 32 or 64) and 256/LPR rows
+// per workgroup multiply the workgroups; a lane's NBL blocks (sub, sub+LPR,
+// ..., nb <= LPR*NBL) are all loaded before the activation row is staged, so
+// the weight loads and the q8 staging share one latency. The lane's fma chain
+// runs in block order and the LPR lanes are summed by xor 1, 2, ..., LPR/2.
+// REC: every block's int32 dot is also stored to a.dots[e][row][block] (test
+// record). Grid (ceil(n_rows / (256/LPR)), n_entries).
+template <int LPR, int NBL, bool REC>
+__global__ __launch_bounds__(256) void k_gemv_q4r_short(GemvArgs a) {
+    extern __shared__ int lds[];
+    constexpr int RPW = 256 / LPR;
+    const int e = blockIdx.y;
+    const int nb = a.k >> 5;
+    const int qs_off = (nb * 2 + 15) / 16 * 16;
+    const int row = blockIdx.x * RPW + (int)threadIdx.x / LPR;
+    const int sub = (int)threadIdx.x % LPR;
+    const bool live = row < a.n_rows;
+    const uint8_t* wr = entry_base(a, e) + (int64_t)(live ? row : 0) * row_bytes_of(FT_LAYOUT_Q4R, a.k);
+    float d4[NBL];
+    uint4 q[NBL];
+#pragma unroll
+    for (int u = 0; u < NBL; ++u) {
+        const int b = sub + LPR * u;
+        if (live && b < nb) {
+            load_block<FT_LAYOUT_Q4R>(wr, b, qs_off, d4[u], q[u]);
+        } else {
+            d4[u] = 0.0f;
+            q[u] = make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    stage_q8(a, e, lds);
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NBL; ++u) {
+        const int b = sub + LPR * u;
+        if (b < nb) {
+            const int* xb = lds + b * 10;
+            const float d8 = __int_as_float(xb[0]);
+            const int diff = block_dot(q[u], xb + 2, xb[1]);
+            if constexpr (REC) {
+                if (live) a.dots[((int64_t)e * a.n_rows + row) * nb + b] = diff;
+            }
+            acc = fmaf((float)diff, d4[u] * d8, acc);
+        }
+    }
+#pragma unroll
+    for (int m = 1; m < LPR; m <<= 1) acc += __shfl_xor(acc, m);
+    if (live && sub == 0) a.y[(int64_t)e * a.y_stride + row] = acc;
 }
 
 // Gate|up GEMV of one pair with GELU(gate)*up and its q8 block in the same
@@ -706,6 +764,33 @@ __global__ __launch_bounds__(256) void k_repack(const uint8_t* src, int sl, uint
         for (int i = 2 * nb; i < qs_off; ++i) d[i] = 0;
 }
 
+// Read-only stream over n16 16-byte words (the achievable HBM read rate):
+// grid-stride, each thread with four 16-byte loads in flight per step; the
+// XOR of everything a workgroup read goes to out[blockIdx.x] so no load is
+// dead code.
+__global__ __launch_bounds__(256) void k_stream_read(const uint4* buf, uint64_t n16, uint32_t* out) {
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t acc = 0;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        uint4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = buf[i + u * stride];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < n16; i += stride) {
+        const uint4 v = buf[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    __shared__ uint32_t red[4];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) out[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
 __global__ __launch_bounds__(256) void k_gen_values(uint64_t key, int64_t start, int64_t n, float scale, float* out) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) out[i] = gen_value(key, (uint64_t)(start + i), scale);
@@ -780,6 +865,35 @@ extern "C" int ft_hip_quantize_q8(ft_hip_ctx* ctx, void* stream, const float* x,
     return launch_status("quantize_q8");
 }
 
+// Lanes per row of a q4r GEMV launch: 0 for k_gemv_q4_grouped (8 lanes, 32
+// rows per workgroup), else 16/32/64 for k_gemv_q4r_short. Automatic (knob 0):
+// launches of at least 2048 workgroups of 32 rows stream at full rate on the
+// 8-lane kernel; smaller ones take the fewest lanes per row that give 1024
+// workgroups (64 when none does), with at most 8 blocks per lane.
+static int short_lanes(const ft_hip_ctx* ctx, int layout, int64_t n_rows, int64_t n_entries, int nb) {
+    if (layout != FT_LAYOUT_Q4R) return 0;
+    const int force = ctx->gemv_lanes;
+    if (force == 8) return 0;
+    if (force) return nb <= 8 * force ? force : 0;
+    if ((n_rows + 31) / 32 * n_entries >= 2048) return 0;
+    for (int lpr : {16, 32, 64})
+        if (nb <= 8 * lpr && (n_rows + 256 / lpr - 1) / (256 / lpr) * n_entries >= 1024) return lpr;
+    return nb <= 8 * 64 ? 64 : 0;
+}
+
+template <int LPR, bool REC>
+static void launch_short_rec(int nbl, dim3 grid, size_t lds, hipStream_t s, const GemvArgs& a) {
+    if (nbl <= 2) hipLaunchKernelGGL((k_gemv_q4r_short<LPR, 2, REC>), grid, dim3(256), lds, s, a);
+    else if (nbl <= 4) hipLaunchKernelGGL((k_gemv_q4r_short<LPR, 4, REC>), grid, dim3(256), lds, s, a);
+    else hipLaunchKernelGGL((k_gemv_q4r_short<LPR, 8, REC>), grid, dim3(256), lds, s, a);
+}
+
+template <int LPR>
+static void launch_short(bool rec, int nbl, dim3 grid, size_t lds, hipStream_t s, const GemvArgs& a) {
+    if (rec) launch_short_rec<LPR, true>(nbl, grid, lds, s, a);
+    else launch_short_rec<LPR, false>(nbl, grid, lds, s, a);
+}
+
 static int gemv_common(ft_hip_ctx* ctx, void* stream, GemvArgs& a, int64_t n_entries, int64_t n_rows, int64_t k,
                        int layout, bool dots, const char* name) {
     if (k <= 0 || k % 32) return fail(FT_HIP_E_SHAPE, "%s: k=%lld must be a positive multiple of 32", name, (long long)k);
@@ -803,9 +917,25 @@ static int gemv_common(ft_hip_ctx* ctx, void* stream, GemvArgs& a, int64_t n_ent
     if (dots) {
         if (layout == FT_LAYOUT_Q4R) hipLaunchKernelGGL(k_block_dots<FT_LAYOUT_Q4R>, grid, dim3(256), lds, S(stream), a);
         else hipLaunchKernelGGL(k_block_dots<FT_LAYOUT_Q4_0>, grid, dim3(256), lds, S(stream), a);
+        return launch_status(name);
+    }
+    // a block-dot record (ft_hip_set_block_dot_record, tests only) selects the
+    // instantiations that also store the dots
+    const bool rec = ctx->rec_gu != nullptr;
+    a.dots = ctx->rec_gu;
+    const int nb = (int)(k / 32);
+    if (const int lpr = short_lanes(ctx, layout, n_rows, n_entries, nb)) {
+        const int nbl = (nb + lpr - 1) / lpr;
+        const dim3 g2((unsigned)((n_rows + 256 / lpr - 1) / (256 / lpr)), (unsigned)n_entries);
+        if (lpr == 16) launch_short<16>(rec, nbl, g2, lds, S(stream), a);
+        else if (lpr == 32) launch_short<32>(rec, nbl, g2, lds, S(stream), a);
+        else launch_short<64>(rec, nbl, g2, lds, S(stream), a);
+    } else if (layout == FT_LAYOUT_Q4R) {
+        hipLaunchKernelGGL((rec ? k_gemv_q4_grouped<FT_LAYOUT_Q4R, true> : k_gemv_q4_grouped<FT_LAYOUT_Q4R, false>),
+                           grid, dim3(256), lds, S(stream), a);
     } else {
-        if (layout == FT_LAYOUT_Q4R) hipLaunchKernelGGL(k_gemv_q4_grouped<FT_LAYOUT_Q4R>, grid, dim3(256), lds, S(stream), a);
-        else hipLaunchKernelGGL(k_gemv_q4_grouped<FT_LAYOUT_Q4_0>, grid, dim3(256), lds, S(stream), a);
+        hipLaunchKernelGGL((rec ? k_gemv_q4_grouped<FT_LAYOUT_Q4_0, true> : k_gemv_q4_grouped<FT_LAYOUT_Q4_0, false>),
+                           grid, dim3(256), lds, S(stream), a);
     }
     return launch_status(name);
 }
@@ -999,6 +1129,20 @@ extern "C" int ft_hip_repack_rows(ft_hip_ctx* ctx, void* stream, const void* src
     hipLaunchKernelGGL(k_repack, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, S(stream),
                        (const uint8_t*)src, src_layout, (uint8_t*)dst, dst_layout, n_rows, (int)k);
     return launch_status("repack_rows");
+}
+
+extern "C" int ft_hip_stream_read(ft_hip_ctx* ctx, void* stream, const void* buf, uint64_t bytes, uint32_t* out,
+                                  int n_workgroups) {
+    clear_error();
+    if (!ctx || !buf || !out) return fail(FT_HIP_E_INVALID, "stream_read: null argument");
+    if (bytes % 16 || (reinterpret_cast<uintptr_t>(buf) & 15))
+        return fail(FT_HIP_E_SHAPE, "stream_read: buf and bytes must be 16-byte aligned");
+    if (n_workgroups <= 0 || n_workgroups > 65536)
+        return fail(FT_HIP_E_SHAPE, "stream_read: n_workgroups=%d not in 1..65536", n_workgroups);
+    if (bytes == 0) return FT_HIP_OK;
+    hipLaunchKernelGGL(k_stream_read, dim3((unsigned)n_workgroups), dim3(256), 0, S(stream),
+                       reinterpret_cast<const uint4*>(buf), bytes / 16, out);
+    return launch_status("stream_read");
 }
 
 extern "C" int ft_hip_gen_values(ft_hip_ctx* ctx, void* stream, uint64_t key, int64_t start, int64_t n, float scale,

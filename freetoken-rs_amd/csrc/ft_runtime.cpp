@@ -57,6 +57,7 @@ extern "C" int ft_hip_create(int device, ft_hip_ctx** out) {
     c->fused_spin_limit = 1 << 21;
     c->fused_prefetch = 1;
     c->grouped_mfma_min = 0;  // automatic
+    c->gemv_lanes = 0;        // automatic
     std::snprintf(c->arch, sizeof c->arch, "%s", p.gcnArchName);
     if (int rc = ft::scratch_setup(c)) {  // once per context, with its device current
         delete c;
@@ -79,6 +80,15 @@ extern "C" int ft_hip_set_grouped_mfma_min(ft_hip_ctx* ctx, int n_tokens) {
     if (!ctx) return fail(FT_HIP_E_INVALID, "set_grouped_mfma_min: null ctx");
     if (n_tokens < 0) return fail(FT_HIP_E_SHAPE, "set_grouped_mfma_min: n_tokens=%d < 0", n_tokens);
     ctx->grouped_mfma_min = n_tokens;
+    return FT_HIP_OK;
+}
+
+extern "C" int ft_hip_set_gemv_lanes(ft_hip_ctx* ctx, int lanes_per_row) {
+    clear_error();
+    if (!ctx) return fail(FT_HIP_E_INVALID, "set_gemv_lanes: null ctx");
+    if (lanes_per_row != 0 && lanes_per_row != 8 && lanes_per_row != 16 && lanes_per_row != 32 && lanes_per_row != 64)
+        return fail(FT_HIP_E_SHAPE, "set_gemv_lanes: lanes_per_row=%d is not 0, 8, 16, 32 or 64", lanes_per_row);
+    ctx->gemv_lanes = lanes_per_row;
     return FT_HIP_OK;
 }
 

@@ -60,6 +60,8 @@ SIGNATURES = {
     "ft_hip_fused_set_prefetch": (_I, [_P, _I]),
     "ft_hip_set_input_norm": (_I, [_P, _I]),
     "ft_hip_set_grouped_mfma_min": (_I, [_P, _I]),
+    "ft_hip_set_gemv_lanes": (_I, [_P, _I]),
+    "ft_hip_stream_read": (_I, [_P, _P, _P, _U64, _P, _I]),
     "ft_hip_set_block_dot_record": (_I, [_P, _P, _P]),
     "ft_hip_fused_workspace_init": (_I, [_P, _P, _P, _SZ]),
     "ft_hip_pack_experts_fused": (_I, [_P, _P, _P, _I, _U64, _P, _I64, _I64, _I64]),
@@ -291,6 +293,15 @@ class Q4Gemv:
         """moe_layer_grouped: experts with >= n_tokens tokens take the MFMA kernels (0, the default:
         all MFMA from 8 pairs per expert on, else all dot4)."""
         check(lib().ft_hip_set_grouped_mfma_min(self._ctx, int(n_tokens)))
+
+    def stream_read(self, buf, out, n_workgroups, nbytes=None, stream=None):
+        """Read all of `buf` (or its first nbytes) once; out: uint32[n_workgroups]."""
+        n = buf.numel() * buf.element_size() if nbytes is None else nbytes
+        check(lib().ft_hip_stream_read(self._ctx, _stream(stream), _ptr(buf), n, _ptr(out), int(n_workgroups)))
+
+    def set_gemv_lanes(self, lanes_per_row):
+        """q4r GEMV lanes per row: 0 automatic (the default), 8, 16, 32 or 64."""
+        check(lib().ft_hip_set_gemv_lanes(self._ctx, int(lanes_per_row)))
 
     def fused_workspace_init(self, ws, stream=None):
         check(lib().ft_hip_fused_workspace_init(self._ctx, _stream(stream), _ptr(ws), ws.numel() * ws.element_size()))

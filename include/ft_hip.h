@@ -168,20 +168,32 @@ int ft_hip_repack_rows(ft_hip_ctx* ctx, void* stream, const void* src, int src_l
  * gen_values writes n f32 values starting at index `start`; gen_q4_rows writes
  * rows [row0, row0 + n_rows) of a seeded [*, k] matrix quantized to q4_0
  * (ft-core/src/q4_0.rs:20-40) in `layout`. */
+/* Measurement utility (no reference counterpart; the reference's own
+ * bandwidth line is ft-bench's "cpu q4_0 gemv GB/s", ft-bench/src/main.rs:
+ * 77-114): reads `bytes` (16-byte aligned) of device memory at buf once with
+ * n_workgroups 256-thread workgroups (grid-stride, four 16-byte loads in
+ * flight per thread) and writes each workgroup's XOR of what it read to
+ * out[n_workgroups]. Its rate is the achievable HBM read bandwidth the GEMV
+ * kernels are compared with, and its known byte count calibrates the
+ * profiler's FETCH_SIZE counter. */
+int ft_hip_stream_read(ft_hip_ctx* ctx, void* stream, const void* buf, uint64_t bytes, uint32_t* out,
+                       int n_workgroups);
+
 int ft_hip_gen_values(ft_hip_ctx* ctx, void* stream, uint64_t key, int64_t start, int64_t n,
                       float scale, float* out);
 int ft_hip_gen_q4_rows(ft_hip_ctx* ctx, void* stream, uint64_t key, int64_t row0,
                        int64_t n_rows, int64_t k, float scale, void* out, int layout);
 
-/* Test hook (no reference counterpart): while set, ft_hip_moe_layer_grouped
- * and ft_hip_moe_stack_fused run instantiations of their kernels that also
- * store every per-block int32 dot sum_i (q4_i - 8) * q8_i their production
- * inner loops compute (v_dot4 and int8 MFMA alike; the production
- * instantiations are unchanged), into
+/* Test hook (no reference counterpart): while set, ft_hip_moe_layer_grouped,
+ * ft_hip_moe_stack_fused and ft_hip_gemv_q4_grouped_ptr/_slots run
+ * instantiations of their kernels that also store every per-block int32 dot
+ * sum_i (q4_i - 8) * q8_i their production inner loops compute (v_dot4 and
+ * int8 MFMA alike; the production instantiations are unchanged), into
  *   grouped: gu_dots [n_seqs*top_k pairs][2*inter rows][hidden/32 blocks],
  *            dn_dots [pairs][hidden rows][inter/32 blocks], pair p = s*top_k + k;
  *   fused:   gu_dots [n_layers][top_k slots][2*inter][hidden/32],
- *            dn_dots [n_layers][top_k][hidden][inter/32] (with the dbg_* record on).
+ *            dn_dots [n_layers][top_k][hidden][inter/32] (with the dbg_* record on);
+ *   gemv:    gu_dots [n_entries][n_rows][k/32] (dn_dots unused).
  * Rows are the expert's gate rows then up rows (gate|up) or its down rows.
  * Both NULL (the state after create) turns it off; give both or neither. */
 int ft_hip_set_block_dot_record(ft_hip_ctx* ctx, int32_t* gu_dots, int32_t* dn_dots);
@@ -258,6 +270,19 @@ int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const float* x, floa
  * the MFMA kernels. No reference counterpart (the reference runs one GEMV
  * per (token, expert) pair, ft-model/src/lib.rs:1507-1606). */
 int ft_hip_set_grouped_mfma_min(ft_hip_ctx* ctx, int n_tokens);
+
+/* ft_hip_gemv_q4_grouped_ptr/_slots on q4r rows: lanes per row of the GEMV
+ * launch. 8 = 32 rows per 256-thread workgroup, each lane streaming its
+ * blocks four at a time (the kernel for long launches); 16, 32 or 64 =
+ * 256/lanes rows per workgroup, each lane loading all of its blocks (at most
+ * 8) at once (for launches of a few MB, such as a decode step's dense
+ * projections, that would otherwise leave CUs idle). 0 (the default) =
+ * automatic: 8 when the launch has at least 2048 workgroups of 32 rows, else
+ * the fewest lanes that give 1024 workgroups (64 when none does). The int32
+ * block dots are the same; y differs by f32 summation order only. No
+ * reference counterpart (gemv_q4r_grouped_*, ft-cuda/src/q4.cu:1466-1567,
+ * runs one warp per row). */
+int ft_hip_set_gemv_lanes(ft_hip_ctx* ctx, int lanes_per_row);
 
 /* Input RMS norm of the layer entry points (ft_hip_moe_layer,
  * ft_hip_moe_layer_grouped, ft_hip_moe_stack_fused); off (0) after create.

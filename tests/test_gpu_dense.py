@@ -36,19 +36,36 @@ def q8_dev(gemv, x):
     return q8
 
 
-def check_gemv(gemv, orc, W, rows, k, x, check_rows):
-    """y = W q8(x) through the grouped entry point with one entry; returns y."""
+def check_gemv(gemv, orc, W, rows, k, x, check_rows, lanes=0):
+    """y = W q8(x) through the grouped entry point with one entry, `lanes`
+    lanes per row (0: automatic); the block dots the GEMV launch itself
+    computes (block-dot record) and those of the dump entry point are both
+    checked bit-exact. Returns y."""
     q8 = q8_dev(gemv, x)
     slots = torch.zeros(1, dtype=torch.int32, device=DEV)
     y = torch.zeros(rows, dtype=torch.float32, device=DEV)
-    gemv.gemv_grouped_slots(W, 0, 0, slots, None, 1, q8, 0, y, rows, rows, k)
     nb = k // 32
+    rec = torch.full((rows * nb,), -(1 << 30), dtype=torch.int32, device=DEV)
+    unused = torch.zeros(1, dtype=torch.int32, device=DEV)
+    gemv.set_gemv_lanes(lanes)
+    gemv.set_block_dot_record(rec, unused)
+    try:
+        gemv.gemv_grouped_slots(W, 0, 0, slots, None, 1, q8, 0, y, rows, rows, k)
+    finally:
+        gemv.set_block_dot_record(None, None)
+    y_rec = host(y)
+    y.zero_()
+    gemv.gemv_grouped_slots(W, 0, 0, slots, None, 1, q8, 0, y, rows, rows, k)
+    gemv.set_gemv_lanes(0)
     dots = torch.zeros(check_rows * nb, dtype=torch.int32, device=DEV)
     gemv.block_dots(W, 0, 0, slots, None, 1, q8, 0, dots, check_rows, k)
     y, dots = host(y), host(dots).reshape(check_rows, nb)
+    assert np.array_equal(y.view(np.uint32), y_rec.view(np.uint32))  # recording changes no bit of y
     raw = q4r_to_q4_0(host(W[:check_rows * ft_hip.row_bytes(k, ft_hip.LAYOUT_Q4R)]), check_rows, k)
     d8, qs8 = orc.q8_quantize(host(x))
-    assert np.array_equal(dots, orc.block_dots(raw, qs8, k))
+    ref_dots = orc.block_dots(raw, qs8, k)
+    assert np.array_equal(dots, ref_dots)
+    assert np.array_equal(host(rec).reshape(rows, nb)[:check_rows], ref_dots)
     ref = orc.gemv_q8(raw, check_rows, d8, qs8, k, threads=8)
     assert np.max(np.abs(y[:check_rows] - ref)) <= 1e-3 * np.linalg.norm(ref)
     from test_oracle import unpack_q4
@@ -59,13 +76,31 @@ def check_gemv(gemv, orc, W, rows, k, x, check_rows):
     return y
 
 
+@pytest.mark.parametrize("lanes", [0, 8, 16, 32, 64])
 @pytest.mark.parametrize("name", ["qkv", "o_proj", "shared_gate_up", "shared_down", "lm_head"])
-def test_dense_gemv(gemv, orc, name):
+def test_dense_gemv(gemv, orc, name, lanes):
     rows, k = moe_synth.DENSE[name]
     W = moe_synth.dense_weights(gemv, name)
     x = torch.from_numpy(np.random.default_rng(rows + k).standard_normal(k).astype(np.float32)).to(DEV)
-    y = check_gemv(gemv, orc, W, rows, k, x, rows if rows <= 8192 else 2048)
+    y = check_gemv(gemv, orc, W, rows, k, x, rows if rows <= 8192 else 2048, lanes)
     assert np.all(np.isfinite(y))  # every row of the launch was written
+
+
+@pytest.mark.parametrize("lanes", [16, 32, 64])
+@pytest.mark.parametrize("rows,k", [(1, 32), (7, 64), (33, 2048), (100, 32 * 17), (257, 4096)])
+def test_short_gemv_ragged(gemv, orc, rows, k, lanes):
+    """The short-launch kernel at ragged row counts (last workgroup partly
+    empty) and row lengths (lanes with fewer blocks than others, nb < lanes)."""
+    W = torch.empty(rows * ft_hip.row_bytes(k, ft_hip.LAYOUT_Q4R), dtype=torch.uint8, device=DEV)
+    gemv.gen_q4_rows(moe_synth.tensor_key(moe_synth.DENSE_CFG, 99, rows, k), 0, rows, k,
+                     moe_synth.gen_scale(0.02), W, ft_hip.LAYOUT_Q4R)
+    x = torch.from_numpy(np.random.default_rng(rows * k).standard_normal(k).astype(np.float32)).to(DEV)
+    check_gemv(gemv, orc, W, rows, k, x, rows, lanes)
+
+
+def test_gemv_lanes_rejects(gemv):
+    with pytest.raises(ft_hip.FtHipError):
+        gemv.set_gemv_lanes(12)
 
 
 def test_shared_mlp_chain(gemv, orc):
