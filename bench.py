@@ -3,7 +3,7 @@
 
 Workload: the 30-layer Gemma-4-26B-A4B-shaped
 expert section (H 2816, I 704, 128 experts, top-8, q4_0 banks of seeded
-N(0, 0.02) weights, f32 routers of N(0, 0.02)), decoding tokens at batch 1
+Irwin-Hall(4) weights of sd 0.02, f32 routers of the same), decoding tokens at batch 1
 with the residual chain x <- x + MoE_l(rmsnorm(x)) between layers (attention
 stubbed as identity; the unweighted pre-norm is the reference model's, and
 without it (--input-norm 0) the chain's GELU*up, quadratic in the scale of x,
@@ -252,7 +252,7 @@ def bench_dense(args, g):
         "value": round(tok_us, 2), "unit": "us/token", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(tok_us / 1000.0, 5), "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None, "dtype": "q4r x q8 (int8 dot, f32 accumulate)",
-        "data": "synthetic (seeded N(0,0.02) q4r weights, N(0,1) input)",
+        "data": "synthetic (seeded Irwin-Hall(4) values of sd 0.02 as q4r weights, sd 1 input)",
         "config": {"workload": "dense q4r GEMVs of the Gemma-4-26B-A4B-shaped decode step, batch 1",
                    "name": "dense", "gemvs": per, "layers": L, "gemv_lanes": args.gemv_lanes or "auto",
                    "launch_floor_us": round(floor_us, 3)},
@@ -308,10 +308,12 @@ def bench_hbm(args, g):
     print(json.dumps(res), flush=True)
 
 
-def cpu_baseline(model, hidden, seconds, threads, input_norm):
+def cpu_baseline(model, hidden, seconds, threads, input_norm, max_tokens=None):
     """The oracle's restatement of ft-core's AVX2 CPU path (row-parallel over
     `threads` host threads, as rayon's par_iter_mut) over the same section,
-    on a time-bounded sample of the same tokens."""
+    on a time-bounded sample of the same tokens, each token free-running
+    through all layers. Returns (us/token, tokens, per-token layer states
+    [L+1][H], per-token routing ids [L][k])."""
     import numpy as np
     import ctypes
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -329,26 +331,125 @@ def cpu_baseline(model, hidden, seconds, threads, input_norm):
     dn_ptrs = [(ctypes.c_void_p * E)(*[base + (l * E + e) * eb + gb for e in range(E)]) for l in range(model.L)]
     L = orc.lib()
     P = ctypes.c_void_p
-    x_out = np.zeros(H, np.float32)
-    n_tok = 0
-    outs = []
+    limit = len(hidden) if max_tokens is None else min(len(hidden), max_tokens)
+    states, ids_all = [], []
     t_start = time.perf_counter()
     while True:
-        x = hidden[n_tok].copy()
+        xs = np.zeros((model.L + 1, H), np.float32)
+        ids = np.zeros((model.L, k), np.int32)
+        xs[0] = hidden[len(states)]
         for l in range(model.L):
             b = None if bias is None else bias[l].ctypes.data_as(P)
-            rc = L.orc_moe_layer(x.ctypes.data_as(P), H, I, E, k, routers[l].ctypes.data_as(P), b, None,
+            rc = L.orc_moe_layer(xs[l].ctypes.data_as(P), H, I, E, k, routers[l].ctypes.data_as(P), b, None,
                                  ctypes.cast(gu_ptrs[l], P), ctypes.cast(dn_ptrs[l], P), model.layout, threads,
-                                 int(input_norm), x_out.ctypes.data_as(P), None, None, None, None, None, None,
-                                 None, None)
+                                 int(input_norm), xs[l + 1].ctypes.data_as(P), None, ids[l].ctypes.data_as(P),
+                                 None, None, None, None, None, None)
             assert rc == 0
-            x, x_out = x_out, x
-        outs.append(x.copy())
-        n_tok += 1
-        if time.perf_counter() - t_start >= seconds or n_tok >= len(hidden):
+        states.append(xs)
+        ids_all.append(ids)
+        if time.perf_counter() - t_start >= seconds or len(states) >= limit:
             break
     dt = time.perf_counter() - t_start
-    return dt * 1e6 / n_tok, n_tok, outs
+    return dt * 1e6 / len(states), len(states), states, ids_all
+
+
+def teacher_forced(model, gpu_states, gpu_ids, threads, input_norm, n_tok):
+    """Each layer of the oracle run on the GPU's own input state of that
+    layer (untimed): per (token, layer) whether the oracle's top-k ids equal
+    the GPU's, and max|x_gpu_{l+1} - x_orc_{l+1}| over the norm of the
+    oracle's update ||x_orc_{l+1} - x_gpu_l||."""
+    import numpy as np
+    import ctypes
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    s = model.shape
+    H, I, E, k = s.hidden, s.inter, s.n_experts, s.top_k
+    banks = model.banks.cpu().numpy()
+    routers = model.routers.cpu().numpy()
+    bias = None if model.bias is None else model.bias.cpu().numpy()
+    eb, gb = model.expert_bytes, model.gu_bytes
+    base = banks.ctypes.data
+    P = ctypes.c_void_p
+    L = orc.lib()
+    same, errs = [], []
+    x_out = np.zeros(H, np.float32)
+    ids = np.zeros(k, np.int32)
+    for l in range(model.L):
+        gu = (ctypes.c_void_p * E)(*[base + (l * E + e) * eb for e in range(E)])
+        dn = (ctypes.c_void_p * E)(*[base + (l * E + e) * eb + gb for e in range(E)])
+        b = None if bias is None else bias[l].ctypes.data_as(P)
+        for t in range(n_tok):
+            xin = np.ascontiguousarray(gpu_states[t][l])
+            rc = L.orc_moe_layer(xin.ctypes.data_as(P), H, I, E, k, routers[l].ctypes.data_as(P), b, None,
+                                 ctypes.cast(gu, P), ctypes.cast(dn, P), model.layout, threads, int(input_norm),
+                                 x_out.ctypes.data_as(P), None, ids.ctypes.data_as(P), None, None, None, None,
+                                 None, None)
+            assert rc == 0
+            same.append(np.array_equal(ids, gpu_ids[t][l]))
+            upd = np.linalg.norm(x_out.astype(np.float64) - xin)
+            errs.append(np.max(np.abs(gpu_states[t][l + 1].astype(np.float64) - x_out)) / max(upd, 1e-30))
+    return {"tokens": n_tok, "layers": model.L, "topk_agreement": round(float(np.mean(same)), 5),
+            "max_err": float(f"{max(errs):.3e}"), "median_err": float(f"{np.median(errs):.3e}")}
+
+
+def host_cpu():
+    """(model name, logical CPUs) of this host."""
+    name = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return name, os.cpu_count() or 1
+
+
+def q8_quants(x):
+    """ft-core's Q8Vec::quantize quants of x (q4_0.rs:62-78; f32 as there)."""
+    import numpy as np
+    b = x.astype(np.float32).reshape(-1, 32)
+    d = (np.fmax.reduce(np.abs(b), axis=1) / np.float32(127.0)).astype(np.float32)  # NaN-skipping, as f32::max
+    with np.errstate(divide="ignore", invalid="ignore"):
+        inv = np.where(d != 0, np.float32(1.0) / d, np.float32(0.0)).astype(np.float32)
+        r = (b * inv[:, None]).astype(np.float32)
+    q = np.sign(r) * np.floor(np.abs(r) + np.float32(0.5))
+    return np.nan_to_num(np.clip(q, -127, 127), nan=0.0).astype(np.int8)
+
+
+def chain_check(gpu_states, gpu_ids, cpu_states, cpu_ids):
+    """GPU vs oracle over free-running chains of the same tokens: per
+    (token, layer) top-k agreement, the first layer whose ids differ, and the
+    error of every layer's state up to it, max|x_gpu - x_cpu| over the norm
+    of the oracle's own update of that layer; also the first layer whose
+    input q8 quants differ (a rounding flip of q8, after which the chains
+    take different integer dots) and the error before it."""
+    import numpy as np
+    n, L = len(cpu_states), cpu_ids[0].shape[0]
+    q8_first = np.array([next((l for l in range(L) if not np.array_equal(q8_quants(gpu_states[t][l]),
+                                                                         q8_quants(cpu_states[t][l]))), L)
+                         for t in range(n)])
+    agree = np.array([[np.array_equal(gpu_ids[t][l], cpu_ids[t][l]) for l in range(L)] for t in range(n)])
+    first = np.array([int(np.argmin(a)) if not a.all() else L for a in agree])
+    errs = np.zeros((n, L))
+    for t in range(n):
+        xc, xg = cpu_states[t], gpu_states[t]
+        for l in range(L):
+            upd = np.linalg.norm(xc[l + 1].astype(np.float64) - xc[l])
+            errs[t, l] = np.max(np.abs(xg[l + 1].astype(np.float64) - xc[l + 1])) / max(upd, 1e-30)
+    before = [errs[t, :first[t]].max() for t in range(n) if first[t] > 0]
+    before_q8 = [errs[t, :q8_first[t] - 1].max() for t in range(n) if q8_first[t] > 1]
+    same = first == L
+    return {"tokens": n, "layers": L, "topk_agreement": round(float(agree.mean()), 5),
+            "first_q8_diff_layer_min": int(q8_first.min()),
+            "first_q8_diff_layer_median": float(np.median(q8_first)),
+            "max_err_before_first_q8_diff": float(f"{max(before_q8):.3e}") if before_q8 else None,
+            "tokens_without_flip": int(same.sum()),
+            "first_flip_layer_min": int(first.min()), "first_flip_layer_median": float(np.median(first)),
+            "max_err_before_first_flip": float(f"{max(before):.3e}") if before else None,
+            "max_err_final_no_flip": float(f"{errs[same, -1].max():.3e}") if same.any() else None,
+            "nonfinite_gpu": int(sum((~np.isfinite(x)).sum() for x in gpu_states[:n]))}
 
 
 def main():
@@ -489,23 +590,63 @@ def main():
     k_gbps = k_bytes / (k_us * 1e-6) / 1e9
     log(f"[kernel] {k_name}: {k_us:.2f} us/launch, {k_bytes} B -> {k_gbps:.0f} GB/s")
 
+    def gpu_states(n_tok):
+        """Per-layer states [L+1][H] and routing ids [L][k] of the first n_tok
+        tokens, run again through the timed path (fused: the dbg_x record;
+        layer paths: each layer into its own buffer), and whether every final
+        state equals the timed run's output bit for bit."""
+        Lm = model.L
+        st, idl = [], []
+        if path == "fused":
+            xs = torch.zeros((Lm + 1) * H, dtype=torch.float32, device=model.device)
+            ids = torch.zeros(Lm * k, dtype=torch.int32, device=model.device)
+            wts = torch.zeros(Lm * k, dtype=torch.float32, device=model.device)
+            tmp = torch.zeros(H, dtype=torch.float32, device=model.device)
+            for t in range(n_tok):
+                stack.run(hidden[t, 0], tmp, ids=ids, wts=wts, dbg_x=xs)
+                stack.check()
+                st.append(xs.cpu().numpy().reshape(Lm + 1, H))
+                idl.append(ids.cpu().numpy().reshape(Lm, k))
+        else:
+            bufs = torch.zeros((Lm + 1, B, H), dtype=torch.float32, device=model.device)
+            ids = torch.zeros((Lm, B * k), dtype=torch.int32, device=model.device)
+            wts = torch.zeros((Lm, B * k), dtype=torch.float32, device=model.device)
+            cur = torch.cuda.current_stream()
+            for c in range((n_tok + B - 1) // B):
+                bufs[0].copy_(hidden[c])
+                for l in range(Lm):
+                    layer(l, bufs[l], bufs[l + 1], ids[l], wts[l], cur)
+                xs_h, ids_h = bufs.cpu().numpy(), ids.cpu().numpy()
+                for b in range(B):
+                    st.append(xs_h[:, b].copy())
+                    idl.append(ids_h[:, b * k:(b + 1) * k].copy())
+        st, idl = st[:n_tok], idl[:n_tok]
+        final = outs.view(n_steps * B, H)[:n_tok].cpu().numpy()
+        same = all(np.array_equal(final[t].view(np.uint32), st[t][-1].view(np.uint32)) for t in range(n_tok))
+        return st, idl, same
+
     cpu = None
+    chain = None
     if not args.no_cpu:
-        threads = min(16, os.cpu_count() or 1)
+        # the GPU box's CPU share for one GPU (OMP_NUM_THREADS there), else every logical CPU
+        threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or (os.cpu_count() or 1)
+        cpu_name, n_logical = host_cpu()
         hid = hidden.view(n_steps * B, H).cpu().numpy()
-        cpu_us, cpu_n, cpu_outs = cpu_baseline(model, hid, args.cpu_seconds, threads, args.input_norm)
-        gpu_outs = outs.view(n_steps * B, H).cpu().numpy()
-        errs = np.array([np.max(np.abs(gpu_outs[i] - cpu_outs[i])) / np.linalg.norm(cpu_outs[i] - hid[i])
-                         for i in range(cpu_n)])
-        bad_gpu = int((~np.isfinite(gpu_outs[:cpu_n])).sum())
-        bad_cpu = int(sum((~np.isfinite(o)).sum() for o in cpu_outs))
-        log(f"[cpu] {cpu_us:.0f} us/token over {cpu_n} tokens on {threads} threads; "
-            f"GPU vs CPU max|dx|/||dx_ref|| = {np.nanmax(errs):.2e} (median {np.nanmedian(errs):.2e}; "
-            f"non-finite values: GPU {bad_gpu}, CPU {bad_cpu}, first bad token "
-            f"{int(np.argmax(~np.isfinite(errs))) if not np.isfinite(errs).all() else -1})")
+        cpu_us, cpu_n, cpu_states, cpu_ids = cpu_baseline(model, hid, args.cpu_seconds, threads, args.input_norm)
+        gst, gids, replay_same = gpu_states(cpu_n)
+        chain = chain_check(gst, gids, cpu_states, cpu_ids)
+        chain["gpu_rerun_bit_identical"] = bool(replay_same)
+        chain["teacher_forced"] = teacher_forced(model, gst, gids, threads, args.input_norm, min(cpu_n, 16))
+        log(f"[cpu] {cpu_us:.0f} us/token over {cpu_n} tokens on {threads} threads ({cpu_name}, "
+            f"{n_logical} logical CPUs)")
+        log(f"[chain] {json.dumps(chain)}")
+        one_us, one_n, _, _ = cpu_baseline(model, hid, args.cpu_seconds / 2, 1, args.input_norm)
+        log(f"[cpu] 1 thread: {one_us:.0f} us/token over {one_n} tokens")
         cpu = {"value": round(cpu_us, 1), "unit": "us/token", "cores": threads, "kind": "port",
                "sample": f"{cpu_n} tokens x {model.L} layers of the same workload, one token at a time "
-                         f"(libm GELU mode)"}
+                         f"(libm GELU and exp), {threads} threads = this host's CPU share for one GPU",
+               "value_1_thread": round(one_us, 1), "sample_1_thread": f"{one_n} tokens",
+               "host_cpu": cpu_name, "host_logical_cpus": n_logical}
 
     workload = {1: "", 2: "", 3: ", Zipf(1.1) router bias", 4: "", 5: ""}[cfg_id]
     res = {
@@ -520,13 +661,14 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "q4_0 x q8 (int8 dot, f32 accumulate)",
-        "data": "synthetic (seeded N(0,0.02) q4_0 banks, N(0,1) hidden)",
+        "data": "synthetic (seeded Irwin-Hall(4) values: sd 0.02 q4_0 banks and f32 routers, sd 1 hidden)",
         "config": {"workload": f"{shape.name} MoE expert FFN, {model.L} layers, batch {B}, residual chain"
                                f"{' on rmsnorm(x)' if args.input_norm else ''}{workload}",
                    "baseline_config": cfg_id, "name": args.config,
                    "hidden": H, "inter": I, "experts": E, "top_k": k, "layers": model.L, "batch": B,
                    "path": path, "prefetch": bool(args.prefetch) if path == "fused" else None,
                    "input_norm": bool(args.input_norm),
+                   "zipf_tau": moe_synth.ZIPF_TAU[(shape.name, zipf_s)] if zipf_s else None,
                    "mfma_min_tokens": args.mfma_min if path == "grouped" else None,
                    "unique_experts_per_layer": round(uniq, 2)},
         "achieved_GBps": round(gbps, 1),
@@ -536,6 +678,7 @@ def main():
                      "kernel": k_name, "bytes_per_launch": k_bytes,
                      "us_per_launch": round(k_us, 3)},
         "cpu_baseline": cpu,
+        "chain_check": chain,
     }
     print(json.dumps(res), flush=True)
 

@@ -5,7 +5,10 @@ buffers (expert banks, routers, hidden states) and drives the library
 through ft_hip.Q4Gemv, like ft-bench's decode microbenchmark does through
 ft_cuda::Q4Gemv (ft-bench/src/bin/decode.rs:93-331). Unlike that bench, whose
 weights are one template block (:111-116), every expert of every layer here
-is distinct seeded N(0, sigma) data quantized to q4_0, generated on the GPU.
+is distinct seeded data quantized to q4_0, generated on the GPU. Values are
+Irwin-Hall(4) sums of hashed 16-bit fields scaled to sd sigma (bounded at
++-3.46 sigma; integer arithmetic, so the device and the host oracle produce
+the same bits), not Gaussian.
 
 Bank layout (the reference's q4r bank layout, ft-model/src/lib.rs:570-609):
 expert (l, e) occupies bytes [(l*E + e) * expert_bytes, +expert_bytes) of one
@@ -128,7 +131,7 @@ class SyntheticMoE:
             self.bias = torch.from_numpy(zipf_router_bias(shape, self.L, zipf_s)).to(device)
 
     def hidden(self, token, out=None):
-        """Seeded ~N(0,1) hidden state of one decode token."""
+        """Seeded hidden state (Irwin-Hall(4), sd 1) of one decode token."""
         H = self.shape.hidden
         if out is None:
             out = torch.empty(H, dtype=torch.float32, device=self.device)
@@ -156,22 +159,88 @@ class SyntheticMoE:
                          None, bank, self.expert_bytes, self.layout, ids, wts, ws, stream)
 
 
-def zipf_router_bias(shape, n_layers, s=1.1, tau=None, seed=SEED):
-    """Per-layer router bias for the skewed-routing config: expert at popularity
-    rank r (a seeded permutation per layer) gets tau * ln(r^-s), so the router
-    favours experts in Zipf(s) order. tau is in units of the logit spread
-    (router sd 0.02 * sqrt(H) for ~N(0,1) hidden states)."""
-    E, H = shape.n_experts, shape.hidden
-    if tau is None:
-        tau = 0.02 * math.sqrt(H)
-    out = np.zeros((n_layers, E), np.float32)
+def gen_values_np(key, n, scale):
+    """Host restatement of the device generator (ft_hip_gen_values): value i
+    is the Irwin-Hall(4) sum of the four 16-bit fields of
+    splitmix64(key + (i+1) * 0x9E3779B97F4A7C15), centred, times scale (an f32
+    product, as on the device)."""
+    i = np.arange(1, n + 1, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = np.uint64(key) + i * np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        z = z ^ (z >> np.uint64(31))
+    m = np.uint64(0xFFFF)
+    f = ((z & m) + ((z >> np.uint64(16)) & m) + ((z >> np.uint64(32)) & m) + (z >> np.uint64(48))).astype(np.int64)
+    return (f - 131070).astype(np.float32) * np.float32(scale)
+
+
+def zipf_mass(n_experts, top_k, s):
+    """Share of Zipf(s) mass over n_experts ranks carried by the top_k ranks."""
+    p = np.arange(1, n_experts + 1, dtype=np.float64) ** -s
+    return float(p[:top_k].sum() / p.sum())
+
+
+def zipf_ranks(shape, n_layers, seed=SEED):
+    """Popularity rank (1 = most popular) of every expert per layer: a seeded
+    permutation per layer."""
+    E = shape.n_experts
+    out = np.empty((n_layers, E), np.int64)
     for l in range(n_layers):
         rng = np.random.default_rng([seed, shape.cfg_id, l, 7])
         perm = rng.permutation(E)
-        ranks = np.empty(E, np.int64)
-        ranks[perm] = np.arange(1, E + 1)
-        out[l] = (tau * (-s) * np.log(ranks)).astype(np.float32)
+        out[l, perm] = np.arange(1, E + 1)
     return out
+
+
+def zipf_top_share(shape, n_layers, s, tau, n_tokens=256, r_sigma=0.02):
+    """Share of the routed (token, expert) pairs that land on each layer's
+    top_k most popular experts, routing the seeded hidden states of n_tokens
+    tokens (RMS-normalised, as the router sees them) through each layer's
+    seeded router plus the Zipf bias with this tau (float64 on the host)."""
+    H, E, k = shape.hidden, shape.n_experts, shape.top_k
+    xs = np.stack([gen_values_np(tensor_key(shape.cfg_id, 0, t, T_HIDDEN), H, gen_scale(1.0))
+                   for t in range(n_tokens)]).astype(np.float64)
+    xs /= np.sqrt((xs * xs).mean(axis=1, keepdims=True) + 1e-6)
+    ranks = zipf_ranks(shape, n_layers)
+    hits = 0
+    for l in range(n_layers):
+        W = gen_values_np(tensor_key(shape.cfg_id, l, 0, T_ROUTER), E * H, gen_scale(r_sigma)).reshape(E, H)
+        logits = xs @ W.astype(np.float64).T - tau * s * np.log(ranks[l])[None, :]
+        top = np.argsort(-logits, axis=1, kind="stable")[:, :k]
+        hits += int((ranks[l][top] <= k).sum())
+    return hits / (n_layers * n_tokens * k)
+
+
+def calibrate_zipf_tau(shape, s=1.1, n_layers=8, n_tokens=256, lo=0.0, hi=4.0, iters=20):
+    """tau for which zipf_top_share equals zipf_mass(E, k, s): the routed
+    pairs' share on the top_k popularity ranks follows Zipf(s) (bisection;
+    the share grows with tau)."""
+    target = zipf_mass(shape.n_experts, shape.top_k, s)
+    for _ in range(iters):
+        mid = 0.5 * (lo + hi)
+        if zipf_top_share(shape, n_layers, s, mid, n_tokens) < target:
+            lo = mid
+        else:
+            hi = mid
+    return 0.5 * (lo + hi)
+
+
+# calibrate_zipf_tau(GEMMA, 1.1) = 0.8949 (8 layers x 256 tokens): the Zipf configuration's bias scale
+ZIPF_TAU = {(GEMMA.name, 1.1): 0.895}
+
+
+def zipf_router_bias(shape, n_layers, s=1.1, tau=None, seed=SEED):
+    """Per-layer router bias for the skewed-routing config: expert at
+    popularity rank r (zipf_ranks) gets tau * ln(r^-s), so the router favours
+    experts in Zipf(s) order. tau defaults to the calibrated ZIPF_TAU, for
+    which the share of routed pairs on the top_k ranks equals Zipf(s)'s mass
+    there (57 % for 8 of 128 experts at s = 1.1)."""
+    E = shape.n_experts
+    if tau is None:
+        tau = ZIPF_TAU[(shape.name, s)]
+    ranks = zipf_ranks(shape, n_layers, seed)
+    return (tau * (-s) * np.log(ranks)).astype(np.float32)
 
 
 class FusedStack:

@@ -242,24 +242,31 @@ float orc_dot_q4r_q8_avx2(const uint8_t* row, const float* d8, const int8_t* qs8
 // and :261-274), with a plain std::thread split of the output rows.
 // ---------------------------------------------------------------------------
 // A persistent worker pool (rayon keeps its pool alive too), so per-call cost
-// is a wake-up, not a thread spawn.
+// is a hand-off, not a thread spawn. Idle workers spin on the job counter
+// for a while before sleeping (rayon's workers also spin between jobs), so
+// back-to-back GEMVs of one token do not pay a futex wake-up each; the
+// caller spins until every worker has checked out of the job, so no worker
+// can still hold it when run() returns.
 namespace {
 struct Pool {
     std::vector<std::thread> workers;
     std::mutex m;
-    std::condition_variable cv, done_cv;
+    std::condition_variable cv;
     const std::function<void(int64_t, int64_t)>* job = nullptr;
     std::atomic<int64_t> next{0};
     int64_t n = 0, chunk = 16;
-    int busy = 0;
-    uint64_t gen = 0;
-    bool stop = false;
+    std::atomic<int> busy{0};
+    std::atomic<uint64_t> gen{0};
+    std::atomic<bool> stop{false};
 
     explicit Pool(int nthreads) {
         for (int t = 0; t < nthreads - 1; ++t) workers.emplace_back([this] { loop(); });
     }
     ~Pool() {
-        { std::lock_guard<std::mutex> g(m); stop = true; }
+        {
+            std::lock_guard<std::mutex> g(m);
+            stop.store(true);
+        }
         cv.notify_all();
         for (auto& w : workers) w.join();
     }
@@ -273,32 +280,33 @@ struct Pool {
     void loop() {
         uint64_t seen = 0;
         for (;;) {
-            {
-                std::unique_lock<std::mutex> g(m);
-                cv.wait(g, [&] { return stop || gen != seen; });
-                if (stop) return;
-                seen = gen;
+            int spins = 0;
+            while (gen.load(std::memory_order_acquire) == seen && !stop.load(std::memory_order_acquire)) {
+                if (++spins < (1 << 18)) {
+                    _mm_pause();
+                } else {
+                    std::unique_lock<std::mutex> g(m);
+                    cv.wait(g, [&] { return stop.load() || gen.load() != seen; });
+                }
             }
+            if (stop.load()) return;
+            seen = gen.load(std::memory_order_acquire);
             drain();
-            {
-                std::lock_guard<std::mutex> g(m);
-                if (--busy == 0) done_cv.notify_all();
-            }
+            busy.fetch_sub(1, std::memory_order_acq_rel);
         }
     }
     void run(int64_t total, const std::function<void(int64_t, int64_t)>& f) {
+        job = &f;
+        n = total;
+        next.store(0);
+        busy.store((int)workers.size());
         {
             std::lock_guard<std::mutex> g(m);
-            job = &f;
-            n = total;
-            next = 0;
-            busy = (int)workers.size();
-            ++gen;
+            gen.fetch_add(1, std::memory_order_acq_rel);
         }
         cv.notify_all();
         drain();
-        std::unique_lock<std::mutex> g(m);
-        done_cv.wait(g, [&] { return busy == 0; });
+        while (busy.load(std::memory_order_acquire) != 0) _mm_pause();
     }
 };
 std::mutex g_pool_mu;
@@ -493,17 +501,36 @@ int orc_moe_layer(const float* x, int H, int I, int E, int k,
     orc_q8_quantize(x, H, xd.data(), xq.data());
     std::vector<float> ygu((size_t)k * 2 * I), ydn((size_t)k * H), av((size_t)k * I), ad((size_t)k * I / 32);
     std::vector<int8_t> aq((size_t)k * I);
+    // The pairs run concurrently, their rows too (ft-model's par_iter over the
+    // pairs around ft-core's row-parallel gemv_q8_r): one parallel pass over
+    // the k*2I gate|up rows, the GELU*up q8 per pair, one pass over the k*H
+    // down rows. Every row's dot is the same call on the same inputs as in a
+    // pair-by-pair loop, so the bits are those of one.
+    const int64_t rb_h = layout == 0 ? orc_row_bytes(H) : orc_q4r_row_bytes(H);
+    const int64_t rb_i = layout == 0 ? orc_row_bytes(I) : orc_q4r_row_bytes(I);
+    auto dot = [&](const uint8_t* row, const float* d8, const int8_t* qs8, int64_t kk) {
+        return layout == 0 ? orc_dot_q4_q8_avx2(row, d8, qs8, kk) : orc_dot_q4r_q8_avx2(row, d8, qs8, kk);
+    };
+    parallel_rows((int64_t)k * 2 * I, threads, [&](int64_t r0, int64_t r1) {
+        for (int64_t r = r0; r < r1; ++r) {
+            const int64_t p = r / (2 * I), rr = r % (2 * I);
+            ygu[(size_t)r] = dot(gu[id[(size_t)p]] + rr * rb_h, xd.data(), xq.data(), H);
+        }
+    });
     for (int p = 0; p < k; ++p) {
-        int e = id[(size_t)p];
         float* yg = ygu.data() + (size_t)p * 2 * I;
-        orc_gemv_q8(gu[e], 2 * I, layout, xd.data(), xq.data(), H, yg, threads);
         if (input_norm)
             for (int r = 0; r < 2 * I; ++r) yg[r] = yg[r] * inv_r;
         orc_gelu_mul_q8(yg, I, av.data() + (size_t)p * I, ad.data() + (size_t)p * I / 32,
                         aq.data() + (size_t)p * I);
-        orc_gemv_q8(dn[e], H, layout, ad.data() + (size_t)p * I / 32, aq.data() + (size_t)p * I, I,
-                    ydn.data() + (size_t)p * H, threads);
     }
+    parallel_rows((int64_t)k * H, threads, [&](int64_t r0, int64_t r1) {
+        for (int64_t r = r0; r < r1; ++r) {
+            const int64_t p = r / H, rr = r % H;
+            ydn[(size_t)r] = dot(dn[id[(size_t)p]] + rr * rb_i, ad.data() + (size_t)p * I / 32,
+                                 aq.data() + (size_t)p * I, I);
+        }
+    });
     orc_combine(ydn.data(), w.data(), k, H, x, x_out);
     if (logits) std::memcpy(logits, lg.data(), sizeof(float) * (size_t)E);
     if (ids) std::memcpy(ids, id.data(), sizeof(int32_t) * (size_t)k);

@@ -26,7 +26,7 @@ CFG = 100  # generator config id reserved for the fixtures
 
 
 def q4_inputs():
-    """Four 64-value rows: seeded N(0,1), a zero block, a single spike, a
+    """Four 64-value rows: seeded Irwin-Hall(4) of sd 1, a zero block, a single spike, a
     negative-extreme block and exact-.5 values after scaling."""
     x = orc.gen_values(orc.tensor_key(CFG, 0, 0, orc.T_HIDDEN), 0, 4 * 64, 1.0).reshape(4, 64)
     x[1, :32] = 0.0
