@@ -1369,14 +1369,19 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
     const bool dbg = dbg_gu || dbg_act || dbg_x || dbg_trace || (ctx->rec_gu && ctx->rec_dn);
     const void* kern = dbg ? reinterpret_cast<const void*>(k_moe_stack_fused<11, 6, 6, true>)
                            : reinterpret_cast<const void*>(k_moe_stack_fused<11, 6, 6, false>);
-    // A plain launch: every workgroup must be resident at once, which holds
-    // when the kernel has the device to itself (nw <= CUs, one workgroup per
-    // CU). A cooperative launch guarantees it but costs ~19 us per launch
-    // against ~1-2 us measured here. If residency ever fails, the resident
-    // workgroups give up their bounded waits and the launch reports
-    // FT_HIP_E_TIMEOUT through ft_hip_fused_status; nothing hangs.
-    hipError_t e = hipLaunchKernel(kern, dim3((unsigned)nw), dim3(FT_THREADS), args, (size_t)P.lds_bytes,
-                                   reinterpret_cast<hipStream_t>(stream));
+    // Plain launch (default): every workgroup must be resident at once, which
+    // holds when the kernel has the device to itself (nw <= CUs, one
+    // workgroup per CU). A cooperative launch (ft_hip_fused_set_cooperative)
+    // guarantees it when kernels of other streams share the device, at ~19 us
+    // more per launch measured here. If residency ever fails in a plain
+    // launch, the resident workgroups give up their bounded waits and the
+    // launch reports FT_HIP_E_TIMEOUT through ft_hip_fused_status; nothing
+    // hangs.
+    hipError_t e = ctx->fused_cooperative
+                       ? hipLaunchCooperativeKernel(kern, dim3((unsigned)nw), dim3(FT_THREADS), args,
+                                                    (unsigned)P.lds_bytes, reinterpret_cast<hipStream_t>(stream))
+                       : hipLaunchKernel(kern, dim3((unsigned)nw), dim3(FT_THREADS), args, (size_t)P.lds_bytes,
+                                         reinterpret_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(FT_HIP_E_LAUNCH, "%s: launch failed: %s", nm, hipGetErrorString(e));
     return FT_HIP_OK;
 }
@@ -1394,6 +1399,14 @@ extern "C" int ft_hip_fused_set_prefetch(ft_hip_ctx* ctx, int on) {
     if (!ctx) return fail(FT_HIP_E_INVALID, "fused_set_prefetch: null ctx");
     if (on != 0 && on != 1) return fail(FT_HIP_E_SHAPE, "fused_set_prefetch: on=%d is not 0 or 1", on);
     ctx->fused_prefetch = on;
+    return FT_HIP_OK;
+}
+
+extern "C" int ft_hip_fused_set_cooperative(ft_hip_ctx* ctx, int on) {
+    clear_error();
+    if (!ctx) return fail(FT_HIP_E_INVALID, "fused_set_cooperative: null ctx");
+    if (on != 0 && on != 1) return fail(FT_HIP_E_SHAPE, "fused_set_cooperative: on=%d is not 0 or 1", on);
+    ctx->fused_cooperative = on;
     return FT_HIP_OK;
 }
 

@@ -56,6 +56,7 @@ extern "C" int ft_hip_create(int device, ft_hip_ctx** out) {
     c->num_xcds = 8;  // MI355X: 8 XCDs of 32 CUs
     c->fused_spin_limit = 1 << 21;
     c->fused_prefetch = 1;
+    c->fused_cooperative = 0;
     c->grouped_mfma_min = 0;  // automatic
     c->gemv_lanes = 0;        // automatic
     std::snprintf(c->arch, sizeof c->arch, "%s", p.gcnArchName);

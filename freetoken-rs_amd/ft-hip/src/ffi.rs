@@ -64,5 +64,6 @@ extern "C" {
     pub fn ft_hip_moe_stack_fused(ctx: *mut FtHipCtx, stream: *mut c_void, x_in: *const f32, x_out: *mut f32, hidden: i64, inter: i64, n_experts: i64, top_k: i64, n_layers: i64, banks: *const c_void, routers: *const f32, bias: *const f32, expert_scale: *const f32, ids: *mut i32, wts: *mut f32, workspace: *mut c_void, workspace_bytes: usize, dbg_gu: *mut f32, dbg_act: *mut c_void, dbg_x: *mut f32, dbg_trace: *mut u64) -> c_int;
     pub fn ft_hip_fused_set_spin_limit(ctx: *mut FtHipCtx, polls: c_int) -> c_int;
     pub fn ft_hip_fused_set_prefetch(ctx: *mut FtHipCtx, on: c_int) -> c_int;
+    pub fn ft_hip_fused_set_cooperative(ctx: *mut FtHipCtx, on: c_int) -> c_int;
     pub fn ft_hip_fused_status(ctx: *mut FtHipCtx, workspace: *mut c_void, aborted: *mut c_int) -> c_int;
 }

@@ -58,6 +58,7 @@ SIGNATURES = {
     "ft_hip_fused_workgroups": (ctypes.c_int, [_I64, _I64, _I64, _I64]),
     "ft_hip_fused_set_spin_limit": (_I, [_P, _I]),
     "ft_hip_fused_set_prefetch": (_I, [_P, _I]),
+    "ft_hip_fused_set_cooperative": (_I, [_P, _I]),
     "ft_hip_set_input_norm": (_I, [_P, _I]),
     "ft_hip_set_grouped_mfma_min": (_I, [_P, _I]),
     "ft_hip_set_gemv_lanes": (_I, [_P, _I]),
@@ -274,6 +275,10 @@ class Q4Gemv:
 
     def fused_set_spin_limit(self, polls):
         check(lib().ft_hip_fused_set_spin_limit(self._ctx, polls))
+
+    def fused_set_cooperative(self, on):
+        """Fused kernel: cooperative launch (1) or plain launch (0, the default)."""
+        check(lib().ft_hip_fused_set_cooperative(self._ctx, int(on)))
 
     def fused_set_prefetch(self, on):
         """1: stream early-routed experts ahead (default); 0: load each layer's experts once routed."""

@@ -301,7 +301,9 @@ int ft_hip_set_input_norm(ft_hip_ctx* ctx, int on);
  * (ft-model/src/lib.rs:1406-1476) and removes host launch cost with a CUDA
  * graph over the whole stack (forward_sample_graphed, ft-model/src/lib.rs:
  * 1062-1121). Here the L-layer section for one token is ONE persistent
- * cooperative kernel: device-side routing, gate|up, GELU*up, q8, down and
+ * kernel whose workgroups hand data to each other through tagged words
+ * (plain launch by default, see ft_hip_fused_set_cooperative): device-side
+ * routing, gate|up, GELU*up, q8, down and
  * combine for every layer, with the same arithmetic as the launch-by-launch
  * entry points (q8 quants, per-block int32 dots, router R-order and top-k are
  * bit-identical; f32 sums may differ in order).
@@ -376,6 +378,17 @@ int ft_hip_fused_set_spin_limit(ft_hip_ctx* ctx, int polls);
  * recently routed experts in device slots and copies misses over PCIe after
  * routing; it predicts nothing). */
 int ft_hip_fused_set_prefetch(ft_hip_ctx* ctx, int on);
+
+/* Fused kernel launch mode. 0 (default): a plain launch, whose workgroups
+ * (one per CU, fewer than the device's CUs) are all resident only while no
+ * kernel of another stream occupies CUs; the fastest mode for a device the
+ * decode loop has to itself. 1: a cooperative launch, which the runtime
+ * starts only with every workgroup resident, for callers that run other
+ * kernels concurrently on other streams (the reference overlaps a copy
+ * stream, ft-model/src/lib.rs:1425-1433; copies use DMA engines, not CUs,
+ * and need no cooperative launch). ~19 us more per launch measured on
+ * MI355X. Results are identical either way. No reference counterpart. */
+int ft_hip_fused_set_cooperative(ft_hip_ctx* ctx, int on);
 
 /* Host-synchronous check of a fused workspace after the stream has been
  * synchronised: FT_HIP_E_TIMEOUT (and *aborted = 1) if a launch gave up a

@@ -382,3 +382,52 @@ def test_fused_plain_build_matches_debug_build(gemv, orc, stack, zstack, which, 
             ie, we = route(orc, host(m.routers[l]), r["xs"][l], bias, K, norm)
             assert np.array_equal(ids[l], ie), (token, l)
             assert np.array_equal(wts[l].view(np.uint32), we.view(np.uint32)), (token, l)
+
+
+def test_fused_many_launches_full_stack(gemv):
+    """Regression test for lost hand-overs: 600 consecutive launches of the
+    production build on one workspace over the full 30-layer stack (the
+    bench's configuration), epochs advancing every launch, prediction on.
+    The workspace status is checked every 100 launches (a lost hand-over
+    shows as an aborted bounded wait), and every token's output and routing
+    must equal its first launch bit for bit."""
+    m = moe_synth.SyntheticMoE(gemv, moe_synth.GEMMA)
+    st = moe_synth.FusedStack(m)
+    K, L = m.shape.top_k, m.L
+    toks = [m.hidden(t) for t in range(8)]
+    outs = torch.zeros((600, m.shape.hidden), dtype=torch.float32, device=DEV)
+    ids = torch.zeros((600, L * K), dtype=torch.int32, device=DEV)
+    gemv.fused_set_prefetch(1)
+    for i in range(600):
+        st.run(toks[i % 8], outs[i], ids[i])
+        if i % 100 == 99:
+            st.check()
+    o, d = host(outs), host(ids)
+    for i in range(8, 600):
+        assert np.array_equal(o[i].view(np.uint32), o[i % 8].view(np.uint32)), i
+        assert np.array_equal(d[i], d[i % 8]), i
+    assert np.all(np.isfinite(o))
+    del st, m
+    torch.cuda.empty_cache()
+
+
+def test_fused_cooperative_launch_matches_plain(gemv, stack):
+    """The cooperative launch mode gives the plain launch's bits."""
+    m = stack.m
+    x = m.hidden(11)
+    res = []
+    for coop in (0, 1, 0):
+        o = torch.zeros_like(x)
+        ids = torch.zeros(m.L * m.shape.top_k, dtype=torch.int32, device=DEV)
+        gemv.fused_set_cooperative(coop)
+        try:
+            stack.run(x, o, ids)
+            stack.check()
+        finally:
+            gemv.fused_set_cooperative(0)
+        res.append((host(o), host(ids)))
+    for o, i in res[1:]:
+        assert np.array_equal(o.view(np.uint32), res[0][0].view(np.uint32))
+        assert np.array_equal(i, res[0][1])
+    with pytest.raises(ft_hip.FtHipError):
+        gemv.fused_set_cooperative(2)
