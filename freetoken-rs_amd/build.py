@@ -20,7 +20,7 @@ OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "lib", "libfthip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["ft_runtime.cpp", "ft_hip_ops.hip", "ft_hip_fused.hip", "ft_hip_grouped.hip"]
+SOURCES = ["ft_runtime.cpp", "ft_gguf.cpp", "ft_hip_ops.hip", "ft_hip_fused.hip", "ft_hip_grouped.hip"]
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
              "-fno-fast-math", "-Wall", "-Wno-unused-function",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]

@@ -14,8 +14,8 @@ struct ft_hip_ctx {
     int fused_prefetch;    // fused kernel: stream predicted experts ahead (1) or not (0)
     int fused_cooperative; // fused kernel: cooperative launch (1) or plain (0)
     int input_norm;        // layer entry points run on rmsnorm(x) (1) or x (0)
-    int grouped_mfma_min;
-    int gemv_lanes;        // q4r GEMV lanes per row (ft_hip_set_gemv_lanes): 0 automatic, 8, 16, 32 or 64  // grouped layer: experts with at least this many tokens take the MFMA kernels (0: auto)
+    int grouped_mfma_min;  // grouped layer: experts with at least this many tokens take the MFMA kernels (0: auto)
+    int gemv_lanes;        // q4r GEMV lanes per row (ft_hip_set_gemv_lanes): 0 automatic, 8, 16, 32 or 64
     int32_t* rec_gu;       // test record of gate|up block dots (ft_hip_set_block_dot_record), or null
     int32_t* rec_dn;       // test record of down block dots, or null
     void* noalloc_scratch; // device address of this device's no-alloc scratch array (ft_hip_moe_layer_noalloc)

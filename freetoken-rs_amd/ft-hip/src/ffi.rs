@@ -14,12 +14,21 @@ pub struct FtHipCtx {
     _private: [u8; 0],
 }
 
+/// Opaque handle of an open GGUF file (`ft_gguf`), created by `ft_gguf_open`.
+#[repr(C)]
+pub struct FtGguf {
+    _private: [u8; 0],
+}
+
 pub const FT_HIP_OK: c_int = 0;
 pub const FT_HIP_E_INVALID: c_int = -1;
 pub const FT_HIP_E_SHAPE: c_int = -2;
 pub const FT_HIP_E_DEVICE: c_int = -3;
 pub const FT_HIP_E_LAUNCH: c_int = -4;
 pub const FT_HIP_E_TIMEOUT: c_int = -5;
+pub const FT_HIP_E_IO: c_int = -6;
+pub const FT_HIP_E_FORMAT: c_int = -7;
+pub const FT_HIP_E_NOT_FOUND: c_int = -8;
 pub const FT_Q8_BLK: usize = 40;
 pub const FT_LAYOUT_Q4_0: c_int = 0;
 pub const FT_LAYOUT_Q4R: c_int = 1;
@@ -66,4 +75,25 @@ extern "C" {
     pub fn ft_hip_fused_set_prefetch(ctx: *mut FtHipCtx, on: c_int) -> c_int;
     pub fn ft_hip_fused_set_cooperative(ctx: *mut FtHipCtx, on: c_int) -> c_int;
     pub fn ft_hip_fused_status(ctx: *mut FtHipCtx, workspace: *mut c_void, aborted: *mut c_int) -> c_int;
+    pub fn ft_gguf_open(path: *const c_char, out: *mut *mut FtGguf) -> c_int;
+    pub fn ft_gguf_close(g: *mut FtGguf) -> c_int;
+    pub fn ft_gguf_version(g: *const FtGguf) -> u32;
+    pub fn ft_gguf_data_start(g: *const FtGguf) -> u64;
+    pub fn ft_gguf_n_kv(g: *const FtGguf) -> i64;
+    pub fn ft_gguf_n_tensors(g: *const FtGguf) -> i64;
+    pub fn ft_gguf_kv_key(g: *const FtGguf, i: i64, key: *mut *const c_char, value_type: *mut u32) -> c_int;
+    pub fn ft_gguf_meta_type(g: *const FtGguf, key: *const c_char, value_type: *mut u32) -> c_int;
+    pub fn ft_gguf_meta_u64(g: *const FtGguf, key: *const c_char, out: *mut u64) -> c_int;
+    pub fn ft_gguf_meta_f32(g: *const FtGguf, key: *const c_char, out: *mut f32) -> c_int;
+    pub fn ft_gguf_meta_str(g: *const FtGguf, key: *const c_char, s: *mut *const c_char, len: *mut u64) -> c_int;
+    pub fn ft_gguf_meta_array(g: *const FtGguf, key: *const c_char, elem_type: *mut u32, n: *mut u64) -> c_int;
+    pub fn ft_gguf_meta_array_u64(g: *const FtGguf, key: *const c_char, i: u64, out: *mut u64) -> c_int;
+    pub fn ft_gguf_meta_array_bool(g: *const FtGguf, key: *const c_char, i: u64, out: *mut c_int) -> c_int;
+    pub fn ft_gguf_meta_array_str(g: *const FtGguf, key: *const c_char, i: u64, s: *mut *const c_char, len: *mut u64) -> c_int;
+    pub fn ft_gguf_tensor_name(g: *const FtGguf, i: i64, name: *mut *const c_char) -> c_int;
+    pub fn ft_gguf_tensor_info(g: *const FtGguf, name: *const c_char, n_dims: *mut u32, dims: *mut u64, ggml_type: *mut u32, offset: *mut u64, nbytes: *mut u64) -> c_int;
+    pub fn ft_gguf_tensor_data(g: *const FtGguf, name: *const c_char, data: *mut *const c_void, nbytes: *mut u64) -> c_int;
+    pub fn ft_gguf_tensor_to_f32(g: *const FtGguf, name: *const c_char, out: *mut f32, n: u64) -> c_int;
+    pub fn ft_gguf_router_f32(g: *const FtGguf, layer: i64, hidden: i64, n_experts: i64, out: *mut f32) -> c_int;
+    pub fn ft_hip_load_expert_banks_gguf(ctx: *mut FtHipCtx, stream: *mut c_void, g: *const FtGguf, layer0: i64, n_layers: i64, hidden: i64, inter: i64, n_experts: i64, banks: *mut c_void, expert_bytes: u64, layout: c_int) -> c_int;
 }

@@ -282,6 +282,119 @@ impl Q4Gemv {
     pub fn set_input_norm(&self, on: bool) -> Result<()> {
         check(unsafe { ffi::ft_hip_set_input_norm(self.ctx, on as i32) })
     }
+
+    /// The expert banks of layers `layer0..layer0 + n_layers` of a GGUF file
+    /// into device `banks` (ft-model/src/lib.rs:570-609): expert (l, e) at
+    /// ((l - layer0) * n_experts + e) * expert_bytes, gate|up rows then down
+    /// rows in `layout`. Synchronises `s`.
+    pub fn load_expert_banks_gguf(&self, s: Stream, g: &Gguf, layer0: usize, n_layers: usize, hidden: usize,
+                                  inter: usize, n_experts: usize, banks: DevPtr, expert_bytes: usize,
+                                  layout: Layout) -> Result<()> {
+        check(unsafe {
+            ffi::ft_hip_load_expert_banks_gguf(self.ctx, s.0, g.h, layer0 as i64, n_layers as i64, hidden as i64,
+                                               inter as i64, n_experts as i64, pm(banks), expert_bytes as u64,
+                                               layout.raw())
+        })
+    }
+}
+
+/// One entry of a GGUF tensor table (`ft_gguf::TensorInfo`).
+#[derive(Debug, Clone, PartialEq)]
+pub struct TensorInfo {
+    /// ne[0] is the contiguous (row/k) dimension, ggml order.
+    pub dims: Vec<u64>,
+    pub ggml_type: u32,
+    /// byte offset within the data section
+    pub offset: u64,
+    pub nbytes: u64,
+}
+
+/// A local GGUF v2/v3 file, mapped read-only (`ft_gguf::Gguf`,
+/// ft-gguf/src/lib.rs:141-206): header, metadata and tensor table parsed at
+/// `open`, tensor bytes borrowed from the mapping.
+pub struct Gguf {
+    h: *mut ffi::FtGguf,
+}
+
+fn cstr(s: &str) -> Result<std::ffi::CString> {
+    Ok(std::ffi::CString::new(s)?)
+}
+
+impl Gguf {
+    pub fn open(path: impl AsRef<std::path::Path>) -> Result<Self> {
+        let p = cstr(&path.as_ref().to_string_lossy())?;
+        let mut h = std::ptr::null_mut();
+        check(unsafe { ffi::ft_gguf_open(p.as_ptr(), &mut h) })?;
+        Ok(Self { h })
+    }
+
+    pub fn tensor(&self, name: &str) -> Result<TensorInfo> {
+        let n = cstr(name)?;
+        let (mut nd, mut ty, mut off, mut nb) = (0u32, 0u32, 0u64, 0u64);
+        let mut dims = [0u64; 8];
+        check(unsafe {
+            ffi::ft_gguf_tensor_info(self.h, n.as_ptr(), &mut nd, dims.as_mut_ptr(), &mut ty, &mut off, &mut nb)
+        })?;
+        Ok(TensorInfo { dims: dims[..nd as usize].to_vec(), ggml_type: ty, offset: off, nbytes: nb })
+    }
+
+    pub fn tensor_data(&self, name: &str) -> Result<&[u8]> {
+        let n = cstr(name)?;
+        let mut data: *const c_void = std::ptr::null();
+        let mut nb = 0u64;
+        check(unsafe { ffi::ft_gguf_tensor_data(self.h, n.as_ptr(), &mut data, &mut nb) })?;
+        Ok(unsafe { std::slice::from_raw_parts(data as *const u8, nb as usize) })
+    }
+
+    /// `Value::as_u64` of a metadata value.
+    pub fn meta_u64(&self, key: &str) -> Result<u64> {
+        let k = cstr(key)?;
+        let mut v = 0u64;
+        check(unsafe { ffi::ft_gguf_meta_u64(self.h, k.as_ptr(), &mut v) })?;
+        Ok(v)
+    }
+
+    pub fn meta_f32(&self, key: &str) -> Result<f32> {
+        let k = cstr(key)?;
+        let mut v = 0f32;
+        check(unsafe { ffi::ft_gguf_meta_f32(self.h, k.as_ptr(), &mut v) })?;
+        Ok(v)
+    }
+
+    pub fn meta_str(&self, key: &str) -> Result<String> {
+        let k = cstr(key)?;
+        let (mut s, mut n) = (std::ptr::null(), 0u64);
+        check(unsafe { ffi::ft_gguf_meta_str(self.h, k.as_ptr(), &mut s, &mut n) })?;
+        let b = unsafe { std::slice::from_raw_parts(s as *const u8, n as usize) };
+        Ok(String::from_utf8_lossy(b).into_owned())
+    }
+
+    /// ft-model's to_f32 (ft-model/src/lib.rs:128-151) of an f32, f16 or q4_0 tensor.
+    pub fn to_f32(&self, name: &str) -> Result<Vec<f32>> {
+        let n: u64 = self.tensor(name)?.dims.iter().product();
+        let mut out = vec![0f32; n as usize];
+        let c = cstr(name)?;
+        check(unsafe { ffi::ft_gguf_tensor_to_f32(self.h, c.as_ptr(), out.as_mut_ptr(), n) })?;
+        Ok(out)
+    }
+
+    /// The router of `layer` with its scale and hidden^-1/2 folded in
+    /// (ft-model/src/lib.rs:506-514), [n_experts][hidden].
+    pub fn router_f32(&self, layer: usize, hidden: usize, n_experts: usize) -> Result<Vec<f32>> {
+        let mut out = vec![0f32; hidden * n_experts];
+        check(unsafe {
+            ffi::ft_gguf_router_f32(self.h, layer as i64, hidden as i64, n_experts as i64, out.as_mut_ptr())
+        })?;
+        Ok(out)
+    }
+}
+
+impl Drop for Gguf {
+    fn drop(&mut self) {
+        unsafe {
+            ffi::ft_gguf_close(self.h);
+        }
+    }
 }
 
 impl Drop for Q4Gemv {

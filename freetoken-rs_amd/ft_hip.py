@@ -16,6 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libfthip.so")
 
 OK, E_INVALID, E_SHAPE, E_DEVICE, E_LAUNCH, E_TIMEOUT = 0, -1, -2, -3, -4, -5
+E_IO, E_FORMAT, E_NOT_FOUND = -6, -7, -8
 NOALLOC_SCRATCH_BYTES = 8 << 20  # FT_HIP_NOALLOC_SCRATCH_BYTES
 Q8_BLK = 40
 LAYOUT_Q4_0, LAYOUT_Q4R = 0, 1
@@ -70,6 +71,28 @@ SIGNATURES = {
     "ft_hip_moe_stack_fused": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P,
                                     _SZ, _P, _P, _P, _P]),
     "ft_hip_fused_status": (_I, [_P, _P, ctypes.POINTER(_I)]),
+    "ft_gguf_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "ft_gguf_close": (_I, [_P]),
+    "ft_gguf_version": (ctypes.c_uint32, [_P]),
+    "ft_gguf_data_start": (_U64, [_P]),
+    "ft_gguf_n_kv": (_I64, [_P]),
+    "ft_gguf_n_tensors": (_I64, [_P]),
+    "ft_gguf_kv_key": (_I, [_P, _I64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_uint32)]),
+    "ft_gguf_meta_type": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32)]),
+    "ft_gguf_meta_u64": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(_U64)]),
+    "ft_gguf_meta_f32": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(_F)]),
+    "ft_gguf_meta_str": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(_P), ctypes.POINTER(_U64)]),
+    "ft_gguf_meta_array": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(_U64)]),
+    "ft_gguf_meta_array_u64": (_I, [_P, ctypes.c_char_p, _U64, ctypes.POINTER(_U64)]),
+    "ft_gguf_meta_array_bool": (_I, [_P, ctypes.c_char_p, _U64, ctypes.POINTER(_I)]),
+    "ft_gguf_meta_array_str": (_I, [_P, ctypes.c_char_p, _U64, ctypes.POINTER(_P), ctypes.POINTER(_U64)]),
+    "ft_gguf_tensor_name": (_I, [_P, _I64, ctypes.POINTER(ctypes.c_char_p)]),
+    "ft_gguf_tensor_info": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(_U64),
+                                 ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(_U64), ctypes.POINTER(_U64)]),
+    "ft_gguf_tensor_data": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(_P), ctypes.POINTER(_U64)]),
+    "ft_gguf_tensor_to_f32": (_I, [_P, ctypes.c_char_p, _P, _U64]),
+    "ft_gguf_router_f32": (_I, [_P, _I64, _I64, _I64, _P]),
+    "ft_hip_load_expert_banks_gguf": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _U64, _I]),
 }
 
 
@@ -315,6 +338,12 @@ class Q4Gemv:
         check(lib().ft_hip_pack_experts_fused(self._ctx, _stream(stream), _ptr(src), src_layout, src_expert_bytes,
                                               _ptr(dst), n_experts, hidden, inter))
 
+    def load_expert_banks_gguf(self, gguf, layer0, n_layers, hidden, inter, n_experts, banks, expert_bytes,
+                               layout=LAYOUT_Q4R, stream=None):
+        """Expert banks of a GGUF file's layers into the device tensor `banks`."""
+        check(lib().ft_hip_load_expert_banks_gguf(self._ctx, _stream(stream), gguf.handle, layer0, n_layers, hidden,
+                                                  inter, n_experts, _ptr(banks), expert_bytes, layout))
+
     def pack_router_fused(self, src, dst, n_layers, n_experts, hidden, stream=None):
         check(lib().ft_hip_pack_router_fused(self._ctx, _stream(stream), _ptr(src), _ptr(dst), n_layers, n_experts,
                                              hidden))
@@ -332,3 +361,114 @@ class Q4Gemv:
         """Raise FtHipError(E_TIMEOUT) if a fused launch on `ws` gave up a wait (sync first)."""
         ab = ctypes.c_int(0)
         check(lib().ft_hip_fused_status(self._ctx, _ptr(ws), ctypes.byref(ab)))
+
+
+class TensorInfo:
+    """One entry of a GGUF tensor table (ft_gguf::TensorInfo)."""
+
+    def __init__(self, dims, ggml_type, offset, nbytes):
+        self.dims, self.ggml_type, self.offset, self.nbytes = dims, ggml_type, offset, nbytes
+
+    def __repr__(self):
+        return f"TensorInfo(dims={self.dims}, ggml_type={self.ggml_type}, offset={self.offset}, nbytes={self.nbytes})"
+
+
+class Gguf:
+    """A local GGUF v2/v3 file through ft_gguf_* (mirrors ft_gguf::Gguf:
+    open, meta, tensors, tensor, tensor_data). Host only."""
+
+    def __init__(self, path):
+        h = _P()
+        check(lib().ft_gguf_open(os.fsencode(path), ctypes.byref(h)))
+        self.handle = h
+        L = lib()
+        self.version = L.ft_gguf_version(h)
+        self.data_start = L.ft_gguf_data_start(h)
+        self.meta = {}
+        for i in range(L.ft_gguf_n_kv(h)):
+            key, ty = ctypes.c_char_p(), ctypes.c_uint32()
+            check(L.ft_gguf_kv_key(h, i, ctypes.byref(key), ctypes.byref(ty)))
+            self.meta[key.value.decode()] = self._value(key.value, ty.value)
+        self.tensors = {}
+        for i in range(L.ft_gguf_n_tensors(h)):
+            name = ctypes.c_char_p()
+            check(L.ft_gguf_tensor_name(h, i, ctypes.byref(name)))
+            nd, ty = ctypes.c_uint32(), ctypes.c_uint32()
+            dims, off, nb = (_U64 * 8)(), _U64(), _U64()
+            check(L.ft_gguf_tensor_info(h, name.value, ctypes.byref(nd), dims, ctypes.byref(ty), ctypes.byref(off),
+                                        ctypes.byref(nb)))
+            self.tensors[name.value.decode()] = TensorInfo(list(dims[:nd.value]), ty.value, off.value, nb.value)
+
+    def _str(self, fn, *args):
+        p, n = _P(), _U64()
+        check(fn(self.handle, *args, ctypes.byref(p), ctypes.byref(n)))
+        return ctypes.string_at(p.value, n.value).decode() if n.value else ""
+
+    def _value(self, key, ty):
+        L = lib()
+        if ty in (0, 1, 2, 3, 4, 5, 10, 11):
+            v = _U64()
+            rc = L.ft_gguf_meta_u64(self.handle, key, ctypes.byref(v))
+            return v.value if rc == OK else ("negative", ty)
+        if ty == 6:
+            v = _F()
+            check(L.ft_gguf_meta_f32(self.handle, key, ctypes.byref(v)))
+            return v.value
+        if ty == 8:
+            return self._str(L.ft_gguf_meta_str, key)
+        if ty == 9:
+            et, n = ctypes.c_uint32(), _U64()
+            check(L.ft_gguf_meta_array(self.handle, key, ctypes.byref(et), ctypes.byref(n)))
+            out = []
+            for i in range(n.value):
+                if et.value == 8:
+                    out.append(self._str(L.ft_gguf_meta_array_str, key, i))
+                elif et.value == 7:
+                    b = _I()
+                    check(L.ft_gguf_meta_array_bool(self.handle, key, i, ctypes.byref(b)))
+                    out.append(bool(b.value))
+                else:
+                    v = _U64()
+                    rc = L.ft_gguf_meta_array_u64(self.handle, key, i, ctypes.byref(v))
+                    out.append(v.value if rc == OK else None)
+            return out
+        return ("type", ty)
+
+    def tensor(self, name):
+        if name not in self.tensors:
+            raise FtHipError(E_NOT_FOUND, f"tensor {name} not found")
+        return self.tensors[name]
+
+    def tensor_data(self, name):
+        """The tensor's bytes (a read-only numpy view of the mapping)."""
+        import numpy as np
+        p, n = _P(), _U64()
+        check(lib().ft_gguf_tensor_data(self.handle, name.encode(), ctypes.byref(p), ctypes.byref(n)))
+        buf = (ctypes.c_uint8 * n.value).from_address(p.value)
+        a = np.frombuffer(buf, dtype=np.uint8)
+        a.flags.writeable = False
+        return a
+
+    def to_f32(self, name):
+        import numpy as np
+        n = int(np.prod(self.tensor(name).dims))
+        out = np.zeros(n, np.float32)
+        check(lib().ft_gguf_tensor_to_f32(self.handle, name.encode(), out.ctypes.data_as(_P), n))
+        return out
+
+    def router_f32(self, layer, hidden, n_experts):
+        import numpy as np
+        out = np.zeros((n_experts, hidden), np.float32)
+        check(lib().ft_gguf_router_f32(self.handle, layer, hidden, n_experts, out.ctypes.data_as(_P)))
+        return out
+
+    def close(self):
+        if self.handle:
+            lib().ft_gguf_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

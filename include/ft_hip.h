@@ -45,6 +45,9 @@ extern "C" {
 #define FT_HIP_E_DEVICE (-3)  /* no usable gfx950 device */
 #define FT_HIP_E_LAUNCH (-4)  /* HIP runtime or launch failure */
 #define FT_HIP_E_TIMEOUT (-5) /* the fused kernel's bounded wait expired */
+#define FT_HIP_E_IO (-6)      /* a file could not be opened or mapped */
+#define FT_HIP_E_FORMAT (-7)  /* a malformed or unsupported file or value */
+#define FT_HIP_E_NOT_FOUND (-8) /* no such tensor, metadata key or index */
 
 #define FT_Q8_BLK 40
 
@@ -161,13 +164,6 @@ int ft_hip_reduce_pairs_weighted(ft_hip_ctx* ctx, void* stream, const float* y,
 int ft_hip_repack_rows(ft_hip_ctx* ctx, void* stream, const void* src, int src_layout,
                        void* dst, int dst_layout, int64_t n_rows, int64_t k);
 
-/* Seeded synthetic inputs (no reference counterpart; the reference's synthetic
- * bench uses templated weights, ft-bench/src/bin/decode.rs:111-116).
- * Value i of the tensor with key `key`: Irwin-Hall(4) over the 16-bit fields of
- * splitmix64(key + (i+1)*0x9E3779B97F4A7C15), centred, times `scale`.
- * gen_values writes n f32 values starting at index `start`; gen_q4_rows writes
- * rows [row0, row0 + n_rows) of a seeded [*, k] matrix quantized to q4_0
- * (ft-core/src/q4_0.rs:20-40) in `layout`. */
 /* Measurement utility (no reference counterpart; the reference's own
  * bandwidth line is ft-bench's "cpu q4_0 gemv GB/s", ft-bench/src/main.rs:
  * 77-114): reads `bytes` (16-byte aligned) of device memory at buf once with
@@ -179,6 +175,13 @@ int ft_hip_repack_rows(ft_hip_ctx* ctx, void* stream, const void* src, int src_l
 int ft_hip_stream_read(ft_hip_ctx* ctx, void* stream, const void* buf, uint64_t bytes, uint32_t* out,
                        int n_workgroups);
 
+/* Seeded synthetic inputs (no reference counterpart; the reference's synthetic
+ * bench uses templated weights, ft-bench/src/bin/decode.rs:111-116).
+ * Value i of the tensor with key `key`: Irwin-Hall(4) over the 16-bit fields of
+ * splitmix64(key + (i+1)*0x9E3779B97F4A7C15), centred, times `scale`.
+ * gen_values writes n f32 values starting at index `start`; gen_q4_rows writes
+ * rows [row0, row0 + n_rows) of a seeded [*, k] matrix quantized to q4_0
+ * (ft-core/src/q4_0.rs:20-40) in `layout`. */
 int ft_hip_gen_values(ft_hip_ctx* ctx, void* stream, uint64_t key, int64_t start, int64_t n,
                       float scale, float* out);
 int ft_hip_gen_q4_rows(ft_hip_ctx* ctx, void* stream, uint64_t key, int64_t row0,
@@ -395,6 +398,66 @@ int ft_hip_fused_set_cooperative(ft_hip_ctx* ctx, int on);
  * bounded wait. Such a workspace stays poisoned -- later launches on it do
  * nothing -- until ft_hip_fused_workspace_init. */
 int ft_hip_fused_status(ft_hip_ctx* ctx, void* workspace, int* aborted);
+
+/* ---- local GGUF model files (ft-gguf/src/lib.rs:141-206) ----
+ * ft_gguf_open maps a GGUF v2/v3 file read-only and parses its header,
+ * metadata and tensor table (ft_gguf::Gguf::open): bad magic, other
+ * versions, truncation, unknown value types and unsupported ggml tensor
+ * types give FT_HIP_E_FORMAT (the reference's bail!s); a missing file
+ * FT_HIP_E_IO. The data section starts at the header's end rounded up to
+ * general.alignment (default 32). Strings returned point into the handle
+ * (not NUL-terminated for values: use the length) and live until
+ * ft_gguf_close. Host only; no GPU needed. Metadata value types follow the
+ * GGUF spec: 0 u8, 1 i8, 2 u16, 3 i16, 4 u32, 5 i32, 6 f32, 7 bool, 8 string,
+ * 9 array, 10 u64, 11 i64, 12 f64. */
+typedef struct ft_gguf ft_gguf;
+int ft_gguf_open(const char* path, ft_gguf** out);
+int ft_gguf_close(ft_gguf* g);
+uint32_t ft_gguf_version(const ft_gguf* g);
+uint64_t ft_gguf_data_start(const ft_gguf* g);
+int64_t ft_gguf_n_kv(const ft_gguf* g);
+int64_t ft_gguf_n_tensors(const ft_gguf* g);
+/* metadata key i (file order) and its value type */
+int ft_gguf_kv_key(const ft_gguf* g, int64_t i, const char** key, uint32_t* value_type);
+int ft_gguf_meta_type(const ft_gguf* g, const char* key, uint32_t* value_type);
+/* Value::as_u64 (ft-gguf/src/lib.rs:29-41): unsigned, or non-negative signed */
+int ft_gguf_meta_u64(const ft_gguf* g, const char* key, uint64_t* out);
+/* f32 values only (ft-model's mf, ft-model/src/lib.rs:57-62) */
+int ft_gguf_meta_f32(const ft_gguf* g, const char* key, float* out);
+int ft_gguf_meta_str(const ft_gguf* g, const char* key, const char** s, uint64_t* len);
+int ft_gguf_meta_array(const ft_gguf* g, const char* key, uint32_t* elem_type, uint64_t* n);
+int ft_gguf_meta_array_u64(const ft_gguf* g, const char* key, uint64_t i, uint64_t* out);
+/* 1 for Bool(true), else 0 (ft-model's arr_b, ft-model/src/lib.rs:70-78) */
+int ft_gguf_meta_array_bool(const ft_gguf* g, const char* key, uint64_t i, int* out);
+int ft_gguf_meta_array_str(const ft_gguf* g, const char* key, uint64_t i, const char** s, uint64_t* len);
+/* tensor i (file order); info of a named tensor (Gguf::tensor): dims[8]
+ * (ne[0], the contiguous dimension, first; unused dims 1), ggml type, offset
+ * in the data section and byte size from the type's block layout */
+int ft_gguf_tensor_name(const ft_gguf* g, int64_t i, const char** name);
+int ft_gguf_tensor_info(const ft_gguf* g, const char* name, uint32_t* n_dims, uint64_t* dims,
+                        uint32_t* ggml_type, uint64_t* offset, uint64_t* nbytes);
+/* Gguf::tensor_data: the tensor's bytes in the mapping (bounds-checked) */
+int ft_gguf_tensor_data(const ft_gguf* g, const char* name, const void** data, uint64_t* nbytes);
+/* ft-model's to_f32 (ft-model/src/lib.rs:128-151): f32, f16 or q4_0 tensor
+ * of exactly n elements to f32 */
+int ft_gguf_tensor_to_f32(const ft_gguf* g, const char* name, float* out, uint64_t n);
+/* The router of `layer` as the expert section takes it: [n_experts][hidden]
+ * f32 from blk.<layer>.ffn_gate_inp.weight with blk.<layer>.ffn_gate_inp.scale
+ * and hidden^-1/2 folded in per column (ft-model/src/lib.rs:506-514). */
+int ft_gguf_router_f32(const ft_gguf* g, int64_t layer, int64_t hidden, int64_t n_experts, float* out);
+/* Expert banks of layers [layer0, layer0 + n_layers) from the file's q4_0
+ * blk.<l>.ffn_gate_up_exps.weight [hidden, 2*inter, n_experts] and
+ * blk.<l>.ffn_down_exps.weight [inter, hidden, n_experts] into device
+ * `banks` (ft-model/src/lib.rs:570-609): expert (l, e) at
+ * ((l - layer0) * n_experts + e) * expert_bytes, its 2*inter gate|up rows
+ * then its hidden down rows, each row in `layout` (the reference repacks to
+ * q4r on the host; here each tensor is uploaded once and repacked on the
+ * device). Every tensor's type and dims are checked before any copy.
+ * Allocates a device staging buffer of n_experts * max(tensor) bytes for the
+ * call and synchronises `stream` before returning. */
+int ft_hip_load_expert_banks_gguf(ft_hip_ctx* ctx, void* stream, const ft_gguf* g, int64_t layer0,
+                                  int64_t n_layers, int64_t hidden, int64_t inter, int64_t n_experts,
+                                  void* banks, uint64_t expert_bytes, int layout);
 
 #ifdef __cplusplus
 }

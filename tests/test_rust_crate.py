@@ -15,7 +15,8 @@ HDR = os.path.join(ROOT, "include", "ft_hip.h")
 CRATE = os.path.join(ROOT, "freetoken-rs_amd", "ft-hip")
 
 C2R = {"int": "c_int", "int64_t": "i64", "uint64_t": "u64", "size_t": "usize", "float": "f32", "void": "c_void",
-       "int32_t": "i32", "uint32_t": "u32", "char": "c_char", "ft_hip_ctx": "FtHipCtx", "uint8_t": "u8"}
+       "int32_t": "i32", "uint32_t": "u32", "char": "c_char", "ft_hip_ctx": "FtHipCtx", "uint8_t": "u8",
+       "ft_gguf": "FtGguf"}
 
 
 def c_type_to_rust(t):
@@ -33,7 +34,7 @@ def c_type_to_rust(t):
 def header_protos():
     src = re.sub(r"/\*.*?\*/", "", open(HDR).read(), flags=re.S)
     out = {}
-    for ret, name, args in re.findall(r"^\s*((?:const\s+)?\w+\s*\**)\s*(ft_hip_\w+)\s*\(([^)]*)\)\s*;", src, re.M):
+    for ret, name, args in re.findall(r"^\s*((?:const\s+)?\w+\s*\**)\s*(ft_(?:hip|gguf)_\w+)\s*\(([^)]*)\)\s*;", src, re.M):
         params = []
         args = " ".join(args.split())
         if args and args != "void":
@@ -48,7 +49,7 @@ def rust_decls():
     src = open(os.path.join(CRATE, "src", "ffi.rs")).read()
     block = src[src.index('extern "C" {'):]
     out = {}
-    for name, args, ret in re.findall(r"pub fn (ft_hip_\w+)\((.*?)\)\s*->\s*([^;]+);", block, re.S):
+    for name, args, ret in re.findall(r"pub fn (ft_(?:hip|gguf)_\w+)\((.*?)\)\s*->\s*([^;]+);", block, re.S):
         params = []
         for a in [x for x in args.split(",") if x.strip()]:
             n, t = a.split(":", 1)
@@ -70,7 +71,7 @@ def test_every_header_prototype_has_a_matching_rust_item():
 def test_wrapper_calls_only_declared_items_and_constants_agree():
     decl = rust_decls()
     lib = open(os.path.join(CRATE, "src", "lib.rs")).read()
-    called = set(re.findall(r"ffi::(ft_hip_\w+)\(", lib))
+    called = set(re.findall(r"ffi::(ft_(?:hip|gguf)_\w+)\(", lib))
     assert called and called <= set(decl), called - set(decl)
     # every Q4Gemv method the reference's MoE path uses is present by name
     for m in ["new", "quantize_q8", "quantize_q8_view", "gemv_grouped_q8_ptr", "gemv_q4r_ptr", "gemv_q4r_idx",
@@ -79,7 +80,8 @@ def test_wrapper_calls_only_declared_items_and_constants_agree():
     hdr = open(HDR).read()
     ffi = open(os.path.join(CRATE, "src", "ffi.rs")).read()
     for c in ["FT_HIP_OK", "FT_HIP_E_INVALID", "FT_HIP_E_SHAPE", "FT_HIP_E_DEVICE", "FT_HIP_E_LAUNCH",
-              "FT_HIP_E_TIMEOUT", "FT_Q8_BLK", "FT_LAYOUT_Q4_0", "FT_LAYOUT_Q4R", "FT_HIP_NOALLOC_SCRATCH_BYTES"]:
+              "FT_HIP_E_TIMEOUT", "FT_HIP_E_IO", "FT_HIP_E_FORMAT", "FT_HIP_E_NOT_FOUND", "FT_Q8_BLK",
+              "FT_LAYOUT_Q4_0", "FT_LAYOUT_Q4R", "FT_HIP_NOALLOC_SCRATCH_BYTES"]:
         hv = re.search(rf"#define {c} \(?([^)\n/]+)\)?", hdr).group(1).strip()
         rv = re.search(rf"pub const {c}: \w+ = ([^;]+);", ffi).group(1).strip()
         assert eval(hv.replace("(", "").replace(")", "")) == eval(rv), (c, hv, rv)
