@@ -92,13 +92,15 @@ def chunk_size(steps, warmup):
 
 class GraphRunner:
     """Layer-by-layer paths: C steps of B tokens through all layers per
-    captured HIP graph. layer(l, src, dst, ids, wts, stream) enqueues one
-    layer for the B tokens of src ([B, H]) into dst. The routing of every
-    step of a chunk lands in ids/wts [C, L, B*k] (read after timing only)."""
+    captured HIP graph. step(src, dst, ids, wts, stream) enqueues all layers
+    for the B tokens of src ([B, H]) into dst, with ids/wts [L, B*k]; or,
+    without it, layer(l, src, dst, ids, wts, stream) enqueues one layer. The
+    routing of every step of a chunk lands in ids/wts [C, L, B*k] (read after
+    timing only)."""
 
-    def __init__(self, model, B, chunk, layer):
+    def __init__(self, model, B, chunk, layer, step=None):
         import torch
-        self.m, self.B, self.C, self.layer = model, B, chunk, layer
+        self.m, self.B, self.C, self.layer, self.step = model, B, chunk, layer, step
         H, k = model.shape.hidden, model.shape.top_k
         dev = model.device
         self.xin = torch.zeros((chunk, B, H), dtype=torch.float32, device=dev)
@@ -118,6 +120,9 @@ class GraphRunner:
         L = self.m.L
         for c in range(self.C):
             src = self.xin[c]
+            if self.step is not None:
+                self.step(src, self.out[c], self.ids[c], self.wts[c], stream)
+                continue
             for l in range(L):
                 dst = self.out[c] if l == L - 1 else self.state[l & 1]
                 self.layer(l, src, dst, self.ids[c, l], self.wts[c, l], stream)
@@ -511,18 +516,24 @@ def main():
             for t in range(t0_, t0_ + n):
                 stack.run(hidden[t, 0], outs[t, 0])
     else:
+        step = None
         if path == "grouped":
-            gstack = moe_synth.GroupedStack(moe_synth.FusedStack(model, workspace=False), B)
+            packed = moe_synth.FusedStack(model, workspace=False)
+            gstack = moe_synth.GroupedStack(packed, B)
+            bstack = moe_synth.BatchedStack(packed, B)
 
             def layer(l, src, dst, ids, wts, stream):
                 gstack.layer(l, src, dst, ids, wts, stream=stream)
+
+            def step(src, dst, ids, wts, stream):  # all layers in one call (ft_hip_moe_stack_grouped)
+                bstack.run(src, dst, B, ids, wts, stream=stream)
         else:
             ws = model.workspace(B)
 
             def layer(l, src, dst, ids, wts, stream):
                 model.layer(l, src, dst, ids, wts, ws, n_seqs=B, stream=stream)
         C = chunk_size(args.steps, args.warmup)
-        runner = GraphRunner(model, B, C, layer)
+        runner = GraphRunner(model, B, C, layer, step)
         log(f"[setup] {C} step(s) per captured HIP graph")
 
         def run(t0_, n):

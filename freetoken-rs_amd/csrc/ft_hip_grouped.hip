@@ -859,3 +859,92 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
                        (const float*)wts, x, x_out, H, K);
     return launch_status("moe_layer_grouped/combine");
 }
+
+// ---------------------------------------------------------------------------
+// The L-layer stack for a batch (forward_batch's expert section for every
+// layer, ft-model/src/lib.rs:1507-1606, called per layer from :1151-1154).
+// Workspace: the layer workspace for max_seqs, then two [max_seqs][H] f32
+// states and [L][max_seqs*K] ids/wts for callers that pass no record.
+// ---------------------------------------------------------------------------
+namespace {
+struct StackWs {
+    void* layer;
+    size_t layer_bytes;
+    float* state[2];
+    int32_t* ids;
+    float* wts;
+    size_t bytes;
+};
+
+StackWs stack_ws(void* base, int64_t max_seqs, int64_t H, int64_t I, int64_t E, int64_t K, int64_t L) {
+    auto up = [](size_t v) { return (v + 255) / 256 * 256; };
+    StackWs w{};
+    uint8_t* p = (uint8_t*)base;
+    size_t off = 0;
+    w.layer = p;
+    w.layer_bytes = group_ws(nullptr, max_seqs, H, I, E, K).bytes;
+    off += up(w.layer_bytes);
+    for (int i = 0; i < 2; ++i) {
+        w.state[i] = (float*)(p + off);
+        off += up(sizeof(float) * max_seqs * H);
+    }
+    w.ids = (int32_t*)(p + off);
+    off += up(sizeof(int32_t) * L * max_seqs * K);
+    w.wts = (float*)(p + off);
+    off += up(sizeof(float) * L * max_seqs * K);
+    w.bytes = off;
+    return w;
+}
+}  // namespace
+
+extern "C" size_t ft_hip_moe_stack_grouped_workspace_bytes(int64_t max_seqs, int64_t hidden, int64_t inter,
+                                                           int64_t n_experts, int64_t top_k, int64_t n_layers) {
+    if (max_seqs < 0 || hidden <= 0 || inter <= 0 || n_experts <= 0 || top_k <= 0 || n_layers <= 0) return 0;
+    return stack_ws(nullptr, max_seqs, hidden, inter, n_experts, top_k, n_layers).bytes;
+}
+
+extern "C" int ft_hip_moe_stack_grouped(ft_hip_ctx* ctx, void* stream, const float* x_in, float* x_out,
+                                        int64_t n_seqs, int64_t max_seqs, int64_t hidden, int64_t inter,
+                                        int64_t n_experts, int64_t top_k, int64_t n_layers, const void* banks,
+                                        const float* routers, const float* router_bias, const float* expert_scale,
+                                        int32_t* ids, float* wts, void* workspace, size_t workspace_bytes) {
+    clear_error();
+    const char* nm = "moe_stack_grouped";
+    if (int rc = check_grouped_shape(nm, max_seqs, hidden, inter, n_experts, top_k)) return rc;
+    if (n_seqs < 0 || n_seqs > max_seqs)
+        return fail(FT_HIP_E_SHAPE, "%s: n_seqs=%lld not in [0, max_seqs=%lld]", nm, (long long)n_seqs, (long long)max_seqs);
+    if (n_layers <= 0) return fail(FT_HIP_E_SHAPE, "%s: n_layers=%lld must be positive", nm, (long long)n_layers);
+    if (!ctx || !x_in || !x_out || !banks || !routers || !workspace) return fail(FT_HIP_E_INVALID, "%s: null argument", nm);
+    if ((ids == nullptr) != (wts == nullptr)) return fail(FT_HIP_E_INVALID, "%s: give ids and wts or neither", nm);
+    const StackWs w = stack_ws(workspace, max_seqs, hidden, inter, n_experts, top_k, n_layers);
+    if (workspace_bytes < w.bytes)
+        return fail(FT_HIP_E_SHAPE, "%s: workspace_bytes=%zu < %zu (for max_seqs %lld)", nm, workspace_bytes, w.bytes,
+                    (long long)max_seqs);
+    if (n_seqs == 0) return FT_HIP_OK;
+    const int64_t eb = ft_hip_fused_expert_bytes(hidden, inter);
+    const int64_t P = n_seqs * top_k;
+    const size_t lbytes = group_ws(nullptr, n_seqs, hidden, inter, n_experts, top_k).bytes;
+    const float* src = x_in;
+    for (int64_t l = 0; l < n_layers; ++l) {
+        // the last layer writes x_out, unless it would overwrite its own input
+        // in a one-layer in-place call
+        const bool last = l == n_layers - 1;
+        float* dst = last && !(n_layers == 1 && x_out == x_in) ? x_out : w.state[l & 1];
+        int32_t* il = ids ? ids + l * P : w.ids + l * P;
+        float* wl = wts ? wts + l * P : w.wts + l * P;
+        const uint8_t* bank = static_cast<const uint8_t*>(banks) + l * n_experts * eb;
+        if (int rc = ft_hip_moe_layer_grouped(ctx, stream, src, dst, n_seqs, hidden, inter, n_experts, top_k,
+                                              routers + l * n_experts * hidden,
+                                              router_bias ? router_bias + l * n_experts : nullptr,
+                                              expert_scale ? expert_scale + l * n_experts : nullptr, bank, il, wl,
+                                              w.layer, lbytes, nullptr, nullptr))
+            return rc;
+        src = dst;
+    }
+    if (src != x_out) {
+        hipError_t e = hipMemcpyAsync(x_out, src, sizeof(float) * n_seqs * hidden, hipMemcpyDeviceToDevice,
+                                      reinterpret_cast<hipStream_t>(stream));
+        if (e != hipSuccess) return fail(FT_HIP_E_LAUNCH, "%s: copy of the result: %s", nm, hipGetErrorString(e));
+    }
+    return FT_HIP_OK;
+}

@@ -54,6 +54,9 @@ SIGNATURES = {
     "ft_hip_moe_layer_grouped_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "ft_hip_moe_layer_grouped": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P,
                                       _SZ, _P, _P]),
+    "ft_hip_moe_stack_grouped_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64]),
+    "ft_hip_moe_stack_grouped": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P,
+                                      _P, _P, _P, _SZ]),
     "ft_hip_fused_expert_bytes": (_I64, [_I64, _I64]),
     "ft_hip_fused_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
     "ft_hip_fused_workgroups": (ctypes.c_int, [_I64, _I64, _I64, _I64]),
@@ -282,6 +285,17 @@ class Q4Gemv:
                                              _ptr(expert_scale), _ptr(bank), _ptr(ids), _ptr(wts), _ptr(workspace),
                                              workspace.numel() * workspace.element_size(), _ptr(dbg_gu),
                                              _ptr(dbg_act)))
+
+    @staticmethod
+    def moe_stack_grouped_workspace_bytes(max_seqs, hidden, inter, n_experts, top_k, n_layers):
+        return lib().ft_hip_moe_stack_grouped_workspace_bytes(max_seqs, hidden, inter, n_experts, top_k, n_layers)
+
+    def moe_stack_grouped(self, x_in, x_out, n_seqs, max_seqs, hidden, inter, n_experts, top_k, n_layers, banks,
+                          routers, router_bias, expert_scale, ids, wts, workspace, stream=None):
+        check(lib().ft_hip_moe_stack_grouped(self._ctx, _stream(stream), _ptr(x_in), _ptr(x_out), n_seqs, max_seqs,
+                                             hidden, inter, n_experts, top_k, n_layers, _ptr(banks), _ptr(routers),
+                                             _ptr(router_bias), _ptr(expert_scale), _ptr(ids), _ptr(wts),
+                                             _ptr(workspace), workspace.numel() * workspace.element_size()))
 
     # -- fused whole-stack path --
     @staticmethod

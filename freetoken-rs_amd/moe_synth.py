@@ -316,3 +316,23 @@ class GroupedStack:
             dst = x_out if l == self.m.L - 1 else self.buf[l & 1]
             self.layer(l, src, dst, stream=stream)
             src = dst
+
+
+class BatchedStack:
+    """Batched decode through ft_hip_moe_stack_grouped: all layers of a step
+    of n_seqs <= max_seqs tokens in one call, on one workspace for every
+    batch size up to max_seqs; the banks are a FusedStack's."""
+
+    def __init__(self, fused, max_seqs):
+        self.f, self.m, self.max_seqs = fused, fused.m, max_seqs
+        g, s = self.m.g, self.m.shape
+        self.g = g
+        nbytes = g.moe_stack_grouped_workspace_bytes(max_seqs, s.hidden, s.inter, s.n_experts, s.top_k, self.m.L)
+        self.ws = torch.empty(nbytes, dtype=torch.uint8, device=self.m.device)
+
+    def run(self, x_in, x_out, n_seqs, ids=None, wts=None, stream=None):
+        """x_out[:n_seqs] = the stack applied to x_in[:n_seqs]; ids/wts: [L][n_seqs*k] or None."""
+        s = self.m.shape
+        self.g.moe_stack_grouped(x_in, x_out, n_seqs, self.max_seqs, s.hidden, s.inter, s.n_experts, s.top_k,
+                                 self.m.L, self.f.banks, self.m.routers, self.m.bias, None, ids, wts, self.ws,
+                                 stream)

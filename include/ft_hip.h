@@ -262,6 +262,28 @@ int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const float* x, floa
                              const void* bank, int32_t* ids, float* wts, void* workspace,
                              size_t workspace_bytes, float* dbg_gu, void* dbg_act);
 
+/* The n_layers-layer expert section for a batch of n_seqs decode tokens:
+ * ft_hip_moe_layer_grouped for each layer in turn, x_{l+1} = x_l +
+ * MoE_l(x_l) (the batched pair section of ft-model/src/lib.rs:1507-1606 for
+ * every layer of a forward_batch step, :1151-1154). banks: the layers'
+ * fused-layout banks back to back (layer l at l * n_experts *
+ * ft_hip_fused_expert_bytes(hidden, inter), 16-byte aligned); routers
+ * [L][E][H]; router_bias and expert_scale [L][E] or NULL; ids/wts
+ * [L][n_seqs][top_k] routing record, or both NULL. x_in, x_out [n_seqs][H]
+ * (x_out may equal x_in). The workspace, sized by
+ * ft_hip_moe_stack_grouped_workspace_bytes(max_seqs, ...), serves every
+ * batch of n_seqs <= max_seqs tokens, so a serving loop whose batch grows
+ * and shrinks between steps keeps one workspace; each call's results are
+ * those of the layer-by-layer calls on the same tokens, bit for bit. No
+ * allocation; the launches can be captured in a HIP graph. */
+size_t ft_hip_moe_stack_grouped_workspace_bytes(int64_t max_seqs, int64_t hidden, int64_t inter,
+                                                int64_t n_experts, int64_t top_k, int64_t n_layers);
+int ft_hip_moe_stack_grouped(ft_hip_ctx* ctx, void* stream, const float* x_in, float* x_out, int64_t n_seqs,
+                             int64_t max_seqs, int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k,
+                             int64_t n_layers, const void* banks, const float* routers, const float* router_bias,
+                             const float* expert_scale, int32_t* ids, float* wts, void* workspace,
+                             size_t workspace_bytes);
+
 /* ft_hip_moe_layer_grouped: experts routed at least n_tokens tokens of the
  * batch take the int8 MFMA tile kernels (16 rows x 16 tokens per
  * v_mfma_i32_16x16x32_i8, one q4_0 block per instruction), the others the

@@ -182,3 +182,55 @@ def test_grouped_large_expert_mfma(gemv, orc, norm):
             assert np.array_equal(blk[:, 8:40].copy().view(np.int8).ravel(), aq)
         dref = r["x_out"] - X[t]
         assert np.max(np.abs((XO[t] - X[t]) - dref)) <= 1e-3 * np.linalg.norm(dref), t
+
+
+@pytest.mark.parametrize("norm", [False, True])
+def test_batched_stack_variable_batch(gemv, norm):
+    """ft_hip_moe_stack_grouped over a 3-layer Zipf stack on ONE workspace
+    sized for 64 tokens, with the batch changing between steps (16, 5, 64,
+    1, 0, 33 tokens, as forward_batch sees under continuous batching): every
+    step's outputs and per-layer routing equal the layer-by-layer calls on
+    the same tokens (each with a workspace of its own size), bit for bit;
+    rows past n_seqs are untouched; an in-place call gives the same bits."""
+    m = moe_synth.SyntheticMoE(gemv, moe_synth.GEMMA, n_layers=3, zipf_s=1.1)
+    st = moe_synth.FusedStack(m, workspace=False)
+    bs = moe_synth.BatchedStack(st, 64)
+    H, k, L = m.shape.hidden, m.shape.top_k, m.L
+    gemv.set_input_norm(int(norm))
+    try:
+        first = 0
+        for B in (16, 5, 64, 1, 0, 33):
+            x = _hidden(m, max(B, 1), first)
+            first += B
+            out = torch.full((64, H), 7.0, dtype=torch.float32, device=DEV)
+            ids = torch.zeros((L, max(B, 1) * k), dtype=torch.int32, device=DEV)
+            wts = torch.zeros((L, max(B, 1) * k), dtype=torch.float32, device=DEV)
+            bs.run(x, out, B, ids, wts)
+            o = host(out)
+            assert np.all(o[B:] == 7.0)
+            if B == 0:
+                continue
+            ref = moe_synth.GroupedStack(st, B)
+            ro = torch.zeros((B, H), dtype=torch.float32, device=DEV)
+            ref.run(x, ro)
+            assert np.array_equal(o[:B].view(np.uint32), host(ro).view(np.uint32)), B
+            assert np.array_equal(host(ids), host(ref.ids)), B
+            assert np.array_equal(host(wts).view(np.uint32), host(ref.wts).view(np.uint32)), B
+            xi = x.clone()
+            bs.run(xi, xi, B)  # in place, no routing record
+            assert np.array_equal(host(xi).view(np.uint32), o[:B].view(np.uint32)), B
+    finally:
+        gemv.set_input_norm(0)
+
+
+def test_batched_stack_rejects(gemv, gstack):
+    m = gstack.m
+    bs = moe_synth.BatchedStack(gstack, 8)
+    x = _hidden(m, 9)
+    with pytest.raises(Exception):
+        bs.run(x, x, 9)  # more tokens than the workspace was sized for
+    s = m.shape
+    small = torch.empty(bs.ws.numel() - 256, dtype=torch.uint8, device=DEV)
+    with pytest.raises(Exception):
+        gemv.moe_stack_grouped(x, x, 4, 8, s.hidden, s.inter, s.n_experts, s.top_k, m.L, gstack.banks, m.routers,
+                               m.bias, None, None, None, small)
