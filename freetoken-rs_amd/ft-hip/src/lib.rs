@@ -250,6 +250,32 @@ impl Q4Gemv {
         })
     }
 
+    pub fn moe_stack_grouped_workspace_bytes(max_seqs: usize, hidden: usize, inter: usize, n_experts: usize,
+                                             top_k: usize, n_layers: usize) -> usize {
+        unsafe {
+            ffi::ft_hip_moe_stack_grouped_workspace_bytes(max_seqs as i64, hidden as i64, inter as i64,
+                                                          n_experts as i64, top_k as i64, n_layers as i64)
+        }
+    }
+
+    /// All layers of a forward_batch step (ft-model/src/lib.rs:1151-1154,
+    /// :1507-1606) for n_seqs <= max_seqs tokens, on one workspace sized for
+    /// max_seqs; `banks` holds the layers' fused-layout banks back to back.
+    #[allow(clippy::too_many_arguments)]
+    pub fn moe_stack_grouped(&self, s: Stream, x_in: DevPtr, x_out: DevPtr, n_seqs: usize, max_seqs: usize,
+                             hidden: usize, inter: usize, n_experts: usize, top_k: usize, n_layers: usize,
+                             banks: DevPtr, routers: DevPtr, router_bias: Option<DevPtr>,
+                             expert_scale: Option<DevPtr>, ids: Option<DevPtr>, wts: Option<DevPtr>,
+                             workspace: DevPtr, workspace_bytes: usize) -> Result<()> {
+        check(unsafe {
+            ffi::ft_hip_moe_stack_grouped(self.ctx, s.0, p(x_in), pm(x_out), n_seqs as i64, max_seqs as i64,
+                                          hidden as i64, inter as i64, n_experts as i64, top_k as i64,
+                                          n_layers as i64, p(banks), p(routers), opt(router_bias), opt(expert_scale),
+                                          ids.map_or(std::ptr::null_mut(), pm), wts.map_or(std::ptr::null_mut(), pm),
+                                          pm(workspace), workspace_bytes)
+        })
+    }
+
     /// The whole L-layer section for one token in one launch (the graphed
     /// token of ft-model/src/lib.rs:1059-1121); Gemma shape.
     #[allow(clippy::too_many_arguments)]
