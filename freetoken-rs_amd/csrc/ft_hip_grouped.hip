@@ -20,6 +20,7 @@
 #include "ft_runtime.hpp"
 
 #include <algorithm>
+#include <type_traits>
 #include <limits>
 
 using namespace ft;
@@ -474,129 +475,233 @@ __device__ __forceinline__ void scales4(const uint16_t* p, float (&sc)[4]) {
     sc[3] = h2f((uint16_t)(s2.y >> 16));
 }
 
-// Gate|up tile j (64 rows: gate rows 32j.., up rows I+32j..) of active expert
-// g for its tokens, 16 at a time. Wave w takes blocks [w*BPW, (w+1)*BPW) of
-// the 64 rows as four 16-row MFMA tiles (qs dwords loaded per token tile,
-// every load of a tile issued before the first MFMA; the tile's scales in
-// LDS); the 8 wave partials of a (row, token) are summed in wave order;
-// then, as k_grouped_gu, the input-norm scale, GELU*up and the q8 of act
-// block j per token.
+// Gate|up tiles of the MFMA groups (tile j: 64 rows, gate rows 32j.. and up
+// rows I+32j..), each for its expert's tokens 16 at a time, then GELU*up and
+// the q8 of act block j per token. Persistent: one workgroup per CU walks a
+// contiguous range of (expert group, tile j) items, each in chunks of 16
+// tokens (units). Wave w takes blocks [w*BPW, (w+1)*BPW) of the 64 rows as
+// four 16-row MFMA tiles; the 8 wave partials of a (row, token) are summed
+// in wave order. The tokens' q8 rows of the current chunk sit in LDS
+// (staged when the group or chunk changes, which a contiguous range makes
+// rare), so the MFMA B operands are LDS reads, read one block ahead. The
+// weights stream through registers: a wave holds its BPW blocks' qs dwords
+// of a unit, and consuming block b refills that slot with block b of the
+// NEXT unit, so the next tile streams during this unit's MFMAs and its
+// epilogue (wave sums, GELU*up, q8). A tile's f16 scales go through two LDS
+// buffers, loaded two units ahead by direct global-to-LDS loads (no
+// registers). Per (row, token): acc = fma(float(D_b), d4_b * d8_b, acc) over
+// the wave's blocks in block order, then the wave partials in wave order.
+
+// s_waitcnt encoding of "vmcnt <= n" (expcnt and lgkmcnt not waited for)
+constexpr int vm_wait_enc(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
+
+struct MfUnit {
+    const uint8_t* T;  // the tile: [nb][64] f16 scales, then [nb][64][16 B] qs
+    int g, s0, n, j, c0, nt, item;
+    bool live;
+};
+
 template <int BPW, bool REC>
-__global__ __launch_bounds__(GT, 2) __attribute__((amdgpu_waves_per_eu(4))) void k_mfma_gu(const uint8_t* bank, int64_t expert_bytes, const int32_t* meta,
-                                                   const int32_t* plist, const uint8_t* q8x, uint32_t q8x_bytes,
-                                                   uint8_t* q8a, float* dbg_gu, const float* in_scale, int H, int I,
-                                                   int E, int K, int n_min, int32_t* rec) {
+__global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ bank, int64_t expert_bytes,
+                                                     const int32_t* __restrict__ meta,
+                                                     const int32_t* __restrict__ plist,
+                                                     const uint8_t* __restrict__ q8x, uint8_t* q8a, float* dbg_gu,
+                                                     const float* __restrict__ in_scale, int H, int I, int E, int K,
+                                                     int32_t* rec) {
     extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int SPT_LDS = (128 * 128 + GW * 1024 - 1) / (GW * 1024);  // scale rounds, up to nb = 128 (H 4096)
     const int nb = H >> 5, nbj = I >> 5;
-    const int j = blockIdx.x, g = blockIdx.y;
-    if (g >= meta[1 + 3 * E]) return;  // groups of >= n_min tokens come first
-    const int e = meta[1 + g], s0 = meta[1 + E + g], n = meta[1 + 2 * E + g];
-    if (n < n_min) return;
-    // LDS: the tile's scales [nb][64] f16; wave partials [GW][64][MT]; sums
-    // [MT][64]; act [MT][32]; act q8 [MT][10]
-    uint16_t* scl = reinterpret_cast<uint16_t*>(lds);
-    float* red = reinterpret_cast<float*>(lds + nb * 128);
+    const int n_items = meta[1 + 3 * E] * nbj;  // (group, tile) pairs of the MFMA groups (first in the list)
+    const int per = (n_items + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int it0 = (int)blockIdx.x * per, it1 = min(n_items, it0 + per);
+    if (it0 >= it1) return;
+    // LDS: scales [2][nb][64] f16 | wave partials [GW][64][MT] | sums [MT][64] |
+    // act [MT][32] | act q8 [MT][10] | the chunk's tokens (pair, norm scale)
+    // [MT] x2 | the chunk's q8 rows [MT][nb*10 + 1] u32
+    uint16_t* scl2 = reinterpret_cast<uint16_t*>(lds);
+    float* red = reinterpret_cast<float*>(lds + 2 * nb * 128);
     float* rows = red + GW * 64 * MT;
     float* actv = rows + MT * 64;
     uint32_t* ablk = reinterpret_cast<uint32_t*>(actv + MT * 32);
-    // the wave index in a scalar register: buffer offsets built from it stay uniform
+    int* tok_p = reinterpret_cast<int*>(ablk + MT * 10);
+    float* tok_s = reinterpret_cast<float*>(tok_p + MT);
+    uint32_t* xq = reinterpret_cast<uint32_t*>(tok_s + MT);
+    const int xs = nb * 10 + 1;  // token stride (dwords), odd: the 16 tokens' rows start in different banks
     const int t = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(t >> 6), li = t & 15, lg = (t >> 4) & 3;
     const int b0 = wave * BPW;
-    const uint8_t* T = bank + (int64_t)e * expert_bytes + (int64_t)j * nb * 1152;
-    // qs of the tile: lane offset li*16 + 4*lg (row li of an MFMA tile, word
-    // lg), uniform offset block*1024 + m*256
-    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(T + nb * 128, (uint32_t)nb * 1024);
-    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(q8x, q8x_bytes);
     const uint32_t vw = li * 16 + 4 * lg;
-    for (int c0 = 0; c0 < n; c0 += MT) {
-        const int nt = min(MT, n - c0);
-        const int p = plist[s0 + c0 + min(li, nt - 1)];
-        const uint32_t vd = (uint32_t)((p / K) * nb + b0) * Q8_BLK, vq = vd + 8 + 4 * lg;
-        // blocks in NBB-block batches, the next batch's loads issued before
-        // the current batch's MFMAs (two register buffers)
-        constexpr int NBB = 1, NBATCH = (BPW + NBB - 1) / NBB;
-        uint32_t aw[2][NBB][4];
-        ActOp av[2][NBB];
-        auto load = [&](int k, int buf) __attribute__((always_inline)) {
+    auto bind = [&](int it, int c, bool live) __attribute__((always_inline)) {
+        MfUnit u;
+        u.live = live;
+        u.item = it;
+        it = live ? it : it0;  // a dead unit is bound to a valid item and never computed
+        u.g = it / nbj;
+        u.j = it - u.g * nbj;
+        const int e = meta[1 + u.g];
+        u.s0 = meta[1 + E + u.g];
+        u.n = meta[1 + 2 * E + u.g];
+        u.c0 = live ? c : 0;
+        u.nt = min(MT, u.n - u.c0);
+        u.T = bank + (int64_t)e * expert_bytes + (int64_t)u.j * nb * 1152;
+        return u;
+    };
+    auto after = [&](const MfUnit& u) __attribute__((always_inline)) {  // the unit after u in this range
+        if (!u.live) return u;
+        if (u.c0 + MT < u.n) return bind(u.item, u.c0 + MT, true);
+        return bind(u.item + 1, 0, u.item + 1 < it1);
+    };
+    auto same_tile = [](const MfUnit& a, const MfUnit& c) { return a.g == c.g && a.j == c.j; };
+    uint32_t aw[BPW][4];
+    // slot b <- block b of unit u (dead: a descriptor of 0 bytes returns zeros and reads nothing)
+    auto issue_block = [&](int b, const MfUnit& u) __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t rw = buf_rsrc(u.T + nb * 128, u.live ? (uint32_t)nb * 1024 : 0u);
 #pragma unroll
-            for (int b = 0; b < NBB; ++b) {
-                const int bb = min(k * NBB + b, BPW - 1);
+        for (int m = 0; m < 4; ++m) aw[b][m] = buf_ld(rw, vw + m * 256, (b0 + b) * 1024);
+    };
+    // the tile's scales (nb * 128 bytes) straight into scale buffer `buf`:
+    // 16 bytes per lane, 1 KB per wave and round. Issued right after every
+    // wave is past its reads of that buffer (the epilogue's first barrier),
+    // two units before the unit that reads it; that unit is preceded by
+    // VM_AFTER_SCALES, which waits for them (the next unit's BPW * 4 weight
+    // loads are issued after them, so at most that many may still be out).
+    auto issue_scales = [&](int buf, const MfUnit& u) __attribute__((always_inline)) {
+        if (!u.live) return;
+        const int lane = t & 63;
 #pragma unroll
-                for (int m = 0; m < 4; ++m) aw[buf][b][m] = buf_ld(rw, vw + m * 256, (b0 + bb) * 1024);
-                av[buf][b] = act_op(rx, vq, vd, bb * Q8_BLK, li < nt);
-            }
+        for (int r = 0; r < SPT_LDS; ++r) {
+            const int off = (r * GW + wave) * 1024;  // uniform per wave
+            if (off + lane * 16 < nb * 128)
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4*>(u.T + off) + lane,
+                                                 (lds_u32*)(scl2 + buf * nb * 64 + off / 2), 16, 0, 0);
+        }
+    };
+    // unit u's tokens (pair, norm scale) into tok_p/tok_s and their q8 rows
+    // into xq (token slots >= nt: the last token again; their MFMA columns
+    // are never read). Only between units; the caller syncs afterwards.
+    auto stage_act = [&](const MfUnit& u) __attribute__((always_inline)) {
+        if (t < MT) {
+            const int pp = plist[u.s0 + u.c0 + min(t, u.nt - 1)];
+            tok_p[t] = pp;
+            tok_s[t] = in_scale ? in_scale[pp / K] : 1.0f;
+        }
+        __syncthreads();
+        const int per_tok = nb * 10;
+        for (int i = t; i < MT * per_tok; i += GT) {
+            const int tt = i / per_tok, w = i - tt * per_tok;
+            xq[tt * xs + w] = reinterpret_cast<const uint32_t*>(q8x + (int64_t)(tok_p[tt] / K) * nb * Q8_BLK)[w];
+        }
+    };
+    // a block's LDS operands: this lane's token words, its d and qsum, and
+    // the 4 scale pairs (rows 16m + 4lg .. +3)
+    struct Ops {
+        uint32_t lo, hi, d, qsum;
+        uint2 sc[4];
+    };
+    MfUnit cur = bind(it0, 0, true);
+    MfUnit nxt = after(cur);
+    issue_scales(0, cur);
+    issue_scales(1, nxt);
+#pragma unroll
+    for (int b = 0; b < BPW; ++b) issue_block(b, cur);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt(0): the scale loads into LDS are done
+    stage_act(cur);
+    int act_g = cur.g, act_c0 = cur.c0;  // the chunk whose q8 rows are in xq
+    __syncthreads();
+    auto step = [&](auto par_c) __attribute__((always_inline)) {
+        constexpr int PAR = decltype(par_c)::value;
+        const MfUnit n2 = after(nxt);
+        const bool n2_scales = n2.live && !same_tile(n2, cur);  // scl[PAR] holds cur's scales until then
+        const uint16_t* scl = scl2 + PAR * nb * 64;
+        const int pme = tok_p[li];  // this lane's token pair (REC)
+        const uint32_t* xl = xq + li * xs;  // this lane's token row
+        auto ops = [&](int blk) __attribute__((always_inline)) {
+            Ops o;
+            o.lo = xl[blk * 10 + 2 + lg];
+            o.hi = xl[blk * 10 + 6 + lg];
+            o.d = xl[blk * 10];
+            o.qsum = xl[blk * 10 + 1];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) o.sc[m] = *reinterpret_cast<const uint2*>(scl + blk * 64 + 16 * m + 4 * lg);
+            return o;
         };
         float acc[4][4];
 #pragma unroll
         for (int m = 0; m < 4; ++m)
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[m][v] = 0.0f;
-        load(0, 0);
-        if (c0 == 0) {  // the tile's scales to LDS, with the first batch in flight
-            stage<8>(
-                nb * 32, [&](int i) { return reinterpret_cast<const uint32_t*>(T)[i]; },
-                [&](int i, uint32_t v) { reinterpret_cast<uint32_t*>(scl)[i] = v; });
-            __syncthreads();
-        }
+        Ops o = ops(b0);
 #pragma unroll
-        for (int k = 0; k < NBATCH; ++k) {
-            if (k + 1 < NBATCH) load(k + 1, (k + 1) & 1);
-            __builtin_amdgcn_sched_barrier(0);
+        for (int b = 0; b < BPW; ++b) {
+            const int blk = b0 + b;
+            const Ops cu = o;
+            if (b + 1 < BPW) o = ops(blk + 1);  // the next block's LDS operands, in flight during these MFMAs
+            const v4i c = c_init((int)cu.qsum);
+            const long bop = (long)(((uint64_t)cu.hi << 32) | cu.lo);
+            v4i d[4];
 #pragma unroll
-            for (int b = 0; b < NBB; ++b) {
-                if (k * NBB + b < BPW) {
-                    const ActOp a = av[k & 1][b];
-                    const v4i c = c_init(a.qsum);
+            for (int m = 0; m < 4; ++m) d[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib_op(aw[b][m]), bop, c, 0, 0, 0);
+            issue_block(b, nxt);
+            const float ad = __uint_as_float(cu.d);
 #pragma unroll
-                    for (int m = 0; m < 4; ++m) {
-                        const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib_op(aw[k & 1][b][m]), a.b, c, 0, 0, 0);
-                        if constexpr (REC) {  // test record: D = the (row, token) blocks' int32 dots
-                            if (li < nt)
+            for (int m = 0; m < 4; ++m) {
+                if constexpr (REC) {  // test record: D = the (row, token) blocks' int32 dots
+                    if (li < cur.nt)
 #pragma unroll
-                                for (int v = 0; v < 4; ++v) {
-                                    const int rr = 16 * m + 4 * lg + v;
-                                    const int row = rr < 32 ? j * 32 + rr : I + j * 32 + (rr - 32);
-                                    rec[((int64_t)p * 2 * I + row) * nb + b0 + k * NBB + b] = d[v];
-                                }
+                        for (int v = 0; v < 4; ++v) {
+                            const int rr = 16 * m + 4 * lg + v;
+                            const int row = rr < 32 ? cur.j * 32 + rr : I + cur.j * 32 + (rr - 32);
+                            rec[((int64_t)pme * 2 * I + row) * nb + blk] = d[m][v];
                         }
-                        float sc[4];
-                        scales4(scl + (b0 + k * NBB + b) * 64 + 16 * m + 4 * lg, sc);
-#pragma unroll
-                        for (int v = 0; v < 4; ++v) acc[m][v] = fmaf((float)d[v], sc[v] * a.d, acc[m][v]);
-                    }
-                    // one block's MFMA results live at a time
-                    __builtin_amdgcn_sched_barrier(0);
                 }
+                const float sc[4] = {h2f((uint16_t)(cu.sc[m].x & 0xFFFF)), h2f((uint16_t)(cu.sc[m].x >> 16)),
+                                     h2f((uint16_t)(cu.sc[m].y & 0xFFFF)), h2f((uint16_t)(cu.sc[m].y >> 16))};
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[m][v] = fmaf((float)d[m][v], sc[v] * ad, acc[m][v]);
             }
+            __builtin_amdgcn_sched_barrier(0);  // one block's MFMA results live at a time
         }
 #pragma unroll
         for (int m = 0; m < 4; ++m)
 #pragma unroll
             for (int v = 0; v < 4; ++v) red[(wave * 64 + 16 * m + 4 * lg + v) * MT + li] = acc[m][v];
-        __syncthreads();
-        for (int i = t; i < nt * 64; i += GT) {  // (token, row) sums over the waves, in wave order
+        __syncthreads();  // every wave is past its MFMAs: act rows and scl[PAR] may change below
+        if (n2_scales) issue_scales(PAR, n2);
+        for (int i = t; i < cur.nt * 64; i += GT) {  // (token, row) sums over the waves, in wave order
             const int tt = i >> 6, rr = i & 63;
             float sv = 0.0f;
 #pragma unroll
             for (int v = 0; v < GW; ++v) sv = sv + red[(v * 64 + rr) * MT + tt];
-            const int pp = plist[s0 + c0 + tt];
-            if (in_scale) sv = sv * in_scale[pp / K];
+            const int pp = tok_p[tt];
+            if (in_scale) sv = sv * tok_s[tt];
             rows[tt * 64 + rr] = sv;
-            if (dbg_gu) dbg_gu[(int64_t)pp * 2 * I + (rr < 32 ? j * 32 + rr : I + j * 32 + (rr - 32))] = sv;
+            if (dbg_gu) dbg_gu[(int64_t)pp * 2 * I + (rr < 32 ? cur.j * 32 + rr : I + cur.j * 32 + (rr - 32))] = sv;
         }
         __syncthreads();
-        for (int i = t; i < nt * 32; i += GT) {
+        for (int i = t; i < cur.nt * 32; i += GT) {
             const int tt = i >> 5, cc = i & 31;
             actv[tt * 32 + cc] = gelu_tanh(rows[tt * 64 + cc]) * rows[tt * 64 + 32 + cc];
         }
         __syncthreads();
-        if (t < 4 * nt) quantize_block_quad(actv + (t >> 2) * 32, t & 3, ablk + (t >> 2) * 10);
+        if (t < 4 * cur.nt) quantize_block_quad(actv + (t >> 2) * 32, t & 3, ablk + (t >> 2) * 10);
         __syncthreads();
-        for (int i = t; i < nt * 10; i += GT) {
+        for (int i = t; i < cur.nt * 10; i += GT) {
             const int tt = i / 10, wd = i - tt * 10;
-            const int pp = plist[s0 + c0 + tt];
-            reinterpret_cast<uint32_t*>(q8a + ((int64_t)pp * nbj + j) * Q8_BLK)[wd] = ablk[tt * 10 + wd];
+            reinterpret_cast<uint32_t*>(q8a + ((int64_t)tok_p[tt] * nbj + cur.j) * Q8_BLK)[wd] = ablk[tt * 10 + wd];
         }
+        if (!nxt.live) return false;
+        __builtin_amdgcn_s_waitcnt(vm_wait_enc(BPW * 4 < 63 ? BPW * 4 : 63));  // nxt's scales are in LDS
+        if (nxt.g != act_g || nxt.c0 != act_c0) {
+            stage_act(nxt);
+            act_g = nxt.g;
+            act_c0 = nxt.c0;
+        }
+        __syncthreads();
+        cur = nxt;
+        nxt = n2;
+        return true;
+    };
+    while (step(std::integral_constant<int, 0>{}) && step(std::integral_constant<int, 1>{})) {
     }
 }
 
@@ -819,12 +924,13 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
         if ((rc = launch_status("moe_layer_grouped/gate_up"))) return rc;
     }
     if (mfma) {
-        const size_t lds_mg = (size_t)nb * 128 + sizeof(float) * (GW * 64 * MT + MT * 64 + MT * 32) + 4 * MT * 10;
+        const size_t lds_mg = (size_t)2 * nb * 128 + sizeof(float) * (GW * 64 * MT + MT * 64 + MT * 32) + 4 * MT * 10 +
+                              8 * MT + 4 * (size_t)MT * (nb * 10 + 1);
         auto kern = H == 2816 ? (rec ? k_mfma_gu<11, true> : k_mfma_gu<11, false>)
                               : (rec ? k_mfma_gu<16, true> : k_mfma_gu<16, false>);
-        hipLaunchKernelGGL(kern, dim3(nbj, gbig), dim3(GT), lds_mg, s, (const uint8_t*)bank, eb, (const int32_t*)w.meta,
-                           (const int32_t*)w.plist, (const uint8_t*)w.q8x, q8x_bytes, w.q8a, dbg_gu, inv, H, I, E, K,
-                           n_mfma, rgu);
+        const int grid = std::min(ctx->num_cus, nbj * gbig);  // persistent: one workgroup per CU
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(GT), lds_mg, s, (const uint8_t*)bank, eb, (const int32_t*)w.meta,
+                           (const int32_t*)w.plist, (const uint8_t*)w.q8x, w.q8a, dbg_gu, inv, H, I, E, K, rgu);
         if ((rc = launch_status("moe_layer_grouped/gate_up_mfma"))) return rc;
     }
     if (dbg_act && hipMemcpyAsync(dbg_act, w.q8a, (size_t)P * nbj * Q8_BLK, hipMemcpyDeviceToDevice, s) != hipSuccess)
