@@ -32,6 +32,20 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "freetoken-rs_amd"))
 
 HBM_PEAK_GBPS = 8000.0
+# HBM bytes per launch of the kernel each config's `roofline` names (per step where that is the
+# whole HIP graph of a step), measured with rocprofv3 --pmc FETCH_SIZE and, in a second run,
+# WRITE_SIZE on `bench.py --config NAME --steps 4 --warmup 2 --no-cpu --copy-calib 256` (default
+# options otherwise): FETCH_SIZE x 1.9982 + WRITE_SIZE x 1.0, the two factors being what a plain
+# 256 MiB torch copy in the same run reads and writes over what the counters report for it.
+# Summaries and commands: profiles/hbm_traffic.md. Reported only for runs with those options.
+MEASURED_TRAFFIC = {
+    "gemma30": 974310331,    # k_moe_stack_fused, one launch (algorithmic 846,151,680 B)
+    "zipf": 990280985,       # k_moe_stack_fused, one launch
+    "batch16": 7910899312,   # whole step, 30 grouped layers
+    "batch64": 11571032200,  # whole step, 30 grouped layers
+    "large32": 24749522440,  # whole step, 32 grouped layers
+    "large1": 135597620,     # k_gemv_gu_act, one launch (algorithmic 132,120,576 B)
+}
 METRIC = "MoE expert-FFN µs/token at batch 1 + achieved HBM GB/s (% of MI355X peak)"
 # name -> (shape, tokens per step, Zipf exponent of the router bias, BASELINE.json config)
 CONFIGS = {
@@ -660,6 +674,9 @@ def main():
                "host_cpu": cpu_name, "host_logical_cpus": n_logical}
 
     workload = {1: "", 2: "", 3: ", Zipf(1.1) router bias", 4: "", 5: ""}[cfg_id]
+    profiled_opts = (args.path == "auto" and args.prefetch == 1 and args.input_norm == 1 and args.mfma_min == 0
+                     and args.layers == 0 and not args.trace)
+    traffic = MEASURED_TRAFFIC.get(args.config) if profiled_opts else None
     res = {
         "metric": METRIC,
         "value": round(us_tok, 2),
@@ -685,7 +702,8 @@ def main():
         "achieved_GBps": round(gbps, 1),
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "roofline": {"bound": "hbm", "achieved": round(k_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(k_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(k_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "traffic_unit": "B per launch" if traffic else None,
                      "kernel": k_name, "bytes_per_launch": k_bytes,
                      "us_per_launch": round(k_us, 3)},
         "cpu_baseline": cpu,

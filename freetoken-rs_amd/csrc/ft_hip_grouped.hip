@@ -710,8 +710,8 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
 // RT tiles of group w/KS (they share each block's activation operand), K
 // slice w%KS (blocks [s*BW, s*BW+BW) below nbj); the KS slice partials of a
 // (row, token) are summed in slice order into y[pair][row].
-template <int KS, int BW, int RT, bool REC>
-__global__ __launch_bounds__(GT, 2) void k_mfma_down(const uint8_t* bank, int64_t expert_bytes, int64_t gu_bytes,
+template <int KS, int BW, int RT, int NBB, bool REC>
+__global__ __launch_bounds__(GT, NBB > 4 ? 1 : 2) void k_mfma_down(const uint8_t* bank, int64_t expert_bytes, int64_t gu_bytes,
                                                      const int32_t* meta, const int32_t* plist, const uint8_t* q8a,
                                                      uint32_t q8a_bytes, float* ydn, int H, int I, int E, int n_min,
                                                      int32_t* rec) {
@@ -741,7 +741,7 @@ __global__ __launch_bounds__(GT, 2) void k_mfma_down(const uint8_t* bank, int64_
         const uint32_t vd = (uint32_t)p * nbj * Q8_BLK, vq = vd + 8 + 4 * lg;
         // blocks in NBB-block batches, the next batch's loads issued before
         // the current batch's MFMAs (two register buffers)
-        constexpr int NBB = 4, NBATCH = BW / NBB;
+        constexpr int NBATCH = BW / NBB;
         uint32_t aw[2][NBB][RT];
         ActOp av[2][NBB];
         auto load = [&](int k, int buf) __attribute__((always_inline)) {
@@ -947,14 +947,14 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
     if (mfma) {
         if (nbj <= 32) {  // one K slice: 8 waves x 2 tiles of 16 rows per workgroup
             const size_t lds_md = (size_t)GW * 2 * nbj * 32 + sizeof(float) * GW * 2 * 16 * MT;
-            auto kern = rec ? k_mfma_down<1, 32, 2, true> : k_mfma_down<1, 32, 2, false>;
+            auto kern = rec ? k_mfma_down<1, 32, 2, 4, true> : k_mfma_down<1, 32, 2, 4, false>;
             hipLaunchKernelGGL(kern, dim3(H / (16 * GW * 2), gbig), dim3(GT), lds_md, s, (const uint8_t*)bank, eb,
                                gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8a,
                                q8a_bytes, w.ydn, H, I, E, n_mfma, rdn);
         } else {  // long rows: DRT tiles per workgroup, 8 K slices of up to 64 blocks
             constexpr int DRT = 4;
             const size_t lds_md = (size_t)DRT * nbj * 32 + sizeof(float) * GW * DRT * 16 * MT;
-            auto kern = rec ? k_mfma_down<GW, 64, DRT, true> : k_mfma_down<GW, 64, DRT, false>;
+            auto kern = rec ? k_mfma_down<GW, 64, DRT, 4, true> : k_mfma_down<GW, 64, DRT, 4, false>;
             hipLaunchKernelGGL(kern, dim3(H / (16 * DRT), gbig), dim3(GT), lds_md, s, (const uint8_t*)bank, eb,
                                gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8a,
                                q8a_bytes, w.ydn, H, I, E, n_mfma, rdn);
