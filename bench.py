@@ -543,9 +543,13 @@ def main():
                 bstack.run(src, dst, B, ids, wts, stream=stream)
         else:
             ws = model.workspace(B)
+            sws = model.stack_workspace(B)
 
             def layer(l, src, dst, ids, wts, stream):
                 model.layer(l, src, dst, ids, wts, ws, n_seqs=B, stream=stream)
+
+            def step(src, dst, ids, wts, stream):  # all layers in one call (ft_hip_moe_stack)
+                model.stack(src, dst, ids, wts, sws, n_seqs=B, stream=stream)
         C = chunk_size(args.steps, args.warmup)
         runner = GraphRunner(model, B, C, layer, step)
         log(f"[setup] {C} step(s) per captured HIP graph")

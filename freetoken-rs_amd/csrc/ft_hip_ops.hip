@@ -266,6 +266,65 @@ __global__ __launch_bounds__(256) void k_gemv_q4r_short(GemvArgs a) {
     if (live && sub == 0) a.y[(int64_t)e * a.y_stride + row] = acc;
 }
 
+// The head of a layer taken from the previous layer's down launch
+// (k_gemv_down_head) instead of a launch of its own: the states x the layer
+// runs on, and the R-order chunk partials part[s][c][e] of its router rows e
+// < E and, at e = E, of x.x (16-element fma chains over chunk c of x_s).
+struct HeadArgs {
+    const float* x;     // [n_seqs][H]
+    const float* part;  // [n_seqs][H/16][E+1]
+    const float* bias;  // [E] or null
+    int norm;           // input RMS norm on
+};
+
+// Prologue of a gate|up launch that computes its layer's head (HeadArgs):
+// the group sums G[e][g] (the C = H/128 chunk partials of group g in order
+// from 0.0f), each logit (groups in order from 0.0f, times the input norm's
+// scale when on, then + bias) into sv, the norm's scale into *irs, and the
+// q8 row of x_s into lds (4 lanes per block): k_route_prep's arithmetic, so
+// its bits. Barriers inside; sv, lds and *irs are read after it returns.
+__device__ __forceinline__ void head_prologue(const HeadArgs& h, int s, int H, int E, float* sv, int* lds, float* hg,
+                                              float* irs) {
+    const int t = threadIdx.x, nt = blockDim.x;
+    const int nch = H >> 4, C = H >> 7, EP = E + 1;
+    const float* ps = h.part + (int64_t)s * nch * EP;
+    for (int q = t; q < 8 * EP; q += nt) {
+        const int e = q >> 3, g = q & 7;
+        const float* p = ps + (int64_t)g * C * EP + e;
+        float acc = 0.0f;
+        int c = 0;
+        for (; c + 8 <= C; c += 8) {  // eight loads issued ahead of their adds
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = p[(int64_t)(c + j) * EP];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc = acc + v[j];
+        }
+        for (; c < C; ++c) acc = acc + p[(int64_t)c * EP];
+        hg[q] = acc;
+    }
+    const float* xs = h.x + (int64_t)s * H;
+    const int nb = H >> 5;
+    for (int q = t; q < 4 * nb; q += nt)  // whole quads: nt and 4*nb are multiples of 4
+        quantize_block_quad(xs + 32 * (q >> 2), q & 3, reinterpret_cast<uint32_t*>(lds + (q >> 2) * 10));
+    __syncthreads();
+    float ir = 1.0f;
+    if (h.norm) {
+        float ss = 0.0f;
+        for (int g = 0; g < 8; ++g) ss = ss + hg[E * 8 + g];
+        ir = 1.0f / sqrtf(ss / (float)H + 1e-6f);  // correctly rounded (HIP default)
+    }
+    for (int e = t; e < E; e += nt) {
+        float tot = 0.0f;
+        for (int g = 0; g < 8; ++g) tot = tot + hg[e * 8 + g];
+        if (h.norm) tot = tot * ir;
+        if (h.bias) tot = tot + h.bias[e];
+        sv[e] = tot;
+    }
+    if (t == 0) *irs = ir;
+    __syncthreads();
+}
+
 // Gate|up GEMV of one pair with GELU(gate)*up and its q8 block in the same
 // launch (replaces gemv_q4r_grouped + gelu_mul_quantize_q8, q4.cu). A
 // workgroup of 64*LPR threads owns gate rows 32j..32j+31 (the first LPR/2
@@ -280,11 +339,16 @@ __global__ __launch_bounds__(256) void k_gemv_q4r_short(GemvArgs a) {
 // workgroup from the logits, the expert of pair blockIdx.y taken from it, and
 // ids/wts written by the seq's workgroup (0, s*div); without TOPK the pair's
 // expert is a.slots[pair].
-template <int LAYOUT, bool TOPK, int LPR = 8>
+//
+// HEAD (with TOPK): the logits, the input norm's scale and q8(x_s) come from
+// head_prologue (HeadArgs: the previous layer's down launch left the router
+// partials) instead of logits, in_scale and a.q8.
+template <int LAYOUT, bool TOPK, int LPR = 8, bool HEAD = false>
 __global__ __launch_bounds__(64 * LPR, 24 / LPR) void k_gemv_gu_act(GemvArgs a, int inter, uint8_t* q8a,
                                                                   const float* in_scale, int div, const float* logits,
                                                                   const float* escale, int32_t* ids, float* wts,
-                                                                  int E) {
+                                                                  int E, HeadArgs h) {
+    static_assert(TOPK || !HEAD, "the head's logits are ranked in the launch");
     extern __shared__ int lds[];
     __shared__ float gs[64];
     const int e = blockIdx.y, t = threadIdx.x;
@@ -292,9 +356,15 @@ __global__ __launch_bounds__(64 * LPR, 24 / LPR) void k_gemv_gu_act(GemvArgs a, 
     __shared__ int seli[TOPK ? 32 : 1];
     __shared__ uint64_t key[TOPK ? 256 : 1];
     __shared__ float exv[TOPK ? 32 : 1];
+    __shared__ float hg[HEAD ? 8 * 257 : 1];
+    __shared__ float irs;
     const int s = e / div;
-    if (TOPK && t < E) sv[t] = logits[(int64_t)s * E + t];
-    stage_q8(a, e, lds);  // its barrier also covers sv
+    if constexpr (HEAD) {
+        head_prologue(h, s, a.k, E, sv, lds, hg, &irs);
+    } else {
+        if (TOPK && t < E) sv[t] = logits[(int64_t)s * E + t];
+        stage_q8(a, e, lds);  // its barrier also covers sv
+    }
     int slot;
     if constexpr (TOPK) {
         topk_rank_select(sv, E, div, key, selv, seli);
@@ -323,8 +393,8 @@ __global__ __launch_bounds__(64 * LPR, 24 / LPR) void k_gemv_gu_act(GemvArgs a, 
     if (threadIdx.x < 64) {  // both half-waves compute block j; the first stores it
         const int l = threadIdx.x & 31;
         float gate = gs[l], up = gs[32 + l];
-        if (in_scale) {
-            const float sc = in_scale[e / div];
+        if (HEAD ? h.norm != 0 : in_scale != nullptr) {
+            const float sc = HEAD ? irs : in_scale[e / div];
             gate = gate * sc;
             up = up * sc;
         }
@@ -372,6 +442,74 @@ __global__ __launch_bounds__(256) void k_gemv_down_combine(GemvArgs a, const flo
             h = h + part;
         }
         out[(int64_t)s * a.n_rows + i] = x[(int64_t)s * a.n_rows + i] + h;
+    }
+}
+
+// k_gemv_down_combine for 16 rows of every pair of seq s per workgroup
+// (16*k*LPR threads: the same per-row arithmetic, so the same bits), which
+// then computes the next layer's head partials of those rows: they are R-order
+// chunk c = blockIdx.x, and the workgroup writes part[s][c][e] = the
+// 16-element fma chain (in row order, from 0.0f) of the next router's row e
+// (wnext, [E][H]) with out, and part[s][c][E] = that of out with itself:
+// k_route_prep's chunk partials P_c, for head_prologue in the next gate|up
+// launch. Grid (H/16, n_seqs), NT = 16*k*LPR threads; E < NT.
+template <int LAYOUT, int LPR, int NT>
+__global__ __launch_bounds__(NT) void k_gemv_down_head(GemvArgs a, const float* wts, const float* x, float* out,
+                                                      int k, const float* wnext, float* part, int E) {
+    extern __shared__ int lds[];
+    __shared__ float ys[NT / LPR];
+    __shared__ float4 xs4[4];
+    float* xs = reinterpret_cast<float*>(xs4);
+    const int s = blockIdx.y, c = blockIdx.x, t = threadIdx.x;
+    const int nb = a.k >> 5, H = a.n_rows;
+    // this chunk of the next router's row t: loaded ahead of the GEMV when the
+    // registers allow (up to 512 threads), else after it
+    constexpr bool EARLY = NT <= 512;
+    float4 wv[4];
+    auto load_w = [&]() __attribute__((always_inline)) {
+        if (t < E) {
+            const float4* w4 = reinterpret_cast<const float4*>(wnext + (int64_t)t * H + 16 * c);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) wv[q] = w4[q];
+        }
+    };
+    if (EARLY) load_w();
+    stage_words<40>(reinterpret_cast<const int*>(a.q8 + (int64_t)s * k * a.q8_stride_blocks * Q8_BLK), k * nb * 10,
+                    lds);
+    const int lane = t & 63, wave = t >> 6;
+    const int re = wave * (64 / LPR) + lane / LPR, sub = lane % LPR;  // row entry: pair kk, local row rl
+    const int kk = re >> 4, rl = re & 15;
+    const int row = c * 16 + rl;
+    float acc = gemv_row_part<LAYOUT, LPR>(entry_base(a, s * k + kk) + (int64_t)row * row_bytes_of(LAYOUT, a.k), sub,
+                                           nb, lds + kk * nb * 10);
+    acc = sum_row_lanes<LPR>(acc);
+    if (sub == 0) ys[re] = acc;
+    if (!EARLY) load_w();
+    __syncthreads();
+    if (t < 16) {
+        const int i = c * 16 + t;
+        float hsum = 0.0f;
+        for (int q = 0; q < k; ++q) {
+            const float p = ys[q * 16 + t] * wts[(int64_t)s * k + q];
+            hsum = hsum + p;
+        }
+        const float v = x[(int64_t)s * H + i] + hsum;
+        out[(int64_t)s * H + i] = v;
+        xs[t] = v;
+    }
+    __syncthreads();
+    if (t <= E) {
+        float p = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 b = xs4[q];
+            const float4 w = t < E ? wv[q] : b;  // t == E: the self-dot
+            p = fmaf(w.x, b.x, p);
+            p = fmaf(w.y, b.y, p);
+            p = fmaf(w.z, b.z, p);
+            p = fmaf(w.w, b.w, p);
+        }
+        part[((int64_t)s * (H >> 4) + c) * (E + 1) + t] = p;
     }
 }
 
@@ -1087,7 +1225,7 @@ extern "C" int ft_hip_gemv_gate_up_act(ft_hip_ctx* ctx, void* stream, const void
     hipLaunchKernelGGL(kern, dim3((unsigned)(inter / 32), (unsigned)n_pairs), dim3(64 * GU_LANES),
                        (size_t)(hidden / 32) * Q8_BLK,
                        S(stream), a, (int)inter, (uint8_t*)q8_act, in_scale, (int)x_div, (const float*)nullptr,
-                       (const float*)nullptr, (int32_t*)nullptr, (float*)nullptr, 0);
+                       (const float*)nullptr, (int32_t*)nullptr, (float*)nullptr, 0, HeadArgs{});
     return launch_status(nm);
 }
 
@@ -1220,11 +1358,47 @@ int scratch_setup(ft_hip_ctx* ctx) {
 }
 }  // namespace ft
 
+// Lanes per row of the down launch with the combine (k_gemv_down_combine):
+// 16 for rows of at least 256 blocks when k divides 16, else 8.
+static int down_lanes(int64_t inter, int64_t top_k) { return inter / 32 >= 256 && 16 % top_k == 0 ? 16 : 8; }
+
+// Whether a stack of layers can take each layer's head from the previous
+// layer's down launch (k_gemv_down_head, then k_gemv_gu_act<HEAD>): the top-k
+// runs in the gate|up launch, the down launch is the combined one, and
+// 16 rows of every pair (16*k*lanes threads) plus the E+1 partials fit one
+// workgroup.
+static bool head_fold_ok(int64_t inter, int64_t n_experts, int64_t top_k) {
+    if (n_experts > 256 || 32 % top_k || top_k * (inter / 32) * Q8_BLK > 64 * 1024) return false;
+    const int64_t nt = 16 * top_k * down_lanes(inter, top_k);
+    return nt >= 256 && nt <= 1024 && n_experts < nt;
+}
+
+// k_gemv_down_head for nt = 16*k*LPR threads (256, 512 or 1024)
+template <int LAYOUT, int LPR>
+static void launch_down_head(int nt, dim3 grid, size_t lds, hipStream_t st, const GemvArgs& a, const float* wts,
+                             const float* x, float* out, int k, const float* wnext, float* part, int E) {
+    if (nt == 256)
+        hipLaunchKernelGGL((k_gemv_down_head<LAYOUT, LPR, 256>), grid, dim3(256), lds, st, a, wts, x, out, k, wnext,
+                           part, E);
+    else if (nt == 512)
+        hipLaunchKernelGGL((k_gemv_down_head<LAYOUT, LPR, 512>), grid, dim3(512), lds, st, a, wts, x, out, k, wnext,
+                           part, E);
+    else
+        hipLaunchKernelGGL((k_gemv_down_head<LAYOUT, LPR, 1024>), grid, dim3(1024), lds, st, a, wts, x, out, k, wnext,
+                           part, E);
+}
+
+// One layer of the launch-by-launch path. In a stack (head_fold_ok): part_in
+// set = this layer's head comes from the partials the previous down launch
+// left in part_in (no head launch; k_gemv_gu_act<HEAD>); wnext set = the down
+// launch also writes the next layer's partials (router rows wnext) to
+// part_out. Either way the bits are those of the plain layer.
 static int moe_layer_impl(const char* nm, ft_hip_ctx* ctx, void* stream, const float* x, float* x_out,
                           int64_t n_seqs, int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k,
                           const float* router_w, const float* router_bias, const float* expert_scale,
                           const void* bank, uint64_t expert_bytes, int layout, int32_t* ids, float* wts,
-                          void* workspace, size_t workspace_bytes) {
+                          void* workspace, size_t workspace_bytes, const float* part_in = nullptr,
+                          const float* wnext = nullptr, float* part_out = nullptr) {
     if (hidden <= 0 || hidden % 128) return fail(FT_HIP_E_SHAPE, "%s: hidden=%lld must be a positive multiple of 128", nm, (long long)hidden);
     if (inter <= 0 || inter % 32) return fail(FT_HIP_E_SHAPE, "%s: inter=%lld must be a positive multiple of 32", nm, (long long)inter);
     if (n_experts <= 0 || n_experts > 1024) return fail(FT_HIP_E_SHAPE, "%s: n_experts not in [1, 1024]", nm);
@@ -1243,7 +1417,11 @@ static int moe_layer_impl(const char* nm, ft_hip_ctx* ctx, void* stream, const f
     if (n_seqs == 0) return FT_HIP_OK;
     int rc;
     const float* inv = ctx->input_norm ? w.inv : nullptr;
-    if (n_experts * 16 >= hidden / 32) {  // logits, norm scale and q8(x) in one launch
+    if ((part_in || wnext) && !head_fold_ok(inter, n_experts, top_k))
+        return fail(FT_HIP_E_SHAPE, "%s: this shape cannot take the layer head from the down launch", nm);
+    if (part_in) {
+        // the head was computed by the previous layer's down launch
+    } else if (n_experts * 16 >= hidden / 32) {  // logits, norm scale and q8(x) in one launch
         if ((rc = ft::launch_route_prep(stream, router_w, x, router_bias, ctx->input_norm, w.inv, w.q8x, w.logits,
                                         hidden, n_experts, n_seqs)))
             return rc;
@@ -1273,14 +1451,21 @@ static int moe_layer_impl(const char* nm, ft_hip_ctx* ctx, void* stream, const f
     a.k = (int)hidden;
     const dim3 g_gu((unsigned)(inter / 32), (unsigned)n_pairs);
     const size_t l_gu = (size_t)(hidden / 32) * Q8_BLK;
-    {
+    if (part_in) {
+        const HeadArgs h{x, part_in, router_bias, ctx->input_norm};
+        auto kern = layout == FT_LAYOUT_Q4R ? k_gemv_gu_act<FT_LAYOUT_Q4R, true, GU_LANES, true>
+                                            : k_gemv_gu_act<FT_LAYOUT_Q4_0, true, GU_LANES, true>;
+        hipLaunchKernelGGL(kern, g_gu, dim3(64 * GU_LANES), l_gu, S(stream), a, (int)inter, w.q8a,
+                           (const float*)nullptr, (int)top_k, (const float*)nullptr, expert_scale, ids, wts,
+                           (int)n_experts, h);
+    } else {
         auto kern = layout == FT_LAYOUT_Q4R
                         ? (topk_in ? k_gemv_gu_act<FT_LAYOUT_Q4R, true, GU_LANES>
                                    : k_gemv_gu_act<FT_LAYOUT_Q4R, false, GU_LANES>)
                         : (topk_in ? k_gemv_gu_act<FT_LAYOUT_Q4_0, true, GU_LANES>
                                    : k_gemv_gu_act<FT_LAYOUT_Q4_0, false, GU_LANES>);
         hipLaunchKernelGGL(kern, g_gu, dim3(64 * GU_LANES), l_gu, S(stream), a, (int)inter, w.q8a, inv, (int)top_k,
-                           (const float*)w.logits, expert_scale, ids, wts, (int)n_experts);
+                           (const float*)w.logits, expert_scale, ids, wts, (int)n_experts, HeadArgs{});
     }
     if ((rc = launch_status("moe_layer/gate_up_act"))) return rc;
     a.bank_off = (uint64_t)gu_bytes;
@@ -1290,11 +1475,22 @@ static int moe_layer_impl(const char* nm, ft_hip_ctx* ctx, void* stream, const f
     a.y = w.ydn;
     a.y_stride = hidden;
     const size_t l_dn = (size_t)top_k * (inter / 32) * Q8_BLK;
+    if (wnext) {  // head_fold_ok: 16 rows of every pair per workgroup, then the next layer's partials
+        a.n_rows = (int)hidden;
+        a.k = (int)inter;
+        const int lpr = down_lanes(inter, top_k), nt = (int)(16 * top_k * lpr);
+        const dim3 g_dn((unsigned)(hidden / 16), (unsigned)n_seqs);
+        auto launch = layout == FT_LAYOUT_Q4R
+                          ? (lpr == 16 ? launch_down_head<FT_LAYOUT_Q4R, 16> : launch_down_head<FT_LAYOUT_Q4R, 8>)
+                          : (lpr == 16 ? launch_down_head<FT_LAYOUT_Q4_0, 16> : launch_down_head<FT_LAYOUT_Q4_0, 8>);
+        launch(nt, g_dn, l_dn, S(stream), a, wts, x, x_out, (int)top_k, wnext, part_out, (int)n_experts);
+        return launch_status("moe_layer/down_head");
+    }
     if (32 % top_k == 0 && l_dn <= 64 * 1024) {
         a.n_rows = (int)hidden;
         a.k = (int)inter;
         // 16 lanes per row for long rows (at least 256 blocks) when k divides 16
-        const bool l16 = inter / 32 >= 256 && 16 % top_k == 0;
+        const bool l16 = down_lanes(inter, top_k) == 16;
         const int R = (int)((l16 ? 16 : 32) / top_k);
         const dim3 g_dn((unsigned)((hidden + R - 1) / R), (unsigned)n_seqs);
         auto kern = layout == FT_LAYOUT_Q4R
@@ -1338,4 +1534,71 @@ extern "C" int ft_hip_moe_layer_noalloc(ft_hip_ctx* ctx, void* stream, const flo
     return moe_layer_impl(nm, ctx, stream, x, x_out, n_seqs, hidden, inter, n_experts, top_k, router_w, router_bias,
                           expert_scale, bank, expert_bytes, layout, ids, wts, ctx->noalloc_scratch,
                           (size_t)FT_HIP_NOALLOC_SCRATCH_BYTES);
+}
+
+// Workspace of ft_hip_moe_stack: a layer's, the two states between layers and
+// the head partials [n_seqs][H/16][E+1].
+struct StackLayerWs {
+    size_t layer_bytes;
+    float* state[2];
+    float* part;
+    size_t bytes;
+};
+
+static StackLayerWs stack_layer_ws(void* base, int64_t B, int64_t H, int64_t I, int64_t E, int64_t K) {
+    auto up = [](size_t v) { return (v + 255) / 256 * 256; };
+    StackLayerWs w{};
+    uint8_t* p = (uint8_t*)base;
+    size_t off = layer_ws(nullptr, B, H, I, E, K).bytes;
+    w.layer_bytes = off;
+    for (int i = 0; i < 2; ++i) {
+        w.state[i] = (float*)(p + off);
+        off += up(sizeof(float) * B * H);
+    }
+    w.part = (float*)(p + off);
+    off += up(sizeof(float) * B * (H / 16) * (E + 1));
+    w.bytes = off;
+    return w;
+}
+
+extern "C" size_t ft_hip_moe_stack_workspace_bytes(int64_t n_seqs, int64_t hidden, int64_t inter, int64_t n_experts,
+                                                   int64_t top_k) {
+    if (n_seqs < 0 || hidden <= 0 || hidden % 16 || inter <= 0 || n_experts <= 0 || top_k <= 0) return 0;
+    return stack_layer_ws(nullptr, n_seqs, hidden, inter, n_experts, top_k).bytes;
+}
+
+extern "C" int ft_hip_moe_stack(ft_hip_ctx* ctx, void* stream, const float* x_in, float* x_out, int64_t n_seqs,
+                                int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k, int64_t n_layers,
+                                const float* routers, const float* router_bias, const float* expert_scale,
+                                const void* banks, uint64_t expert_bytes, int layout, int32_t* ids, float* wts,
+                                void* workspace, size_t workspace_bytes) {
+    clear_error();
+    const char* nm = "moe_stack";
+    if (n_layers <= 0) return fail(FT_HIP_E_SHAPE, "%s: n_layers must be positive", nm);
+    if (!ctx || !x_in || !x_out || !routers || !banks || !ids || !wts || !workspace)
+        return fail(FT_HIP_E_INVALID, "%s: null argument", nm);
+    if (hidden <= 0 || hidden % 128 || n_experts <= 0 || top_k <= 0 || n_seqs < 0)
+        return fail(FT_HIP_E_SHAPE, "%s: hidden=%lld n_experts=%lld top_k=%lld n_seqs=%lld", nm, (long long)hidden,
+                    (long long)n_experts, (long long)top_k, (long long)n_seqs);
+    const StackLayerWs sw = stack_layer_ws(workspace, n_seqs, hidden, inter, n_experts, top_k);
+    if (workspace_bytes < sw.bytes)
+        return fail(FT_HIP_E_SHAPE, "%s: workspace_bytes=%zu < %zu", nm, workspace_bytes, sw.bytes);
+    if (n_seqs == 0) return FT_HIP_OK;
+    const bool fold = head_fold_ok(inter, n_experts, top_k);
+    const int64_t per = n_seqs * top_k;
+    for (int64_t l = 0; l < n_layers; ++l) {
+        const float* xl = l == 0 ? x_in : sw.state[(l - 1) & 1];
+        float* out = l == n_layers - 1 ? x_out : sw.state[l & 1];
+        const bool last = l == n_layers - 1;
+        const uint8_t* bank = (const uint8_t*)banks + (uint64_t)l * n_experts * expert_bytes;
+        if (int rc = moe_layer_impl(nm, ctx, stream, xl, out, n_seqs, hidden, inter, n_experts, top_k,
+                                    routers + l * n_experts * hidden, router_bias ? router_bias + l * n_experts : nullptr,
+                                    expert_scale ? expert_scale + l * n_experts : nullptr, bank, expert_bytes, layout,
+                                    ids + l * per, wts + l * per, workspace, sw.layer_bytes,
+                                    fold && l > 0 ? sw.part : nullptr,
+                                    fold && !last ? routers + (l + 1) * n_experts * hidden : nullptr,
+                                    fold && !last ? sw.part : nullptr))
+            return rc;
+    }
+    return FT_HIP_OK;
 }

@@ -58,6 +58,8 @@ extern "C" {
     pub fn ft_hip_moe_layer_workspace_bytes(n_seqs: i64, hidden: i64, inter: i64, n_experts: i64, top_k: i64) -> usize;
     pub fn ft_hip_moe_layer(ctx: *mut FtHipCtx, stream: *mut c_void, x: *const f32, x_out: *mut f32, n_seqs: i64, hidden: i64, inter: i64, n_experts: i64, top_k: i64, router_w: *const f32, router_bias: *const f32, expert_scale: *const f32, bank: *const c_void, expert_bytes: u64, layout: c_int, ids: *mut i32, wts: *mut f32, workspace: *mut c_void, workspace_bytes: usize) -> c_int;
     pub fn ft_hip_moe_layer_noalloc(ctx: *mut FtHipCtx, stream: *mut c_void, x: *const f32, x_out: *mut f32, n_seqs: i64, hidden: i64, inter: i64, n_experts: i64, top_k: i64, router_w: *const f32, router_bias: *const f32, expert_scale: *const f32, bank: *const c_void, expert_bytes: u64, layout: c_int, ids: *mut i32, wts: *mut f32) -> c_int;
+    pub fn ft_hip_moe_stack_workspace_bytes(n_seqs: i64, hidden: i64, inter: i64, n_experts: i64, top_k: i64) -> usize;
+    pub fn ft_hip_moe_stack(ctx: *mut FtHipCtx, stream: *mut c_void, x_in: *const f32, x_out: *mut f32, n_seqs: i64, hidden: i64, inter: i64, n_experts: i64, top_k: i64, n_layers: i64, routers: *const f32, router_bias: *const f32, expert_scale: *const f32, banks: *const c_void, expert_bytes: u64, layout: c_int, ids: *mut i32, wts: *mut f32, workspace: *mut c_void, workspace_bytes: usize) -> c_int;
     pub fn ft_hip_moe_layer_grouped_workspace_bytes(n_seqs: i64, hidden: i64, inter: i64, n_experts: i64, top_k: i64) -> usize;
     pub fn ft_hip_moe_layer_grouped(ctx: *mut FtHipCtx, stream: *mut c_void, x: *const f32, x_out: *mut f32, n_seqs: i64, hidden: i64, inter: i64, n_experts: i64, top_k: i64, router_w: *const f32, router_bias: *const f32, expert_scale: *const f32, bank: *const c_void, ids: *mut i32, wts: *mut f32, workspace: *mut c_void, workspace_bytes: usize, dbg_gu: *mut f32, dbg_act: *mut c_void) -> c_int;
     pub fn ft_hip_moe_stack_grouped_workspace_bytes(max_seqs: i64, hidden: i64, inter: i64, n_experts: i64, top_k: i64, n_layers: i64) -> usize;

@@ -227,6 +227,29 @@ impl Q4Gemv {
         })
     }
 
+    pub fn moe_stack_workspace_bytes(n_seqs: usize, hidden: usize, inter: usize, n_experts: usize,
+                                     top_k: usize) -> usize {
+        unsafe {
+            ffi::ft_hip_moe_stack_workspace_bytes(n_seqs as i64, hidden as i64, inter as i64, n_experts as i64,
+                                                  top_k as i64)
+        }
+    }
+
+    /// The MoE sections of every layer of the decode stack (ft-model/src/lib.rs:778-1056) on the
+    /// launch-by-launch path: moe_layer for each layer, two launches per layer after the first.
+    #[allow(clippy::too_many_arguments)]
+    pub fn moe_stack(&self, s: Stream, x_in: DevPtr, x_out: DevPtr, n_seqs: usize, hidden: usize, inter: usize,
+                     n_experts: usize, top_k: usize, n_layers: usize, routers: DevPtr, router_bias: Option<DevPtr>,
+                     expert_scale: Option<DevPtr>, banks: DevPtr, expert_bytes: usize, layout: Layout, ids: DevPtr,
+                     wts: DevPtr, workspace: DevPtr, workspace_bytes: usize) -> Result<()> {
+        check(unsafe {
+            ffi::ft_hip_moe_stack(self.ctx, s.0, p(x_in), pm(x_out), n_seqs as i64, hidden as i64, inter as i64,
+                                  n_experts as i64, top_k as i64, n_layers as i64, p(routers), opt(router_bias),
+                                  opt(expert_scale), p(banks), expert_bytes as u64, layout.raw(), pm(ids), pm(wts),
+                                  pm(workspace), workspace_bytes)
+        })
+    }
+
     pub fn moe_layer_grouped_workspace_bytes(n_seqs: usize, hidden: usize, inter: usize, n_experts: usize,
                                              top_k: usize) -> usize {
         unsafe {

@@ -51,6 +51,9 @@ SIGNATURES = {
                               _P, _SZ]),
     "ft_hip_moe_layer_noalloc": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _U64, _I, _P,
                                       _P]),
+    "ft_hip_moe_stack_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
+    "ft_hip_moe_stack": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _U64, _I, _P,
+                              _P, _P, _SZ]),
     "ft_hip_moe_layer_grouped_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "ft_hip_moe_layer_grouped": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P,
                                       _SZ, _P, _P]),
@@ -272,6 +275,18 @@ class Q4Gemv:
                                              inter, n_experts, top_k, _ptr(router_w), _ptr(router_bias),
                                              _ptr(expert_scale), _ptr(bank), expert_bytes, layout, _ptr(ids),
                                              _ptr(wts)))
+
+    @staticmethod
+    def moe_stack_workspace_bytes(n_seqs, hidden, inter, n_experts, top_k):
+        return lib().ft_hip_moe_stack_workspace_bytes(n_seqs, hidden, inter, n_experts, top_k)
+
+    def moe_stack(self, x_in, x_out, n_seqs, hidden, inter, n_experts, top_k, n_layers, routers, router_bias,
+                  expert_scale, banks, expert_bytes, layout, ids, wts, workspace, stream=None):
+        """n_layers launch-by-launch layers in one call (ft_hip_moe_stack); ids/wts [L][n_seqs*top_k]."""
+        check(lib().ft_hip_moe_stack(self._ctx, _stream(stream), _ptr(x_in), _ptr(x_out), n_seqs, hidden, inter,
+                                     n_experts, top_k, n_layers, _ptr(routers), _ptr(router_bias),
+                                     _ptr(expert_scale), _ptr(banks), expert_bytes, layout, _ptr(ids), _ptr(wts),
+                                     _ptr(workspace), workspace.numel() * workspace.element_size()))
 
     # -- grouped batched layer (ft-model/src/lib.rs:1507-1606) --
     @staticmethod

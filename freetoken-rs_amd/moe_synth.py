@@ -158,6 +158,18 @@ class SyntheticMoE:
         self.g.moe_layer(x, x_out, n_seqs, s.hidden, s.inter, E, s.top_k, self.routers[l], self.layer_bias(l),
                          None, bank, self.expert_bytes, self.layout, ids, wts, ws, stream)
 
+    def stack_workspace(self, n_seqs):
+        s = self.shape
+        nbytes = ft_hip.Q4Gemv.moe_stack_workspace_bytes(n_seqs, s.hidden, s.inter, s.n_experts, s.top_k)
+        return torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+
+    def stack(self, x, x_out, ids, wts, ws, n_seqs=1, stream=None):
+        """All L layers through ft_hip_moe_stack (the launch-by-launch kernels, each
+        layer's router head folded into the previous down launch); ids/wts [L][n_seqs*k]."""
+        s = self.shape
+        self.g.moe_stack(x, x_out, n_seqs, s.hidden, s.inter, s.n_experts, s.top_k, self.L, self.routers,
+                         self.bias, None, self.banks, self.expert_bytes, self.layout, ids, wts, ws, stream)
+
 
 def gen_values_np(key, n, scale):
     """Host restatement of the device generator (ft_hip_gen_values): value i

@@ -223,6 +223,29 @@ int ft_hip_moe_layer(ft_hip_ctx* ctx, void* stream, const float* x, float* x_out
                      int layout, int32_t* ids, float* wts, void* workspace,
                      size_t workspace_bytes);
 
+/* The n_layers-layer expert section of the launch-by-launch path:
+ * ft_hip_moe_layer for each layer in turn, x_{l+1} = x_l + MoE_l(x_l) (the
+ * MoE section of every layer of ft-model's decode stack, lib.rs:778-1056,
+ * per-layer body :1406-1476). Where the shape allows (n_experts <= 256,
+ * top_k dividing 32 with at most 8, the k activation rows of a token within
+ * 64 KB), each layer's down launch also computes the next layer's router
+ * partials, so layers after the first take two launches instead of three;
+ * the results are those of the layer-by-layer calls, bit for bit, either way.
+ * banks: the layers' banks back to back (layer l at l * n_experts *
+ * expert_bytes, each as ft_hip_moe_layer's `bank`); routers [L][E][H];
+ * router_bias and expert_scale [L][E] or NULL; ids/wts [L][n_seqs*top_k]
+ * (device) receive the routing. x_in, x_out [n_seqs][H]. workspace: device
+ * scratch of ft_hip_moe_stack_workspace_bytes() bytes. No allocation; the
+ * launches can be captured in a HIP graph. */
+size_t ft_hip_moe_stack_workspace_bytes(int64_t n_seqs, int64_t hidden, int64_t inter,
+                                        int64_t n_experts, int64_t top_k);
+int ft_hip_moe_stack(ft_hip_ctx* ctx, void* stream, const float* x_in, float* x_out,
+                     int64_t n_seqs, int64_t hidden, int64_t inter, int64_t n_experts,
+                     int64_t top_k, int64_t n_layers, const float* routers,
+                     const float* router_bias, const float* expert_scale, const void* banks,
+                     uint64_t expert_bytes, int layout, int32_t* ids, float* wts,
+                     void* workspace, size_t workspace_bytes);
+
 /* ft_hip_moe_layer without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). No counterpart in the reference. Its
