@@ -178,11 +178,10 @@ __device__ __forceinline__ uint32_t q8_quantize_lanes32(float v, float* d_out, i
 
 // A lane quad quantizes one 32-value block to q8 {d, qsum, qs[32]}
 // (ft-core/src/q4_0.rs:62-78; the same arithmetic as q8_quantize_half): lane
-// part (0..3) owns values 8*part..8*part+7 and writes output words 2+2*part
-// and 3+2*part; part 0 also writes d and qsum. All four lanes must be active.
-__device__ __forceinline__ void quantize_block_quad(const float* v, int part, uint32_t* out) {
-    const float4 a = reinterpret_cast<const float4*>(v)[2 * part];
-    const float4 b = reinterpret_cast<const float4*>(v)[2 * part + 1];
+// part (0..3) owns values 8*part..8*part+7 (a, b) and writes output words
+// 2+2*part and 3+2*part; part 0 also writes d and qsum. All four lanes must be
+// active.
+__device__ __forceinline__ void quantize_block_quad_v(const float4 a, const float4 b, int part, uint32_t* out) {
     const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
     float amax = 0.0f;
 #pragma unroll
@@ -210,6 +209,12 @@ __device__ __forceinline__ void quantize_block_quad(const float* v, int part, ui
         out[0] = __float_as_uint(d);
         out[1] = (uint32_t)qsum;
     }
+}
+
+// The same, with the lane's 8 values read from the block at v.
+__device__ __forceinline__ void quantize_block_quad(const float* v, int part, uint32_t* out) {
+    const float4* v4 = reinterpret_cast<const float4*>(v);
+    quantize_block_quad_v(v4[2 * part], v4[2 * part + 1], part, out);
 }
 
 // Router order as one unsigned compare: a larger key sorts first. Monotone

@@ -282,31 +282,38 @@ struct HeadArgs {
 // from 0.0f), each logit (groups in order from 0.0f, times the input norm's
 // scale when on, then + bias) into sv, the norm's scale into *irs, and the
 // q8 row of x_s into lds (4 lanes per block): k_route_prep's arithmetic, so
-// its bits. Barriers inside; sv, lds and *irs are read after it returns.
-__device__ __forceinline__ void head_prologue(const HeadArgs& h, int s, int H, int E, float* sv, int* lds, float* hg,
-                                              float* irs) {
+// its bits. The seq's partials are copied to hp (LDS, H/16 * (E+1) floats)
+// with the thread's first q8 quad of x loaded alongside, so the prologue costs
+// one load latency. Barriers inside; sv, lds and *irs are read after it
+// returns.
+__device__ __forceinline__ void head_prologue(const HeadArgs& h, int s, int H, int E, float* sv, int* lds, float* hp,
+                                              float* hg, float* irs) {
     const int t = threadIdx.x, nt = blockDim.x;
-    const int nch = H >> 4, C = H >> 7, EP = E + 1;
-    const float* ps = h.part + (int64_t)s * nch * EP;
+    const int nch = H >> 4, C = H >> 7, EP = E + 1, nb = H >> 5;
+    const float* xs = h.x + (int64_t)s * H;
+    float4 xa = make_float4(0.f, 0.f, 0.f, 0.f), xb = xa;
+    if (t < 4 * nb) {
+        const float4* v = reinterpret_cast<const float4*>(xs + 32 * (t >> 2));
+        xa = v[2 * (t & 3)];
+        xb = v[2 * (t & 3) + 1];
+    }
+    stage_words(reinterpret_cast<const int*>(h.part + (int64_t)s * nch * EP), nch * EP,
+                reinterpret_cast<int*>(hp));
+    for (int q = t; q < 4 * nb; q += nt) {  // whole quads: nt and 4*nb are multiples of 4
+        if (q != t) {
+            const float4* v = reinterpret_cast<const float4*>(xs + 32 * (q >> 2));
+            xa = v[2 * (q & 3)];
+            xb = v[2 * (q & 3) + 1];
+        }
+        quantize_block_quad_v(xa, xb, q & 3, reinterpret_cast<uint32_t*>(lds + (q >> 2) * 10));
+    }
     for (int q = t; q < 8 * EP; q += nt) {
         const int e = q >> 3, g = q & 7;
-        const float* p = ps + (int64_t)g * C * EP + e;
+        const float* p = hp + g * C * EP + e;
         float acc = 0.0f;
-        int c = 0;
-        for (; c + 8 <= C; c += 8) {  // eight loads issued ahead of their adds
-            float v[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = p[(int64_t)(c + j) * EP];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc = acc + v[j];
-        }
-        for (; c < C; ++c) acc = acc + p[(int64_t)c * EP];
+        for (int c = 0; c < C; ++c) acc = acc + p[c * EP];
         hg[q] = acc;
     }
-    const float* xs = h.x + (int64_t)s * H;
-    const int nb = H >> 5;
-    for (int q = t; q < 4 * nb; q += nt)  // whole quads: nt and 4*nb are multiples of 4
-        quantize_block_quad(xs + 32 * (q >> 2), q & 3, reinterpret_cast<uint32_t*>(lds + (q >> 2) * 10));
     __syncthreads();
     float ir = 1.0f;
     if (h.norm) {
@@ -342,7 +349,8 @@ __device__ __forceinline__ void head_prologue(const HeadArgs& h, int s, int H, i
 //
 // HEAD (with TOPK): the logits, the input norm's scale and q8(x_s) come from
 // head_prologue (HeadArgs: the previous layer's down launch left the router
-// partials) instead of logits, in_scale and a.q8.
+// partials) instead of logits, in_scale and a.q8; the dynamic LDS then holds
+// the q8 row and, after it, the seq's partials (H/16 * (E+1) floats).
 template <int LAYOUT, bool TOPK, int LPR = 8, bool HEAD = false>
 __global__ __launch_bounds__(64 * LPR, 24 / LPR) void k_gemv_gu_act(GemvArgs a, int inter, uint8_t* q8a,
                                                                   const float* in_scale, int div, const float* logits,
@@ -360,7 +368,7 @@ __global__ __launch_bounds__(64 * LPR, 24 / LPR) void k_gemv_gu_act(GemvArgs a, 
     __shared__ float irs;
     const int s = e / div;
     if constexpr (HEAD) {
-        head_prologue(h, s, a.k, E, sv, lds, hg, &irs);
+        head_prologue(h, s, a.k, E, sv, lds, reinterpret_cast<float*>(lds + (a.k >> 5) * 10), hg, &irs);
     } else {
         if (TOPK && t < E) sv[t] = logits[(int64_t)s * E + t];
         stage_q8(a, e, lds);  // its barrier also covers sv
@@ -1364,11 +1372,12 @@ static int down_lanes(int64_t inter, int64_t top_k) { return inter / 32 >= 256 &
 
 // Whether a stack of layers can take each layer's head from the previous
 // layer's down launch (k_gemv_down_head, then k_gemv_gu_act<HEAD>): the top-k
-// runs in the gate|up launch, the down launch is the combined one, and
-// 16 rows of every pair (16*k*lanes threads) plus the E+1 partials fit one
-// workgroup.
-static bool head_fold_ok(int64_t inter, int64_t n_experts, int64_t top_k) {
+// runs in the gate|up launch, the down launch is the combined one, 16 rows
+// of every pair (16*k*lanes threads) plus the E+1 partials fit one
+// workgroup, and the gate|up launch's q8 row and partials fit 32 KB of LDS.
+static bool head_fold_ok(int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k) {
     if (n_experts > 256 || 32 % top_k || top_k * (inter / 32) * Q8_BLK > 64 * 1024) return false;
+    if ((hidden / 32) * Q8_BLK + (hidden / 16) * (n_experts + 1) * 4 > 32 * 1024) return false;  // the gate|up LDS
     const int64_t nt = 16 * top_k * down_lanes(inter, top_k);
     return nt >= 256 && nt <= 1024 && n_experts < nt;
 }
@@ -1417,7 +1426,7 @@ static int moe_layer_impl(const char* nm, ft_hip_ctx* ctx, void* stream, const f
     if (n_seqs == 0) return FT_HIP_OK;
     int rc;
     const float* inv = ctx->input_norm ? w.inv : nullptr;
-    if ((part_in || wnext) && !head_fold_ok(inter, n_experts, top_k))
+    if ((part_in || wnext) && !head_fold_ok(hidden, inter, n_experts, top_k))
         return fail(FT_HIP_E_SHAPE, "%s: this shape cannot take the layer head from the down launch", nm);
     if (part_in) {
         // the head was computed by the previous layer's down launch
@@ -1455,7 +1464,8 @@ static int moe_layer_impl(const char* nm, ft_hip_ctx* ctx, void* stream, const f
         const HeadArgs h{x, part_in, router_bias, ctx->input_norm};
         auto kern = layout == FT_LAYOUT_Q4R ? k_gemv_gu_act<FT_LAYOUT_Q4R, true, GU_LANES, true>
                                             : k_gemv_gu_act<FT_LAYOUT_Q4_0, true, GU_LANES, true>;
-        hipLaunchKernelGGL(kern, g_gu, dim3(64 * GU_LANES), l_gu, S(stream), a, (int)inter, w.q8a,
+        const size_t l_head = l_gu + (size_t)(hidden / 16) * (n_experts + 1) * 4;
+        hipLaunchKernelGGL(kern, g_gu, dim3(64 * GU_LANES), l_head, S(stream), a, (int)inter, w.q8a,
                            (const float*)nullptr, (int)top_k, (const float*)nullptr, expert_scale, ids, wts,
                            (int)n_experts, h);
     } else {
@@ -1584,7 +1594,7 @@ extern "C" int ft_hip_moe_stack(ft_hip_ctx* ctx, void* stream, const float* x_in
     if (workspace_bytes < sw.bytes)
         return fail(FT_HIP_E_SHAPE, "%s: workspace_bytes=%zu < %zu", nm, workspace_bytes, sw.bytes);
     if (n_seqs == 0) return FT_HIP_OK;
-    const bool fold = head_fold_ok(inter, n_experts, top_k);
+    const bool fold = head_fold_ok(hidden, inter, n_experts, top_k);
     const int64_t per = n_seqs * top_k;
     for (int64_t l = 0; l < n_layers; ++l) {
         const float* xl = l == 0 ? x_in : sw.state[(l - 1) & 1];
