@@ -212,21 +212,63 @@ __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t* ids, int P,
     }
 }
 
+// The pairs p < P routed to expert e (ids[p] == e), ascending, into lst
+// (LDS, at most SCAN_MAX); returns their count (the same in every thread).
+// Lets a layer whose experts all take the dot4 kernels skip the grouping
+// launch: each (tile, expert) workgroup finds its expert's pairs itself.
+constexpr int SCAN_MAX = 1024;
+__device__ __forceinline__ int scan_pairs(const int32_t* ids, int P, int e, int* lst, int* wcnt) {
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    int total = 0;
+    for (int base = 0; base < P; base += GT) {
+        const int p = base + t;
+        const bool m = p < P && ids[p] == e;
+        const uint64_t bal = __ballot(m);
+        if (lane == 0) wcnt[wv] = __popcll(bal);
+        __syncthreads();
+        int off = total, sum = 0;
+#pragma unroll
+        for (int q = 0; q < GW; ++q) {
+            off += q < wv ? wcnt[q] : 0;
+            sum += wcnt[q];
+        }
+        if (m) lst[off + __popcll(bal & ((1ull << lane) - 1))] = p;
+        total += sum;
+        __syncthreads();  // wcnt is rewritten in the next round
+    }
+    return total;
+}
+
 // Gate|up tile j of active expert g for all of its tokens, then GELU*up and
 // the q8 of act block j per token. BPW = H/32/8 blocks per wave. in_scale
 // (input RMS norm, or null): a token's gate|up sums are first multiplied by
-// in_scale[token].
-template <int BPW, bool REC>
+// in_scale[token]. SCAN: the grid's y is the expert, whose pairs the
+// workgroup finds in ids[0..P) (scan_pairs) instead of the group list.
+template <int BPW, bool REC, bool SCAN>
 __global__ __launch_bounds__(GT, 2) void k_grouped_gu(const uint8_t* bank, int64_t expert_bytes, const int32_t* meta,
                                                       const int32_t* plist, const uint8_t* q8x, uint8_t* q8a,
                                                       float* dbg_gu, const float* in_scale, int H, int I, int E,
-                                                      int K, int n_mfma, int32_t* rec) {
+                                                      int K, int n_mfma, int32_t* rec, const int32_t* ids, int P) {
     extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ int slst[SCAN ? SCAN_MAX : 1];
+    __shared__ int wcnt[GW];
     const int nb = H >> 5, nbj = I >> 5;
-    const int j = blockIdx.x, g = blockIdx.y + meta[1 + 3 * E];  // after the MFMA kernels' groups
-    if (g >= meta[0]) return;
-    const int e = meta[1 + g], s0 = meta[1 + E + g], n = meta[1 + 2 * E + g];
-    if (n >= n_mfma) return;
+    const int j = blockIdx.x;
+    int e, n;
+    const int32_t* lst;
+    if constexpr (SCAN) {
+        e = blockIdx.y;
+        n = scan_pairs(ids, P, e, slst, wcnt);
+        if (n == 0) return;
+        lst = slst;
+    } else {
+        const int g = blockIdx.y + meta[1 + 3 * E];  // after the MFMA kernels' groups
+        if (g >= meta[0]) return;
+        e = meta[1 + g];
+        n = meta[1 + 2 * E + g];
+        if (n >= n_mfma) return;
+        lst = plist + meta[1 + E + g];
+    }
     // LDS: x q8 of NT tokens as [NT][nb][8 words] qs + [NT][nb] (d, qsum) pairs;
     // wave partial sums [GW][NT][64]; row sums [NT][64]; act [NT][32]
     uint4* xq = reinterpret_cast<uint4*>(lds);
@@ -249,7 +291,7 @@ __global__ __launch_bounds__(GT, 2) void k_grouped_gu(const uint8_t* bank, int64
     for (int c0 = 0; c0 < n; c0 += NT) {
         const int nt = min(NT, n - c0);
         __syncthreads();  // the previous chunk's LDS is consumed
-        if (t < nt) ctok[t] = plist[s0 + c0 + t] / K;
+        if (t < nt) ctok[t] = lst[c0 + t] / K;
         __syncthreads();
         {  // x q8 of this chunk's tokens: every load issued before the first store
             constexpr int W = 80 * BPW;  // q8 words per token (nb = 8 * BPW blocks of 10)
@@ -301,7 +343,7 @@ __global__ __launch_bounds__(GT, 2) void k_grouped_gu(const uint8_t* bank, int64
                 acc = fmaf((float)dot, h2f((uint16_t)sc[i]) * __int_as_float(dq.x), acc);
                 if constexpr (REC) {  // test record: the block's int32 dot
                     const int row = r < 32 ? j * 32 + r : I + j * 32 + (r - 32);
-                    rec[((int64_t)plist[s0 + c0 + tt] * 2 * I + row) * nb + b0 + i] = dot;
+                    rec[((int64_t)lst[c0 + tt] * 2 * I + row) * nb + b0 + i] = dot;
                 }
             }
             red[(wave * NT + tt) * 64 + r] = acc;
@@ -312,10 +354,10 @@ __global__ __launch_bounds__(GT, 2) void k_grouped_gu(const uint8_t* bank, int64
             float sv = 0.0f;
 #pragma unroll
             for (int v = 0; v < GW; ++v) sv = sv + red[(v * NT + tt) * 64 + rr];
-            if (in_scale) sv = sv * in_scale[plist[s0 + c0 + tt] / K];
+            if (in_scale) sv = sv * in_scale[lst[c0 + tt] / K];
             rows[tt * 64 + rr] = sv;
             if (dbg_gu) {
-                const int p = plist[s0 + c0 + tt];
+                const int p = lst[c0 + tt];
                 const int row = rr < 32 ? j * 32 + rr : I + j * 32 + (rr - 32);
                 dbg_gu[(int64_t)p * 2 * I + row] = sv;
             }
@@ -330,7 +372,7 @@ __global__ __launch_bounds__(GT, 2) void k_grouped_gu(const uint8_t* bank, int64
         __syncthreads();
         for (int i = t; i < nt * 10; i += GT) {
             const int tt = i / 10, wd = i - tt * 10;
-            const int p = plist[s0 + c0 + tt];
+            const int p = lst[c0 + tt];
             reinterpret_cast<uint32_t*>(q8a + ((int64_t)p * nbj + j) * Q8_BLK)[wd] = ablk[tt * 10 + wd];
         }
     }
@@ -338,16 +380,32 @@ __global__ __launch_bounds__(GT, 2) void k_grouped_gu(const uint8_t* bank, int64
 
 // Down rows 128u..128u+127 of active expert g (one 16-row tile per wave;
 // thread (rr, s4) holds row rr's blocks s4, s4+4, ...) for all of its tokens.
-template <int DB, bool REC>
+// SCAN: as k_grouped_gu's.
+template <int DB, bool REC, bool SCAN>
 __global__ __launch_bounds__(GT, 1) void k_grouped_down(const uint8_t* bank, int64_t expert_bytes, int64_t gu_bytes,
                                                         const int32_t* meta, const int32_t* plist, const uint8_t* q8a,
-                                                        float* ydn, int H, int I, int E, int n_mfma, int32_t* rec) {
+                                                        float* ydn, int H, int I, int E, int n_mfma, int32_t* rec,
+                                                        const int32_t* ids, int P) {
     extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ int slst[SCAN ? SCAN_MAX : 1];
+    __shared__ int wcnt[GW];
     const int nbj = I >> 5;
-    const int u = blockIdx.x, g = blockIdx.y + meta[1 + 3 * E];  // after the MFMA kernels' groups
-    if (g >= meta[0]) return;
-    const int e = meta[1 + g], s0 = meta[1 + E + g], n = meta[1 + 2 * E + g];
-    if (n >= n_mfma) return;
+    const int u = blockIdx.x;
+    int e, n;
+    const int32_t* lst;
+    if constexpr (SCAN) {
+        e = blockIdx.y;
+        n = scan_pairs(ids, P, e, slst, wcnt);
+        if (n == 0) return;
+        lst = slst;
+    } else {
+        const int g = blockIdx.y + meta[1 + 3 * E];  // after the MFMA kernels' groups
+        if (g >= meta[0]) return;
+        e = meta[1 + g];
+        n = meta[1 + 2 * E + g];
+        if (n >= n_mfma) return;
+        lst = plist + meta[1 + E + g];
+    }
     uint4* aq = reinterpret_cast<uint4*>(lds);                  // [NTD][nbj][2 uint4]
     int2* ap = reinterpret_cast<int2*>(lds + NTD * nbj * 32);   // [NTD][nbj]
     const int t = threadIdx.x, wave = t >> 6, s4 = t & 3, rr = (t >> 2) & 15;
@@ -374,7 +432,7 @@ __global__ __launch_bounds__(GT, 1) void k_grouped_down(const uint8_t* bank, int
             nt * nbj * 10,
             [&](int i) {
                 const int tt = i / (nbj * 10), rem = i - tt * nbj * 10;
-                const int p = plist[s0 + c0 + tt];
+                const int p = lst[c0 + tt];
                 return reinterpret_cast<const uint32_t*>(q8a + (int64_t)p * nbj * Q8_BLK)[rem];
             },
             [&](int i, uint32_t v) {
@@ -395,13 +453,13 @@ __global__ __launch_bounds__(GT, 1) void k_grouped_down(const uint8_t* bank, int
                 acc = b < nbj ? acc + v : acc;
                 if constexpr (REC) {  // test record: the block's int32 dot
                     if (b < nbj)
-                        rec[((int64_t)plist[s0 + c0 + tt] * H + u * DU + wave * 16 + rr) * nbj + b] = dot;
+                        rec[((int64_t)lst[c0 + tt] * H + u * DU + wave * 16 + rr) * nbj + b] = dot;
                 }
             }
             acc += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(acc), 0xB1, 0xF, 0xF, false));
             acc += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(acc), 0x4E, 0xF, 0xF, false));
             if (s4 == 0) {
-                const int p = plist[s0 + c0 + tt];
+                const int p = lst[c0 + tt];
                 ydn[(int64_t)p * H + u * DU + wave * 16 + rr] = acc;
             }
         }
@@ -902,10 +960,15 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
     int n_mfma = ctx->grouped_mfma_min;
     if (n_mfma <= 0) n_mfma = (int64_t)P >= 8 * n_experts ? 1 : std::numeric_limits<int>::max();
     if (nbj > 32) n_mfma = 1;
-    hipLaunchKernelGGL(topk_in ? k_group_pairs<true> : k_group_pairs<false>, dim3(1), dim3(1024), 0, s,
-                       (const int32_t*)ids, P, E, n_mfma, w.meta, w.plist, w.ppos, (const float*)w.logits, expert_scale,
-                       ids, wts, K);
-    if ((rc = launch_status("moe_layer_grouped/group"))) return rc;
+    // every expert on the dot4 kernels, routing already in ids: the dot4
+    // workgroups find their expert's pairs themselves (no grouping launch)
+    const bool scan = !topk_in && n_mfma > P && P <= SCAN_MAX;
+    if (!scan) {
+        hipLaunchKernelGGL(topk_in ? k_group_pairs<true> : k_group_pairs<false>, dim3(1), dim3(1024), 0, s,
+                           (const int32_t*)ids, P, E, n_mfma, w.meta, w.plist, w.ppos, (const float*)w.logits,
+                           expert_scale, ids, wts, K);
+        if ((rc = launch_status("moe_layer_grouped/group"))) return rc;
+    }
     const int gmax = std::min(E, P);
     const int gbig = std::min(gmax, n_mfma > P ? 0 : P / n_mfma);  // at most this many groups of >= n_mfma tokens
     const bool dot4 = n_mfma > 1, mfma = n_seqs >= n_mfma;
@@ -917,10 +980,13 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
     const bool rec = rgu && rdn;
     if (dot4) {
         const size_t lds_gu = (size_t)NT * nb * 40 + sizeof(float) * (GW * NT * 64 + NT * 64 + NT * 32) + 4 * NT * 10;
-        auto kern = H == 2816 ? (rec ? k_grouped_gu<11, true> : k_grouped_gu<11, false>)
-                              : (rec ? k_grouped_gu<16, true> : k_grouped_gu<16, false>);
-        hipLaunchKernelGGL(kern, dim3(nbj, gmax), dim3(GT), lds_gu, s, (const uint8_t*)bank, eb, (const int32_t*)w.meta,
-                           (const int32_t*)w.plist, (const uint8_t*)w.q8x, w.q8a, dbg_gu, inv, H, I, E, K, n_mfma, rgu);
+        auto kern = scan ? (H == 2816 ? (rec ? k_grouped_gu<11, true, true> : k_grouped_gu<11, false, true>)
+                                      : (rec ? k_grouped_gu<16, true, true> : k_grouped_gu<16, false, true>))
+                         : (H == 2816 ? (rec ? k_grouped_gu<11, true, false> : k_grouped_gu<11, false, false>)
+                                      : (rec ? k_grouped_gu<16, true, false> : k_grouped_gu<16, false, false>));
+        hipLaunchKernelGGL(kern, dim3(nbj, scan ? E : gmax), dim3(GT), lds_gu, s, (const uint8_t*)bank, eb,
+                           (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8x, w.q8a, dbg_gu, inv, H,
+                           I, E, K, n_mfma, rgu, (const int32_t*)ids, P);
         if ((rc = launch_status("moe_layer_grouped/gate_up"))) return rc;
     }
     if (mfma) {
@@ -937,11 +1003,13 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
         return fail(FT_HIP_E_LAUNCH, "%s: debug copy failed", nm);
     if (dot4) {
         const size_t lds_dn = (size_t)NTD * nbj * 40;
-        auto kern = nbj <= 24 ? (rec ? k_grouped_down<6, true> : k_grouped_down<6, false>)
-                              : (rec ? k_grouped_down<8, true> : k_grouped_down<8, false>);
-        hipLaunchKernelGGL(kern, dim3(H / DU, gmax), dim3(GT), lds_dn, s, (const uint8_t*)bank, eb, gu_bytes,
+        auto kern = scan ? (nbj <= 24 ? (rec ? k_grouped_down<6, true, true> : k_grouped_down<6, false, true>)
+                                      : (rec ? k_grouped_down<8, true, true> : k_grouped_down<8, false, true>))
+                         : (nbj <= 24 ? (rec ? k_grouped_down<6, true, false> : k_grouped_down<6, false, false>)
+                                      : (rec ? k_grouped_down<8, true, false> : k_grouped_down<8, false, false>));
+        hipLaunchKernelGGL(kern, dim3(H / DU, scan ? E : gmax), dim3(GT), lds_dn, s, (const uint8_t*)bank, eb, gu_bytes,
                            (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8a, w.ydn, H, I, E,
-                           n_mfma, rdn);
+                           n_mfma, rdn, (const int32_t*)ids, P);
         if ((rc = launch_status("moe_layer_grouped/down"))) return rc;
     }
     if (mfma) {
