@@ -1019,10 +1019,11 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
             hipLaunchKernelGGL(kern, dim3(H / (16 * GW * 2), gbig), dim3(GT), lds_md, s, (const uint8_t*)bank, eb,
                                gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8a,
                                q8a_bytes, w.ydn, H, I, E, n_mfma, rdn);
-        } else {  // long rows: DRT tiles per workgroup, 8 K slices of up to 64 blocks
+        } else {  // long rows: DRT tiles per workgroup, 8 K slices of 56 (rows up to 448 blocks) or 64 blocks
             constexpr int DRT = 4;
             const size_t lds_md = (size_t)DRT * nbj * 32 + sizeof(float) * GW * DRT * 16 * MT;
-            auto kern = rec ? k_mfma_down<GW, 64, DRT, 4, true> : k_mfma_down<GW, 64, DRT, 4, false>;
+            auto kern = nbj <= 8 * 56 ? (rec ? k_mfma_down<GW, 56, DRT, 4, true> : k_mfma_down<GW, 56, DRT, 4, false>)
+                                      : (rec ? k_mfma_down<GW, 64, DRT, 4, true> : k_mfma_down<GW, 64, DRT, 4, false>);
             hipLaunchKernelGGL(kern, dim3(H / (16 * DRT), gbig), dim3(GT), lds_md, s, (const uint8_t*)bank, eb,
                                gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8a,
                                q8a_bytes, w.ydn, H, I, E, n_mfma, rdn);
