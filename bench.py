@@ -41,10 +41,10 @@ HBM_PEAK_GBPS = 8000.0
 MEASURED_TRAFFIC = {
     "gemma30": 974310331,    # k_moe_stack_fused, one launch (algorithmic 846,151,680 B)
     "zipf": 990280985,       # k_moe_stack_fused, one launch
-    "batch16": 7910899312,   # whole step, 30 grouped layers
-    "batch64": 11571032200,  # whole step, 30 grouped layers
-    "large32": 24749522440,  # whole step, 32 grouped layers
-    "large1": 135597620,     # k_gemv_gu_act, one launch (algorithmic 132,120,576 B)
+    "batch16": 7918487317,   # whole step, 30 grouped layers
+    "batch64": 11568345493,  # whole step, 30 grouped layers
+    "large32": 24747104682,  # whole step, 32 grouped layers
+    "large1": 135508959,     # k_gemv_gu_act, one launch (algorithmic 132,120,576 B)
 }
 METRIC = "MoE expert-FFN µs/token at batch 1 + achieved HBM GB/s (% of MI355X peak)"
 # name -> (shape, tokens per step, Zipf exponent of the router bias, BASELINE.json config)
