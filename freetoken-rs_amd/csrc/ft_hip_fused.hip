@@ -825,9 +825,10 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     // This unit's share of its expert, in registers from the load to the dots
     // (a prefetch holds it across the end of the previous layer):
     //   gate|up tile j, 64 rows x BPW blocks per wave: qv (16 B of nibbles per
-    //   row and block), sc (the f16 scale, widened to 32 bits so that loads
-    //   do not pair up and wait for each other);
-    //   down rows 128j + 16*wave + rr, blocks s4, s4+4, ...: dq, dsc.
+    //   row and block), sc (the dword holding the row's f16 scale and its
+    //   neighbour row's);
+    //   down rows 128j + 16*wave + rr, blocks s4, s4+4, ...: dq, dsc (the
+    //   same pairing of scales).
     // Missed tiles (K == 8): the gate|up tile j of a unit group whose held
     // expert was not routed is computed by the 8 units with index j, one wave
     // slice (64 rows x BPW blocks) each, in a wave of theirs otherwise idle
@@ -855,12 +856,16 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         const uint8_t* T = gm ? xb + (int64_t)j * nb * 1152 : P.banks;
         const uint8_t* Ts = T + b0 * 128 + r * 2;
         const uint8_t* Tq = T + nb * 128 + b0 * 1024 + r * 16;
-        // all 16-byte loads first, then the 2-byte scales: interleaving them
-        // more than doubled the time to stream a layer in a probe
+        // all 16-byte loads first, then the scales: interleaving them more
+        // than doubled the time to stream a layer in a probe. A lane loads
+        // the aligned dword holding its row's f16 scale and its neighbour's
+        // (rows r & ~1 and r | 1, one cache line either way) and picks its
+        // half in the dots: a 2-byte load is widened by a separate
+        // instruction, which makes the wave wait for the load at once.
 #pragma unroll
         for (int i = 0; i < BPW; ++i) q[i] = *reinterpret_cast<const uint4*>(Tq + i * 1024);
 #pragma unroll
-        for (int i = 0; i < BPW; ++i) c[i] = *reinterpret_cast<const uint16_t*>(Ts + i * 128);
+        for (int i = 0; i < BPW; ++i) c[i] = *reinterpret_cast<const uint32_t*>(Ts - (r & 1) * 2 + i * 128);
         asm volatile("" ::: "memory");  // issued here, not sunk towards the first use
     };
     auto load_dn = [&](int layer, int eid) __attribute__((always_inline)) {
@@ -877,7 +882,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
 #pragma unroll
         for (int k = 0; k < DB; ++k) {
             const int b = min(s4 + 4 * k, nbj - 1);
-            dsc[k] = *reinterpret_cast<const uint16_t*>(D + b * 32 + rr * 2);
+            dsc[k] = *reinterpret_cast<const uint32_t*>(D + b * 32 + (rr & ~1) * 2);  // rows rr & ~1, rr | 1
         }
         asm volatile("" ::: "memory");
     };
@@ -974,7 +979,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                     const uint4 lo = xq4[(b0 + i) * 2], hi = xq4[(b0 + i) * 2 + 1];
                     const int2 dq8 = xdp[b0 + i];
                     const int diff = block_dot_v(q[i], lo, hi, dq8.y);
-                    acc = fmaf((float)diff, h2f((uint16_t)c[i]) * __int_as_float(dq8.x), acc);
+                    acc = fmaf((float)diff, h2f((uint16_t)(c[i] >> ((r & 1) * 16))) * __int_as_float(dq8.x), acc);
                     if (DBG && P.rec_gu) {  // test record: the block's int32 dot
                         const int row = r < 32 ? j * 32 + r : I + j * 32 + (r - 32);
                         P.rec_gu[(((int64_t)l * K + slot) * 2 * I + row) * nb + b0 + i] = diff;
@@ -1042,7 +1047,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
 #pragma unroll
             for (int k = 0; k < DB; ++k) {
                 const int dot = block_dot_v(dq[k], alo[k], ahi[k], ap[k].y);
-                const float v = (float)dot * (h2f((uint16_t)dsc[k]) * __int_as_float(ap[k].x));
+                const float v = (float)dot * (h2f((uint16_t)(dsc[k] >> ((rr & 1) * 16))) * __int_as_float(ap[k].x));
                 acc = s4o + 4 * k < nbj ? acc + v : acc;
                 if (DBG && P.rec_dn && s4o + 4 * k < nbj)  // test record: the block's int32 dot
                     P.rec_dn[(((int64_t)l * K + p) * H + j * DN_UNIT + wave * DN_ROWS + rr) * nbj + s4o + 4 * k] = dot;
