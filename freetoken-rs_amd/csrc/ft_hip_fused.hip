@@ -124,6 +124,11 @@ struct alignas(16) Misc {       // placed 16-byte aligned
     int abort_flag;
     float inv_r;                // the input RMS norm's scale of the current layer (1 without the norm)
     uint64_t exp2[32];          // libm::exp2_table() for the routing weights' expf
+    // expert units' routing (route_units)
+    alignas(16) uint64_t cand[64];  // rank keys of the 8 best logits of each 16
+    int slotheld[MAX_K];        // 1: routed slot s runs on the unit group holding its expert
+    int freeslot[MAX_K];        // the routed slots no unit group holds, ascending
+    int ufor[MAX_K];            // the slot unit group u runs
 };
 
 // The expf table read from the copy in LDS.
@@ -404,22 +409,120 @@ __device__ __forceinline__ int unit_slot(const Misc* m, int K, int u, bool first
     return fr ? (int)__builtin_ctz(fr) : 0;
 }
 
-// Expert units, wave 0, after route_rank: the unit groups whose held expert
-// was not routed (every group when `first`), ascending, with the expert each
-// runs instead, into m->mlist / m->mexp / m->mcount. The caller synchronizes.
-__device__ __forceinline__ void miss_list(Misc* m, int K, bool first) {
-    const int t = tid_here();
-    if (t >= 64) return;
-    const bool mis = t < K && (first || m->uslot[t] < 0);
-    const uint64_t mm = __ballot(mis);
-    if (mis) {
-        const int mi = __popcll(mm & ((1ull << t) - 1));
-        const int sl = unit_slot(m, K, t, first);
-        m->mlist[mi] = t;
-        m->mexp[mi] = m->sel_i[sl];
-        m->mslot[mi] = sl;
+// Routing of the expert units (the top-K ids, the slot of every unit group
+// and the missed unit groups; no logits or weights, which only the group
+// units need), with the same results as route_rank and unit_slot's rule:
+//   logits as route_rank's (R-order group sums from 0.0f, times inv_r, +
+//   bias_t), one rank key each (threads < 128);
+//   top-K by a two-stage tournament on the keys (distinct: the index is in
+//   the low word): each wavefront ranks 16 keys among themselves (four lanes
+//   per key) and keeps its 8 best as candidates; every global top-8 key is a
+//   candidate, and its rank among the 64 candidates is its global rank
+//   (eight lanes per candidate). A routed expert held by unit group u gives
+//   uslot[u] and marks its slot held;
+//   wavefront 0, lane u < K: a unit group whose held expert was not routed
+//   (a miss; every group when held is null) takes the r-th routed slot no
+//   group holds, r = its rank among the missed groups, ascending: ufor[u],
+//   mlist/mexp/mslot/mcount. Ends with a barrier.
+__device__ __forceinline__ void route_units(const FusedParams& P, Misc* m, const float* gs, float bias_t,
+                                            const int* held) {
+    static_assert(NGROUP == 8 && MAX_E == 128 && MAX_K == 8 && FT_THREADS == 512, "the layouts below assume these");
+    const int E = P.E, K = P.K, t = tid_here();
+    if (t < MAX_E) {  // whole wavefronts
+        float ir = 1.0f;
+        if (P.input_norm) {
+            const float4 a = reinterpret_cast<const float4*>(gs + E * NGROUP)[0];
+            const float4 b = reinterpret_cast<const float4*>(gs + E * NGROUP)[1];
+            const float gv[NGROUP] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            float ss = 0.0f;
+#pragma unroll
+            for (int g = 0; g < NGROUP; ++g) ss = ss + gv[g];
+            ir = 1.0f / sqrtf(ss / (float)P.H + 1e-6f);  // correctly rounded (HIP default)
+        }
+        uint64_t key = 0xFFFFFFFFu - (uint32_t)t;  // indices >= E: distinct, below every real key
+        if (t < E) {
+            const float4 a = reinterpret_cast<const float4*>(gs + t * NGROUP)[0];
+            const float4 b = reinterpret_cast<const float4*>(gs + t * NGROUP)[1];
+            const float gv[NGROUP] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            float total = 0.0f;
+#pragma unroll
+            for (int g = 0; g < NGROUP; ++g) total = total + gv[g];
+            total = total * ir;
+            if (P.bias) total = total + bias_t;
+            key = rank_key(total, t);
+        }
+        m->keys[t] = key;
+        if (t == 0) m->inv_r = ir;
     }
-    if (t == 0) m->mcount = __popcll(mm);
+    if (t < MAX_K) {
+        m->uslot[t] = -1;
+        m->slotheld[t] = 0;
+    }
+    __syncthreads();
+    {  // stage 1: wavefront w, keys 16w..16w+15; lane (i, part) against keys 16w+4part..+3
+        const int w = t >> 6, l = t & 63, part = l & 3;
+        const int i = 16 * w + (l >> 2);
+        const uint64_t ki = m->keys[i];
+        const uint4* kk = reinterpret_cast<const uint4*>(m->keys + 16 * w + 4 * part);
+        const uint4 a = kk[0], b = kk[1];
+        int lr = (int)((((uint64_t)a.y << 32) | a.x) > ki) + (int)((((uint64_t)a.w << 32) | a.z) > ki) +
+                 (int)((((uint64_t)b.y << 32) | b.x) > ki) + (int)((((uint64_t)b.w << 32) | b.z) > ki);
+        lr += quad_xor1i(lr);
+        lr += quad_xor2i(lr);
+        if (part == 0 && lr < 8) m->cand[8 * w + lr] = ki;
+    }
+    __syncthreads();
+    {  // stage 2: candidate c = t/8 against candidates 8p..8p+7 (p = t%8)
+        const int c = t >> 3, pp = t & 7;
+        const uint64_t kc = m->cand[c];
+        const uint4* kk = reinterpret_cast<const uint4*>(m->cand + 8 * pp);
+        int4 h0 = make_int4(-1, -1, -1, -1), h1 = h0;
+        if (held) {  // issued with the candidate reads
+            h0 = reinterpret_cast<const int4*>(held)[0];
+            h1 = reinterpret_cast<const int4*>(held)[1];
+        }
+        int rk = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint4 v = kk[j];
+            rk += (int)((((uint64_t)v.y << 32) | v.x) > kc) + (int)((((uint64_t)v.w << 32) | v.z) > kc);
+        }
+        rk += quad_xor1i(rk);
+        rk += quad_xor2i(rk);
+        rk += __shfl_xor(rk, 4);
+        if (pp == 0 && rk < K) {  // ranks are distinct: each slot written once
+            const int i = (int)(0xFFFFFFFFu - (uint32_t)kc);
+            m->sel_i[rk] = i;
+            const int hv[MAX_K] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+            for (int u = 0; u < MAX_K; ++u)
+                if (u < K && hv[u] == i) {  // held experts are distinct
+                    m->uslot[u] = rk;
+                    m->slotheld[rk] = 1;
+                }
+        }
+    }
+    __syncthreads();
+    if (t < 64) {  // wavefront 0: lane u is unit group u and also routed slot u
+        const bool v8 = t < K;
+        const int us = v8 ? m->uslot[t] : 0;
+        const int hs = v8 ? m->slotheld[t] : 1;
+        const uint64_t missm = __ballot(v8 && us < 0);
+        const uint64_t freem = __ballot(v8 && hs == 0);
+        if (v8 && hs == 0) m->freeslot[__builtin_amdgcn_mbcnt_lo((uint32_t)freem, 0)] = t;
+        // (lanes of one wavefront: its LDS accesses complete in program order)
+        int slot = us;
+        if (v8 && us < 0) {
+            const int r = __builtin_amdgcn_mbcnt_lo((uint32_t)missm, 0);  // missed groups below u
+            slot = m->freeslot[r];
+            m->mlist[r] = t;
+            m->mslot[r] = slot;
+            m->mexp[r] = m->sel_i[slot];
+        }
+        if (v8) m->ufor[t] = slot;
+        if (t == 0) m->mcount = __popcll(missm);
+    }
+    __syncthreads();
 }
 
 // Group and pred units, wave 0, after route_rank: softmax over the chosen in
@@ -820,7 +923,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         trace_value<DBG>(P, -1, 28, xcc_id());
     }
     stamp<DBG>(P, -1, 12);
-    route_rank(P, m, reinterpret_cast<const float*>(gq), bias_n, -1, nullptr);
+    route_units(P, m, reinterpret_cast<const float*>(gq), bias_n, nullptr);
 
     // This unit's share of its expert, in registers from the load to the dots
     // (a prefetch holds it across the end of the previous layer):
@@ -895,9 +998,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     int p = u, eid = 0, hug = 0, hslot = 0;  // hslot: the missed tile's slot (debug records only)
     bool own_miss = true, hm = false;
     auto decide = [&](int layer, bool first) __attribute__((always_inline)) {
-        miss_list(m, K, first);
-        __syncthreads();
-        p = unit_slot(m, K, u, first);
+        p = m->ufor[u];
         // the routed id is in [0, E) by construction; the clamp keeps any
         // future logic error from turning into an out-of-bounds weight read
         eid = min(max(m->sel_i[p], 0), E - 1);
@@ -1082,7 +1183,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         if (!wait_words<DBG, UW_X>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * nq, xidx, tag_g(l + 1), gq, xdst, l, 24))
             return;
         stamp<DBG>(P, l, 12);
-        route_rank(P, m, reinterpret_cast<const float*>(gq), bias_n, -1, pf ? m->pid[(l + 1) & 1] : nullptr);
+        route_units(P, m, reinterpret_cast<const float*>(gq), bias_n, pf ? m->pid[(l + 1) & 1] : nullptr);
         stamp<DBG>(P, l, 13);
         decide(l + 1, !pf);
         trace_value<DBG>(P, l + 1, 10, own_miss ? 1u : 0u);
