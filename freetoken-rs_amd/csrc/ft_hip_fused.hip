@@ -21,7 +21,7 @@
 // stay with the unit group that holds them; only the remaining unit groups
 // load the experts nobody predicted (a miss).
 //
-// Workgroups (G shape: H 2816, I 704, E 128, top-8): 192.
+// Workgroups (G shape: H 2816, I 704, E 128, top-8): 216.
 //   expert unit (u, j), 176 of them, unit group u = w % K, j = w / K:
 //     gate|up : 64 rows (32 gate, 32 up) of its expert for act block j
 //               (32 columns), H/32 blocks held in registers by 8 waves;
@@ -34,20 +34,22 @@
 //     round-robin; each checks this at start through the XCD id register),
 //     so hop A stays in that XCD's L2: plain stores, agent-scope polls.
 //     If the placement check fails, hop A stores write through instead.
-//   group unit g, 8 of them (one per R-order group of H/8 rows):
-//     waits for y of its rows from every routed slot (hop B); x_{l+1} =
-//     x_l + sum_p w_p y_p in routing order; router chunk partials of its
-//     H/128 chunks and their group sum for every expert (layer l+1's router
-//     weights were streamed into registers meanwhile); q8 of its x rows;
-//     publishes group sums + q8 blocks (hop C), double-buffered by parity.
+//   group units (g, s), 4 per R-order group of H/8 rows (32 of them, the
+//     four of group g on XCD g): each waits for y of the group's rows from
+//     every routed slot (hop B); x_{l+1} = x_l + sum_p w_p y_p in routing
+//     order; router chunk partials of the group's H/128 chunks and their
+//     group sum for a quarter of the experts, s*E/4.. (layer l+1's router
+//     weights were streamed into registers meanwhile); split 0 also the q8
+//     of the rows and their sum of squares; publishes them (hop C),
+//     double-buffered by parity.
 //   pred unit g, 8 of them: the same combine of group g's rows, then the
 //     group sums of layer l+2's router over x_{l+1}; the pred units exchange
 //     them, rank them (the same top-k as the true routing) and publish the
 //     predicted experts of layer l+2, one copy per XCD.
 //   every expert and group unit: reads the 8 group sums of every expert
 //     (and, expert units, the 88 q8 blocks of x_{l+1}) (hop C), logits =
-//     sum over groups in order + bias, top-k and softmax, then the
-//     assignment of routed slots to unit groups.
+//     sum over groups in order + bias, top-k (and, group units, softmax),
+//     then the assignment of routed slots to unit groups.
 // Weight layouts are lossless repacks of q4_0 with its byte count.
 
 #include "ft_device.hpp"
@@ -61,7 +63,8 @@ constexpr int FT_THREADS = 512;
 constexpr int FT_WAVES = FT_THREADS / 64;
 constexpr int MAX_K = 8;
 constexpr int MAX_E = 128;      // group partials use four threads per expert
-constexpr int NGROUP = 8;       // R-order groups, one group unit each
+constexpr int NGROUP = 8;       // R-order groups
+constexpr int GSPLIT = 4;       // group units per R-order group, each with E / GSPLIT experts' router sums
 constexpr int DN_ROWS = 16;     // rows per router chunk and per down tile
 constexpr int DN_UNIT = DN_ROWS * FT_WAVES;  // rows per down unit: one tile per wave
 constexpr int POLL_SLEEP = 1;   // s_sleep units (64 clocks) between polls
@@ -553,18 +556,21 @@ __device__ __forceinline__ void route_weights(const FusedParams& P, Misc* m, int
     }
 }
 
-// Router weights of `layer` for group g into registers: thread (e = t/4,
-// q = t%4) holds chunks q, q+4, ... of the group (16 rows each).
-template <int CPT, int C>
-__device__ __forceinline__ void group_load_router(const FusedParams& P, int layer, int g, float4 (&wv)[CPT][4]) {
+// Router weights of `layer` for group g into registers, experts e0.. (LPE
+// threads per expert, FT_THREADS / LPE experts): thread (e = e0 + t/LPE,
+// q = t%LPE) holds chunks q, q+LPE, ... of the group (16 rows each).
+template <int CPT, int C, int LPE>
+__device__ __forceinline__ void group_load_router(const FusedParams& P, int layer, int g, int e0,
+                                                  float4 (&wv)[CPT][4]) {
+    static_assert(CPT * LPE >= C, "every chunk has a thread");
     int t = threadIdx.x;
     asm volatile("" : "+v"(t));  // keeps the per-thread offsets inside the layer loop
     const int E = P.E;
-    const int e = min(t >> 2, E - 1), q = t & 3;
+    const int e = min(e0 + t / LPE, E - 1), q = t % LPE;
     const float* base = P.routers + (int64_t)layer * (P.H / DN_ROWS) * E * DN_ROWS;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-        const int c = min(q + 4 * i, C - 1);
+        const int c = min(q + LPE * i, C - 1);
         const float4* s = reinterpret_cast<const float4*>(base + ((int64_t)(g * C + c) * E + e) * DN_ROWS);
 #pragma unroll
         for (int k = 0; k < 4; ++k) wv[i][k] = s[k];
@@ -575,22 +581,27 @@ __device__ __forceinline__ void group_load_router(const FusedParams& P, int laye
 // the R-order: chunk partials (fma chain over the chunk's 16 rows, from
 // 0.0f), summed over the group's C chunks in order (from 0.0f); and the q8
 // blocks of the rows; and the sum of squares of the rows in the same order
-// (chunk fma chains of x*x). Publishes [E sums][sum of squares][qw q8 words]
-// tagged, to each replica; pred: [E sums][sum of squares] to
-// dst[g * (E + 1) + k] (no q8, one copy).
-template <int CPT, int C, bool DBG>
-__device__ __forceinline__ void group_publish(const FusedParams& P, int g, const float4 (&wv)[CPT][4], const float* gx, float* gp,
-                              uint32_t* q8w, uint64_t* dst, uint32_t tag, int sl, bool pred = false) {
+// (chunk fma chains of x*x). The sums are those of experts e0..e0 +
+// FT_THREADS/LPE - 1 (the router weights group_load_router<CPT, C, LPE>
+// gave); the q8 blocks and the sum of squares only when `primary`.
+// Publishes, tagged, the unit's words of [E sums][sum of squares][qw q8
+// words] into group g's slot of each replica; pred (all E experts):
+// [E sums][sum of squares] to dst[g * (E + 1) + k] (no q8, one copy).
+template <int CPT, int C, int LPE, bool DBG>
+__device__ __forceinline__ void group_publish(const FusedParams& P, int g, int e0, const float4 (&wv)[CPT][4],
+                                              const float* gx, float* gp, uint32_t* q8w, uint64_t* dst, uint32_t tag,
+                                              int sl, bool pred, bool primary) {
+    constexpr int NE = FT_THREADS / LPE;  // experts of this unit
     // E behind an opaque move: the C chunk offsets c*E are formed here, not
     // hoisted to the kernel's start and kept (spilled) for its lifetime
     int E = P.E;
     asm volatile("" : "+s"(E));
     const int t = tid_here();
-    const int e = t >> 2, q = t & 3;
+    const int e = e0 + t / LPE, q = t % LPE;
     if (e < E) {
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
-            const int c = q + 4 * i;
+            const int c = q + LPE * i;
             if (c < C) {
                 const float4* x4 = reinterpret_cast<const float4*>(gx + c * DN_ROWS);
                 float s = 0.0f;
@@ -608,12 +619,12 @@ __device__ __forceinline__ void group_publish(const FusedParams& P, int g, const
     }
     const int nbq = (P.H / NGROUP) >> 5;  // q8 blocks per group; one lane quad each
     float* sq = reinterpret_cast<float*>(q8w + P.qw);  // [C] chunk partials of x*x, then their sum
-    if (!pred && t < 4 * nbq) quantize_block_quad(gx + 32 * (t >> 2), t & 3, q8w + (t >> 2) * 10);
+    if (!pred && primary && t < 4 * nbq) quantize_block_quad(gx + 32 * (t >> 2), t & 3, q8w + (t >> 2) * 10);
     // sum of squares: chunk c on thread SQ0 + c, in the last wavefront (the
     // q8 quads are in the first)
     constexpr int SQ0 = FT_THREADS - 64;
     static_assert(C <= 64, "one thread per chunk");
-    if (t >= SQ0 && t < SQ0 + C) {
+    if (primary && t >= SQ0 && t < SQ0 + C) {
         const int c = t - SQ0;
         const float4* x4 = reinterpret_cast<const float4*>(gx + c * DN_ROWS);
         float s = 0.0f;
@@ -630,16 +641,17 @@ __device__ __forceinline__ void group_publish(const FusedParams& P, int g, const
     stamp<DBG>(P, sl, 20);
     __syncthreads();
     stamp<DBG>(P, sl, 21);
-    if (t < E) {
+    if (t < NE && e0 + t < E) {
+        const int et = e0 + t;
         float pv[C];
 #pragma unroll
-        for (int c = 0; c < C; ++c) pv[c] = gp[c * E + t];
+        for (int c = 0; c < C; ++c) pv[c] = gp[c * E + et];
         float s = 0.0f;
 #pragma unroll
         for (int c = 0; c < C; ++c) s = s + pv[c];
-        gp[C * E + t] = s;
+        gp[C * E + et] = s;
     }
-    if (t == MAX_E) {
+    if (primary && t == MAX_E) {
         float s = 0.0f;
         for (int c = 0; c < C; ++c) s = s + sq[c];
         sq[C] = s;
@@ -653,6 +665,7 @@ __device__ __forceinline__ void group_publish(const FusedParams& P, int g, const
     const int n = E + 1 + P.qw;
     for (int i = t; i < n * NREP; i += FT_THREADS) {
         const int rep = i / n, k = i - rep * n;
+        if (k < E ? (k < e0 || k >= e0 + NE) : !primary) continue;  // another unit's words
         const uint32_t v = k < E ? __float_as_uint(gp[C * E + k]) : (k == E ? __float_as_uint(sq[C]) : q8w[k - E - 1]);
         st_tag(dst + rep * P.rs_gq + (int64_t)g * P.gq_stride + k, tag, v);
     }
@@ -689,7 +702,11 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     constexpr int C = 2 * BPW;  // router chunks per group = H/128
     // words per thread of each wait (H = 256 * BPW, E <= 128, K <= 8):
     constexpr int UW_G = NGROUP * MAX_E / FT_THREADS;                              // group sums (prediction)
-    static_assert((NGROUP - 1) * (MAX_E + 1) <= UW_G * FT_THREADS, "group units poll 7 groups' sums in UW_G rounds");
+    static_assert((NGROUP - 1) * (MAX_E + 1) <= UW_G * FT_THREADS, "pred units poll 7 groups' sums in UW_G rounds");
+    constexpr int UW_GA = (NGROUP * (MAX_E + 1) + FT_THREADS - 1) / FT_THREADS;       // all 8 groups' sums
+    // group units: the experts of one split, LPE threads each
+    constexpr int LPE_G = FT_THREADS / (MAX_E / GSPLIT), CPT_G = (C + LPE_G - 1) / LPE_G;
+    static_assert(CPT_G <= CPT, "a split's router registers fit the pred units' array");
     constexpr int UW_Y = (BPW + 1) / 2;                                            // y of a group's rows
     constexpr int UW_X = (NGROUP * (MAX_E + 1 + 10 * BPW) + FT_THREADS - 1) / FT_THREADS;  // sums + q8 of x
     extern __shared__ __align__(16) uint8_t lds[];
@@ -755,25 +772,36 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         //   pid_t (by parity): rewritten for l+2 after the routing of l+1 from
         //     every group unit (each read pid(l) before publishing it), and so
         //     after every y(l), i.e. after every expert unit took pid(l).
-        const bool pu = w >= P.n_unit + NGROUP;
-        const int g = w - P.n_unit - (pu ? NGROUP : 0), r0 = g * HG;
-        const bool record = !pu && g == 0;  // group unit 0 writes ids/wts
+        // Group units: GSPLIT per group, w - n_unit = sp * NGROUP + g (all on
+        // XCD g); split sp publishes the router sums of experts sp*E/GSPLIT..,
+        // split 0 also the sum of squares and the q8 blocks, and it writes
+        // x_out and the debug records. Every split combines the same rows
+        // bit for bit and computes the same routing.
+        const int ngu = NGROUP * GSPLIT;
+        const bool pu = w >= P.n_unit + ngu;
+        const int gi = w - P.n_unit;
+        const int g = pu ? gi - ngu : gi % NGROUP, r0 = g * HG;
+        const int e0 = pu ? 0 : (gi / NGROUP) * (MAX_E / GSPLIT);  // first expert of this split
+        const bool primary = !pu && gi < NGROUP;
+        const bool record = primary && g == 0;  // writes ids/wts
         auto fail = [&]() __attribute__((always_inline)) {  // a wait gave up: mark the outputs
-            if (!pu) poison_outputs(P, g);
+            if (primary) poison_outputs(P, g);
         };
         if (pu && (!pf || L < 2)) return;    // nothing to predict
         uint32_t* q8w = reinterpret_cast<uint32_t*>(gp + (C + 1) * E);
         float4 wv[CPT][4];
         // Group sums and sums of squares -> LDS [E+1][NGROUP] (row E: the
-        // sums of squares). A unit takes its own group's row from gp
-        // (own_sums, before the wait) and polls the 7 other groups: group
-        // units the broadcast (oidx), pred units the prediction exchange
-        // (opidx), which carries the same sums of squares (both combine the
-        // same x); pred units then poll the broadcast's E sums alone (gidx_e,
-        // into rows < E, keeping row E).
+        // sums of squares). Group units poll every group's row of the
+        // broadcast (aidx; their own group's too, which the other splits
+        // write). Pred units take their own group's row from gp (own_sums,
+        // before the wait) and poll the 7 other groups of the prediction
+        // exchange (opidx), which carries the same sums of squares (both
+        // combine the same x); they then poll the broadcast's E sums alone
+        // (gidx_e, into rows < E, keeping row E).
         const int ES = E + 1;
         auto ogrp = [=](int i) { const int o = i / ES; return o < g ? o : o + 1; };
-        auto oidx = [=](int i) { return (int64_t)ogrp(i) * P.gq_stride + i % ES; };
+        auto aidx = [=](int i) { return (int64_t)(i / ES) * P.gq_stride + i % ES; };
+        auto adst = [=](int i) { return (i % ES) * NGROUP + i / ES; };
         auto opidx = [=](int i) { return (int64_t)ogrp(i) * ES + i % ES; };
         auto odst = [=](int i) { return (i % ES) * NGROUP + ogrp(i); };
         auto gidx_e = [=](int i) { return (int64_t)(i / E) * P.gq_stride + i % E; };
@@ -782,26 +810,31 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
             if (t <= E) gq[t * NGROUP + g] = __float_as_uint(t < E ? gp[C * E + t] : sq[C]);
         };
         auto pdst = [=](int i) { return (i % E) * NGROUP + i / E; };  // E sums of 8 groups -> LDS rows < E
+        // a split's router weights: the first CPT_G rows of wv
+        auto& wvg = reinterpret_cast<float4(&)[CPT_G][4]>(wv);
+        auto load_router = [&](int layer) __attribute__((always_inline)) {
+            if (pu) group_load_router<CPT, C, 4>(P, layer, g, 0, wv);
+            else group_load_router<CPT_G, C, LPE_G>(P, layer, g, e0, wvg);
+        };
         stamp<DBG>(P, -1, 0);
-        group_load_router<CPT, C>(P, pu ? 1 : 0, g, wv);
+        load_router(pu ? 1 : 0);
         float bias_n = ld_bias(P, 0), bias_p = pu ? ld_bias(P, 1) : 0.0f;
         for (int i = t; i < HG; i += FT_THREADS) {
             gx[i] = P.x_in[r0 + i];
-            if (DBG && P.dbg_x && !pu) P.dbg_x[r0 + i] = gx[i];
+            if (DBG && P.dbg_x && primary) P.dbg_x[r0 + i] = gx[i];
         }
         __syncthreads();
         if (pu) {
-            group_publish<CPT, C, DBG>(P, g, wv, gx, gp, q8w, pp_buf(1), tag_g(1), -1, true);
+            group_publish<CPT, C, 4, DBG>(P, g, 0, wv, gx, gp, q8w, pp_buf(1), tag_g(1), -1, true, true);
             own_sums();
             if (!wait_words<DBG, UW_G>(P, m, epoch, pp_buf(1), (NGROUP - 1) * ES, opidx, tag_g(1), gq, odst)) { fail(); return; }
             route_rank(P, m, reinterpret_cast<const float*>(gq), bias_p, 1, nullptr);
             if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * E, gidx_e, tag_g(0), gq, pdst)) { fail(); return; }
             if (t < K) st_tag(pid_buf(1) + g * PID_STRIDE + t, tag_g(1), (uint32_t)m->pid[1][t]);
         } else {
-            group_publish<CPT, C, DBG>(P, g, wv, gx, gp, q8w, gq_buf(0), tag_g(0), -1);
+            group_publish<CPT_G, C, LPE_G, DBG>(P, g, e0, wvg, gx, gp, q8w, gq_buf(0), tag_g(0), -1, false, primary);
             stamp<DBG>(P, -1, 11);
-            own_sums();
-            if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, (NGROUP - 1) * ES, oidx, tag_g(0), gq, odst)) {
+            if (!wait_words<DBG, UW_GA>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * ES, aidx, tag_g(0), gq, adst)) {
                 fail();
                 return;
             }
@@ -816,7 +849,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
             if (pu && l + 2 >= L) return;
             stamp<DBG>(P, l, 0);
             const int rl = pu ? l + 2 : l + 1;  // the router layer applied after this layer's combine
-            if (rl < L) group_load_router<CPT, C>(P, rl, g, wv);
+            if (rl < L) load_router(rl);
             if (l + 1 < L) bias_n = ld_bias(P, l + 1);
             if (pu && l + 2 < L) bias_p = ld_bias(P, l + 2);
             stamp<DBG>(P, l, 1);
@@ -844,7 +877,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                 }
                 const float xn = gx[r] + h;
                 gx[r] = xn;
-                if (!pu) {
+                if (primary) {
                     if (l == L - 1) P.x_out[r0 + r] = xn;
                     if (DBG && P.dbg_x) P.dbg_x[(int64_t)(l + 1) * H + r0 + r] = xn;
                 }
@@ -853,7 +886,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
             stamp<DBG>(P, l, 9);
             if (l + 1 == L) break;
             if (pu) {  // here l + 2 < L
-                group_publish<CPT, C, DBG>(P, g, wv, gx, gp, q8w, pp_buf(l + 2), tag_g(l + 2), l, true);
+                group_publish<CPT, C, 4, DBG>(P, g, 0, wv, gx, gp, q8w, pp_buf(l + 2), tag_g(l + 2), l, true, true);
                 stamp<DBG>(P, l, 11);
                 own_sums();
                 if (!wait_words<DBG, UW_G>(P, m, epoch, pp_buf(l + 2), (NGROUP - 1) * ES, opidx, tag_g(l + 2), gq, odst, l,
@@ -870,11 +903,11 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                 stamp<DBG>(P, l, 12);
                 if (t < K) st_tag(pid_buf(l + 2) + g * PID_STRIDE + t, tag_g(l + 2), (uint32_t)m->pid[l & 1][t]);
             } else {
-                group_publish<CPT, C, DBG>(P, g, wv, gx, gp, q8w, gq_buf(l + 1), tag_g(l + 1), l);
+                group_publish<CPT_G, C, LPE_G, DBG>(P, g, e0, wvg, gx, gp, q8w, gq_buf(l + 1), tag_g(l + 1), l, false,
+                                                    primary);
                 stamp<DBG>(P, l, 11);
-                own_sums();
-                if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, (NGROUP - 1) * ES, oidx, tag_g(l + 1),
-                                           gq, odst, l, 24)) {
+                if (!wait_words<DBG, UW_GA>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * ES, aidx, tag_g(l + 1),
+                                            gq, adst, l, 24)) {
                     fail();
                     return;
                 }
@@ -1300,7 +1333,7 @@ WsLayout ws_layout(int64_t H, int64_t I, int64_t E, int64_t K) {
     w.gq = off; off += 2 * NREP * up(w.rs_gq * 8);
     w.pp = off; off += 2 * up(NGROUP * (E + 1) * 8);
     w.pid = off; off += 2 * up(NGROUP * PID_STRIDE * 8);
-    w.pl = off; off += up(((int64_t)std::max(K * (I / 32), K * (H / DN_UNIT)) + 2 * NGROUP) * 8);
+    w.pl = off; off += up(((int64_t)std::max(K * (I / 32), K * (H / DN_UNIT)) + (GSPLIT + 1) * NGROUP) * 8);
     w.total = off;
     return w;
 }
@@ -1339,7 +1372,7 @@ extern "C" size_t ft_hip_fused_workspace_bytes(int64_t hidden, int64_t inter, in
 extern "C" int ft_hip_fused_workgroups(int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k) {
     if (hidden <= 0 || hidden % 256 || inter <= 0 || inter % 32 || n_experts <= 0 || top_k <= 0) return -1;
     int n_gu, n_dn;
-    return fused_units(hidden, inter, top_k, &n_gu, &n_dn) + 2 * NGROUP;
+    return fused_units(hidden, inter, top_k, &n_gu, &n_dn) + (GSPLIT + 1) * NGROUP;
 }
 
 extern "C" int ft_hip_fused_workspace_init(ft_hip_ctx* ctx, void* stream, void* workspace, size_t workspace_bytes) {
@@ -1417,7 +1450,7 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
     P.K = (int)top_k;
     P.L = (int)n_layers;
     P.n_unit = fused_units(hidden, inter, top_k, &P.n_gu, &P.n_dn);
-    const int nw = P.n_unit + 2 * NGROUP;
+    const int nw = P.n_unit + (GSPLIT + 1) * NGROUP;
     P.gq_stride = wl.gq_stride;
     P.qw = wl.qw;
     P.rs_gq = (wl.rs_gq * 8 + 255) / 256 * 256 / 8;
