@@ -44,7 +44,7 @@ MEASURED_TRAFFIC = {
     "batch16": 7918487317,   # whole step, 30 grouped layers
     "batch64": 11568345493,  # whole step, 30 grouped layers
     "large32": 24747104682,  # whole step, 32 grouped layers
-    "large1": 135508959,     # k_gemv_gu_act, one launch (algorithmic 132,120,576 B)
+    "large1": 132300061,     # k_gemv_gu_long, one launch (algorithmic 132,120,576 B)
 }
 METRIC = "MoE expert-FFN µs/token at batch 1 + achieved HBM GB/s (% of MI355X peak)"
 # name -> (shape, tokens per step, Zipf exponent of the router bias, BASELINE.json config)
@@ -149,8 +149,9 @@ class GraphRunner:
 
 
 def time_dominant_kernel(g, model, reps=3):
-    """Average duration of the layer's gate|up launch (k_gemv_gu_act: the
-    grouped gate|up GEMV with GELU*up and q8, moving 2/3 of the bytes) with
+    """Average duration of the layer's gate|up launch (k_gemv_gu_long for q4r
+    rows of 64 or 128 blocks, else k_gemv_gu_act: the gate|up GEMV with
+    GELU*up and q8, moving 2/3 of the bytes) with
     HIP events on the stream it runs on, rotating over all layers so that no
     layer's bank is cache-resident."""
     import torch
@@ -612,7 +613,8 @@ def main():
         k_name = f"k_moe_stack_fused (whole {model.L}-layer section, one launch per token)"
     elif B == 1:
         k_us, k_bytes = time_dominant_kernel(g, model)
-        k_name = f"k_gemv_gu_act (gate|up GEMV + GELU*up q8, {k} experts)"
+        gu = "k_gemv_gu_long" if model.layout == ft_hip.LAYOUT_Q4R and shape.hidden in (2048, 4096) else "k_gemv_gu_act"
+        k_name = f"{gu} (gate|up GEMV + GELU*up q8, {k} experts)"
     else:  # the step's graph as a whole: its expert bytes over the step time
         k_us, k_bytes = us_step, step_bytes
         k_name = f"whole step ({model.L} {path} layers of {B} tokens in one HIP graph; not a single kernel)"

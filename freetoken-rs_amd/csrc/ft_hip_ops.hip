@@ -521,6 +521,145 @@ __global__ __launch_bounds__(NT) void k_gemv_down_head(GemvArgs a, const float* 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Long rows (q4r, nb = 64*BPL blocks: gate|up rows of 64 or 128 blocks, the
+// large-expert shape's hidden 2048 or 4096): a wavefront owns whole rows, lane l
+// blocks l, l+64, ... of each, so one load instruction of the wave is 1 KB of
+// contiguous qs (and 128 B of scales), every row's loads are issued before
+// any of its dots, and a lane's q8 operands are the same for every row of
+// its entry (held in registers). Per row: acc = fma chain over the lane's
+// blocks in block order, then the 64 lanes summed by an xor tree (32, 16, ...,
+// 1). The int32 block dots are those of every other GEMV; the f32 order is
+// this kernel's own, the same in every launch that uses it.
+// ---------------------------------------------------------------------------
+template <int BPL>
+struct LongRow {
+    uint4 q[BPL];
+    uint32_t s[BPL];  // the aligned dword holding this lane's block scale and the neighbour lane's
+};
+
+template <int BPL>
+__device__ __forceinline__ void long_row_load(const uint8_t* wr, int lane, LongRow<BPL>& r) {
+    constexpr int NB = 64 * BPL, QS_OFF = (NB * 2 + 15) / 16 * 16;
+#pragma unroll
+    for (int i = 0; i < BPL; ++i) r.q[i] = *reinterpret_cast<const uint4*>(wr + QS_OFF + 16 * (lane + 64 * i));
+#pragma unroll
+    for (int i = 0; i < BPL; ++i) r.s[i] = *reinterpret_cast<const uint32_t*>(wr + ((2 * (lane + 64 * i)) & ~3));
+}
+
+// this lane's q8 operand blocks (lane + 64*i) of an activation row in LDS
+template <int BPL>
+struct LongAct {
+    int w[BPL][10];
+};
+template <int BPL>
+__device__ __forceinline__ void long_act_load(const int* lds, int lane, LongAct<BPL>& x) {
+#pragma unroll
+    for (int i = 0; i < BPL; ++i)
+#pragma unroll
+        for (int k = 0; k < 10; ++k) x.w[i][k] = lds[(lane + 64 * i) * 10 + k];
+}
+
+template <int BPL>
+__device__ __forceinline__ float long_row_dot(const LongRow<BPL>& r, const LongAct<BPL>& x, int lane) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < BPL; ++i) {
+        const int diff = block_dot(r.q[i], x.w[i] + 2, x.w[i][1]);
+        const float d4 = h2f((uint16_t)(r.s[i] >> ((lane & 1) * 16)));
+        acc = fmaf((float)diff, d4 * __int_as_float(x.w[i][0]), acc);
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+    return acc;
+}
+
+// k_gemv_gu_act for rows of 64*BPL blocks (q4r): the same work per (act
+// block j, pair) workgroup and the same prologues (logits or head, top-k)
+// and tail (GELU*up, q8). 256 threads: wave w owns gate rows 32j+8w..+7 and
+// up rows I+32j+8w..+7, four rows in flight, a row's slot refilled with the
+// row four later once its dots are done. The activation row's loads go out
+// before the weights' (loads complete in order), their LDS stores after.
+template <bool TOPK, int BPL, bool HEAD = false>
+__global__ __launch_bounds__(256, 4) void k_gemv_gu_long(GemvArgs a, int inter, uint8_t* q8a, const float* in_scale,
+                                                         int div, const float* logits, const float* escale,
+                                                         int32_t* ids, float* wts, int E, HeadArgs h) {
+    static_assert(TOPK || !HEAD, "the head's logits are ranked in the launch");
+    constexpr int RPW = 16, RIF = 4;  // rows per wave, rows in flight
+    extern __shared__ int lds[];
+    __shared__ float gs[64];
+    const int e = blockIdx.y, t = threadIdx.x;
+    __shared__ float sv[TOPK ? 256 : 1], selv[TOPK ? 32 : 1];
+    __shared__ int seli[TOPK ? 32 : 1];
+    __shared__ uint64_t key[TOPK ? 256 : 1];
+    __shared__ float exv[TOPK ? 32 : 1];
+    __shared__ float hg[HEAD ? 8 * 257 : 1];
+    __shared__ float irs;
+    const int s = e / div;
+    const int lane = t & 63, wave = t >> 6;
+    constexpr int RB = (64 * BPL * 2 + 15) / 16 * 16 + 64 * BPL * 16;  // q4r row bytes
+    LongRow<BPL> rr[RIF];
+    const uint8_t* eb = nullptr;
+    auto row_of = [&](int i) { return (i < 8 ? 0 : inter) + (int)blockIdx.x * 32 + 8 * wave + (i & 7); };
+    auto load_row = [&](int i) __attribute__((always_inline)) {
+        long_row_load<BPL>(eb + (int64_t)row_of(i) * RB, lane, rr[i % RIF]);
+    };
+    auto issue = [&](int slot) __attribute__((always_inline)) {
+        eb = a.base + (uint64_t)slot * a.expert_bytes + a.bank_off;
+#pragma unroll
+        for (int i = 0; i < RIF; ++i) load_row(i);
+    };
+    if constexpr (HEAD) {
+        head_prologue(h, s, a.k, E, sv, lds, reinterpret_cast<float*>(lds + (a.k >> 5) * 10), hg, &irs);
+    } else {
+        // the q8 row of x (10 words per block: 64*BPL*10 words, XW per thread)
+        constexpr int XW = (64 * BPL * 10 + 255) / 256;
+        const int nw = (a.k >> 5) * 10;
+        const int* src = reinterpret_cast<const int*>(a.q8 + (int64_t)entry_xrow(a, e) * a.q8_stride_blocks * Q8_BLK);
+        int v[XW];
+#pragma unroll
+        for (int r = 0; r < XW; ++r) v[r] = t + 256 * r < nw ? src[t + 256 * r] : 0;
+        if (TOPK && t < E) sv[t] = logits[(int64_t)s * E + t];
+        if constexpr (!TOPK) issue(a.slots[e]);  // the pair's expert is known: weights behind the q8 row
+#pragma unroll
+        for (int r = 0; r < XW; ++r)
+            if (t + 256 * r < nw) lds[t + 256 * r] = v[r];
+        __syncthreads();
+    }
+    if constexpr (TOPK) {
+        topk_rank_select(sv, E, div, key, selv, seli);
+        if (blockIdx.x == 0 && e == s * div) {  // the seq's writer (uniform per workgroup): the weights too
+            const float w = topk_softmax(selv, seli, div, escale, exv);
+            if (t < div) {
+                ids[(int64_t)s * div + t] = seli[t];
+                wts[(int64_t)s * div + t] = w;
+            }
+        }
+        issue(seli[e - s * div]);
+    }
+    LongAct<BPL> xa;
+    long_act_load<BPL>(lds, lane, xa);
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        const float acc = long_row_dot<BPL>(rr[i % RIF], xa, lane);
+        if (lane == 0) gs[(i < 8 ? 0 : 32) + 8 * wave + (i & 7)] = acc;
+        if (i + RIF < RPW) load_row(i + RIF);
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {  // both half-waves compute block j; the first stores it
+        const int l = threadIdx.x & 31;
+        float gate = gs[l], up = gs[32 + l];
+        if (HEAD ? h.norm != 0 : in_scale != nullptr) {
+            const float sc = HEAD ? irs : in_scale[e / div];
+            gate = gate * sc;
+            up = up * sc;
+        }
+        const float v = gelu_tanh(gate) * up;
+        const Q8Lane r = q8_quantize_half(v);
+        if (threadIdx.x < 32) q8_store_half(q8a + ((int64_t)e * (inter >> 5) + blockIdx.x) * Q8_BLK, l, r);
+    }
+}
+
 // Block-dot dump: the same addressing and block_dot() as k_gemv_q4_grouped.
 template <int LAYOUT>
 __global__ __launch_bounds__(256) void k_block_dots(GemvArgs a) {
@@ -1027,6 +1166,24 @@ static int short_lanes(const ft_hip_ctx* ctx, int layout, int64_t n_rows, int64_
     return nb <= 8 * 64 ? 64 : 0;
 }
 
+// The long-row gate|up kernel (k_gemv_gu_long) takes q4r banks whose
+// gate|up rows are 64 or 128 blocks (BPL = blocks per lane = 1, 2); 0 = the
+// other kernels.
+static int gu_long_bpl(int layout, int64_t hidden) {
+    return layout == FT_LAYOUT_Q4R && (hidden == 2048 || hidden == 4096) ? (int)(hidden / 2048) : 0;
+}
+template <bool TOPK, bool HEAD>
+static void launch_gu_long(int bpl, dim3 grid, size_t lds, hipStream_t st, const GemvArgs& a, int inter, uint8_t* q8a,
+                           const float* in_scale, int div, const float* logits, const float* escale, int32_t* ids,
+                           float* wts, int E, const HeadArgs& h) {
+    if (bpl == 1)
+        hipLaunchKernelGGL((k_gemv_gu_long<TOPK, 1, HEAD>), grid, dim3(256), lds, st, a, inter, q8a, in_scale, div,
+                           logits, escale, ids, wts, E, h);
+    else
+        hipLaunchKernelGGL((k_gemv_gu_long<TOPK, 2, HEAD>), grid, dim3(256), lds, st, a, inter, q8a, in_scale, div,
+                           logits, escale, ids, wts, E, h);
+}
+
 template <int LPR, bool REC>
 static void launch_short_rec(int nbl, dim3 grid, size_t lds, hipStream_t s, const GemvArgs& a) {
     if (nbl <= 2) hipLaunchKernelGGL((k_gemv_q4r_short<LPR, 2, REC>), grid, dim3(256), lds, s, a);
@@ -1228,12 +1385,18 @@ extern "C" int ft_hip_gemv_gate_up_act(ft_hip_ctx* ctx, void* stream, const void
     a.q8_stride_blocks = hidden / 32;
     a.n_rows = (int)(2 * inter);
     a.k = (int)hidden;
+    const dim3 grid((unsigned)(inter / 32), (unsigned)n_pairs);
+    const size_t lds = (size_t)(hidden / 32) * Q8_BLK;
+    if (const int bpl = gu_long_bpl(layout, hidden)) {
+        launch_gu_long<false, false>(bpl, grid, lds, S(stream), a, (int)inter, (uint8_t*)q8_act, in_scale, (int)x_div,
+                                     nullptr, nullptr, nullptr, nullptr, 0, HeadArgs{});
+        return launch_status(nm);
+    }
     auto kern = layout == FT_LAYOUT_Q4R ? k_gemv_gu_act<FT_LAYOUT_Q4R, false, GU_LANES>
                                         : k_gemv_gu_act<FT_LAYOUT_Q4_0, false, GU_LANES>;
-    hipLaunchKernelGGL(kern, dim3((unsigned)(inter / 32), (unsigned)n_pairs), dim3(64 * GU_LANES),
-                       (size_t)(hidden / 32) * Q8_BLK,
-                       S(stream), a, (int)inter, (uint8_t*)q8_act, in_scale, (int)x_div, (const float*)nullptr,
-                       (const float*)nullptr, (int32_t*)nullptr, (float*)nullptr, 0, HeadArgs{});
+    hipLaunchKernelGGL(kern, grid, dim3(64 * GU_LANES), lds, S(stream), a, (int)inter, (uint8_t*)q8_act, in_scale,
+                       (int)x_div, (const float*)nullptr, (const float*)nullptr, (int32_t*)nullptr, (float*)nullptr, 0,
+                       HeadArgs{});
     return launch_status(nm);
 }
 
@@ -1460,14 +1623,27 @@ static int moe_layer_impl(const char* nm, ft_hip_ctx* ctx, void* stream, const f
     a.k = (int)hidden;
     const dim3 g_gu((unsigned)(inter / 32), (unsigned)n_pairs);
     const size_t l_gu = (size_t)(hidden / 32) * Q8_BLK;
+    const int gbpl = gu_long_bpl(layout, hidden);
     if (part_in) {
         const HeadArgs h{x, part_in, router_bias, ctx->input_norm};
-        auto kern = layout == FT_LAYOUT_Q4R ? k_gemv_gu_act<FT_LAYOUT_Q4R, true, GU_LANES, true>
-                                            : k_gemv_gu_act<FT_LAYOUT_Q4_0, true, GU_LANES, true>;
         const size_t l_head = l_gu + (size_t)(hidden / 16) * (n_experts + 1) * 4;
-        hipLaunchKernelGGL(kern, g_gu, dim3(64 * GU_LANES), l_head, S(stream), a, (int)inter, w.q8a,
-                           (const float*)nullptr, (int)top_k, (const float*)nullptr, expert_scale, ids, wts,
-                           (int)n_experts, h);
+        if (gbpl) {
+            launch_gu_long<true, true>(gbpl, g_gu, l_head, S(stream), a, (int)inter, w.q8a, nullptr, (int)top_k,
+                                       nullptr, expert_scale, ids, wts, (int)n_experts, h);
+        } else {
+            auto kern = layout == FT_LAYOUT_Q4R ? k_gemv_gu_act<FT_LAYOUT_Q4R, true, GU_LANES, true>
+                                                : k_gemv_gu_act<FT_LAYOUT_Q4_0, true, GU_LANES, true>;
+            hipLaunchKernelGGL(kern, g_gu, dim3(64 * GU_LANES), l_head, S(stream), a, (int)inter, w.q8a,
+                               (const float*)nullptr, (int)top_k, (const float*)nullptr, expert_scale, ids, wts,
+                               (int)n_experts, h);
+        }
+    } else if (gbpl) {
+        if (topk_in)
+            launch_gu_long<true, false>(gbpl, g_gu, l_gu, S(stream), a, (int)inter, w.q8a, inv, (int)top_k, w.logits,
+                                        expert_scale, ids, wts, (int)n_experts, HeadArgs{});
+        else
+            launch_gu_long<false, false>(gbpl, g_gu, l_gu, S(stream), a, (int)inter, w.q8a, inv, (int)top_k, w.logits,
+                                         expert_scale, ids, wts, (int)n_experts, HeadArgs{});
     } else {
         auto kern = layout == FT_LAYOUT_Q4R
                         ? (topk_in ? k_gemv_gu_act<FT_LAYOUT_Q4R, true, GU_LANES>

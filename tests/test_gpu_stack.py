@@ -78,7 +78,7 @@ def test_stack_equals_layers(gemv, H, I, E, K, L, layout, zipf, B, norm):
         ref, rid, rwt = _layer_by_layer(m, x, B)
         out, ids, wts = _stack(m, x, B)
     finally:
-        gemv.set_input_norm(1)
+        gemv.set_input_norm(0)
     assert torch.equal(ids, rid)
     assert _same(wts, rwt)
     assert _same(out, ref)
