@@ -41,6 +41,7 @@ struct GroupWs {
     int32_t* plist;     // [P] pairs grouped by expert
     int32_t* ppos;      // [P] scratch
     uint8_t* q8a;       // [P][I/32][40]
+    uint8_t* q8m;       // the MFMA groups' act quants by group position q: [I/32][4][P] (qs words g, g+4), then [I/32][P] (d, qsum)
     float* ydn;         // [P][H]
     float* inv;         // [B] input RMS norm scales
     size_t bytes;
@@ -58,6 +59,7 @@ GroupWs group_ws(void* base, int64_t B, int64_t H, int64_t I, int64_t E, int64_t
     w.plist = (int32_t*)(p + off); off += up(sizeof(int32_t) * P);
     w.ppos = (int32_t*)(p + off); off += up(sizeof(int32_t) * P);
     w.q8a = p + off; off += up((size_t)P * (I / 32) * Q8_BLK);
+    w.q8m = p + off; off += up((size_t)P * (I / 32) * Q8_BLK);
     w.ydn = (float*)(p + off); off += up(sizeof(float) * P * H);
     w.inv = (float*)(p + off); off += up(sizeof(float) * B);
     w.bytes = off;
@@ -483,6 +485,7 @@ __global__ __launch_bounds__(GT, 1) void k_grouped_down(const uint8_t* bank, int
 // ---------------------------------------------------------------------------
 typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int MT = 16;  // tokens per MFMA tile
+static_assert(MT * 10 <= GT, "k_mfma_gu stores a chunk's q8 words with one thread each");
 
 struct ActOp {
     long b;    // B operand: q8 words g and 4+g
@@ -508,6 +511,19 @@ __device__ __forceinline__ ActOp act_op(__amdgpu_buffer_rsrc_t r, uint32_t vq, u
     const u32x2 dq = __builtin_amdgcn_raw_buffer_load_b64(r, vd, soff, 0);
     ActOp a;
     a.b = (long)(((uint64_t)(ok ? hi : 0u) << 32) | (ok ? lo : 0u));
+    a.d = ok ? __uint_as_float(dq.x) : 0.0f;
+    a.qsum = ok ? (int)dq.y : 0;
+    return a;
+}
+
+// The same operand from the q8m layout (GroupWs::q8m): the words (g, g+4) at
+// vq + sq, {d, qsum} at vd + sd; one 8-byte load each.
+__device__ __forceinline__ ActOp act_op_m(__amdgpu_buffer_rsrc_t r, uint32_t vq, uint32_t vd, uint32_t sq, uint32_t sd,
+                                          bool ok) {
+    const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(r, vq, sq, 0);
+    const u32x2 dq = __builtin_amdgcn_raw_buffer_load_b64(r, vd, sd, 0);
+    ActOp a;
+    a.b = (long)(((uint64_t)(ok ? w.y : 0u) << 32) | (ok ? w.x : 0u));
     a.d = ok ? __uint_as_float(dq.x) : 0.0f;
     a.qsum = ok ? (int)dq.y : 0;
     return a;
@@ -564,9 +580,9 @@ template <int BPW, bool REC>
 __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ bank, int64_t expert_bytes,
                                                      const int32_t* __restrict__ meta,
                                                      const int32_t* __restrict__ plist,
-                                                     const uint8_t* __restrict__ q8x, uint8_t* q8a, float* dbg_gu,
+                                                     const uint8_t* __restrict__ q8x, uint8_t* q8m, float* dbg_gu,
                                                      const float* __restrict__ in_scale, int H, int I, int E, int K,
-                                                     int32_t* rec) {
+                                                     int P, int32_t* rec) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int SPT_LDS = (128 * 128 + GW * 1024 - 1) / (GW * 1024);  // scale rounds, up to nb = 128 (H 4096)
     const int nb = H >> 5, nbj = I >> 5;
@@ -743,9 +759,11 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
         __syncthreads();
         if (t < 4 * cur.nt) quantize_block_quad(actv + (t >> 2) * 32, t & 3, ablk + (t >> 2) * 10);
         __syncthreads();
-        for (int i = t; i < cur.nt * 10; i += GT) {
-            const int tt = i / 10, wd = i - tt * 10;
-            reinterpret_cast<uint32_t*>(q8a + ((int64_t)tok_p[tt] * nbj + cur.j) * Q8_BLK)[wd] = ablk[tt * 10 + wd];
+        if (t < cur.nt * 10) {  // q8m at group position q (MT * 10 <= GT)
+            const int tt = t / 10, wd = t - tt * 10, q = cur.s0 + cur.c0 + tt, wq = wd - 2;
+            const uint32_t o = wd < 2 ? (uint32_t)((P * nbj * 4 + cur.j * P + q) * 2 + wd)
+                                      : (uint32_t)(((cur.j * 4 + (wq & 3)) * P + q) * 2 + (wq >> 2));
+            reinterpret_cast<uint32_t*>(q8m)[o] = ablk[t];
         }
         if (!nxt.live) return false;
         __builtin_amdgcn_s_waitcnt(vm_wait_enc(BPW * 4 < 63 ? BPW * 4 : 63));  // nxt's scales are in LDS
@@ -767,11 +785,14 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
 // takes GW/KS groups of RT consecutive 16-row down tiles; wave w works on the
 // RT tiles of group w/KS (they share each block's activation operand), K
 // slice w%KS (blocks [s*BW, s*BW+BW) below nbj); the KS slice partials of a
-// (row, token) are summed in slice order into y[pair][row].
-template <int KS, int BW, int RT, int NBB, bool REC>
-__global__ __launch_bounds__(GT, NBB > 4 ? 1 : 2) void k_mfma_down(const uint8_t* bank, int64_t expert_bytes, int64_t gu_bytes,
-                                                     const int32_t* meta, const int32_t* plist, const uint8_t* q8a,
-                                                     uint32_t q8a_bytes, float* ydn, int H, int I, int E, int n_min,
+// (row, token) are summed in slice order into y[pair][row]. With KS > 1 the
+// partials overlay the tiles' scales in LDS (restaged for each 16 tokens),
+// so two workgroups fit a CU. Blocks go in NBB-block batches, NBUF batches in
+// flight (register buffers).
+template <int KS, int BW, int RT, int NBB, int NBUF, bool REC>
+__global__ __launch_bounds__(GT, 4) void k_mfma_down(const uint8_t* bank, int64_t expert_bytes, int64_t gu_bytes,
+                                                     const int32_t* meta, const int32_t* plist, const uint8_t* q8m,
+                                                     int P, float* ydn, int H, int I, int E, int n_min,
                                                      int32_t* rec) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int TPW = GW / KS;   // tile groups per workgroup
@@ -782,8 +803,9 @@ __global__ __launch_bounds__(GT, NBB > 4 ? 1 : 2) void k_mfma_down(const uint8_t
     const int e = meta[1 + g], s0 = meta[1 + E + g], n = meta[1 + 2 * E + g];
     if (n < n_min) return;
     // LDS: the tiles' scales [TW][nbj][16] f16; slice partials [GW][RT][16][MT]
+    // in the same bytes once the K loop is done
     uint16_t* scl = reinterpret_cast<uint16_t*>(lds);
-    float* red = reinterpret_cast<float*>(lds + TW * nbj * 32);
+    float* red = reinterpret_cast<float*>(lds);
     const int t = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(t >> 6), li = t & 15, lg = (t >> 4) & 3;
     const int tl = wave / KS, sl = wave % KS, bs = sl * BW;
     const int tile0 = (u * TPW + tl) * RT;  // this wave's first tile
@@ -791,24 +813,27 @@ __global__ __launch_bounds__(GT, NBB > 4 ? 1 : 2) void k_mfma_down(const uint8_t
     const uint16_t* st = scl + tl * RT * nbj * 16;
     // the wave's RT tiles: qs of tile tile0+m at m*dn_tile + nbj*32 from D0 + tile0*dn_tile
     const __amdgpu_buffer_rsrc_t rw = buf_rsrc(D0 + (int64_t)tile0 * dn_tile, (uint32_t)(RT * dn_tile));
-    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(q8a, q8a_bytes);
+    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(q8m, (uint32_t)P * nbj * Q8_BLK);
     const uint32_t vw = nbj * 32 + li * 16 + 4 * lg;
     for (int c0 = 0; c0 < n; c0 += MT) {
         const int nt = min(MT, n - c0);
-        const int p = plist[s0 + c0 + min(li, nt - 1)];
-        const uint32_t vd = (uint32_t)p * nbj * Q8_BLK, vq = vd + 8 + 4 * lg;
-        // blocks in NBB-block batches, the next batch's loads issued before
-        // the current batch's MFMAs (two register buffers)
+        const int q = s0 + c0 + min(li, nt - 1), p = plist[q];
+        // this lane's operand words of block bb: 8 bytes at bb * 32P + vq (the
+        // 16 tokens' words of a lane group in 128 contiguous bytes), d and
+        // qsum at P * nbj * 32 + bb * 8P + vd
+        const uint32_t vq = (uint32_t)(lg * P + q) * 8, vd = (uint32_t)P * nbj * 32 + (uint32_t)q * 8;
+        // blocks in NBB-block batches, the loads of the batch NBUF - 1 ahead
+        // issued before the current batch's MFMAs (NBUF register buffers)
         constexpr int NBATCH = BW / NBB;
-        uint32_t aw[2][NBB][RT];
-        ActOp av[2][NBB];
+        uint32_t aw[NBUF][NBB][RT];
+        ActOp av[NBUF][NBB];
         auto load = [&](int k, int buf) __attribute__((always_inline)) {
 #pragma unroll
             for (int b = 0; b < NBB; ++b) {
                 const int bb = min(bs + k * NBB + b, nbj - 1);
 #pragma unroll
                 for (int m = 0; m < RT; ++m) aw[buf][b][m] = buf_ld(rw, vw, m * dn_tile + bb * 256);
-                av[buf][b] = act_op(ra, vq, vd, bb * Q8_BLK, li < nt);
+                av[buf][b] = act_op_m(ra, vq, vd, bb * 32 * P, bb * 8 * P, li < nt);
             }
         };
         float acc[RT][4];
@@ -816,8 +841,10 @@ __global__ __launch_bounds__(GT, NBB > 4 ? 1 : 2) void k_mfma_down(const uint8_t
         for (int m = 0; m < RT; ++m)
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[m][v] = 0.0f;
-        load(0, 0);
-        if (c0 == 0) {  // the tiles' scales to LDS, with the first batch in flight
+#pragma unroll
+        for (int k = 0; k < NBUF - 1; ++k)
+            if (k < NBATCH && bs + k * NBB < nbj) load(k, k);
+        if (c0 == 0 || KS > 1) {  // the tiles' scales to LDS, with the first batches in flight
             stage<8>(
                 TW * nbj * 8,
                 [&](int i) {
@@ -830,16 +857,16 @@ __global__ __launch_bounds__(GT, NBB > 4 ? 1 : 2) void k_mfma_down(const uint8_t
 #pragma unroll
         for (int k = 0; k < NBATCH; ++k) {
             if (bs + k * NBB >= nbj) break;  // uniform: this slice ends here
-            if (k + 1 < NBATCH && bs + (k + 1) * NBB < nbj) load(k + 1, (k + 1) & 1);
+            if (k + NBUF - 1 < NBATCH && bs + (k + NBUF - 1) * NBB < nbj) load(k + NBUF - 1, (k + NBUF - 1) % NBUF);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int b = 0; b < NBB; ++b) {
                 if (bs + k * NBB + b < nbj) {  // uniform
-                    const ActOp a = av[k & 1][b];
+                    const ActOp a = av[k % NBUF][b];
                     const v4i c = c_init(a.qsum);
 #pragma unroll
                     for (int m = 0; m < RT; ++m) {
-                        const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib_op(aw[k & 1][b][m]), a.b, c, 0, 0, 0);
+                        const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib_op(aw[k % NBUF][b][m]), a.b, c, 0, 0, 0);
                         if constexpr (REC) {  // test record: D = the (row, token) blocks' int32 dots
                             if (li < nt)
 #pragma unroll
@@ -863,6 +890,7 @@ __global__ __launch_bounds__(GT, NBB > 4 ? 1 : 2) void k_mfma_down(const uint8_t
                     for (int v = 0; v < 4; ++v) ydn[(int64_t)p * H + (tile0 + m) * 16 + 4 * lg + v] = acc[m][v];
             }
         } else {
+            __syncthreads();  // every wave is done with the scales
 #pragma unroll
             for (int m = 0; m < RT; ++m)
 #pragma unroll
@@ -878,6 +906,22 @@ __global__ __launch_bounds__(GT, NBB > 4 ? 1 : 2) void k_mfma_down(const uint8_t
             }
             __syncthreads();
         }
+    }
+}
+
+// The MFMA groups' act quants from q8m back into the pairs' rows of q8a
+// ([P][nbj][40]), for the debug copy: MFMA group blockIdx.y, one thread per
+// (position, block, word) of the group.
+__global__ __launch_bounds__(256) void k_q8m_rows(const uint32_t* q8m, const int32_t* meta, const int32_t* plist,
+                                                  uint8_t* q8a, int P, int nbj, int E) {
+    const int g = blockIdx.y;
+    if (g >= meta[1 + 3 * E]) return;  // not an MFMA group
+    const int s0 = meta[1 + E + g], n = meta[1 + 2 * E + g];
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n * nbj * 10; i += gridDim.x * 256) {
+        const int wd = i % 10, j = i / 10 % nbj, q = s0 + i / (10 * nbj), wq = wd - 2;
+        const int64_t o = wd < 2 ? ((int64_t)P * nbj * 4 + (int64_t)j * P + q) * 2 + wd
+                                 : (((int64_t)j * 4 + (wq & 3)) * P + q) * 2 + (wq >> 2);
+        reinterpret_cast<uint32_t*>(q8a + ((int64_t)plist[q] * nbj + j) * Q8_BLK)[wd] = q8m[o];
     }
 }
 
@@ -972,7 +1016,7 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
     const int gmax = std::min(E, P);
     const int gbig = std::min(gmax, n_mfma > P ? 0 : P / n_mfma);  // at most this many groups of >= n_mfma tokens
     const bool dot4 = n_mfma > 1, mfma = n_seqs >= n_mfma;
-    const uint32_t q8x_bytes = (uint32_t)(n_seqs * nb * Q8_BLK), q8a_bytes = (uint32_t)((int64_t)P * nbj * Q8_BLK);
+    const uint32_t q8x_bytes = (uint32_t)(n_seqs * nb * Q8_BLK);
     // a block-dot record (ft_hip_set_block_dot_record, tests only) selects
     // the instantiations that store every int32 block dot
     int32_t* rgu = ctx->rec_gu;
@@ -996,8 +1040,14 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
                               : (rec ? k_mfma_gu<16, true> : k_mfma_gu<16, false>);
         const int grid = std::min(ctx->num_cus, nbj * gbig);  // persistent: one workgroup per CU
         hipLaunchKernelGGL(kern, dim3(grid), dim3(GT), lds_mg, s, (const uint8_t*)bank, eb, (const int32_t*)w.meta,
-                           (const int32_t*)w.plist, (const uint8_t*)w.q8x, w.q8a, dbg_gu, inv, H, I, E, K, rgu);
+                           (const int32_t*)w.plist, (const uint8_t*)w.q8x, w.q8m, dbg_gu, inv, H, I, E, K, P, rgu);
         if ((rc = launch_status("moe_layer_grouped/gate_up_mfma"))) return rc;
+        if (dbg_act) {  // the debug copy below reads q8a's pair rows
+            hipLaunchKernelGGL(k_q8m_rows, dim3(64, (unsigned)gbig), dim3(256), 0, s,
+                               (const uint32_t*)w.q8m, (const int32_t*)w.meta, (const int32_t*)w.plist, w.q8a, P, nbj,
+                               E);
+            if ((rc = launch_status("moe_layer_grouped/q8m_rows"))) return rc;
+        }
     }
     if (dbg_act && hipMemcpyAsync(dbg_act, w.q8a, (size_t)P * nbj * Q8_BLK, hipMemcpyDeviceToDevice, s) != hipSuccess)
         return fail(FT_HIP_E_LAUNCH, "%s: debug copy failed", nm);
@@ -1015,18 +1065,18 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
     if (mfma) {
         if (nbj <= 32) {  // one K slice: 8 waves x 2 tiles of 16 rows per workgroup
             const size_t lds_md = (size_t)GW * 2 * nbj * 32 + sizeof(float) * GW * 2 * 16 * MT;
-            auto kern = rec ? k_mfma_down<1, 32, 2, 4, true> : k_mfma_down<1, 32, 2, 4, false>;
+            auto kern = rec ? k_mfma_down<1, 32, 2, 4, 2, true> : k_mfma_down<1, 32, 2, 4, 2, false>;
             hipLaunchKernelGGL(kern, dim3(H / (16 * GW * 2), gbig), dim3(GT), lds_md, s, (const uint8_t*)bank, eb,
-                               gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8a,
-                               q8a_bytes, w.ydn, H, I, E, n_mfma, rdn);
+                               gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8m, P,
+                               w.ydn, H, I, E, n_mfma, rdn);
         } else {  // long rows: DRT tiles per workgroup, 8 K slices of 56 (rows up to 448 blocks) or 64 blocks
             constexpr int DRT = 4;
-            const size_t lds_md = (size_t)DRT * nbj * 32 + sizeof(float) * GW * DRT * 16 * MT;
-            auto kern = nbj <= 8 * 56 ? (rec ? k_mfma_down<GW, 56, DRT, 4, true> : k_mfma_down<GW, 56, DRT, 4, false>)
-                                      : (rec ? k_mfma_down<GW, 64, DRT, 4, true> : k_mfma_down<GW, 64, DRT, 4, false>);
+            const size_t lds_md = std::max((size_t)DRT * nbj * 32, sizeof(float) * GW * DRT * 16 * MT);
+            auto kern = nbj <= 8 * 56 ? (rec ? k_mfma_down<GW, 56, DRT, 2, 2, true> : k_mfma_down<GW, 56, DRT, 2, 2, false>)
+                                      : (rec ? k_mfma_down<GW, 64, DRT, 2, 2, true> : k_mfma_down<GW, 64, DRT, 2, 2, false>);
             hipLaunchKernelGGL(kern, dim3(H / (16 * DRT), gbig), dim3(GT), lds_md, s, (const uint8_t*)bank, eb,
-                               gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8a,
-                               q8a_bytes, w.ydn, H, I, E, n_mfma, rdn);
+                               gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8m, P,
+                               w.ydn, H, I, E, n_mfma, rdn);
         }
         if ((rc = launch_status("moe_layer_grouped/down_mfma"))) return rc;
     }
