@@ -517,15 +517,17 @@ __device__ __forceinline__ ActOp act_op(__amdgpu_buffer_rsrc_t r, uint32_t vq, u
 }
 
 // The same operand from the q8m layout (GroupWs::q8m): the words (g, g+4) at
-// vq + sq, {d, qsum} at vd + sd; one 8-byte load each.
-__device__ __forceinline__ ActOp act_op_m(__amdgpu_buffer_rsrc_t r, uint32_t vq, uint32_t vd, uint32_t sq, uint32_t sd,
-                                          bool ok) {
+// vq + sq, {d, qsum} at vd + sd; one 8-byte load each. A lane without a
+// token passes offsets past the buffer's end and gets zeros.
+constexpr uint32_t NO_TOKEN = 0x80000000u;
+__device__ __forceinline__ ActOp act_op_m(__amdgpu_buffer_rsrc_t r, uint32_t vq, uint32_t vd, uint32_t sq,
+                                          uint32_t sd) {
     const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(r, vq, sq, 0);
     const u32x2 dq = __builtin_amdgcn_raw_buffer_load_b64(r, vd, sd, 0);
     ActOp a;
-    a.b = (long)(((uint64_t)(ok ? w.y : 0u) << 32) | (ok ? w.x : 0u));
-    a.d = ok ? __uint_as_float(dq.x) : 0.0f;
-    a.qsum = ok ? (int)dq.y : 0;
+    a.b = (long)(((uint64_t)w.y << 32) | w.x);
+    a.d = __uint_as_float(dq.x);
+    a.qsum = (int)dq.y;
     return a;
 }
 
@@ -813,7 +815,7 @@ __global__ __launch_bounds__(GT, 4) void k_mfma_down(const uint8_t* bank, int64_
     const uint16_t* st = scl + tl * RT * nbj * 16;
     // the wave's RT tiles: qs of tile tile0+m at m*dn_tile + nbj*32 from D0 + tile0*dn_tile
     const __amdgpu_buffer_rsrc_t rw = buf_rsrc(D0 + (int64_t)tile0 * dn_tile, (uint32_t)(RT * dn_tile));
-    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(q8m, (uint32_t)P * nbj * Q8_BLK);
+    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(q8m, (uint32_t)P * nbj * Q8_BLK);  // < NO_TOKEN bytes
     const uint32_t vw = nbj * 32 + li * 16 + 4 * lg;
     for (int c0 = 0; c0 < n; c0 += MT) {
         const int nt = min(MT, n - c0);
@@ -821,7 +823,9 @@ __global__ __launch_bounds__(GT, 4) void k_mfma_down(const uint8_t* bank, int64_
         // this lane's operand words of block bb: 8 bytes at bb * 32P + vq (the
         // 16 tokens' words of a lane group in 128 contiguous bytes), d and
         // qsum at P * nbj * 32 + bb * 8P + vd
-        const uint32_t vq = (uint32_t)(lg * P + q) * 8, vd = (uint32_t)P * nbj * 32 + (uint32_t)q * 8;
+        const bool ok = li < nt;
+        const uint32_t vq = ok ? (uint32_t)(lg * P + q) * 8 : NO_TOKEN;
+        const uint32_t vd = ok ? (uint32_t)P * nbj * 32 + (uint32_t)q * 8 : NO_TOKEN;
         // blocks in NBB-block batches, the loads of the batch NBUF - 1 ahead
         // issued before the current batch's MFMAs (NBUF register buffers)
         constexpr int NBATCH = BW / NBB;
@@ -833,7 +837,7 @@ __global__ __launch_bounds__(GT, 4) void k_mfma_down(const uint8_t* bank, int64_
                 const int bb = min(bs + k * NBB + b, nbj - 1);
 #pragma unroll
                 for (int m = 0; m < RT; ++m) aw[buf][b][m] = buf_ld(rw, vw, m * dn_tile + bb * 256);
-                av[buf][b] = act_op_m(ra, vq, vd, bb * 32 * P, bb * 8 * P, li < nt);
+                av[buf][b] = act_op_m(ra, vq, vd, bb * 32 * P, bb * 8 * P);
             }
         };
         float acc[RT][4];
@@ -841,9 +845,11 @@ __global__ __launch_bounds__(GT, 4) void k_mfma_down(const uint8_t* bank, int64_
         for (int m = 0; m < RT; ++m)
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[m][v] = 0.0f;
+        // this slice's batches (uniform; none when the slice starts past nbj)
+        const int nbat = max(0, min(NBATCH, (nbj - bs + NBB - 1) / NBB));
 #pragma unroll
         for (int k = 0; k < NBUF - 1; ++k)
-            if (k < NBATCH && bs + k * NBB < nbj) load(k, k);
+            if (k < nbat) load(k, k);
         if (c0 == 0 || KS > 1) {  // the tiles' scales to LDS, with the first batches in flight
             stage<8>(
                 TW * nbj * 8,
@@ -854,19 +860,27 @@ __global__ __launch_bounds__(GT, 4) void k_mfma_down(const uint8_t* bank, int64_
                 [&](int i, uint32_t v) { reinterpret_cast<uint32_t*>(scl)[i] = v; });
             __syncthreads();
         }
+        // rounds of NBUF batches, register buffer j holding batch kb + j; the
+        // rounds are a loop (not unrolled), so a block's offsets are scalar
+        // adds rather than registers held across the slice
+#pragma unroll 1
+        for (int kb = 0; kb < nbat; kb += NBUF) {
 #pragma unroll
-        for (int k = 0; k < NBATCH; ++k) {
-            if (bs + k * NBB >= nbj) break;  // uniform: this slice ends here
-            if (k + NBUF - 1 < NBATCH && bs + (k + NBUF - 1) * NBB < nbj) load(k + NBUF - 1, (k + NBUF - 1) % NBUF);
+          for (int j = 0; j < NBUF; ++j) {
+            const int k = kb + j;
+            if (k >= nbat) break;  // uniform
+            // unconditional (past the slice: the last block again), so the
+            // wait below counts only this batch's loads, not the prefetch's
+            load(k + NBUF - 1, (j + NBUF - 1) % NBUF);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int b = 0; b < NBB; ++b) {
                 if (bs + k * NBB + b < nbj) {  // uniform
-                    const ActOp a = av[k % NBUF][b];
+                    const ActOp a = av[j][b];
                     const v4i c = c_init(a.qsum);
 #pragma unroll
                     for (int m = 0; m < RT; ++m) {
-                        const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib_op(aw[k % NBUF][b][m]), a.b, c, 0, 0, 0);
+                        const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib_op(aw[j][b][m]), a.b, c, 0, 0, 0);
                         if constexpr (REC) {  // test record: D = the (row, token) blocks' int32 dots
                             if (li < nt)
 #pragma unroll
@@ -881,6 +895,7 @@ __global__ __launch_bounds__(GT, 4) void k_mfma_down(const uint8_t* bank, int64_
                 }
                 __builtin_amdgcn_sched_barrier(0);  // one block's MFMA results live at a time
             }
+          }
         }
         if (KS == 1) {
             if (li < nt) {
