@@ -21,7 +21,7 @@
 // stay with the unit group that holds them; only the remaining unit groups
 // load the experts nobody predicted (a miss).
 //
-// Workgroups (G shape: H 2816, I 704, E 128, top-8): 216.
+// Workgroups (G shape: H 2816, I 704, E 128, top-8): 200.
 //   expert unit (u, j), 176 of them, unit group u = w % K, j = w / K:
 //     gate|up : 64 rows (32 gate, 32 up) of its expert for act block j
 //               (32 columns), H/32 blocks held in registers by 8 waves;
@@ -34,11 +34,11 @@
 //     round-robin; each checks this at start through the XCD id register),
 //     so hop A stays in that XCD's L2: plain stores, agent-scope polls.
 //     If the placement check fails, hop A stores write through instead.
-//   group units (g, s), 4 per R-order group of H/8 rows (32 of them, the
-//     four of group g on XCD g): each waits for y of the group's rows from
-//     every routed slot (hop B); x_{l+1} = x_l + sum_p w_p y_p in routing
-//     order; router chunk partials of the group's H/128 chunks and their
-//     group sum for a quarter of the experts, s*E/4.. (layer l+1's router
+//   group units (g, s), GSPLIT = 2 per R-order group of H/8 rows (16 of
+//     them, both of group g on XCD g): each waits for y of the group's rows
+//     from every routed slot (hop B); x_{l+1} = x_l + sum_p w_p y_p in
+//     routing order; router chunk partials of the group's H/128 chunks and
+//     their group sum for half of the experts, s*E/2.. (layer l+1's router
 //     weights were streamed into registers meanwhile); split 0 also the q8
 //     of the rows and their sum of squares; publishes them (hop C),
 //     double-buffered by parity.
@@ -64,7 +64,7 @@ constexpr int FT_WAVES = FT_THREADS / 64;
 constexpr int MAX_K = 8;
 constexpr int MAX_E = 128;      // group partials use four threads per expert
 constexpr int NGROUP = 8;       // R-order groups
-constexpr int GSPLIT = 4;       // group units per R-order group, each with E / GSPLIT experts' router sums
+constexpr int GSPLIT = 2;       // group units per R-order group, each with E / GSPLIT experts' router sums
 constexpr int DN_ROWS = 16;     // rows per router chunk and per down tile
 constexpr int DN_UNIT = DN_ROWS * FT_WAVES;  // rows per down unit: one tile per wave
 constexpr int POLL_SLEEP = 1;   // s_sleep units (64 clocks) between polls

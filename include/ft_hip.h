@@ -358,8 +358,8 @@ int ft_hip_set_input_norm(ft_hip_ctx* ctx, int on);
  *
  * Workgroups: K*max(I/32, H/128) expert units (routed slot p, index j: the
  * gate|up rows of act block j and the down rows 128j..128j+127 of expert
- * ids[p]) plus 32 group units (four per R-order group of H/8 rows: combine,
- * the router sums of a quarter of the experts, q8 of x) and 8 prediction
+ * ids[p]) plus 16 group units (two per R-order group of H/8 rows: combine,
+ * the router sums of half of the experts, q8 of x) and 8 prediction
  * units -- see ft_hip_fused_workgroups. Supported shape: the Gemma expert section (hidden
  * 2816, inter 704, 128 experts, top-8), the one its tests cover; other
  * shapes return FT_HIP_E_SHAPE (use ft_hip_moe_layer).

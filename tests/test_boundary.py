@@ -92,9 +92,9 @@ def test_shape_errors_are_reported_before_any_gpu_call():
 
 
 def test_fused_workgroups_formula():
-    """K*max(I/32, H/128) expert units, four group units (each with a quarter
-    of the experts' router sums) and a pred unit per R-order group."""
-    assert ft_hip.Q4Gemv.fused_workgroups(2816, 704, 128, 8) == 8 * 22 + 5 * 8
-    assert ft_hip.Q4Gemv.fused_workgroups(2816, 352, 128, 4) == 4 * 22 + 5 * 8
-    assert ft_hip.Q4Gemv.fused_workgroups(4096, 512, 64, 2) == 2 * 32 + 5 * 8
+    """K*max(I/32, H/128) expert units, two group units (each with half of
+    the experts' router sums) and a pred unit per R-order group."""
+    assert ft_hip.Q4Gemv.fused_workgroups(2816, 704, 128, 8) == 8 * 22 + 3 * 8
+    assert ft_hip.Q4Gemv.fused_workgroups(2816, 352, 128, 4) == 4 * 22 + 3 * 8
+    assert ft_hip.Q4Gemv.fused_workgroups(4096, 512, 64, 2) == 2 * 32 + 3 * 8
     assert ft_hip.Q4Gemv.fused_workgroups(2816, 700, 128, 8) == -1
