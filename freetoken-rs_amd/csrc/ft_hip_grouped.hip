@@ -504,21 +504,10 @@ __device__ __forceinline__ uint32_t buf_ld(__amdgpu_buffer_rsrc_t r, uint32_t vo
     return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
 }
 
-// The q8 block at byte soff + vd of buffer r ({d, qsum, qs[32]}) for lane
-// group g (vq = vd + 8 + 4g); zeros if !ok (loads unconditional, then selects).
-__device__ __forceinline__ ActOp act_op(__amdgpu_buffer_rsrc_t r, uint32_t vq, uint32_t vd, uint32_t soff, bool ok) {
-    const uint32_t lo = buf_ld(r, vq, soff), hi = buf_ld(r, vq + 16, soff);
-    const u32x2 dq = __builtin_amdgcn_raw_buffer_load_b64(r, vd, soff, 0);
-    ActOp a;
-    a.b = (long)(((uint64_t)(ok ? hi : 0u) << 32) | (ok ? lo : 0u));
-    a.d = ok ? __uint_as_float(dq.x) : 0.0f;
-    a.qsum = ok ? (int)dq.y : 0;
-    return a;
-}
-
-// The same operand from the q8m layout (GroupWs::q8m): the words (g, g+4) at
-// vq + sq, {d, qsum} at vd + sd; one 8-byte load each. A lane without a
-// token passes offsets past the buffer's end and gets zeros.
+// A token's q8 block as the B operand of lane group g, from the q8m layout
+// (GroupWs::q8m): q8 words (g, g+4) at vq + sq, {d, qsum} at vd + sd, one
+// 8-byte load each. A lane without a token passes offsets past the buffer's
+// end (NO_TOKEN; the buffer is smaller) and gets zeros.
 constexpr uint32_t NO_TOKEN = 0x80000000u;
 __device__ __forceinline__ ActOp act_op_m(__amdgpu_buffer_rsrc_t r, uint32_t vq, uint32_t vd, uint32_t sq,
                                           uint32_t sd) {
@@ -1031,7 +1020,9 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
     const int gmax = std::min(E, P);
     const int gbig = std::min(gmax, n_mfma > P ? 0 : P / n_mfma);  // at most this many groups of >= n_mfma tokens
     const bool dot4 = n_mfma > 1, mfma = n_seqs >= n_mfma;
-    const uint32_t q8x_bytes = (uint32_t)(n_seqs * nb * Q8_BLK);
+    if (mfma && (int64_t)P * nbj * Q8_BLK >= (int64_t)NO_TOKEN)
+        return fail(FT_HIP_E_SHAPE, "%s: %d pairs x %d act blocks: the MFMA path's activation buffer must stay under 2 GiB",
+                    nm, P, nbj);
     // a block-dot record (ft_hip_set_block_dot_record, tests only) selects
     // the instantiations that store every int32 block dot
     int32_t* rgu = ctx->rec_gu;
