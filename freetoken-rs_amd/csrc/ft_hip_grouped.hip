@@ -520,6 +520,23 @@ __device__ __forceinline__ ActOp act_op_m(__amdgpu_buffer_rsrc_t r, uint32_t vq,
     return a;
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 4x4 transpose across the 16-lane rows of a wavefront: on entry lane row g
+// holds M[g][0..3] in (a0..a3), on exit T[g][j] = M[j][g]. Two 32-lane swaps
+// exchange the off-diagonal 2x2 blocks, two 16-lane swaps the off-diagonal
+// elements inside each block.
+__device__ __forceinline__ void quad_transpose(uint32_t& a0, uint32_t& a1, uint32_t& a2, uint32_t& a3) {
+    const auto s0 = __builtin_amdgcn_permlane32_swap(a0, a2, false, false);
+    const auto s1 = __builtin_amdgcn_permlane32_swap(a1, a3, false, false);
+    const auto s2 = __builtin_amdgcn_permlane16_swap(s0[0], s1[0], false, false);
+    const auto s3 = __builtin_amdgcn_permlane16_swap(s0[1], s1[1], false, false);
+    a0 = s2[0];
+    a1 = s2[1];
+    a2 = s3[0];
+    a3 = s3[1];
+}
+
 // A operand from qs word g of a row's block: low nibbles, then high nibbles.
 __device__ __forceinline__ long nib_op(uint32_t w) {
     return (long)(((uint64_t)((w >> 4) & 0x0F0F0F0Fu) << 32) | (w & 0x0F0F0F0Fu));
@@ -805,7 +822,7 @@ __global__ __launch_bounds__(GT, 4) void k_mfma_down(const uint8_t* bank, int64_
     // the wave's RT tiles: qs of tile tile0+m at m*dn_tile + nbj*32 from D0 + tile0*dn_tile
     const __amdgpu_buffer_rsrc_t rw = buf_rsrc(D0 + (int64_t)tile0 * dn_tile, (uint32_t)(RT * dn_tile));
     const __amdgpu_buffer_rsrc_t ra = buf_rsrc(q8m, (uint32_t)P * nbj * Q8_BLK);  // < NO_TOKEN bytes
-    const uint32_t vw = nbj * 32 + li * 16 + 4 * lg;
+    const uint32_t vw = nbj * 32 + li * 16 + 4 * lg, vw4 = nbj * 32 + lg * 256 + li * 16;
     for (int c0 = 0; c0 < n; c0 += MT) {
         const int nt = min(MT, n - c0);
         const int q = s0 + c0 + min(li, nt - 1), p = plist[q];
@@ -820,12 +837,29 @@ __global__ __launch_bounds__(GT, 4) void k_mfma_down(const uint8_t* bank, int64_
         constexpr int NBATCH = BW / NBB;
         uint32_t aw[NBUF][NBB][RT];
         ActOp av[NBUF][NBB];
+        // NBB == 4: one 16-byte load per tile for the batch's four blocks,
+        // lane group g taking all four qs words of its row in block 4k+g (1 KB
+        // contiguous per wave), turned into word g of each block by
+        // quad_transpose when the batch is consumed (blocks past the row are
+        // read, never used: the descriptor bounds the reads)
         auto load = [&](int k, int buf) __attribute__((always_inline)) {
+            if constexpr (NBB == 4) {
+#pragma unroll
+                for (int m = 0; m < RT; ++m) {
+                    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, vw4, m * dn_tile + (bs + k * 4) * 256, 0);
+                    aw[buf][0][m] = v.x;
+                    aw[buf][1][m] = v.y;
+                    aw[buf][2][m] = v.z;
+                    aw[buf][3][m] = v.w;
+                }
+            }
 #pragma unroll
             for (int b = 0; b < NBB; ++b) {
                 const int bb = min(bs + k * NBB + b, nbj - 1);
+                if constexpr (NBB != 4) {
 #pragma unroll
-                for (int m = 0; m < RT; ++m) aw[buf][b][m] = buf_ld(rw, vw, m * dn_tile + bb * 256);
+                    for (int m = 0; m < RT; ++m) aw[buf][b][m] = buf_ld(rw, vw, m * dn_tile + bb * 256);
+                }
                 av[buf][b] = act_op_m(ra, vq, vd, bb * 32 * P, bb * 8 * P);
             }
         };
@@ -862,6 +896,10 @@ __global__ __launch_bounds__(GT, 4) void k_mfma_down(const uint8_t* bank, int64_
             // wait below counts only this batch's loads, not the prefetch's
             load(k + NBUF - 1, (j + NBUF - 1) % NBUF);
             __builtin_amdgcn_sched_barrier(0);
+            if constexpr (NBB == 4) {
+#pragma unroll
+                for (int m = 0; m < RT; ++m) quad_transpose(aw[j][0][m], aw[j][1][m], aw[j][2][m], aw[j][3][m]);
+            }
 #pragma unroll
             for (int b = 0; b < NBB; ++b) {
                 if (bs + k * NBB + b < nbj) {  // uniform
@@ -1078,8 +1116,8 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
         } else {  // long rows: DRT tiles per workgroup, 8 K slices of 56 (rows up to 448 blocks) or 64 blocks
             constexpr int DRT = 4;
             const size_t lds_md = std::max((size_t)DRT * nbj * 32, sizeof(float) * GW * DRT * 16 * MT);
-            auto kern = nbj <= 8 * 56 ? (rec ? k_mfma_down<GW, 56, DRT, 2, 2, true> : k_mfma_down<GW, 56, DRT, 2, 2, false>)
-                                      : (rec ? k_mfma_down<GW, 64, DRT, 2, 2, true> : k_mfma_down<GW, 64, DRT, 2, 2, false>);
+            auto kern = nbj <= 8 * 56 ? (rec ? k_mfma_down<GW, 56, DRT, 4, 2, true> : k_mfma_down<GW, 56, DRT, 4, 2, false>)
+                                      : (rec ? k_mfma_down<GW, 64, DRT, 4, 2, true> : k_mfma_down<GW, 64, DRT, 4, 2, false>);
             hipLaunchKernelGGL(kern, dim3(H / (16 * DRT), gbig), dim3(GT), lds_md, s, (const uint8_t*)bank, eb,
                                gu_bytes, (const int32_t*)w.meta, (const int32_t*)w.plist, (const uint8_t*)w.q8m, P,
                                w.ydn, H, I, E, n_mfma, rdn);
