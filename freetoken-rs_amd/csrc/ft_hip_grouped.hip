@@ -612,7 +612,7 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
     const int xs = nb * 10 + 1;  // token stride (dwords), odd: the 16 tokens' rows start in different banks
     const int t = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(t >> 6), li = t & 15, lg = (t >> 4) & 3;
     const int b0 = wave * BPW;
-    const uint32_t vw = li * 16 + 4 * lg;
+    const uint32_t vw16 = lg * 256 + li * 16;
     auto bind = [&](int it, int c, bool live) __attribute__((always_inline)) {
         MfUnit u;
         u.live = live;
@@ -637,9 +637,15 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
     uint32_t aw[BPW][4];
     // slot b <- block b of unit u (dead: a descriptor of 0 bytes returns zeros and reads nothing)
     auto issue_block = [&](int b, const MfUnit& u) __attribute__((always_inline)) {
+        // one 16-byte load: lane group g takes the four qs words of row
+        // 16g + li (1 KB contiguous per wave); quad_transpose turns them into
+        // word g of rows li, 16 + li, 32 + li, 48 + li when the block is used
         const __amdgpu_buffer_rsrc_t rw = buf_rsrc(u.T + nb * 128, u.live ? (uint32_t)nb * 1024 : 0u);
-#pragma unroll
-        for (int m = 0; m < 4; ++m) aw[b][m] = buf_ld(rw, vw + m * 256, (b0 + b) * 1024);
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, vw16, (b0 + b) * 1024, 0);
+        aw[b][0] = v.x;
+        aw[b][1] = v.y;
+        aw[b][2] = v.z;
+        aw[b][3] = v.w;
     };
     // the tile's scales (nb * 128 bytes) straight into scale buffer `buf`:
     // 16 bytes per lane, 1 KB per wave and round. Issued right after every
@@ -721,6 +727,7 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
             const v4i c = c_init((int)cu.qsum);
             const long bop = (long)(((uint64_t)cu.hi << 32) | cu.lo);
             v4i d[4];
+            quad_transpose(aw[b][0], aw[b][1], aw[b][2], aw[b][3]);
 #pragma unroll
             for (int m = 0; m < 4; ++m) d[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(nib_op(aw[b][m]), bop, c, 0, 0, 0);
             issue_block(b, nxt);
