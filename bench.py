@@ -43,7 +43,7 @@ MEASURED_TRAFFIC = {
     "zipf": 991925124,       # k_moe_stack_fused, one launch
     "batch16": 7918487317,   # whole step, 30 grouped layers
     "batch64": 11568345493,  # whole step, 30 grouped layers
-    "large32": 24990478392,  # whole step, 32 grouped layers
+    "large32": 25267396511,  # whole step, 32 grouped layers
     "large1": 132300061,     # k_gemv_gu_long, one launch (algorithmic 132,120,576 B)
 }
 METRIC = "MoE expert-FFN µs/token at batch 1 + achieved HBM GB/s (% of MI355X peak)"
