@@ -42,7 +42,7 @@ MEASURED_TRAFFIC = {
     "gemma30": 974172036,    # k_moe_stack_fused, one launch (algorithmic 846,151,680 B)
     "zipf": 991925124,       # k_moe_stack_fused, one launch
     "batch16": 7918487317,   # whole step, 30 grouped layers
-    "batch64": 11568345493,  # whole step, 30 grouped layers
+    "batch64": 11709776088,  # whole step, 30 grouped layers (MFMA)
     "large32": 25267396511,  # whole step, 32 grouped layers
     "large1": 132300061,     # k_gemv_gu_long, one launch (algorithmic 132,120,576 B)
 }

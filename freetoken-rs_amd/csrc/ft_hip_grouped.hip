@@ -1047,11 +1047,12 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
         return rc;
     // groups of >= n_mfma tokens take the MFMA tile kernels, the others the
     // dot4 kernels; rows longer than 32 blocks (I > 1024) only the former.
-    // Automatic (0): every group on one family, MFMA from 8 pairs per expert
-    // on (measured on the Gemma shape: dot4 faster at 4 pairs per expert,
-    // MFMA at 8 and 16; one family's launches beat a split of both)
+    // Automatic (0): every group on one family, MFMA from 4 pairs per expert
+    // on (measured on the Gemma shape: dot4 faster at 1 pair per expert,
+    // 168.9 vs 217.5 us/token at batch 16; MFMA at 4, 73.5 vs 76.7 at batch
+    // 64, and above; one family's launches beat a split of both)
     int n_mfma = ctx->grouped_mfma_min;
-    if (n_mfma <= 0) n_mfma = (int64_t)P >= 8 * n_experts ? 1 : std::numeric_limits<int>::max();
+    if (n_mfma <= 0) n_mfma = (int64_t)P >= 4 * n_experts ? 1 : std::numeric_limits<int>::max();
     if (nbj > 32) n_mfma = 1;
     // every expert on the dot4 kernels, routing already in ids: the dot4
     // workgroups find their expert's pairs themselves (no grouping launch)
