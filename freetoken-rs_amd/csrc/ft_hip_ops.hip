@@ -30,7 +30,9 @@ struct GemvArgs {
     const uint8_t* q8;
     int64_t q8_stride_blocks;
     float* y;                  // GEMV output
-    int32_t* dots;             // block-dot dump output
+    int32_t* dots;             // block-dot dump output (layer kernels: the REC record, or null)
+    float* sums;               // layer record (REC): gate|up sums as GELU takes them, [pair][2*inter], or null
+    uint8_t* x8rec;            // layer record (REC, head in the launch): q8 of x per seq, [seq][k/32][40], or null
     int64_t y_stride;
     int n_rows;
     int k;
@@ -165,7 +167,7 @@ __device__ __forceinline__ float gemv_row_part(const uint8_t* wr, int sub, int n
             const int* xb = lds + (b + LPR * u) * 10;
             const float d8 = __int_as_float(xb[0]);
             const int diff = block_dot(q[u], xb + 2, xb[1]);
-            if constexpr (REC) rec[b + LPR * u] = diff;
+            if constexpr (REC) if (rec) rec[b + LPR * u] = diff;
             acc = fmaf((float)diff, d4[u] * d8, acc);
         }
     }
@@ -176,7 +178,7 @@ __device__ __forceinline__ float gemv_row_part(const uint8_t* wr, int sub, int n
         const int* xb = lds + b * 10;
         const float d8 = __int_as_float(xb[0]);
         const int diff = block_dot(q, xb + 2, xb[1]);
-        if constexpr (REC) rec[b] = diff;
+        if constexpr (REC) if (rec) rec[b] = diff;
         acc = fmaf((float)diff, d4 * d8, acc);
     }
     return acc;
@@ -332,6 +334,23 @@ __device__ __forceinline__ void head_prologue(const HeadArgs& h, int s, int H, i
     __syncthreads();
 }
 
+// Layer-record helpers of the REC instantiations (tests only).
+// The q8 row of x_s that a head prologue left in LDS, stored by the seq's
+// first workgroup (blockIdx.x 0 of pair s*div).
+__device__ __forceinline__ void record_x8(const GemvArgs& a, int e, int s, int div, const int* lds) {
+    if (!a.x8rec || blockIdx.x != 0 || e != s * div) return;
+    const int nw = (a.k >> 5) * 10;
+    int* dst = reinterpret_cast<int*>(a.x8rec + (int64_t)s * (a.k >> 5) * Q8_BLK);
+    for (int i = threadIdx.x; i < nw; i += blockDim.x) dst[i] = lds[i];
+}
+// Lane l < 32 of the tail: the scaled gate and up sums of act block blockIdx.x.
+__device__ __forceinline__ void record_sums(const GemvArgs& a, int e, int inter, float gate, float up) {
+    if (!a.sums || threadIdx.x >= 32) return;
+    float* dst = a.sums + (int64_t)e * 2 * inter + (int)blockIdx.x * 32 + threadIdx.x;
+    dst[0] = gate;
+    dst[inter] = up;
+}
+
 // Gate|up GEMV of one pair with GELU(gate)*up and its q8 block in the same
 // launch (replaces gemv_q4r_grouped + gelu_mul_quantize_q8, q4.cu). A
 // workgroup of 64*LPR threads owns gate rows 32j..32j+31 (the first LPR/2
@@ -351,7 +370,13 @@ __device__ __forceinline__ void head_prologue(const HeadArgs& h, int s, int H, i
 // head_prologue (HeadArgs: the previous layer's down launch left the router
 // partials) instead of logits, in_scale and a.q8; the dynamic LDS then holds
 // the q8 row and, after it, the seq's partials (H/16 * (E+1) floats).
-template <int LAYOUT, bool TOPK, int LPR = 8, bool HEAD = false>
+//
+// REC (test record, ft_hip_set_layer_record): the same arithmetic, and the
+// workgroup also stores every int32 block dot of its rows to
+// a.dots[pair][row][block], the scaled gate and up sums it hands to GELU to
+// a.sums[pair][row], and (HEAD) the seq's first workgroup the q8 row of x it
+// computed to a.x8rec[seq]; null pointers are skipped.
+template <int LAYOUT, bool TOPK, int LPR = 8, bool HEAD = false, bool REC = false>
 __global__ __launch_bounds__(64 * LPR, 24 / LPR) void k_gemv_gu_act(GemvArgs a, int inter, uint8_t* q8a,
                                                                   const float* in_scale, int div, const float* logits,
                                                                   const float* escale, int32_t* ids, float* wts,
@@ -369,6 +394,7 @@ __global__ __launch_bounds__(64 * LPR, 24 / LPR) void k_gemv_gu_act(GemvArgs a, 
     const int s = e / div;
     if constexpr (HEAD) {
         head_prologue(h, s, a.k, E, sv, lds, reinterpret_cast<float*>(lds + (a.k >> 5) * 10), hg, &irs);
+        if (REC) record_x8(a, e, s, div, lds);
     } else {
         if (TOPK && t < E) sv[t] = logits[(int64_t)s * E + t];
         stage_q8(a, e, lds);  // its barrier also covers sv
@@ -394,7 +420,8 @@ __global__ __launch_bounds__(64 * LPR, 24 / LPR) void k_gemv_gu_act(GemvArgs a, 
     const bool up = wave >= LPR / 2;
     const int rl = (wave - (up ? LPR / 2 : 0)) * (64 / LPR) + lane / LPR, sub = lane % LPR;
     const int row = (up ? inter : 0) + (int)blockIdx.x * 32 + rl;
-    float acc = gemv_row_part<LAYOUT, LPR>(eb + (int64_t)row * row_bytes_of(LAYOUT, a.k), sub, nb, lds);
+    int32_t* rec = REC && a.dots ? a.dots + ((int64_t)e * 2 * inter + row) * nb : nullptr;
+    float acc = gemv_row_part<LAYOUT, LPR, REC>(eb + (int64_t)row * row_bytes_of(LAYOUT, a.k), sub, nb, lds, rec);
     acc = sum_row_lanes<LPR>(acc);
     if (sub == 0) gs[(up ? 32 : 0) + rl] = acc;
     __syncthreads();
@@ -406,6 +433,7 @@ __global__ __launch_bounds__(64 * LPR, 24 / LPR) void k_gemv_gu_act(GemvArgs a, 
             gate = gate * sc;
             up = up * sc;
         }
+        if (REC) record_sums(a, e, inter, gate, up);
         const float v = gelu_tanh(gate) * up;
         const Q8Lane r = q8_quantize_half(v);
         if (threadIdx.x < 32) q8_store_half(q8a + ((int64_t)e * (inter >> 5) + blockIdx.x) * Q8_BLK, l, r);
@@ -419,7 +447,8 @@ __global__ __launch_bounds__(64 * LPR, 24 / LPR) void k_gemv_gu_act(GemvArgs a, 
 // + ...) for them, pairs in order. LPR lanes per row: 8 is
 // k_gemv_q4_grouped's arithmetic; 16 (long rows) sums each row's blocks in
 // 16 lane chains instead, twice the workgroups. Grid (ceil(H/R), n_seqs).
-template <int LAYOUT, int LPR>
+// REC (test record): every int32 block dot also goes to a.dots[pair][row][block].
+template <int LAYOUT, int LPR, bool REC = false>
 __global__ __launch_bounds__(256) void k_gemv_down_combine(GemvArgs a, const float* wts, const float* x, float* out,
                                                            int k) {
     extern __shared__ int lds[];
@@ -436,9 +465,11 @@ __global__ __launch_bounds__(256) void k_gemv_down_combine(GemvArgs a, const flo
     const int kk = re / R, rl = re - kk * R;
     const int row = (int)blockIdx.x * R + rl;
     float acc = 0.0f;
-    if (row < a.n_rows)
-        acc = gemv_row_part<LAYOUT, LPR>(entry_base(a, s * k + kk) + (int64_t)row * row_bytes_of(LAYOUT, a.k), sub,
-                                         nb, lds + kk * nb * 10);
+    if (row < a.n_rows) {
+        int32_t* rec = REC && a.dots ? a.dots + ((int64_t)(s * k + kk) * a.n_rows + row) * nb : nullptr;
+        acc = gemv_row_part<LAYOUT, LPR, REC>(entry_base(a, s * k + kk) + (int64_t)row * row_bytes_of(LAYOUT, a.k),
+                                              sub, nb, lds + kk * nb * 10, rec);
+    }
     acc = sum_row_lanes<LPR>(acc);
     if (sub == 0) ys[re] = acc;
     __syncthreads();
@@ -461,7 +492,8 @@ __global__ __launch_bounds__(256) void k_gemv_down_combine(GemvArgs a, const flo
 // (wnext, [E][H]) with out, and part[s][c][E] = that of out with itself:
 // k_route_prep's chunk partials P_c, for head_prologue in the next gate|up
 // launch. Grid (H/16, n_seqs), NT = 16*k*LPR threads; E < NT.
-template <int LAYOUT, int LPR, int NT>
+// REC (test record): every int32 block dot also goes to a.dots[pair][row][block].
+template <int LAYOUT, int LPR, int NT, bool REC = false>
 __global__ __launch_bounds__(NT) void k_gemv_down_head(GemvArgs a, const float* wts, const float* x, float* out,
                                                       int k, const float* wnext, float* part, int E) {
     extern __shared__ int lds[];
@@ -488,8 +520,9 @@ __global__ __launch_bounds__(NT) void k_gemv_down_head(GemvArgs a, const float* 
     const int re = wave * (64 / LPR) + lane / LPR, sub = lane % LPR;  // row entry: pair kk, local row rl
     const int kk = re >> 4, rl = re & 15;
     const int row = c * 16 + rl;
-    float acc = gemv_row_part<LAYOUT, LPR>(entry_base(a, s * k + kk) + (int64_t)row * row_bytes_of(LAYOUT, a.k), sub,
-                                           nb, lds + kk * nb * 10);
+    int32_t* rec = REC && a.dots ? a.dots + ((int64_t)(s * k + kk) * H + row) * nb : nullptr;
+    float acc = gemv_row_part<LAYOUT, LPR, REC>(entry_base(a, s * k + kk) + (int64_t)row * row_bytes_of(LAYOUT, a.k),
+                                                sub, nb, lds + kk * nb * 10, rec);
     acc = sum_row_lanes<LPR>(acc);
     if (sub == 0) ys[re] = acc;
     if (!EARLY) load_w();
@@ -561,11 +594,13 @@ __device__ __forceinline__ void long_act_load(const int* lds, int lane, LongAct<
 }
 
 template <int BPL>
-__device__ __forceinline__ float long_row_dot(const LongRow<BPL>& r, const LongAct<BPL>& x, int lane) {
+__device__ __forceinline__ float long_row_dot(const LongRow<BPL>& r, const LongAct<BPL>& x, int lane,
+                                              int32_t* rec = nullptr) {
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < BPL; ++i) {
         const int diff = block_dot(r.q[i], x.w[i] + 2, x.w[i][1]);
+        if (rec) rec[lane + 64 * i] = diff;  // test record (REC launches only pass one)
         const float d4 = h2f((uint16_t)(r.s[i] >> ((lane & 1) * 16)));
         acc = fmaf((float)diff, d4 * __int_as_float(x.w[i][0]), acc);
     }
@@ -580,7 +615,8 @@ __device__ __forceinline__ float long_row_dot(const LongRow<BPL>& r, const LongA
 // up rows I+32j+8w..+7, four rows in flight, a row's slot refilled with the
 // row four later once its dots are done. The activation row's loads go out
 // before the weights' (loads complete in order), their LDS stores after.
-template <bool TOPK, int BPL, bool HEAD = false>
+// REC: the test record of k_gemv_gu_act (block dots, sums, head q8 row).
+template <bool TOPK, int BPL, bool HEAD = false, bool REC = false>
 __global__ __launch_bounds__(256, 4) void k_gemv_gu_long(GemvArgs a, int inter, uint8_t* q8a, const float* in_scale,
                                                          int div, const float* logits, const float* escale,
                                                          int32_t* ids, float* wts, int E, HeadArgs h) {
@@ -611,6 +647,7 @@ __global__ __launch_bounds__(256, 4) void k_gemv_gu_long(GemvArgs a, int inter, 
     };
     if constexpr (HEAD) {
         head_prologue(h, s, a.k, E, sv, lds, reinterpret_cast<float*>(lds + (a.k >> 5) * 10), hg, &irs);
+        if (REC) record_x8(a, e, s, div, lds);
     } else {
         // the q8 row of x (10 words per block: 64*BPL*10 words, XW per thread)
         constexpr int XW = (64 * BPL * 10 + 255) / 256;
@@ -641,7 +678,8 @@ __global__ __launch_bounds__(256, 4) void k_gemv_gu_long(GemvArgs a, int inter, 
     long_act_load<BPL>(lds, lane, xa);
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
-        const float acc = long_row_dot<BPL>(rr[i % RIF], xa, lane);
+        int32_t* rec = REC && a.dots ? a.dots + ((int64_t)e * 2 * inter + row_of(i)) * (64 * BPL) : nullptr;
+        const float acc = long_row_dot<BPL>(rr[i % RIF], xa, lane, rec);
         if (lane == 0) gs[(i < 8 ? 0 : 32) + 8 * wave + (i & 7)] = acc;
         if (i + RIF < RPW) load_row(i + RIF);
     }
@@ -654,6 +692,7 @@ __global__ __launch_bounds__(256, 4) void k_gemv_gu_long(GemvArgs a, int inter, 
             gate = gate * sc;
             up = up * sc;
         }
+        if (REC) record_sums(a, e, inter, gate, up);
         const float v = gelu_tanh(gate) * up;
         const Q8Lane r = q8_quantize_half(v);
         if (threadIdx.x < 32) q8_store_half(q8a + ((int64_t)e * (inter >> 5) + blockIdx.x) * Q8_BLK, l, r);
@@ -1172,16 +1211,43 @@ static int short_lanes(const ft_hip_ctx* ctx, int layout, int64_t n_rows, int64_
 static int gu_long_bpl(int layout, int64_t hidden) {
     return layout == FT_LAYOUT_Q4R && (hidden == 2048 || hidden == 4096) ? (int)(hidden / 2048) : 0;
 }
+template <bool TOPK, bool HEAD, bool REC = false>
+static void launch_gu_long_r(int bpl, dim3 grid, size_t lds, hipStream_t st, const GemvArgs& a, int inter,
+                             uint8_t* q8a, const float* in_scale, int div, const float* logits, const float* escale,
+                             int32_t* ids, float* wts, int E, const HeadArgs& h) {
+    if (bpl == 1)
+        hipLaunchKernelGGL((k_gemv_gu_long<TOPK, 1, HEAD, REC>), grid, dim3(256), lds, st, a, inter, q8a, in_scale,
+                           div, logits, escale, ids, wts, E, h);
+    else
+        hipLaunchKernelGGL((k_gemv_gu_long<TOPK, 2, HEAD, REC>), grid, dim3(256), lds, st, a, inter, q8a, in_scale,
+                           div, logits, escale, ids, wts, E, h);
+}
+// rec: the record instantiation (a layer record is set)
 template <bool TOPK, bool HEAD>
 static void launch_gu_long(int bpl, dim3 grid, size_t lds, hipStream_t st, const GemvArgs& a, int inter, uint8_t* q8a,
                            const float* in_scale, int div, const float* logits, const float* escale, int32_t* ids,
-                           float* wts, int E, const HeadArgs& h) {
-    if (bpl == 1)
-        hipLaunchKernelGGL((k_gemv_gu_long<TOPK, 1, HEAD>), grid, dim3(256), lds, st, a, inter, q8a, in_scale, div,
-                           logits, escale, ids, wts, E, h);
+                           float* wts, int E, const HeadArgs& h, bool rec = false) {
+    if (rec)
+        launch_gu_long_r<TOPK, HEAD, true>(bpl, grid, lds, st, a, inter, q8a, in_scale, div, logits, escale, ids, wts,
+                                           E, h);
     else
-        hipLaunchKernelGGL((k_gemv_gu_long<TOPK, 2, HEAD>), grid, dim3(256), lds, st, a, inter, q8a, in_scale, div,
-                           logits, escale, ids, wts, E, h);
+        launch_gu_long_r<TOPK, HEAD, false>(bpl, grid, lds, st, a, inter, q8a, in_scale, div, logits, escale, ids,
+                                            wts, E, h);
+}
+
+// The gate|up launch with the activation, k_gemv_gu_act<LAYOUT, TOPK,
+// GU_LANES, HEAD> or its record instantiation.
+template <bool TOPK, bool HEAD>
+static void launch_gu_act(int layout, bool rec, dim3 grid, size_t lds, hipStream_t st, const GemvArgs& a, int inter,
+                          uint8_t* q8a, const float* in_scale, int div, const float* logits, const float* escale,
+                          int32_t* ids, float* wts, int E, const HeadArgs& h) {
+    auto kern = layout == FT_LAYOUT_Q4R
+                    ? (rec ? k_gemv_gu_act<FT_LAYOUT_Q4R, TOPK, GU_LANES, HEAD, true>
+                           : k_gemv_gu_act<FT_LAYOUT_Q4R, TOPK, GU_LANES, HEAD, false>)
+                    : (rec ? k_gemv_gu_act<FT_LAYOUT_Q4_0, TOPK, GU_LANES, HEAD, true>
+                           : k_gemv_gu_act<FT_LAYOUT_Q4_0, TOPK, GU_LANES, HEAD, false>);
+    hipLaunchKernelGGL(kern, grid, dim3(64 * GU_LANES), lds, st, a, inter, q8a, in_scale, div, logits, escale, ids,
+                       wts, E, h);
 }
 
 template <int LPR, bool REC>
@@ -1385,18 +1451,19 @@ extern "C" int ft_hip_gemv_gate_up_act(ft_hip_ctx* ctx, void* stream, const void
     a.q8_stride_blocks = hidden / 32;
     a.n_rows = (int)(2 * inter);
     a.k = (int)hidden;
+    // the layer record (tests): the gate|up sums and block dots of the pairs
+    const bool rec = ctx->lrec.on;
+    a.sums = ctx->lrec.gu;
+    a.dots = ctx->lrec.gu_dots;
     const dim3 grid((unsigned)(inter / 32), (unsigned)n_pairs);
     const size_t lds = (size_t)(hidden / 32) * Q8_BLK;
     if (const int bpl = gu_long_bpl(layout, hidden)) {
         launch_gu_long<false, false>(bpl, grid, lds, S(stream), a, (int)inter, (uint8_t*)q8_act, in_scale, (int)x_div,
-                                     nullptr, nullptr, nullptr, nullptr, 0, HeadArgs{});
+                                     nullptr, nullptr, nullptr, nullptr, 0, HeadArgs{}, rec);
         return launch_status(nm);
     }
-    auto kern = layout == FT_LAYOUT_Q4R ? k_gemv_gu_act<FT_LAYOUT_Q4R, false, GU_LANES>
-                                        : k_gemv_gu_act<FT_LAYOUT_Q4_0, false, GU_LANES>;
-    hipLaunchKernelGGL(kern, grid, dim3(64 * GU_LANES), lds, S(stream), a, (int)inter, (uint8_t*)q8_act, in_scale,
-                       (int)x_div, (const float*)nullptr, (const float*)nullptr, (int32_t*)nullptr, (float*)nullptr, 0,
-                       HeadArgs{});
+    launch_gu_act<false, false>(layout, rec, grid, lds, S(stream), a, (int)inter, (uint8_t*)q8_act, in_scale,
+                                (int)x_div, nullptr, nullptr, nullptr, nullptr, 0, HeadArgs{});
     return launch_status(nm);
 }
 
@@ -1546,18 +1613,54 @@ static bool head_fold_ok(int64_t hidden, int64_t inter, int64_t n_experts, int64
 }
 
 // k_gemv_down_head for nt = 16*k*LPR threads (256, 512 or 1024)
-template <int LAYOUT, int LPR>
-static void launch_down_head(int nt, dim3 grid, size_t lds, hipStream_t st, const GemvArgs& a, const float* wts,
-                             const float* x, float* out, int k, const float* wnext, float* part, int E) {
+template <int LAYOUT, int LPR, bool REC>
+static void launch_down_head_r(int nt, dim3 grid, size_t lds, hipStream_t st, const GemvArgs& a, const float* wts,
+                               const float* x, float* out, int k, const float* wnext, float* part, int E) {
     if (nt == 256)
-        hipLaunchKernelGGL((k_gemv_down_head<LAYOUT, LPR, 256>), grid, dim3(256), lds, st, a, wts, x, out, k, wnext,
-                           part, E);
+        hipLaunchKernelGGL((k_gemv_down_head<LAYOUT, LPR, 256, REC>), grid, dim3(256), lds, st, a, wts, x, out, k,
+                           wnext, part, E);
     else if (nt == 512)
-        hipLaunchKernelGGL((k_gemv_down_head<LAYOUT, LPR, 512>), grid, dim3(512), lds, st, a, wts, x, out, k, wnext,
-                           part, E);
+        hipLaunchKernelGGL((k_gemv_down_head<LAYOUT, LPR, 512, REC>), grid, dim3(512), lds, st, a, wts, x, out, k,
+                           wnext, part, E);
     else
-        hipLaunchKernelGGL((k_gemv_down_head<LAYOUT, LPR, 1024>), grid, dim3(1024), lds, st, a, wts, x, out, k, wnext,
-                           part, E);
+        hipLaunchKernelGGL((k_gemv_down_head<LAYOUT, LPR, 1024, REC>), grid, dim3(1024), lds, st, a, wts, x, out, k,
+                           wnext, part, E);
+}
+template <int LAYOUT, int LPR>
+static void launch_down_head(bool rec, int nt, dim3 grid, size_t lds, hipStream_t st, const GemvArgs& a,
+                             const float* wts, const float* x, float* out, int k, const float* wnext, float* part,
+                             int E) {
+    if (rec) launch_down_head_r<LAYOUT, LPR, true>(nt, grid, lds, st, a, wts, x, out, k, wnext, part, E);
+    else launch_down_head_r<LAYOUT, LPR, false>(nt, grid, lds, st, a, wts, x, out, k, wnext, part, E);
+}
+
+// Test record of one layer of the launch-by-launch path (ft_hip_set_layer_record):
+// where this layer's records go, or all null.
+struct LayerRecPtrs {
+    bool on;
+    float* x;
+    uint8_t* q8x;
+    float* gu;
+    uint8_t* act;
+    int32_t* gu_dots;
+    int32_t* dn_dots;
+};
+
+// Layer l's slice of the context's layer record for n_seqs seqs of top_k pairs.
+static LayerRecPtrs layer_rec(const ft_hip_ctx* ctx, int64_t l, int64_t B, int64_t H, int64_t I, int64_t K) {
+    const LayerRecord& r = ctx->lrec;
+    LayerRecPtrs p{};
+    p.on = r.on;
+    if (!r.on) return p;
+    const int64_t P = B * K;
+    auto off = [&](auto* base, int64_t per) { return base ? base + l * per : nullptr; };
+    p.x = off(r.x, B * H);
+    p.q8x = off(r.q8x, B * (H / 32) * Q8_BLK);
+    p.gu = off(r.gu, P * 2 * I);
+    p.act = off(r.act, P * (I / 32) * Q8_BLK);
+    p.gu_dots = off(r.gu_dots, P * 2 * I * (H / 32));
+    p.dn_dots = off(r.dn_dots, P * H * (I / 32));
+    return p;
 }
 
 // One layer of the launch-by-launch path. In a stack (head_fold_ok): part_in
@@ -1570,7 +1673,8 @@ static int moe_layer_impl(const char* nm, ft_hip_ctx* ctx, void* stream, const f
                           const float* router_w, const float* router_bias, const float* expert_scale,
                           const void* bank, uint64_t expert_bytes, int layout, int32_t* ids, float* wts,
                           void* workspace, size_t workspace_bytes, const float* part_in = nullptr,
-                          const float* wnext = nullptr, float* part_out = nullptr) {
+                          const float* wnext = nullptr, float* part_out = nullptr,
+                          const LayerRecPtrs& rec = LayerRecPtrs{}) {
     if (hidden <= 0 || hidden % 128) return fail(FT_HIP_E_SHAPE, "%s: hidden=%lld must be a positive multiple of 128", nm, (long long)hidden);
     if (inter <= 0 || inter % 32) return fail(FT_HIP_E_SHAPE, "%s: inter=%lld must be a positive multiple of 32", nm, (long long)inter);
     if (n_experts <= 0 || n_experts > 1024) return fail(FT_HIP_E_SHAPE, "%s: n_experts not in [1, 1024]", nm);
@@ -1588,6 +1692,10 @@ static int moe_layer_impl(const char* nm, ft_hip_ctx* ctx, void* stream, const f
         return fail(FT_HIP_E_SHAPE, "%s: q4r banks need 16-byte aligned base and expert_bytes", nm);
     if (n_seqs == 0) return FT_HIP_OK;
     int rc;
+    hipStream_t st = S(stream);
+    // test record: this layer's input as read, then (below) q8(x) and the activations
+    if (rec.x && hipMemcpyAsync(rec.x, x, sizeof(float) * n_seqs * hidden, hipMemcpyDeviceToDevice, st) != hipSuccess)
+        return launch_status("moe_layer/record");
     const float* inv = ctx->input_norm ? w.inv : nullptr;
     if ((part_in || wnext) && !head_fold_ok(hidden, inter, n_experts, top_k))
         return fail(FT_HIP_E_SHAPE, "%s: this shape cannot take the layer head from the down launch", nm);
@@ -1603,6 +1711,10 @@ static int moe_layer_impl(const char* nm, ft_hip_ctx* ctx, void* stream, const f
             return rc;
         if ((rc = ft_hip_quantize_q8(ctx, stream, x, hidden, w.q8x, hidden, n_seqs))) return rc;
     }
+    if (!part_in && rec.q8x &&
+        hipMemcpyAsync(rec.q8x, w.q8x, (size_t)n_seqs * (hidden / 32) * Q8_BLK, hipMemcpyDeviceToDevice, st) !=
+            hipSuccess)
+        return launch_status("moe_layer/record");
     // top-k in the gate|up launch when the logits fit one thread each
     const bool topk_in = n_experts <= 256;
     if (!topk_in && (rc = ft_hip_topk_router(ctx, stream, w.logits, expert_scale, ids, wts, n_experts, top_k, n_seqs)))
@@ -1624,36 +1736,39 @@ static int moe_layer_impl(const char* nm, ft_hip_ctx* ctx, void* stream, const f
     const dim3 g_gu((unsigned)(inter / 32), (unsigned)n_pairs);
     const size_t l_gu = (size_t)(hidden / 32) * Q8_BLK;
     const int gbpl = gu_long_bpl(layout, hidden);
+    a.sums = rec.gu;
+    a.dots = rec.gu_dots;
+    a.x8rec = rec.q8x;
     if (part_in) {
         const HeadArgs h{x, part_in, router_bias, ctx->input_norm};
         const size_t l_head = l_gu + (size_t)(hidden / 16) * (n_experts + 1) * 4;
-        if (gbpl) {
-            launch_gu_long<true, true>(gbpl, g_gu, l_head, S(stream), a, (int)inter, w.q8a, nullptr, (int)top_k,
-                                       nullptr, expert_scale, ids, wts, (int)n_experts, h);
-        } else {
-            auto kern = layout == FT_LAYOUT_Q4R ? k_gemv_gu_act<FT_LAYOUT_Q4R, true, GU_LANES, true>
-                                                : k_gemv_gu_act<FT_LAYOUT_Q4_0, true, GU_LANES, true>;
-            hipLaunchKernelGGL(kern, g_gu, dim3(64 * GU_LANES), l_head, S(stream), a, (int)inter, w.q8a,
-                               (const float*)nullptr, (int)top_k, (const float*)nullptr, expert_scale, ids, wts,
-                               (int)n_experts, h);
-        }
+        if (gbpl)
+            launch_gu_long<true, true>(gbpl, g_gu, l_head, st, a, (int)inter, w.q8a, nullptr, (int)top_k, nullptr,
+                                       expert_scale, ids, wts, (int)n_experts, h, rec.on);
+        else
+            launch_gu_act<true, true>(layout, rec.on, g_gu, l_head, st, a, (int)inter, w.q8a, nullptr, (int)top_k,
+                                      nullptr, expert_scale, ids, wts, (int)n_experts, h);
     } else if (gbpl) {
         if (topk_in)
-            launch_gu_long<true, false>(gbpl, g_gu, l_gu, S(stream), a, (int)inter, w.q8a, inv, (int)top_k, w.logits,
-                                        expert_scale, ids, wts, (int)n_experts, HeadArgs{});
+            launch_gu_long<true, false>(gbpl, g_gu, l_gu, st, a, (int)inter, w.q8a, inv, (int)top_k, w.logits,
+                                        expert_scale, ids, wts, (int)n_experts, HeadArgs{}, rec.on);
         else
-            launch_gu_long<false, false>(gbpl, g_gu, l_gu, S(stream), a, (int)inter, w.q8a, inv, (int)top_k, w.logits,
-                                         expert_scale, ids, wts, (int)n_experts, HeadArgs{});
+            launch_gu_long<false, false>(gbpl, g_gu, l_gu, st, a, (int)inter, w.q8a, inv, (int)top_k, w.logits,
+                                         expert_scale, ids, wts, (int)n_experts, HeadArgs{}, rec.on);
+    } else if (topk_in) {
+        launch_gu_act<true, false>(layout, rec.on, g_gu, l_gu, st, a, (int)inter, w.q8a, inv, (int)top_k, w.logits,
+                                   expert_scale, ids, wts, (int)n_experts, HeadArgs{});
     } else {
-        auto kern = layout == FT_LAYOUT_Q4R
-                        ? (topk_in ? k_gemv_gu_act<FT_LAYOUT_Q4R, true, GU_LANES>
-                                   : k_gemv_gu_act<FT_LAYOUT_Q4R, false, GU_LANES>)
-                        : (topk_in ? k_gemv_gu_act<FT_LAYOUT_Q4_0, true, GU_LANES>
-                                   : k_gemv_gu_act<FT_LAYOUT_Q4_0, false, GU_LANES>);
-        hipLaunchKernelGGL(kern, g_gu, dim3(64 * GU_LANES), l_gu, S(stream), a, (int)inter, w.q8a, inv, (int)top_k,
-                           (const float*)w.logits, expert_scale, ids, wts, (int)n_experts, HeadArgs{});
+        launch_gu_act<false, false>(layout, rec.on, g_gu, l_gu, st, a, (int)inter, w.q8a, inv, (int)top_k, w.logits,
+                                    expert_scale, ids, wts, (int)n_experts, HeadArgs{});
     }
     if ((rc = launch_status("moe_layer/gate_up_act"))) return rc;
+    a.sums = nullptr;
+    a.x8rec = nullptr;
+    a.dots = rec.dn_dots;
+    if (rec.act && hipMemcpyAsync(rec.act, w.q8a, (size_t)n_pairs * (inter / 32) * Q8_BLK, hipMemcpyDeviceToDevice,
+                                  st) != hipSuccess)
+        return launch_status("moe_layer/record");
     a.bank_off = (uint64_t)gu_bytes;
     a.x_div = 1;
     a.q8 = w.q8a;
@@ -1669,7 +1784,7 @@ static int moe_layer_impl(const char* nm, ft_hip_ctx* ctx, void* stream, const f
         auto launch = layout == FT_LAYOUT_Q4R
                           ? (lpr == 16 ? launch_down_head<FT_LAYOUT_Q4R, 16> : launch_down_head<FT_LAYOUT_Q4R, 8>)
                           : (lpr == 16 ? launch_down_head<FT_LAYOUT_Q4_0, 16> : launch_down_head<FT_LAYOUT_Q4_0, 8>);
-        launch(nt, g_dn, l_dn, S(stream), a, wts, x, x_out, (int)top_k, wnext, part_out, (int)n_experts);
+        launch(rec.on, nt, g_dn, l_dn, st, a, wts, x, x_out, (int)top_k, wnext, part_out, (int)n_experts);
         return launch_status("moe_layer/down_head");
     }
     if (32 % top_k == 0 && l_dn <= 64 * 1024) {
@@ -1680,12 +1795,30 @@ static int moe_layer_impl(const char* nm, ft_hip_ctx* ctx, void* stream, const f
         const int R = (int)((l16 ? 16 : 32) / top_k);
         const dim3 g_dn((unsigned)((hidden + R - 1) / R), (unsigned)n_seqs);
         auto kern = layout == FT_LAYOUT_Q4R
-                        ? (l16 ? k_gemv_down_combine<FT_LAYOUT_Q4R, 16> : k_gemv_down_combine<FT_LAYOUT_Q4R, 8>)
-                        : (l16 ? k_gemv_down_combine<FT_LAYOUT_Q4_0, 16> : k_gemv_down_combine<FT_LAYOUT_Q4_0, 8>);
-        hipLaunchKernelGGL(kern, g_dn, dim3(256), l_dn, S(stream), a, (const float*)wts, x, x_out, (int)top_k);
+                        ? (l16 ? (rec.on ? k_gemv_down_combine<FT_LAYOUT_Q4R, 16, true>
+                                         : k_gemv_down_combine<FT_LAYOUT_Q4R, 16, false>)
+                               : (rec.on ? k_gemv_down_combine<FT_LAYOUT_Q4R, 8, true>
+                                         : k_gemv_down_combine<FT_LAYOUT_Q4R, 8, false>))
+                        : (l16 ? (rec.on ? k_gemv_down_combine<FT_LAYOUT_Q4_0, 16, true>
+                                         : k_gemv_down_combine<FT_LAYOUT_Q4_0, 16, false>)
+                               : (rec.on ? k_gemv_down_combine<FT_LAYOUT_Q4_0, 8, true>
+                                         : k_gemv_down_combine<FT_LAYOUT_Q4_0, 8, false>));
+        hipLaunchKernelGGL(kern, g_dn, dim3(256), l_dn, st, a, (const float*)wts, x, x_out, (int)top_k);
         return launch_status("moe_layer/down_combine");
     }
-    if ((rc = gemv_common(ctx, stream, a, n_pairs, hidden, inter, layout, false, "moe_layer/down"))) return rc;
+    if (rec.dn_dots) {  // the record instantiation of the grouped GEMV, dots to the layer record
+        a.n_rows = (int)hidden;
+        a.k = (int)inter;
+        const dim3 g_dn((unsigned)((hidden + 31) / 32), (unsigned)n_pairs);
+        const size_t l_q8 = (size_t)(inter / 32) * Q8_BLK;
+        hipLaunchKernelGGL((layout == FT_LAYOUT_Q4R ? k_gemv_q4_grouped<FT_LAYOUT_Q4R, true>
+                                                    : k_gemv_q4_grouped<FT_LAYOUT_Q4_0, true>),
+                           g_dn, dim3(256), l_q8, st, a);
+        if ((rc = launch_status("moe_layer/down"))) return rc;
+    } else {
+        a.dots = nullptr;
+        if ((rc = gemv_common(ctx, stream, a, n_pairs, hidden, inter, layout, false, "moe_layer/down"))) return rc;
+    }
     hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)((hidden + 255) / 256), (unsigned)n_seqs), dim3(256), 0,
                        S(stream), w.ydn, wts, x, x_out, (int)hidden, (int)top_k);
     return launch_status("moe_layer/combine");
@@ -1697,8 +1830,11 @@ extern "C" int ft_hip_moe_layer(ft_hip_ctx* ctx, void* stream, const float* x, f
                                 const void* bank, uint64_t expert_bytes, int layout, int32_t* ids, float* wts,
                                 void* workspace, size_t workspace_bytes) {
     clear_error();
+    // (shape errors are reported before a null context: the record is read only with one)
     return moe_layer_impl("moe_layer", ctx, stream, x, x_out, n_seqs, hidden, inter, n_experts, top_k, router_w,
-                          router_bias, expert_scale, bank, expert_bytes, layout, ids, wts, workspace, workspace_bytes);
+                          router_bias, expert_scale, bank, expert_bytes, layout, ids, wts, workspace, workspace_bytes,
+                          nullptr, nullptr, nullptr,
+                          ctx ? layer_rec(ctx, 0, n_seqs, hidden, inter, top_k) : LayerRecPtrs{});
 }
 
 extern "C" int ft_hip_moe_layer_noalloc(ft_hip_ctx* ctx, void* stream, const float* x, float* x_out,
@@ -1719,7 +1855,8 @@ extern "C" int ft_hip_moe_layer_noalloc(ft_hip_ctx* ctx, void* stream, const flo
                     (long long)top_k, need, FT_HIP_NOALLOC_SCRATCH_BYTES);
     return moe_layer_impl(nm, ctx, stream, x, x_out, n_seqs, hidden, inter, n_experts, top_k, router_w, router_bias,
                           expert_scale, bank, expert_bytes, layout, ids, wts, ctx->noalloc_scratch,
-                          (size_t)FT_HIP_NOALLOC_SCRATCH_BYTES);
+                          (size_t)FT_HIP_NOALLOC_SCRATCH_BYTES, nullptr, nullptr, nullptr,
+                          layer_rec(ctx, 0, n_seqs, hidden, inter, top_k));
 }
 
 // Workspace of ft_hip_moe_stack: a layer's, the two states between layers and
@@ -1783,7 +1920,7 @@ extern "C" int ft_hip_moe_stack(ft_hip_ctx* ctx, void* stream, const float* x_in
                                     ids + l * per, wts + l * per, workspace, sw.layer_bytes,
                                     fold && l > 0 ? sw.part : nullptr,
                                     fold && !last ? routers + (l + 1) * n_experts * hidden : nullptr,
-                                    fold && !last ? sw.part : nullptr))
+                                    fold && !last ? sw.part : nullptr, layer_rec(ctx, l, n_seqs, hidden, inter, top_k)))
             return rc;
     }
     return FT_HIP_OK;

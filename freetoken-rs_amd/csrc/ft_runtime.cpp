@@ -103,6 +103,21 @@ extern "C" int ft_hip_set_block_dot_record(ft_hip_ctx* ctx, int32_t* gu_dots, in
     return FT_HIP_OK;
 }
 
+extern "C" int ft_hip_set_layer_record(ft_hip_ctx* ctx, float* x, void* q8x, float* gu, void* act, int32_t* gu_dots,
+                                       int32_t* dn_dots) {
+    clear_error();
+    if (!ctx) return fail(FT_HIP_E_INVALID, "set_layer_record: null ctx");
+    LayerRecord& r = ctx->lrec;
+    r.x = x;
+    r.q8x = (uint8_t*)q8x;
+    r.gu = gu;
+    r.act = (uint8_t*)act;
+    r.gu_dots = gu_dots;
+    r.dn_dots = dn_dots;
+    r.on = x || q8x || gu || act || gu_dots || dn_dots;
+    return FT_HIP_OK;
+}
+
 extern "C" int ft_hip_destroy(ft_hip_ctx* ctx) {
     clear_error();
     delete ctx;

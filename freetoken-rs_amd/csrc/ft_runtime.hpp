@@ -6,6 +6,18 @@
 
 #include "../../include/ft_hip.h"
 
+// Where ft_hip_set_layer_record sends the launch-by-launch layer path's
+// stage records (tests only); on = any of them set.
+struct LayerRecord {
+    bool on;
+    float* x;
+    uint8_t* q8x;
+    float* gu;
+    uint8_t* act;
+    int32_t* gu_dots;
+    int32_t* dn_dots;
+};
+
 struct ft_hip_ctx {
     int device;
     int num_cus;
@@ -18,6 +30,7 @@ struct ft_hip_ctx {
     int gemv_lanes;        // q4r GEMV lanes per row (ft_hip_set_gemv_lanes): 0 automatic, 8, 16, 32 or 64
     int32_t* rec_gu;       // test record of gate|up block dots (ft_hip_set_block_dot_record), or null
     int32_t* rec_dn;       // test record of down block dots, or null
+    LayerRecord lrec;      // test record of the launch-by-launch layer path (ft_hip_set_layer_record)
     void* noalloc_scratch; // device address of this device's no-alloc scratch array (ft_hip_moe_layer_noalloc)
     char arch[64];
 };

@@ -55,6 +55,15 @@ extern "C" {
     pub fn ft_hip_gen_values(ctx: *mut FtHipCtx, stream: *mut c_void, key: u64, start: i64, n: i64, scale: f32, out: *mut f32) -> c_int;
     pub fn ft_hip_gen_q4_rows(ctx: *mut FtHipCtx, stream: *mut c_void, key: u64, row0: i64, n_rows: i64, k: i64, scale: f32, out: *mut c_void, layout: c_int) -> c_int;
     pub fn ft_hip_set_block_dot_record(ctx: *mut FtHipCtx, gu_dots: *mut i32, dn_dots: *mut i32) -> c_int;
+    pub fn ft_hip_set_layer_record(
+        ctx: *mut FtHipCtx,
+        x: *mut f32,
+        q8x: *mut c_void,
+        gu: *mut f32,
+        act: *mut c_void,
+        gu_dots: *mut i32,
+        dn_dots: *mut i32,
+    ) -> c_int;
     pub fn ft_hip_moe_layer_workspace_bytes(n_seqs: i64, hidden: i64, inter: i64, n_experts: i64, top_k: i64) -> usize;
     pub fn ft_hip_moe_layer(ctx: *mut FtHipCtx, stream: *mut c_void, x: *const f32, x_out: *mut f32, n_seqs: i64, hidden: i64, inter: i64, n_experts: i64, top_k: i64, router_w: *const f32, router_bias: *const f32, expert_scale: *const f32, bank: *const c_void, expert_bytes: u64, layout: c_int, ids: *mut i32, wts: *mut f32, workspace: *mut c_void, workspace_bytes: usize) -> c_int;
     pub fn ft_hip_moe_layer_noalloc(ctx: *mut FtHipCtx, stream: *mut c_void, x: *const f32, x_out: *mut f32, n_seqs: i64, hidden: i64, inter: i64, n_experts: i64, top_k: i64, router_w: *const f32, router_bias: *const f32, expert_scale: *const f32, bank: *const c_void, expert_bytes: u64, layout: c_int, ids: *mut i32, wts: *mut f32) -> c_int;

@@ -71,6 +71,7 @@ SIGNATURES = {
     "ft_hip_set_gemv_lanes": (_I, [_P, _I]),
     "ft_hip_stream_read": (_I, [_P, _P, _P, _U64, _P, _I]),
     "ft_hip_set_block_dot_record": (_I, [_P, _P, _P]),
+    "ft_hip_set_layer_record": (_I, [_P, _P, _P, _P, _P, _P, _P]),
     "ft_hip_fused_workspace_init": (_I, [_P, _P, _P, _SZ]),
     "ft_hip_pack_experts_fused": (_I, [_P, _P, _P, _I, _U64, _P, _I64, _I64, _I64]),
     "ft_hip_pack_router_fused": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
@@ -340,6 +341,12 @@ class Q4Gemv:
         """1: the layer entry points run on rmsnorm(x) (logits and gate|up sums times
         1/sqrt(mean(x*x) + 1e-6)); 0 (default): on x as given."""
         check(lib().ft_hip_set_input_norm(self._ctx, int(on)))
+
+    def set_layer_record(self, x=None, q8x=None, gu=None, act=None, gu_dots=None, dn_dots=None):
+        """Test hook: stage records of the launch-by-launch layer path (see the
+        header); all None turns it off."""
+        check(lib().ft_hip_set_layer_record(self._ctx, _ptr(x), _ptr(q8x), _ptr(gu), _ptr(act), _ptr(gu_dots),
+                                            _ptr(dn_dots)))
 
     def set_block_dot_record(self, gu_dots, dn_dots):
         """Test hook: record every int32 block dot of the grouped / fused

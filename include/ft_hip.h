@@ -201,6 +201,23 @@ int ft_hip_gen_q4_rows(ft_hip_ctx* ctx, void* stream, uint64_t key, int64_t row0
  * Both NULL (the state after create) turns it off; give both or neither. */
 int ft_hip_set_block_dot_record(ft_hip_ctx* ctx, int32_t* gu_dots, int32_t* dn_dots);
 
+/* Test hook (no reference counterpart): while any pointer is set,
+ * ft_hip_moe_layer, ft_hip_moe_layer_noalloc and ft_hip_moe_stack run
+ * instantiations of the launch-by-launch layer kernels that also store the
+ * stages they compute (the production instantiations are unchanged), per
+ * layer l of the call (l = 0 for one layer), seq s and pair p = s*top_k + k:
+ *   x       [l][s][hidden]             f32 layer input as the layer read it
+ *   q8x     [l][s][hidden/32] x 40 B   its q8 blocks as the gate|up launch took them
+ *   gu      [l][p][2*inter]            f32 gate sums then up sums as GELU takes them
+ *                                      (times the input norm's scale when on)
+ *   act     [l][p][inter/32] x 40 B    the activation's q8 blocks
+ *   gu_dots [l][p][2*inter][hidden/32] int32 block dots of the gate|up rows
+ *   dn_dots [l][p][hidden][inter/32]   int32 block dots of the down rows
+ * ft_hip_gemv_gate_up_act stores gu and gu_dots of its pairs ([p][...]).
+ * NULL pointers are skipped; all NULL (the state after create) turns it off. */
+int ft_hip_set_layer_record(ft_hip_ctx* ctx, float* x, void* q8x, float* gu, void* act, int32_t* gu_dots,
+                            int32_t* dn_dots);
+
 /* One MoE expert-FFN layer for n_seqs tokens (the composition of
  * ft-model/src/lib.rs:1406-1476 with host routing replaced by device routing):
  *   logits = router(W_r, x) (+bias) -> top-k/softmax -> q8(x) -> grouped
