@@ -208,6 +208,7 @@ static int parse(ft_gguf* g) {
         uint64_t be, bb;
         if (!block_layout(t.ggml_type, be, bb)) return fail(FT_HIP_E_FORMAT, "gguf: unsupported ggml type %u (tensor %s)", t.ggml_type, t.name.c_str());
         if (nel % be) return fail(FT_HIP_E_FORMAT, "gguf: tensor %s: %llu elements not divisible by block %llu", t.name.c_str(), (unsigned long long)nel, (unsigned long long)be);
+        if (nel / be > UINT64_MAX / bb) return fail(FT_HIP_E_FORMAT, "gguf: tensor %s too large", t.name.c_str());
         t.nbytes = nel / be * bb;
         g->t_index[t.name] = g->tensors.size();
         g->tensors.push_back(std::move(t));
@@ -218,6 +219,7 @@ static int parse(ft_gguf* g) {
         if (!as_u64(g->kv[it->second].second, align) || align == 0)
             return fail(FT_HIP_E_FORMAT, "gguf: general.alignment is not a positive integer");
     }
+    if (align - 1 > UINT64_MAX - c.pos) return fail(FT_HIP_E_FORMAT, "gguf: general.alignment %llu too large", (unsigned long long)align);
     g->data_start = (c.pos + align - 1) / align * align;
     return FT_HIP_OK;
 }

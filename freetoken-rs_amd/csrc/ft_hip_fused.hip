@@ -71,6 +71,8 @@ constexpr int POLL_SLEEP = 1;   // s_sleep units (64 clocks) between polls
 constexpr int NREP = 1;         // replicas of the group broadcast
 constexpr int CTL_EPOCH = 0;    // control words (u32 indices)
 constexpr int CTL_ABORT = 32;
+// CTL_ABORT value of a launch refused because its tags would pass 2^32
+constexpr uint32_t ABORT_EPOCH_WRAP = 0xFFFFFFFFu;
 constexpr int TRACE_SLOTS = 32; // stamps per workgroup per layer in the debug trace
 constexpr int PID_STRIDE = 16;  // words per copy of the predicted experts
 
@@ -156,9 +158,15 @@ __device__ __forceinline__ void st_tag(uint64_t* p, uint32_t tag, uint32_t v) {
 __device__ __forceinline__ uint64_t ld_tag_agent(const uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// Plain store (stays in this XCD's L2): only for consumers on the same XCD.
+// Store that stays in this XCD's L2: only for consumers on the same XCD. A
+// relaxed atomic store (one 64-bit store, never torn) with no cache-policy
+// bits, which is what wavefront scope emits on gfx950 (workgroup scope adds
+// sc0); the L1 writes through, so the line lands in the L2 that the
+// consumer's agent-scope load reads. The scope is narrower than the
+// consumer's: this relies on the two workgroups sharing the XCD's L2, which
+// every unit checks at start (the placement words) before using this form.
 __device__ __forceinline__ void st_tag_local(uint64_t* p, uint32_t tag, uint32_t v) {
-    *p = ((uint64_t)tag << 32) | v;
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
 }
 __device__ __forceinline__ uint32_t xcc_id() {
     return __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20);  // HW_REG_XCC_ID bits 3:0
@@ -736,6 +744,17 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         return;
     }
     const uint32_t epoch = ld_ctl(P.ctl + CTL_EPOCH);
+    // A launch's tags are epoch + 1 .. epoch + 4L + 3 and the next launch
+    // starts at epoch + 4(L+1): that must stay below 2^32, or a tag would wrap
+    // and could match a word not rewritten since an early launch. The host
+    // re-initialises a workspace before that (ft_hip_moe_stack_fused); an
+    // epoch it did not track is refused here, uniformly by every workgroup.
+    if (epoch > 0xFFFFFFFFu - 4u * (uint32_t)(L + 1)) {
+        if (w >= P.n_unit && w < P.n_unit + NGROUP) poison_outputs(P, w - P.n_unit);
+        if (w == 0 && t == 0)
+            __hip_atomic_store(P.ctl + CTL_ABORT, ABORT_EPOCH_WRAP, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     auto tag_g = [&](int l) { return epoch + 4u * l + 1u; };
     auto tag_a = [&](int l) { return epoch + 4u * l + 2u; };
     auto tag_y = [&](int l) { return epoch + 4u * l + 3u; };
@@ -1379,6 +1398,7 @@ extern "C" int ft_hip_fused_workspace_init(ft_hip_ctx* ctx, void* stream, void* 
     clear_error();
     if (!ctx || !workspace) return fail(FT_HIP_E_INVALID, "fused_workspace_init: null argument");
     if (workspace_bytes % 4) return fail(FT_HIP_E_SHAPE, "fused_workspace_init: size not a multiple of 4");
+    if (workspace_bytes < 256) return fail(FT_HIP_E_SHAPE, "fused_workspace_init: workspace too small");
     const int64_t n = (int64_t)(workspace_bytes / 4);
     hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
                        (uint32_t*)workspace, n, 0u);
@@ -1386,7 +1406,20 @@ extern "C" int ft_hip_fused_workspace_init(ft_hip_ctx* ctx, void* stream, void* 
     // epoch 1: tags of zero-filled words never match
     hipLaunchKernelGGL(k_fill_u32, dim3(1), dim3(1), 0, reinterpret_cast<hipStream_t>(stream),
                        (uint32_t*)workspace + CTL_EPOCH, (int64_t)1, 1u);
-    return launch_status("fused_workspace_init");
+    if (int rc = launch_status("fused_workspace_init")) return rc;
+    ctx->fused_epochs[workspace] = 1;
+    return FT_HIP_OK;
+}
+
+extern "C" int ft_hip_fused_workspace_set_epoch(ft_hip_ctx* ctx, void* stream, void* workspace, uint32_t epoch) {
+    clear_error();
+    if (!ctx || !workspace) return fail(FT_HIP_E_INVALID, "fused_workspace_set_epoch: null argument");
+    if (epoch == 0) return fail(FT_HIP_E_SHAPE, "fused_workspace_set_epoch: epoch 0 is reserved");
+    hipLaunchKernelGGL(k_fill_u32, dim3(1), dim3(1), 0, reinterpret_cast<hipStream_t>(stream),
+                       (uint32_t*)workspace + CTL_EPOCH, (int64_t)1, epoch);
+    if (int rc = launch_status("fused_workspace_set_epoch")) return rc;
+    ctx->fused_epochs[workspace] = epoch;
+    return FT_HIP_OK;
 }
 
 extern "C" int ft_hip_pack_experts_fused(ft_hip_ctx* ctx, void* stream, const void* src, int src_layout,
@@ -1501,6 +1534,21 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
     P.spin_limit = ctx->fused_spin_limit;
     P.prefetch = ctx->fused_prefetch;
     P.input_norm = ctx->input_norm;
+    // The epoch guard: a launch advances the workspace's epoch by 4(L+1) and
+    // its tags must stay below 2^32. For a workspace this context initialised
+    // (ft_hip_fused_workspace_init) the epoch is tracked here, and a launch
+    // that would pass the limit is preceded by a re-initialisation on the same
+    // stream (every ~2^32/(4(L+1)) launches: 34.6M for 30 layers, 4 h of
+    // decode at 420 us). An untracked workspace near the limit is refused by
+    // the kernel (ft_hip_fused_status).
+    const uint64_t step = 4ull * (uint64_t)(n_layers + 1);
+    if (step > 0xFFFFFFFFull / 2) return fail(FT_HIP_E_SHAPE, "%s: n_layers=%lld too large", nm, (long long)n_layers);
+    auto ep = ctx->fused_epochs.find(workspace);
+    if (ep != ctx->fused_epochs.end() && ep->second > 0xFFFFFFFFull - step) {
+        if (int rc = ft_hip_fused_workspace_init(ctx, stream, workspace, workspace_bytes)) return rc;
+        clear_error();
+        ep = ctx->fused_epochs.find(workspace);
+    }
     void* args[] = {&P};
     // the Gemma shape (check_fused_shape): 11 gate|up blocks per wave, 6 down
     // blocks per thread, 6 router chunks per group-unit thread; debug records
@@ -1522,6 +1570,7 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
                        : hipLaunchKernel(kern, dim3((unsigned)nw), dim3(FT_THREADS), args, (size_t)P.lds_bytes,
                                          reinterpret_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(FT_HIP_E_LAUNCH, "%s: launch failed: %s", nm, hipGetErrorString(e));
+    if (ep != ctx->fused_epochs.end()) ep->second += step;
     return FT_HIP_OK;
 }
 
@@ -1556,6 +1605,9 @@ extern "C" int ft_hip_fused_status(ft_hip_ctx* ctx, void* workspace, int* aborte
     hipError_t e = hipMemcpy(ctl, workspace, sizeof ctl, hipMemcpyDeviceToHost);
     if (e != hipSuccess) return fail(FT_HIP_E_LAUNCH, "fused_status: %s", hipGetErrorString(e));
     *aborted = ctl[CTL_ABORT] != 0;
+    if (ctl[CTL_ABORT] == ABORT_EPOCH_WRAP)
+        return fail(FT_HIP_E_TIMEOUT, "fused kernel refused a launch whose tags would pass 2^32 (epoch %u); "
+                                      "re-initialise the workspace (ft_hip_fused_workspace_init)", ctl[CTL_EPOCH]);
     if (*aborted) return fail(FT_HIP_E_TIMEOUT, "fused kernel aborted a bounded wait (epoch %u)", ctl[CTL_ABORT]);
     return FT_HIP_OK;
 }

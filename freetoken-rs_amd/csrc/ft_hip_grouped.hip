@@ -635,6 +635,10 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
     };
     auto same_tile = [](const MfUnit& a, const MfUnit& c) { return a.g == c.g && a.j == c.j; };
     uint32_t aw[BPW][4];
+    // vector-memory instructions issue_block issues per block (one 16-byte
+    // buffer load); the wait for a unit's scale loads below counts on it
+    constexpr int VM_PER_BLOCK = 1;
+    static_assert(BPW * VM_PER_BLOCK <= 63, "vmcnt holds at most 63");
     // slot b <- block b of unit u (dead: a descriptor of 0 bytes returns zeros and reads nothing)
     auto issue_block = [&](int b, const MfUnit& u) __attribute__((always_inline)) {
         // one 16-byte load: lane group g takes the four qs words of row
@@ -650,9 +654,15 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
     // the tile's scales (nb * 128 bytes) straight into scale buffer `buf`:
     // 16 bytes per lane, 1 KB per wave and round. Issued right after every
     // wave is past its reads of that buffer (the epilogue's first barrier),
-    // two units before the unit that reads it; that unit is preceded by
-    // VM_AFTER_SCALES, which waits for them (the next unit's BPW * 4 weight
-    // loads are issued after them, so at most that many may still be out).
+    // two units before the unit that reads it. The wait at the end of the
+    // step before that unit (vmcnt <= BPW * VM_PER_BLOCK) covers them: every
+    // wave issues the BPW ring loads of that unit unconditionally after its
+    // scale loads, and loads complete in order, so once at most that many
+    // vector-memory instructions are outstanding the scale loads have landed.
+    // (In the gfx950 build the compiler also places a vmcnt(0) before the
+    // epilogue's later barriers, which drains the ring loads of the next unit
+    // as well; the explicit wait is the one the scales need, not the binding
+    // one.)
     auto issue_scales = [&](int buf, const MfUnit& u) __attribute__((always_inline)) {
         if (!u.live) return;
         const int lane = t & 63;
@@ -781,7 +791,7 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
             reinterpret_cast<uint32_t*>(q8m)[o] = ablk[t];
         }
         if (!nxt.live) return false;
-        __builtin_amdgcn_s_waitcnt(vm_wait_enc(BPW * 4 < 63 ? BPW * 4 : 63));  // nxt's scales are in LDS
+        __builtin_amdgcn_s_waitcnt(vm_wait_enc(BPW * VM_PER_BLOCK));  // nxt's scales are in LDS (see issue_scales)
         if (nxt.g != act_g || nxt.c0 != act_c0) {
             stage_act(nxt);
             act_g = nxt.g;
@@ -1003,7 +1013,10 @@ int check_grouped_shape(const char* nm, int64_t B, int64_t H, int64_t I, int64_t
 
 extern "C" size_t ft_hip_moe_layer_grouped_workspace_bytes(int64_t n_seqs, int64_t hidden, int64_t inter,
                                                            int64_t n_experts, int64_t top_k) {
-    if (n_seqs < 0 || hidden <= 0 || inter <= 0 || n_experts <= 0 || top_k <= 0) return 0;
+    // by division, so that no product below can wrap
+    if (n_seqs < 0 || top_k <= 0 || top_k > 1024 || n_seqs > 65535 / top_k || hidden <= 0 || hidden > 32 * 4096 ||
+        inter <= 0 || inter > 32 * 4096 || n_experts <= 0 || n_experts > 65535)
+        return 0;
     return group_ws(nullptr, n_seqs, hidden, inter, n_experts, top_k).bytes;
 }
 

@@ -809,6 +809,57 @@ __device__ __forceinline__ float rorder_dot(const float* w, const float* xs, int
 // Router logits in the R-order (replaces gemv_f32_rows, q4.cu:1153-1174),
 // times in_scale[s] (input RMS norm) when given, then + bias.
 // Grid (n_rows, n_seqs), one 256-thread workgroup per logit.
+// Grouped activations of Q4Gemv's batched surface, one thread per output:
+// gu [n][2*inter] (gate then up), out [n][inter].
+// SiLU*up: the CPU expression of ft-bench/src/bin/decode.rs:300,
+// g / (1 + expf(-g)) * up, one rounding per op, glibc's expf (restated in
+// ft_libm.hpp): bit-exact with it (replaces silu_mul_grouped, q4.cu:169-179).
+// GELU*up: gelu_tanh of ft-model/src/lib.rs:435-437 (replaces
+// gelu_mul_grouped, q4.cu:289-300).
+template <bool SILU>
+__global__ __launch_bounds__(256) void k_act_mul_grouped(const float* gu, float* out, int64_t inter, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n * inter) return;
+    const int64_t e = i / inter, j = i - e * inter;
+    const float g = gu[e * 2 * inter + j], up = gu[e * 2 * inter + inter + j];
+    float a;
+    if constexpr (SILU) {
+        const float t = expf_libm(-g);
+        const float den = 1.0f + t;
+        a = g / den;  // correctly rounded (HIP default)
+    } else {
+        a = gelu_tanh(g);
+    }
+    out[i] = a * up;
+}
+
+// Weighted reductions over experts (replace reduce_expert_weighted,
+// q4.cu:303-314, and reduce_weighted, q4.cu:182-192): one thread per i,
+// experts in order from 0.0f, one rounding per op:
+//   W: out[i] = out[i] + sum_e (w[e] * y[e][i]);  else out[i] = out[i] + a * sum_e y[e][i].
+template <bool W>
+__global__ __launch_bounds__(256) void k_reduce_experts(const float* y, const float* w, float a, float* out,
+                                                        int64_t hidden, int n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= hidden) return;
+    float s = 0.0f;
+    for (int e = 0; e < n; ++e) {
+        const float v = y[(int64_t)e * hidden + i];
+        if constexpr (W) {
+            const float part = w[e] * v;
+            s = s + part;
+        } else {
+            s = s + v;
+        }
+    }
+    if constexpr (W) {
+        out[i] = out[i] + s;
+    } else {
+        const float as = a * s;
+        out[i] = out[i] + as;
+    }
+}
+
 __global__ __launch_bounds__(256) void k_router_logits(const float* W, const float* x, const float* bias,
                                                       const float* in_scale, float* y, int dim, int n_rows) {
     extern __shared__ float P[];  // dim/16 chunk partials
@@ -1376,6 +1427,54 @@ extern "C" int ft_hip_gelu_mul_q8(ft_hip_ctx* ctx, void* stream, const float* gu
     return launch_status("gelu_mul_q8");
 }
 
+static int act_mul_grouped(bool silu, ft_hip_ctx* ctx, void* stream, const float* gu, float* out, int64_t inter,
+                           int64_t n, const char* nm) {
+    if (inter <= 0) return fail(FT_HIP_E_SHAPE, "%s: inter=%lld must be positive", nm, (long long)inter);
+    if (n < 0) return fail(FT_HIP_E_SHAPE, "%s: negative n_experts", nm);
+    if (n > 0 && inter > ((int64_t)1 << 40) / n) return fail(FT_HIP_E_SHAPE, "%s: inter * n_experts too large", nm);
+    if (!ctx || !gu || !out) return fail(FT_HIP_E_INVALID, "%s: null argument", nm);
+    if (n == 0) return FT_HIP_OK;
+    const int64_t total = n * inter;
+    hipLaunchKernelGGL(silu ? k_act_mul_grouped<true> : k_act_mul_grouped<false>,
+                       dim3((unsigned)((total + 255) / 256)), dim3(256), 0, S(stream), gu, out, inter, n);
+    return launch_status(nm);
+}
+
+extern "C" int ft_hip_silu_mul_grouped(ft_hip_ctx* ctx, void* stream, const float* gu, float* out, int64_t inter,
+                                       int64_t n_experts) {
+    clear_error();
+    return act_mul_grouped(true, ctx, stream, gu, out, inter, n_experts, "silu_mul_grouped");
+}
+
+extern "C" int ft_hip_gelu_mul_grouped(ft_hip_ctx* ctx, void* stream, const float* gu, float* out, int64_t inter,
+                                       int64_t n_experts) {
+    clear_error();
+    return act_mul_grouped(false, ctx, stream, gu, out, inter, n_experts, "gelu_mul_grouped");
+}
+
+static int reduce_experts(bool weighted, ft_hip_ctx* ctx, void* stream, const float* y, const float* wts, float a,
+                          float* out, int64_t hidden, int64_t n, const char* nm) {
+    if (hidden <= 0 || hidden > ((int64_t)1 << 34)) return fail(FT_HIP_E_SHAPE, "%s: hidden out of range", nm);
+    if (n < 0 || n > 65535) return fail(FT_HIP_E_SHAPE, "%s: n_experts not in [0, 65535]", nm);
+    if (!ctx || !y || !out || (weighted && !wts)) return fail(FT_HIP_E_INVALID, "%s: null argument", nm);
+    hipLaunchKernelGGL(weighted ? k_reduce_experts<true> : k_reduce_experts<false>,
+                       dim3((unsigned)((hidden + 255) / 256)), dim3(256), 0, S(stream), y, wts, a, out, hidden,
+                       (int)n);
+    return launch_status(nm);
+}
+
+extern "C" int ft_hip_reduce_expert_weighted(ft_hip_ctx* ctx, void* stream, const float* y, const float* wts,
+                                             float* out, int64_t hidden, int64_t n_experts) {
+    clear_error();
+    return reduce_experts(true, ctx, stream, y, wts, 0.0f, out, hidden, n_experts, "reduce_expert_weighted");
+}
+
+extern "C" int ft_hip_reduce_weighted(ft_hip_ctx* ctx, void* stream, const float* y, float* out, float a,
+                                      int64_t hidden, int64_t n_experts) {
+    clear_error();
+    return reduce_experts(false, ctx, stream, y, nullptr, a, out, hidden, n_experts, "reduce_weighted");
+}
+
 extern "C" int ft_hip_router_logits(ft_hip_ctx* ctx, void* stream, const float* w, const float* x, const float* bias,
                                     float* y, int64_t dim, int64_t n_rows, int64_t n_seqs) {
     clear_error();
@@ -1570,9 +1669,17 @@ static LayerWs layer_ws(void* base, int64_t B, int64_t H, int64_t I, int64_t E, 
     return w;
 }
 
+// The shapes a layer entry point accepts, checked by division so that no
+// product below can overflow: at most 65535 (seq, expert) pairs, rows of at
+// most 131072 weights, at most 1024 experts.
+static bool layer_shape_in_range(int64_t n_seqs, int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k) {
+    return n_seqs >= 0 && top_k > 0 && n_seqs <= 65535 / top_k && hidden > 0 && hidden <= 32 * 4096 && inter > 0 &&
+           inter <= 32 * 4096 && n_experts > 0 && n_experts <= 1024;
+}
+
 extern "C" size_t ft_hip_moe_layer_workspace_bytes(int64_t n_seqs, int64_t hidden, int64_t inter, int64_t n_experts,
                                                    int64_t top_k) {
-    if (n_seqs < 0 || hidden <= 0 || inter <= 0 || n_experts <= 0 || top_k <= 0) return 0;
+    if (!layer_shape_in_range(n_seqs, hidden, inter, n_experts, top_k)) return 0;
     return layer_ws(nullptr, n_seqs, hidden, inter, n_experts, top_k).bytes;
 }
 
@@ -1679,7 +1786,8 @@ static int moe_layer_impl(const char* nm, ft_hip_ctx* ctx, void* stream, const f
     if (inter <= 0 || inter % 32) return fail(FT_HIP_E_SHAPE, "%s: inter=%lld must be a positive multiple of 32", nm, (long long)inter);
     if (n_experts <= 0 || n_experts > 1024) return fail(FT_HIP_E_SHAPE, "%s: n_experts not in [1, 1024]", nm);
     if (top_k <= 0 || top_k > 32 || top_k > n_experts) return fail(FT_HIP_E_SHAPE, "%s: top_k not in [1, min(32, n_experts)]", nm);
-    if (n_seqs < 0 || n_seqs * top_k > 65535) return fail(FT_HIP_E_SHAPE, "%s: n_seqs out of range", nm);
+    // by division: a product of a huge n_seqs could wrap
+    if (n_seqs < 0 || n_seqs > 65535 / top_k) return fail(FT_HIP_E_SHAPE, "%s: n_seqs out of range", nm);
     if (int rc = check_layout(layout)) return rc;
     const int64_t gu_bytes = 2 * inter * row_bytes_of(layout, (int)hidden);
     const int64_t need = gu_bytes + hidden * row_bytes_of(layout, (int)inter);
@@ -1846,6 +1954,9 @@ extern "C" int ft_hip_moe_layer_noalloc(ft_hip_ctx* ctx, void* stream, const flo
     const char* nm = "moe_layer_noalloc";
     if (!ctx) return fail(FT_HIP_E_INVALID, "%s: null ctx", nm);
     if (!ctx->noalloc_scratch) return fail(FT_HIP_E_DEVICE, "%s: the context has no scratch address", nm);
+    if (!layer_shape_in_range(n_seqs, hidden, inter, n_experts, top_k))
+        return fail(FT_HIP_E_SHAPE, "%s: n_seqs=%lld hidden=%lld inter=%lld n_experts=%lld top_k=%lld out of range", nm,
+                    (long long)n_seqs, (long long)hidden, (long long)inter, (long long)n_experts, (long long)top_k);
     const size_t need = ft_hip_moe_layer_workspace_bytes(n_seqs, hidden, inter, n_experts, top_k);
     if (need > (size_t)FT_HIP_NOALLOC_SCRATCH_BYTES)
         return fail(FT_HIP_E_SHAPE,
@@ -1886,7 +1997,7 @@ static StackLayerWs stack_layer_ws(void* base, int64_t B, int64_t H, int64_t I, 
 
 extern "C" size_t ft_hip_moe_stack_workspace_bytes(int64_t n_seqs, int64_t hidden, int64_t inter, int64_t n_experts,
                                                    int64_t top_k) {
-    if (n_seqs < 0 || hidden <= 0 || hidden % 16 || inter <= 0 || n_experts <= 0 || top_k <= 0) return 0;
+    if (!layer_shape_in_range(n_seqs, hidden, inter, n_experts, top_k) || hidden % 16) return 0;
     return stack_layer_ws(nullptr, n_seqs, hidden, inter, n_experts, top_k).bytes;
 }
 

@@ -4,6 +4,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <unordered_map>
+
 #include "../../include/ft_hip.h"
 
 // Where ft_hip_set_layer_record sends the launch-by-launch layer path's
@@ -32,6 +34,8 @@ struct ft_hip_ctx {
     int32_t* rec_dn;       // test record of down block dots, or null
     LayerRecord lrec;      // test record of the launch-by-launch layer path (ft_hip_set_layer_record)
     void* noalloc_scratch; // device address of this device's no-alloc scratch array (ft_hip_moe_layer_noalloc)
+    // fused workspaces this context initialised -> their epoch after the launches it made (the wrap guard)
+    std::unordered_map<const void*, uint64_t> fused_epochs;
     char arch[64];
 };
 

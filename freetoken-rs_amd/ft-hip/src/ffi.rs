@@ -47,6 +47,10 @@ extern "C" {
     pub fn ft_hip_gemv_q4_grouped_slots(ctx: *mut FtHipCtx, stream: *mut c_void, base: *const c_void, expert_bytes: u64, bank_off: u64, slots: *const i32, x_idx: *const i32, n_entries: i64, q8: *const c_void, q8_stride_blocks: i64, y: *mut f32, y_stride: i64, n_rows: i64, k: i64, layout: c_int) -> c_int;
     pub fn ft_hip_q4q8_block_dots(ctx: *mut FtHipCtx, stream: *mut c_void, base: *const c_void, expert_bytes: u64, bank_off: u64, slots: *const i32, x_idx: *const i32, n_entries: i64, q8: *const c_void, q8_stride_blocks: i64, out: *mut i32, n_rows: i64, k: i64, layout: c_int) -> c_int;
     pub fn ft_hip_gelu_mul_q8(ctx: *mut FtHipCtx, stream: *mut c_void, gu: *const f32, q8: *mut c_void, inter: i64, n: i64) -> c_int;
+    pub fn ft_hip_silu_mul_grouped(ctx: *mut FtHipCtx, stream: *mut c_void, gu: *const f32, out: *mut f32, inter: i64, n_experts: i64) -> c_int;
+    pub fn ft_hip_gelu_mul_grouped(ctx: *mut FtHipCtx, stream: *mut c_void, gu: *const f32, out: *mut f32, inter: i64, n_experts: i64) -> c_int;
+    pub fn ft_hip_reduce_expert_weighted(ctx: *mut FtHipCtx, stream: *mut c_void, y: *const f32, wts: *const f32, out: *mut f32, hidden: i64, n_experts: i64) -> c_int;
+    pub fn ft_hip_reduce_weighted(ctx: *mut FtHipCtx, stream: *mut c_void, y: *const f32, out: *mut f32, a: f32, hidden: i64, n_experts: i64) -> c_int;
     pub fn ft_hip_gemv_gate_up_act(ctx: *mut FtHipCtx, stream: *mut c_void, base: *const c_void, expert_bytes: u64, slots: *const i32, n_pairs: i64, x_div: i64, q8x: *const c_void, hidden: i64, inter: i64, layout: c_int, in_scale: *const f32, q8_act: *mut c_void) -> c_int;
     pub fn ft_hip_router_logits(ctx: *mut FtHipCtx, stream: *mut c_void, w: *const f32, x: *const f32, bias: *const f32, y: *mut f32, dim: i64, n_rows: i64, n_seqs: i64) -> c_int;
     pub fn ft_hip_topk_router(ctx: *mut FtHipCtx, stream: *mut c_void, logits: *const f32, expert_scale: *const f32, ids: *mut i32, wts: *mut f32, e_count: i64, k: i64, n_seqs: i64) -> c_int;
@@ -81,6 +85,7 @@ extern "C" {
     pub fn ft_hip_fused_workspace_bytes(hidden: i64, inter: i64, n_experts: i64, top_k: i64) -> usize;
     pub fn ft_hip_fused_workgroups(hidden: i64, inter: i64, n_experts: i64, top_k: i64) -> c_int;
     pub fn ft_hip_fused_workspace_init(ctx: *mut FtHipCtx, stream: *mut c_void, workspace: *mut c_void, workspace_bytes: usize) -> c_int;
+    pub fn ft_hip_fused_workspace_set_epoch(ctx: *mut FtHipCtx, stream: *mut c_void, workspace: *mut c_void, epoch: u32) -> c_int;
     pub fn ft_hip_pack_experts_fused(ctx: *mut FtHipCtx, stream: *mut c_void, src: *const c_void, src_layout: c_int, src_expert_bytes: u64, dst: *mut c_void, n_experts: i64, hidden: i64, inter: i64) -> c_int;
     pub fn ft_hip_pack_router_fused(ctx: *mut FtHipCtx, stream: *mut c_void, src: *const f32, dst: *mut f32, n_layers: i64, n_experts: i64, hidden: i64) -> c_int;
     pub fn ft_hip_moe_stack_fused(ctx: *mut FtHipCtx, stream: *mut c_void, x_in: *const f32, x_out: *mut f32, hidden: i64, inter: i64, n_experts: i64, top_k: i64, n_layers: i64, banks: *const c_void, routers: *const f32, bias: *const f32, expert_scale: *const f32, ids: *mut i32, wts: *mut f32, workspace: *mut c_void, workspace_bytes: usize, dbg_gu: *mut f32, dbg_act: *mut c_void, dbg_x: *mut f32, dbg_trace: *mut u64) -> c_int;

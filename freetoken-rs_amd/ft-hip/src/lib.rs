@@ -131,6 +131,53 @@ impl Q4Gemv {
         })
     }
 
+    /// `gemv_grouped_q8` (ft-cuda/src/lib.rs:926-957): y[e] = W_{slots[e]} q8[e]
+    /// over q4_0 rows at cache + slots[e]*expert_bytes + bank_off;
+    /// q8_stride_blocks = 0 shares one activation row across the experts.
+    #[allow(clippy::too_many_arguments)]
+    pub fn gemv_grouped_q8(&self, s: Stream, cache: DevPtr, expert_bytes: usize, bank_off: usize, slots: DevPtr,
+                           n_experts: usize, q8: DevPtr, q8_stride_blocks: usize, y: DevPtr, y_stride: usize,
+                           n_rows: usize, k: usize) -> Result<()> {
+        self.gemv_grouped_slots(s, cache, expert_bytes, bank_off, slots, None, n_experts, q8, q8_stride_blocks, y,
+                                y_stride, n_rows, k, Layout::Q4_0)
+    }
+
+    /// `gemv_grouped_q8_idx` (ft-cuda/src/lib.rs:772-804): as gemv_grouped_q8,
+    /// entry e reading q8 row x_idx[e].
+    #[allow(clippy::too_many_arguments)]
+    pub fn gemv_grouped_q8_idx(&self, s: Stream, cache: DevPtr, expert_bytes: usize, bank_off: usize, slots: DevPtr,
+                               x_idx: DevPtr, n_entries: usize, q8: DevPtr, q8_stride_blocks: usize, y: DevPtr,
+                               y_stride: usize, n_rows: usize, k: usize) -> Result<()> {
+        self.gemv_grouped_slots(s, cache, expert_bytes, bank_off, slots, Some(x_idx), n_entries, q8,
+                                q8_stride_blocks, y, y_stride, n_rows, k, Layout::Q4_0)
+    }
+
+    /// `silu_mul_grouped` (ft-cuda/src/lib.rs:1053-1072): out[e] = silu(gate)*up,
+    /// bit-exact with the CPU expression of ft-bench/src/bin/decode.rs:300.
+    pub fn silu_mul_grouped(&self, s: Stream, gu: DevPtr, out: DevPtr, inter: usize, n_experts: usize) -> Result<()> {
+        check(unsafe { ffi::ft_hip_silu_mul_grouped(self.ctx, s.0, p(gu), pm(out), inter as i64, n_experts as i64) })
+    }
+
+    /// `gelu_mul_grouped` (ft-cuda/src/lib.rs:1009-1028): out[e] = gelu_tanh(gate)*up
+    /// (ft-model/src/lib.rs:435-437).
+    pub fn gelu_mul_grouped(&self, s: Stream, gu: DevPtr, out: DevPtr, inter: usize, n_experts: usize) -> Result<()> {
+        check(unsafe { ffi::ft_hip_gelu_mul_grouped(self.ctx, s.0, p(gu), pm(out), inter as i64, n_experts as i64) })
+    }
+
+    /// `reduce_expert_weighted` (ft-cuda/src/lib.rs:1031-1050): out += sum_e wts[e] * y[e].
+    pub fn reduce_expert_weighted(&self, s: Stream, y: DevPtr, wts: DevPtr, out: DevPtr, hidden: usize,
+                                  n_experts: usize) -> Result<()> {
+        check(unsafe {
+            ffi::ft_hip_reduce_expert_weighted(self.ctx, s.0, p(y), p(wts), pm(out), hidden as i64, n_experts as i64)
+        })
+    }
+
+    /// `reduce_weighted` (ft-cuda/src/lib.rs:1075-1094): out += a * sum_e y[e].
+    pub fn reduce_weighted(&self, s: Stream, y: DevPtr, out: DevPtr, a: f32, hidden: usize,
+                           n_experts: usize) -> Result<()> {
+        check(unsafe { ffi::ft_hip_reduce_weighted(self.ctx, s.0, p(y), pm(out), a, hidden as i64, n_experts as i64) })
+    }
+
     /// `gemv_q4r_idx` (ft-cuda/src/lib.rs:699-732).
     #[allow(clippy::too_many_arguments)]
     pub fn gemv_q4r_idx(&self, s: Stream, base: DevPtr, expert_bytes: usize, bank_off: usize, slots: DevPtr,
@@ -392,6 +439,10 @@ impl Gguf {
         let mut data: *const c_void = std::ptr::null();
         let mut nb = 0u64;
         check(unsafe { ffi::ft_gguf_tensor_data(self.h, n.as_ptr(), &mut data, &mut nb) })?;
+        // from_raw_parts needs a non-null pointer even for an empty slice
+        if data.is_null() || nb == 0 {
+            return Ok(&[]);
+        }
         Ok(unsafe { std::slice::from_raw_parts(data as *const u8, nb as usize) })
     }
 
@@ -414,6 +465,9 @@ impl Gguf {
         let k = cstr(key)?;
         let (mut s, mut n) = (std::ptr::null(), 0u64);
         check(unsafe { ffi::ft_gguf_meta_str(self.h, k.as_ptr(), &mut s, &mut n) })?;
+        if s.is_null() || n == 0 {
+            return Ok(String::new());
+        }
         let b = unsafe { std::slice::from_raw_parts(s as *const u8, n as usize) };
         Ok(String::from_utf8_lossy(b).into_owned())
     }

@@ -39,6 +39,10 @@ SIGNATURES = {
                                           _I64, _I]),
     "ft_hip_q4q8_block_dots": (_I, [_P, _P, _P, _U64, _U64, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _I]),
     "ft_hip_gelu_mul_q8": (_I, [_P, _P, _P, _P, _I64, _I64]),
+    "ft_hip_silu_mul_grouped": (_I, [_P, _P, _P, _P, _I64, _I64]),
+    "ft_hip_gelu_mul_grouped": (_I, [_P, _P, _P, _P, _I64, _I64]),
+    "ft_hip_reduce_expert_weighted": (_I, [_P, _P, _P, _P, _P, _I64, _I64]),
+    "ft_hip_reduce_weighted": (_I, [_P, _P, _P, _P, ctypes.c_float, _I64, _I64]),
     "ft_hip_gemv_gate_up_act": (_I, [_P, _P, _P, _U64, _P, _I64, _I64, _P, _I64, _I64, _I, _P, _P]),
     "ft_hip_router_logits": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64]),
     "ft_hip_topk_router": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64]),
@@ -73,6 +77,7 @@ SIGNATURES = {
     "ft_hip_set_block_dot_record": (_I, [_P, _P, _P]),
     "ft_hip_set_layer_record": (_I, [_P, _P, _P, _P, _P, _P, _P]),
     "ft_hip_fused_workspace_init": (_I, [_P, _P, _P, _SZ]),
+    "ft_hip_fused_workspace_set_epoch": (_I, [_P, _P, _P, ctypes.c_uint32]),
     "ft_hip_pack_experts_fused": (_I, [_P, _P, _P, _I, _U64, _P, _I64, _I64, _I64]),
     "ft_hip_pack_router_fused": (_I, [_P, _P, _P, _P, _I64, _I64, _I64]),
     "ft_hip_moe_stack_fused": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P,
@@ -224,6 +229,21 @@ class Q4Gemv:
     def gelu_mul_q8(self, gu, q8, inter, n, stream=None):
         check(lib().ft_hip_gelu_mul_q8(self._ctx, _stream(stream), _ptr(gu), _ptr(q8), inter, n))
 
+    # -- ft-cuda/src/lib.rs:1009-1094: grouped activations and expert reductions --
+    def silu_mul_grouped(self, gu, out, inter, n_experts, stream=None):
+        check(lib().ft_hip_silu_mul_grouped(self._ctx, _stream(stream), _ptr(gu), _ptr(out), inter, n_experts))
+
+    def gelu_mul_grouped(self, gu, out, inter, n_experts, stream=None):
+        check(lib().ft_hip_gelu_mul_grouped(self._ctx, _stream(stream), _ptr(gu), _ptr(out), inter, n_experts))
+
+    def reduce_expert_weighted(self, y, wts, out, hidden, n_experts, stream=None):
+        check(lib().ft_hip_reduce_expert_weighted(self._ctx, _stream(stream), _ptr(y), _ptr(wts), _ptr(out), hidden,
+                                                  n_experts))
+
+    def reduce_weighted(self, y, out, a, hidden, n_experts, stream=None):
+        check(lib().ft_hip_reduce_weighted(self._ctx, _stream(stream), _ptr(y), _ptr(out), float(a), hidden,
+                                           n_experts))
+
     # -- ft-model/src/lib.rs:1584-1593 (gate|up GEMV then gelu_mul_q8), one launch --
     def gemv_gate_up_act(self, bank, expert_bytes, slots, n_pairs, x_div, q8x, hidden, inter, q8_act,
                          layout=LAYOUT_Q4R, in_scale=None, stream=None):
@@ -355,7 +375,7 @@ class Q4Gemv:
 
     def set_grouped_mfma_min(self, n_tokens):
         """moe_layer_grouped: experts with >= n_tokens tokens take the MFMA kernels (0, the default:
-        all MFMA from 8 pairs per expert on, else all dot4)."""
+        all MFMA from 4 pairs per expert on, else all dot4)."""
         check(lib().ft_hip_set_grouped_mfma_min(self._ctx, int(n_tokens)))
 
     def stream_read(self, buf, out, n_workgroups, nbytes=None, stream=None):
@@ -369,6 +389,10 @@ class Q4Gemv:
 
     def fused_workspace_init(self, ws, stream=None):
         check(lib().ft_hip_fused_workspace_init(self._ctx, _stream(stream), _ptr(ws), ws.numel() * ws.element_size()))
+
+    def fused_workspace_set_epoch(self, ws, epoch, stream=None):
+        """Test hook: the workspace's epoch (device and this context's wrap guard)."""
+        check(lib().ft_hip_fused_workspace_set_epoch(self._ctx, _stream(stream), _ptr(ws), int(epoch)))
 
     def pack_experts_fused(self, src, src_layout, src_expert_bytes, dst, n_experts, hidden, inter, stream=None):
         check(lib().ft_hip_pack_experts_fused(self._ctx, _stream(stream), _ptr(src), src_layout, src_expert_bytes,

@@ -120,6 +120,36 @@ int ft_hip_q4q8_block_dots(ft_hip_ctx* ctx, void* stream, const void* base,
 int ft_hip_gelu_mul_q8(ft_hip_ctx* ctx, void* stream, const float* gu, void* q8, int64_t inter,
                        int64_t n);
 
+/* Replaces silu_mul_grouped (ft-cuda/src/lib.rs:1053-1072; kernel q4.cu:169-179):
+ * out[e][j] = (g / (1 + expf(-g))) * gu[e][inter + j], g = gu[e][j], for
+ * e < n_experts, j < inter; gu [n_experts][2*inter] f32, out [n_experts][inter].
+ * The f32 expression of the reference's CPU twin (ft-bench/src/bin/decode.rs:300),
+ * one rounding per operation, with glibc's expf: bit-exact with it. */
+int ft_hip_silu_mul_grouped(ft_hip_ctx* ctx, void* stream, const float* gu, float* out, int64_t inter,
+                            int64_t n_experts);
+
+/* Replaces gelu_mul_grouped (ft-cuda/src/lib.rs:1009-1028; kernel q4.cu:289-300):
+ * out[e][j] = gelu_tanh(gu[e][j]) * gu[e][inter + j] with ft-model's CPU GELU
+ * (ft-model/src/lib.rs:435-437; glibc's tanhf), the f32 activations
+ * ft_hip_gelu_mul_q8 quantizes. Shapes as ft_hip_silu_mul_grouped. */
+int ft_hip_gelu_mul_grouped(ft_hip_ctx* ctx, void* stream, const float* gu, float* out, int64_t inter,
+                            int64_t n_experts);
+
+/* Replaces reduce_expert_weighted (ft-cuda/src/lib.rs:1031-1050; kernel
+ * q4.cu:303-314): out[i] = out[i] + s, s = sum over e = 0..n_experts-1 (in
+ * order, from 0) of wts[e] * y[e][i]; y [n_experts][hidden], wts [n_experts],
+ * one rounding per operation (the pair combine's f32 order,
+ * ft-model/src/lib.rs:1634-1646). n_experts = 0 leaves out unchanged. */
+int ft_hip_reduce_expert_weighted(ft_hip_ctx* ctx, void* stream, const float* y, const float* wts,
+                                  float* out, int64_t hidden, int64_t n_experts);
+
+/* Replaces reduce_weighted (ft-cuda/src/lib.rs:1075-1094; kernel q4.cu:182-192):
+ * out[i] = out[i] + a * s, s = sum over e (in order, from 0) of y[e][i], one
+ * rounding per operation (the reference kernel's expression order without
+ * contraction). */
+int ft_hip_reduce_weighted(ft_hip_ctx* ctx, void* stream, const float* y, float* out, float a,
+                           int64_t hidden, int64_t n_experts);
+
 /* Gate|up GEMV and the activation in one launch: replaces gemv_q4r_ptr over
  * the gate|up rows followed by gelu_mul_q8 (ft-model/src/lib.rs:1584-1593;
  * ft-cuda/src/lib.rs:354-374). Pair p runs expert slots[p] (gate|up rows
@@ -329,8 +359,9 @@ int ft_hip_moe_stack_grouped(ft_hip_ctx* ctx, void* stream, const float* x_in, f
  * v_mfma_i32_16x16x32_i8, one q4_0 block per instruction), the others the
  * v_dot4 kernels; results agree to f32 summation order (q8 quants, int32
  * block dots, routing and GELU q8 are the same). 0 (the default) = automatic:
- * every expert on the MFMA kernels when the batch has at least 8 (token,
- * expert) pairs per expert, else every expert on the dot4 kernels; 1 = MFMA
+ * every expert on the MFMA kernels when the batch has at least 4 (token,
+ * expert) pairs per expert (n_seqs * top_k >= 4 * n_experts), else every
+ * expert on the dot4 kernels; 1 = MFMA
  * for every expert. Rows longer than 1024 weights (inter > 1024) always take
  * the MFMA kernels. No reference counterpart (the reference runs one GEMV
  * per (token, expert) pair, ft-model/src/lib.rs:1507-1606). */
@@ -396,8 +427,20 @@ size_t ft_hip_fused_workspace_bytes(int64_t hidden, int64_t inter, int64_t n_exp
 int ft_hip_fused_workgroups(int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k);
 
 /* Zero a fused workspace and set its epoch; call once after allocating it,
- * and again after a launch reported FT_HIP_E_TIMEOUT. */
+ * and again after a launch reported FT_HIP_E_TIMEOUT.
+ * Epoch guard: every launch advances the workspace's 32-bit epoch by
+ * 4*(n_layers+1), and the hand-over tags of a launch must stay below 2^32.
+ * For a workspace initialised through this context, ft_hip_moe_stack_fused
+ * tracks the epoch and re-initialises the workspace on the launch stream
+ * before a launch that would pass the limit (every ~2^32/(4*(L+1)) launches:
+ * 34.6M for 30 layers); a workspace near the limit that this context did not
+ * initialise is refused by the kernel, which ft_hip_fused_status reports. */
 int ft_hip_fused_workspace_init(ft_hip_ctx* ctx, void* stream, void* workspace, size_t workspace_bytes);
+
+/* Test hook (no reference counterpart): set an initialised workspace's epoch
+ * (nonzero) on the device and in this context's epoch guard, so tests can run
+ * launches across the 2^32 limit of the tags. */
+int ft_hip_fused_workspace_set_epoch(ft_hip_ctx* ctx, void* stream, void* workspace, uint32_t epoch);
 
 /* Repack n_experts expert banks (gate rows, up rows, down rows, each in
  * src_layout, src_expert_bytes apart) into the fused layout
@@ -457,8 +500,10 @@ int ft_hip_fused_set_cooperative(ft_hip_ctx* ctx, int on);
 
 /* Host-synchronous check of a fused workspace after the stream has been
  * synchronised: FT_HIP_E_TIMEOUT (and *aborted = 1) if a launch gave up a
- * bounded wait. Such a workspace stays poisoned -- later launches on it do
- * nothing -- until ft_hip_fused_workspace_init. */
+ * bounded wait, or was refused because its tags would have passed 2^32 (the
+ * epoch guard above). Such a workspace stays poisoned -- later launches on it
+ * do nothing but set x_out to NaN and the routing record to -1/NaN -- until
+ * ft_hip_fused_workspace_init. */
 int ft_hip_fused_status(ft_hip_ctx* ctx, void* workspace, int* aborted);
 
 /* ---- local GGUF model files (ft-gguf/src/lib.rs:141-206) ----

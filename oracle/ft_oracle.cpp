@@ -369,6 +369,58 @@ void orc_gelu_mul_q8(const float* gu, int64_t inter, float* act, float* d, int8_
 }
 
 // ---------------------------------------------------------------------------
+// The grouped activations and combines of Q4Gemv's batched MoE surface, as
+// their CPU counterparts compute them, one f32 op at a time:
+// SiLU*up (ft-bench/src/bin/decode.rs:300, the CPU twin of silu_mul_grouped,
+// ft-cuda/src/q4.cu:169-179): g / (1.0 + (-g).exp()) * up, exp = libm expf;
+// GELU*up per expert (gelu_mul_grouped, q4.cu:289-300, with ft-model's CPU
+// GELU of lib.rs:435-437 and :1625-1628).
+// gu [n][2*inter] (gate then up rows), out [n][inter].
+// ---------------------------------------------------------------------------
+void orc_silu_mul_grouped(const float* gu, int64_t inter, int64_t n, float* out) {
+    for (int64_t e = 0; e < n; ++e)
+        for (int64_t j = 0; j < inter; ++j) {
+            const float g = gu[e * 2 * inter + j];
+            const float t = expf(-g);
+            const float den = 1.0f + t;
+            const float sg = g / den;
+            out[e * inter + j] = sg * gu[e * 2 * inter + inter + j];
+        }
+}
+
+void orc_gelu_mul_grouped(const float* gu, int64_t inter, int64_t n, float* out) {
+    for (int64_t e = 0; e < n; ++e)
+        for (int64_t j = 0; j < inter; ++j)
+            out[e * inter + j] = orc_gelu_tanh(gu[e * 2 * inter + j]) * gu[e * 2 * inter + inter + j];
+}
+
+// reduce_expert_weighted (q4.cu:303-314): out[i] = out[i] + s, s = sum over
+// experts in order from 0.0f of (w[e] * y[e][i]) (f32 mul, then add: the
+// pair combine of ft-model/src/lib.rs:1634-1646, without contraction).
+void orc_reduce_expert_weighted(const float* y, const float* w, int64_t H, int64_t n, float* out) {
+    for (int64_t i = 0; i < H; ++i) {
+        float s = 0.0f;
+        for (int64_t e = 0; e < n; ++e) {
+            const float part = w[e] * y[e * H + i];
+            s = s + part;
+        }
+        out[i] = out[i] + s;
+    }
+}
+
+// reduce_weighted (q4.cu:182-192): out[i] = out[i] + a * s, s = sum over
+// experts in order from 0.0f of y[e][i] (definition of this build: the
+// reference's GPU expression order, with no contraction).
+void orc_reduce_weighted(const float* y, float a, int64_t H, int64_t n, float* out) {
+    for (int64_t i = 0; i < H; ++i) {
+        float s = 0.0f;
+        for (int64_t e = 0; e < n; ++e) s = s + y[e * H + i];
+        const float as = a * s;
+        out[i] = out[i] + as;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Router logits in the R-order (definition of this build; the reference has
 // no CPU router and its GPU order is q4.cu:1160-1173).
 //   logit[e] = sum over 8 groups g (in order, from 0.0f) of

@@ -64,6 +64,10 @@ def _declare(L):
         "orc_router_logits": (i32, [P, P, i32, i32, P, P]),
         "orc_topk_softmax": (i32, [P, i32, i32, P, P, P]),
         "orc_combine": (None, [P, P, i32, i64, P, P]),
+        "orc_silu_mul_grouped": (None, [P, i64, i64, P]),
+        "orc_gelu_mul_grouped": (None, [P, i64, i64, P]),
+        "orc_reduce_expert_weighted": (None, [P, P, i64, i64, P]),
+        "orc_reduce_weighted": (None, [P, f32, i64, i64, P]),
         "orc_moe_layer": (i32, [P, i32, i32, i32, i32, P, P, P, P, P, i32, i32, i32,
                                 P, P, P, P, P, P, P, P, P]),
         "orc_rms_inv": (f32, [P, i32]),
@@ -198,6 +202,41 @@ def gelu_mul_q8(gu, inter):
     qs = np.zeros(inter, np.int8)
     lib().orc_gelu_mul_q8(_p(gu), inter, _p(act), _p(d), _p(qs))
     return act, d, qs
+
+
+def silu_mul_grouped(gu, inter):
+    """ft-bench/src/bin/decode.rs:300 per expert: gu [n, 2*inter] -> [n, inter],
+    g / (1 + expf(-g)) * up in f32 (exp is the host libm's expf, as Rust's f32::exp)."""
+    gu = _f32(gu).reshape(-1, 2 * inter)
+    out = np.zeros((gu.shape[0], inter), np.float32)
+    lib().orc_silu_mul_grouped(_p(gu), inter, gu.shape[0], _p(out))
+    return out
+
+
+def gelu_mul_grouped(gu, inter):
+    """ft-model/src/lib.rs:435-437, :1625-1628 per expert: gu [n, 2*inter] -> [n, inter]."""
+    gu = _f32(gu).reshape(-1, 2 * inter)
+    out = np.zeros((gu.shape[0], inter), np.float32)
+    lib().orc_gelu_mul_grouped(_p(gu), inter, gu.shape[0], _p(out))
+    return out
+
+
+def reduce_expert_weighted(y, w, out):
+    """out + sum_e w[e] * y[e] (experts in order; q4.cu:303-314, no contraction)."""
+    y = _f32(y)
+    n, H = y.shape
+    out = _f32(out).ravel().copy()
+    lib().orc_reduce_expert_weighted(_p(y), _p(_f32(w).ravel()), H, n, _p(out))
+    return out
+
+
+def reduce_weighted(y, a, out):
+    """out + a * (sum_e y[e]) (experts in order; q4.cu:182-192, no contraction)."""
+    y = _f32(y)
+    n, H = y.shape
+    out = _f32(out).ravel().copy()
+    lib().orc_reduce_weighted(_p(y), np.float32(a), H, n, _p(out))
+    return out
 
 
 def router_logits(W, x, bias=None):

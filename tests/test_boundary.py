@@ -91,6 +91,41 @@ def test_shape_errors_are_reported_before_any_gpu_call():
     assert rc == ft_hip.E_SHAPE                                          # workspace too small
 
 
+def test_huge_n_seqs_cannot_wrap_the_shape_checks():
+    """A huge n_seqs (2^61 + 1 with top_k 4: the pair count wraps in 64 bits)
+    is rejected by division, and the workspace sizes of such shapes are 0."""
+    L = ft_hip.lib()
+    P = ctypes.c_void_p(16)
+    huge = (1 << 61) + 1
+    rc, msg = _err(L.ft_hip_moe_layer(None, None, P, P, huge, 2816, 704, 128, 4, P, None, None, P, 1 << 30, 1, P,
+                                      P, P, 1 << 30))
+    assert rc == ft_hip.E_SHAPE and "n_seqs" in msg
+    rc, _ = _err(L.ft_hip_moe_layer(None, None, P, P, 65535 // 4 + 1, 2816, 704, 128, 4, P, None, None, P, 1 << 30,
+                                    1, P, P, P, 1 << 30))
+    assert rc == ft_hip.E_SHAPE
+    for fn in ("ft_hip_moe_layer_workspace_bytes", "ft_hip_moe_stack_workspace_bytes",
+               "ft_hip_moe_layer_grouped_workspace_bytes"):
+        assert getattr(L, fn)(huge, 2816, 704, 128, 4) == 0, fn
+        assert getattr(L, fn)(16383, 2816, 704, 128, 4) > 0, fn
+    assert L.ft_hip_moe_layer_workspace_bytes(1, 1 << 40, 704, 128, 8) == 0
+
+
+def test_new_surface_shape_errors():
+    """silu/gelu_mul_grouped and the expert reductions reject bad shapes before any GPU call."""
+    L = ft_hip.lib()
+    P = ctypes.c_void_p(16)
+    for fn in (L.ft_hip_silu_mul_grouped, L.ft_hip_gelu_mul_grouped):
+        assert _err(fn(None, None, P, P, 0, 4))[0] == ft_hip.E_SHAPE          # inter 0
+        assert _err(fn(None, None, P, P, 64, -1))[0] == ft_hip.E_SHAPE        # negative n_experts
+        assert _err(fn(None, None, P, P, 1 << 40, 1 << 20))[0] == ft_hip.E_SHAPE  # inter * n too large
+        assert _err(fn(None, None, None, P, 64, 4))[0] == ft_hip.E_INVALID
+    assert _err(L.ft_hip_reduce_expert_weighted(None, None, P, P, P, 0, 4))[0] == ft_hip.E_SHAPE
+    assert _err(L.ft_hip_reduce_expert_weighted(None, None, P, P, P, 64, 70000))[0] == ft_hip.E_SHAPE
+    assert _err(L.ft_hip_reduce_expert_weighted(None, None, P, None, P, 64, 4))[0] == ft_hip.E_INVALID
+    assert _err(L.ft_hip_reduce_weighted(None, None, P, P, 1.0, -5, 4))[0] == ft_hip.E_SHAPE
+    assert _err(L.ft_hip_reduce_weighted(None, None, P, None, 1.0, 64, 4))[0] == ft_hip.E_INVALID
+
+
 def test_fused_workgroups_formula():
     """K*max(I/32, H/128) expert units, two group units (each with half of
     the experts' router sums) and a pred unit per R-order group."""

@@ -201,6 +201,13 @@ def test_errors(tmp_path):
     assert _err(write(tmp_path, "gt.gguf", bad_ggml)) == ft_hip.E_FORMAT
     ragged, _ = gguf_bytes([], [("t", [33], GG_Q4_0, b"\0" * 18)])
     assert _err(write(tmp_path, "rag.gguf", ragged)) == ft_hip.E_FORMAT
+    # byte sizes that would wrap 64 bits: an f32 tensor of 2^62 elements (the
+    # element count fits, elements x 4 bytes does not), and an alignment so
+    # large that rounding the data start up wraps
+    huge, _ = gguf_bytes([], [("t", [1 << 31, 1 << 31], 0, b"\0" * 4)])
+    assert _err(write(tmp_path, "huge.gguf", huge)) == ft_hip.E_FORMAT
+    big_align, _ = gguf_bytes([("general.alignment", T_U64, (1 << 64) - 8)], [])
+    assert _err(write(tmp_path, "align.gguf", big_align)) == ft_hip.E_FORMAT
     # a tensor whose data runs past the end of the file: open succeeds (as the
     # reference's), tensor_data fails
     short, _ = gguf_bytes([], [("t", [64], GG_Q4_0, b"\0" * 36)])

@@ -384,6 +384,65 @@ def test_fused_plain_build_matches_debug_build(gemv, orc, stack, zstack, which, 
             assert np.array_equal(wts[l].view(np.uint32), we.view(np.uint32)), (token, l)
 
 
+def _epoch(ws):
+    torch.cuda.synchronize()
+    return int(ws[:4].view(torch.int32).cpu().numpy()[0]) & 0xFFFFFFFF
+
+
+def test_fused_epoch_guard_reinitialises_before_wrap(gemv, stack):
+    """Launches across the 2^32 limit of the hand-over tags: with the epoch
+    set so that two launches fit below 2^32, the third is preceded by a
+    re-initialisation of the workspace (epoch back to 1), and every launch
+    gives the first one's bits."""
+    m = stack.m
+    K, L = m.shape.top_k, m.L
+    step = 4 * (L + 1)
+    x = m.hidden(13)
+    stack.reset()
+    ref, ref_ids = torch.zeros_like(x), torch.zeros(L * K, dtype=torch.int32, device=DEV)
+    stack.run(x, ref, ref_ids)
+    stack.check()
+    start = 2 ** 32 - 1 - 2 * step
+    gemv.fused_workspace_set_epoch(stack.ws, start)
+    assert _epoch(stack.ws) == start
+    seen = []
+    for i in range(4):
+        o, ids = torch.zeros_like(x), torch.zeros(L * K, dtype=torch.int32, device=DEV)
+        stack.run(x, o, ids)
+        stack.check()
+        seen.append(_epoch(stack.ws))
+        assert np.array_equal(host(o).view(np.uint32), host(ref).view(np.uint32)), i
+        assert torch.equal(ids, ref_ids), i
+    assert seen == [start + step, 2 ** 32 - 1, 1 + step, 1 + 2 * step]
+
+
+def test_fused_kernel_refuses_untracked_epoch_near_wrap(gemv, stack):
+    """An epoch close to 2^32 that this context did not set (written to the
+    workspace behind the guard's back) is refused by the kernel: outputs
+    marked (NaN, ids -1), the status names the cause, and after
+    ft_hip_fused_workspace_init the stack runs normally again."""
+    m = stack.m
+    K, L = m.shape.top_k, m.L
+    x = m.hidden(14)
+    stack.reset()
+    ref, ref_ids = torch.zeros_like(x), torch.zeros(L * K, dtype=torch.int32, device=DEV)
+    stack.run(x, ref, ref_ids)
+    stack.check()
+    stack.reset()
+    stack.ws[:4].view(torch.int32)[0] = -2  # epoch 0xFFFFFFFE
+    o, ids = torch.zeros_like(x), torch.zeros(L * K, dtype=torch.int32, device=DEV)
+    stack.run(x, o, ids)
+    with pytest.raises(ft_hip.FtHipError) as ei:
+        stack.check()
+    assert "2^32" in str(ei.value)
+    assert np.all(np.isnan(host(o))) and np.all(host(ids) == -1)
+    stack.reset()
+    stack.run(x, o, ids)
+    stack.check()
+    assert np.array_equal(host(o).view(np.uint32), host(ref).view(np.uint32))
+    assert torch.equal(ids, ref_ids)
+
+
 def test_fused_many_launches_full_stack(gemv):
     """Regression test for lost hand-overs: 600 consecutive launches of the
     production build on one workspace over the full 30-layer stack (the

@@ -10,8 +10,8 @@ The ungrouped launch-by-launch layer (one GEMV per pair, as the reference's
 batched path, ft-model/src/lib.rs:1507-1606) must pick the same experts with
 the same weights. With the input RMS norm on, its scale enters the logits
 and the gate|up sums; the same checks hold. The default (mfma_min 0) puts every
-expert on the int8 MFMA tile kernels from 8 pairs per expert on (B = 128) and
-on the dot4 kernels below (B = 16, 64); cases also split the experts at 16 tokens
+expert on the int8 MFMA tile kernels from 4 pairs per expert on (B = 64, 128)
+and on the dot4 kernels below (B = 16); cases also split the experts at 16 tokens
 (both families in one layer) and force every expert onto one family (mfma_min
 1 or 10**6); the large-expert shape (inter 14336) always takes the MFMA
 kernels.

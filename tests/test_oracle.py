@@ -315,6 +315,88 @@ def test_gelu_mul_q8_composition(orc):
 
 
 # ---------------------------------------------------------------------------
+# grouped activations and expert reductions of Q4Gemv's batched surface
+# ---------------------------------------------------------------------------
+
+SPECIAL = np.array([0.0, -0.0, 1.0, -1.0, 88.0, -88.0, 104.0, -104.0, 1e-40, -1e-40, 3.4e38, -3.4e38,
+                    np.inf, -np.inf, np.nan], np.float32)
+
+
+def test_silu_mul_grouped_is_cpu_expression_with_libm_expf(orc):
+    """ft-bench/src/bin/decode.rs:300: g / (1.0 + (-g).exp()) * up, each f32 op
+    rounded in order, exp = libm's expf (called here through ctypes, the
+    arithmetic in numpy f32): a sign slip (exp(g)), a contraction or another
+    order changes bits on these inputs."""
+    I = 64
+    rng = np.random.default_rng(21)
+    g = np.concatenate([SPECIAL, (rng.standard_normal(3 * I - SPECIAL.size) * 6).astype(np.float32)])
+    up = (rng.standard_normal(3 * I) * 3).astype(np.float32)
+    gu = np.concatenate([g.reshape(3, I), up.reshape(3, I)], axis=1)
+    out = orc.silu_mul_grouped(gu, I)
+    expf = libm_f32("expf")
+    f = np.float32
+    with np.errstate(all="ignore"):
+        t = np.array([expf(float(-v)) for v in g], np.float32)
+        expect = ((g / (f(1.0) + t)) * up).reshape(3, I)
+    assert np.array_equal(out.view(np.uint32), expect.view(np.uint32))
+    # closed forms: silu(0) = 0, silu(+inf) * up = inf * up, large negative g -> -0 * up
+    assert out[0, 0] == 0.0 and np.isnan(out[0, 14])
+    assert np.isposinf(out[0, 12]) == (up[12] > 0)
+
+
+def test_gelu_mul_grouped_equals_gelu_mul_q8_activation(orc):
+    """Per expert the f32 activation of gelu_mul_q8 (pinned above against libm's tanhf)."""
+    I = 96
+    rng = np.random.default_rng(22)
+    gu = (rng.standard_normal((5, 2 * I)) * 3).astype(np.float32)
+    gu[0, :SPECIAL.size] = SPECIAL
+    out = orc.gelu_mul_grouped(gu, I)
+    for e in range(5):
+        act, _, _ = orc.gelu_mul_q8(gu[e], I)
+        assert np.array_equal(out[e].view(np.uint32), act.view(np.uint32))
+
+
+def test_reduce_expert_weighted_order_and_no_contraction(orc):
+    """out + sum_e (w[e] * y[e]): exact on small integers; experts summed in
+    order (1e8, -1e8, 1 gives 1, reversed it gives 0); the product rounded
+    before the add (an fma would keep (1+2^-12)^2's low bits)."""
+    rng = np.random.default_rng(23)
+    y = rng.integers(-50, 50, (6, 40)).astype(np.float32)
+    w = np.array([0.5, 2, 1, 0.25, 4, 1], np.float32)
+    out0 = rng.integers(-9, 9, 40).astype(np.float32)
+    assert np.array_equal(orc.reduce_expert_weighted(y, w, out0), out0 + (y * w[:, None]).sum(axis=0))
+    yo = np.array([[1e8], [-1e8], [1.0]], np.float32)
+    assert orc.reduce_expert_weighted(yo, np.ones(3, np.float32), np.zeros(1, np.float32))[0] == 1.0
+    assert orc.reduce_expert_weighted(yo[::-1], np.ones(3, np.float32), np.zeros(1, np.float32))[0] == 0.0
+    a = np.float32(1 + 2.0 ** -12)
+    r = orc.reduce_expert_weighted(np.array([[-1.0], [a]], np.float32), np.array([1.0, a], np.float32),
+                                   np.zeros(1, np.float32))[0]
+    assert r == np.float32(a * a) - np.float32(1.0) and r != np.float32(2.0 ** -11 + 2.0 ** -24)
+    # no experts: out unchanged; f64 agreement on random data
+    assert np.array_equal(orc.reduce_expert_weighted(np.zeros((0, 40), np.float32), np.zeros(0, np.float32),
+                                                     out0), out0)
+    yr = rng.standard_normal((8, 512)).astype(np.float32)
+    wr = rng.random(8).astype(np.float32)
+    ref = (yr.astype(np.float64) * wr[:, None]).sum(axis=0)
+    assert np.max(np.abs(orc.reduce_expert_weighted(yr, wr, np.zeros(512, np.float32)) - ref)) <= 1e-5
+
+
+def test_reduce_weighted_order_and_scale(orc):
+    """out + a * (sum_e y[e]): experts summed in order, then one product, then the add."""
+    rng = np.random.default_rng(24)
+    y = rng.integers(-50, 50, (5, 33)).astype(np.float32)
+    out0 = rng.integers(-9, 9, 33).astype(np.float32)
+    assert np.array_equal(orc.reduce_weighted(y, 0.5, out0), out0 + np.float32(0.5) * y.sum(axis=0))
+    yo = np.array([[1e8], [-1e8], [1.0]], np.float32)
+    assert orc.reduce_weighted(yo, 3.0, np.zeros(1, np.float32))[0] == 3.0
+    assert orc.reduce_weighted(yo[::-1], 3.0, np.zeros(1, np.float32))[0] == 0.0
+    # a * s rounded before the add: out = 1, a = 1 + 2^-12, s = 1 + 2^-12
+    a = np.float32(1 + 2.0 ** -12)
+    r = orc.reduce_weighted(np.array([[a]], np.float32), a, np.array([-1.0], np.float32))[0]
+    assert r == np.float32(a * a) - np.float32(1.0)
+
+
+# ---------------------------------------------------------------------------
 # router logits (R-order), top-k, combine
 # ---------------------------------------------------------------------------
 

@@ -73,3 +73,18 @@ def test_noalloc_rejects_oversized_shape(gemv, layer):
                                m.banks, m.expert_bytes, m.layout, ids, wts)
     assert ei.value.code == ft_hip.E_SHAPE
     assert "scratch" in str(ei.value)
+
+
+def test_noalloc_rejects_wrapping_n_seqs(gemv, layer):
+    """n_seqs = 2^61 + 1 with top_k 4: n_seqs * top_k wraps in 64 bits; the
+    shape is refused by division before any size or offset is formed (no
+    kernel runs: the pointers are never dereferenced)."""
+    m = layer
+    s = m.shape
+    x = torch.zeros(s.hidden, dtype=torch.float32, device=DEV)
+    ids = torch.zeros(4, dtype=torch.int32, device=DEV)
+    wts = torch.zeros(4, dtype=torch.float32, device=DEV)
+    with pytest.raises(ft_hip.FtHipError) as ei:
+        gemv.moe_layer_noalloc(x, x, (1 << 61) + 1, s.hidden, s.inter, s.n_experts, 4, m.routers[0], None, None,
+                               m.banks, m.expert_bytes, m.layout, ids, wts)
+    assert ei.value.code == ft_hip.E_SHAPE
