@@ -569,14 +569,21 @@ __device__ __forceinline__ void scales4(const uint16_t* p, float (&sc)[4]) {
 // weights stream through registers: a wave holds its BPW blocks' qs dwords
 // of a unit, and consuming block b refills that slot with block b of the
 // NEXT unit, so the next tile streams during this unit's MFMAs and its
-// epilogue (wave sums, GELU*up, q8). A tile's f16 scales go through two LDS
-// buffers, loaded two units ahead by direct global-to-LDS loads (no
-// registers). Per (row, token): acc = fma(float(D_b), d4_b * d8_b, acc) over
-// the wave's blocks in block order, then the wave partials in wave order.
-
-// s_waitcnt encoding of "vmcnt <= n" (expcnt and lgkmcnt not waited for)
-constexpr int vm_wait_enc(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
-typedef __attribute__((address_space(3))) uint32_t lds_u32;
+// epilogue (wave sums, GELU*up, q8). A tile's f16 scales go through one LDS
+// buffer as f32 (widened once there, not by each of the 16 lanes of a lane
+// group per block): the next unit's are loaded into registers (16 bytes per
+// thread and round) once every wave is past this unit's MFMAs, and stored to
+// LDS at the end of this unit's epilogue. Per (row, token): acc = fma(float(D_b), d4_b *
+// d8_b, acc) over the wave's blocks in block order, then the wave partials in
+// wave order.
+//
+// The scales once went to LDS by direct global-to-LDS loads two units ahead.
+// A load into LDS completes in order behind the ring's weight loads, and the
+// compiler cannot tell it apart from the epilogue's LDS traffic: the fence of
+// the next barrier and the next LDS read each waited for it with s_waitcnt
+// vmcnt(0), which drained the next unit's weight loads at the start of every
+// epilogue. Loaded into registers, the only wait is the one before their LDS
+// store at the end of the epilogue.
 
 struct MfUnit {
     const uint8_t* T;  // the tile: [nb][64] f16 scales, then [nb][64][16 B] qs
@@ -592,17 +599,17 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
                                                      const float* __restrict__ in_scale, int H, int I, int E, int K,
                                                      int P, int32_t* rec) {
     extern __shared__ __align__(16) uint8_t lds[];
-    constexpr int SPT_LDS = (128 * 128 + GW * 1024 - 1) / (GW * 1024);  // scale rounds, up to nb = 128 (H 4096)
+    constexpr int SPT = (128 * 128 + GT * 16 - 1) / (GT * 16);  // scale rounds, up to nb = 128 (H 4096)
     const int nb = H >> 5, nbj = I >> 5;
     const int n_items = meta[1 + 3 * E] * nbj;  // (group, tile) pairs of the MFMA groups (first in the list)
     const int per = (n_items + (int)gridDim.x - 1) / (int)gridDim.x;
     const int it0 = (int)blockIdx.x * per, it1 = min(n_items, it0 + per);
     if (it0 >= it1) return;
-    // LDS: scales [2][nb][64] f16 | wave partials [GW][64][MT] | sums [MT][64] |
+    // LDS: scales [nb][64] f32 | wave partials [GW][64][MT] | sums [MT][64] |
     // act [MT][32] | act q8 [MT][10] | the chunk's tokens (pair, norm scale)
     // [MT] x2 | the chunk's q8 rows [MT][nb*10 + 1] u32
-    uint16_t* scl2 = reinterpret_cast<uint16_t*>(lds);
-    float* red = reinterpret_cast<float*>(lds + 2 * nb * 128);
+    float* scl = reinterpret_cast<float*>(lds);
+    float* red = reinterpret_cast<float*>(lds + nb * 256);
     float* rows = red + GW * 64 * MT;
     float* actv = rows + MT * 64;
     uint32_t* ablk = reinterpret_cast<uint32_t*>(actv + MT * 32);
@@ -635,10 +642,6 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
     };
     auto same_tile = [](const MfUnit& a, const MfUnit& c) { return a.g == c.g && a.j == c.j; };
     uint32_t aw[BPW][4];
-    // vector-memory instructions issue_block issues per block (one 16-byte
-    // buffer load); the wait for a unit's scale loads below counts on it
-    constexpr int VM_PER_BLOCK = 1;
-    static_assert(BPW * VM_PER_BLOCK <= 63, "vmcnt holds at most 63");
     // slot b <- block b of unit u (dead: a descriptor of 0 bytes returns zeros and reads nothing)
     auto issue_block = [&](int b, const MfUnit& u) __attribute__((always_inline)) {
         // one 16-byte load: lane group g takes the four qs words of row
@@ -651,27 +654,28 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
         aw[b][2] = v.z;
         aw[b][3] = v.w;
     };
-    // the tile's scales (nb * 128 bytes) straight into scale buffer `buf`:
-    // 16 bytes per lane, 1 KB per wave and round. Issued right after every
-    // wave is past its reads of that buffer (the epilogue's first barrier),
-    // two units before the unit that reads it. The wait at the end of the
-    // step before that unit (vmcnt <= BPW * VM_PER_BLOCK) covers them: every
-    // wave issues the BPW ring loads of that unit unconditionally after its
-    // scale loads, and loads complete in order, so once at most that many
-    // vector-memory instructions are outstanding the scale loads have landed.
-    // (In the gfx950 build the compiler also places a vmcnt(0) before the
-    // epilogue's later barriers, which drains the ring loads of the next unit
-    // as well; the explicit wait is the one the scales need, not the binding
-    // one.)
-    auto issue_scales = [&](int buf, const MfUnit& u) __attribute__((always_inline)) {
-        if (!u.live) return;
-        const int lane = t & 63;
+    // unit u's tile scales (nb * 128 bytes of f16) into registers, 16 bytes
+    // per thread and round (dead or past the end: zeros, nothing read), and
+    // from there, widened, into scl once no wave reads the previous tile's
+    u32x4 sst[SPT];
+    auto load_scales = [&](const MfUnit& u) __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t rs = buf_rsrc(u.T, u.live ? (uint32_t)nb * 128 : 0u);
 #pragma unroll
-        for (int r = 0; r < SPT_LDS; ++r) {
-            const int off = (r * GW + wave) * 1024;  // uniform per wave
-            if (off + lane * 16 < nb * 128)
-                __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4*>(u.T + off) + lane,
-                                                 (lds_u32*)(scl2 + buf * nb * 64 + off / 2), 16, 0, 0);
+        for (int r = 0; r < SPT; ++r)  // the offset in the per-lane part: that is the part the range check sees
+            sst[r] = __builtin_amdgcn_raw_buffer_load_b128(rs, (r * GT + t) * 16, 0, 0);
+    };
+    auto store_scales = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < SPT; ++r) {
+            const int i = (r * GT + t) * 8;  // the first of this thread's 8 scales
+            if (i < nb * 64) {
+                const u32x4 h = sst[r];
+                float4* d = reinterpret_cast<float4*>(scl + i);
+                d[0] = make_float4(h2f((uint16_t)(h.x & 0xFFFF)), h2f((uint16_t)(h.x >> 16)),
+                                   h2f((uint16_t)(h.y & 0xFFFF)), h2f((uint16_t)(h.y >> 16)));
+                d[1] = make_float4(h2f((uint16_t)(h.z & 0xFFFF)), h2f((uint16_t)(h.z >> 16)),
+                                   h2f((uint16_t)(h.w & 0xFFFF)), h2f((uint16_t)(h.w >> 16)));
+            }
         }
     };
     // unit u's tokens (pair, norm scale) into tok_p/tok_s and their q8 rows
@@ -691,26 +695,23 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
         }
     };
     // a block's LDS operands: this lane's token words, its d and qsum, and
-    // the 4 scale pairs (rows 16m + 4lg .. +3)
+    // the scales of rows 16m + 4lg .. +3 for the 4 tiles m
     struct Ops {
         uint32_t lo, hi, d, qsum;
-        uint2 sc[4];
+        float4 sc[4];
     };
     MfUnit cur = bind(it0, 0, true);
     MfUnit nxt = after(cur);
-    issue_scales(0, cur);
-    issue_scales(1, nxt);
+    load_scales(cur);
 #pragma unroll
     for (int b = 0; b < BPW; ++b) issue_block(b, cur);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt(0): the scale loads into LDS are done
+    store_scales();
     stage_act(cur);
     int act_g = cur.g, act_c0 = cur.c0;  // the chunk whose q8 rows are in xq
     __syncthreads();
-    auto step = [&](auto par_c) __attribute__((always_inline)) {
-        constexpr int PAR = decltype(par_c)::value;
+    auto step = [&]() __attribute__((always_inline)) {
         const MfUnit n2 = after(nxt);
-        const bool n2_scales = n2.live && !same_tile(n2, cur);  // scl[PAR] holds cur's scales until then
-        const uint16_t* scl = scl2 + PAR * nb * 64;
+        const bool nxt_scales = nxt.live && !same_tile(nxt, cur);  // a new tile (else scl already holds them)
         const int pme = tok_p[li];  // this lane's token pair (REC)
         const uint32_t* xl = xq + li * xs;  // this lane's token row
         auto ops = [&](int blk) __attribute__((always_inline)) {
@@ -720,7 +721,7 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
             o.d = xl[blk * 10];
             o.qsum = xl[blk * 10 + 1];
 #pragma unroll
-            for (int m = 0; m < 4; ++m) o.sc[m] = *reinterpret_cast<const uint2*>(scl + blk * 64 + 16 * m + 4 * lg);
+            for (int m = 0; m < 4; ++m) o.sc[m] = *reinterpret_cast<const float4*>(scl + blk * 64 + 16 * m + 4 * lg);
             return o;
         };
         float acc[4][4];
@@ -753,8 +754,7 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
                             rec[((int64_t)pme * 2 * I + row) * nb + blk] = d[m][v];
                         }
                 }
-                const float sc[4] = {h2f((uint16_t)(cu.sc[m].x & 0xFFFF)), h2f((uint16_t)(cu.sc[m].x >> 16)),
-                                     h2f((uint16_t)(cu.sc[m].y & 0xFFFF)), h2f((uint16_t)(cu.sc[m].y >> 16))};
+                const float sc[4] = {cu.sc[m].x, cu.sc[m].y, cu.sc[m].z, cu.sc[m].w};
 #pragma unroll
                 for (int v = 0; v < 4; ++v) acc[m][v] = fmaf((float)d[m][v], sc[v] * ad, acc[m][v]);
             }
@@ -764,8 +764,8 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
         for (int m = 0; m < 4; ++m)
 #pragma unroll
             for (int v = 0; v < 4; ++v) red[(wave * 64 + 16 * m + 4 * lg + v) * MT + li] = acc[m][v];
-        __syncthreads();  // every wave is past its MFMAs: act rows and scl[PAR] may change below
-        if (n2_scales) issue_scales(PAR, n2);
+        __syncthreads();  // every wave is past its MFMAs: act rows and scl may change below
+        if (nxt_scales) load_scales(nxt);
         for (int i = t; i < cur.nt * 64; i += GT) {  // (token, row) sums over the waves, in wave order
             const int tt = i >> 6, rr = i & 63;
             float sv = 0.0f;
@@ -791,7 +791,7 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
             reinterpret_cast<uint32_t*>(q8m)[o] = ablk[t];
         }
         if (!nxt.live) return false;
-        __builtin_amdgcn_s_waitcnt(vm_wait_enc(BPW * VM_PER_BLOCK));  // nxt's scales are in LDS (see issue_scales)
+        if (nxt_scales) store_scales();
         if (nxt.g != act_g || nxt.c0 != act_c0) {
             stage_act(nxt);
             act_g = nxt.g;
@@ -802,7 +802,7 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
         nxt = n2;
         return true;
     };
-    while (step(std::integral_constant<int, 0>{}) && step(std::integral_constant<int, 1>{})) {
+    while (step()) {
     }
 }
 
@@ -1099,7 +1099,7 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
         if ((rc = launch_status("moe_layer_grouped/gate_up"))) return rc;
     }
     if (mfma) {
-        const size_t lds_mg = (size_t)2 * nb * 128 + sizeof(float) * (GW * 64 * MT + MT * 64 + MT * 32) + 4 * MT * 10 +
+        const size_t lds_mg = (size_t)nb * 256 + sizeof(float) * (GW * 64 * MT + MT * 64 + MT * 32) + 4 * MT * 10 +
                               8 * MT + 4 * (size_t)MT * (nb * 10 + 1);
         auto kern = H == 2816 ? (rec ? k_mfma_gu<11, true> : k_mfma_gu<11, false>)
                               : (rec ? k_mfma_gu<16, true> : k_mfma_gu<16, false>);
