@@ -194,7 +194,11 @@ def bench_dense(args, g):
     the 256 MB last-level cache; `args.steps` launches per GEMV are captured
     in one HIP graph and timed with HIP events on the graph's stream. value =
     30 x (qkv + o_proj + shared gate|up + shared down) + lm_head, the dense
-    GEMV time of one decoded token."""
+    GEMV time of one decoded token. The shared MLP is also timed as the chain
+    a step runs (its input q8 and GELU*up included): the reference's four
+    launches and this library's three with the gate|up launch applying
+    GELU*up and the q8 (config.shared_mlp_chain_us; the token with the faster
+    chain: config.us_per_token_with_shared_chain)."""
     import numpy as np
     import torch
     import ft_hip
@@ -241,6 +245,51 @@ def bench_dense(args, g):
             f"({gbps / HBM_PEAK_GBPS:.1%} of peak), {copies} rotating copies")
         del W, graph
         torch.cuda.empty_cache()
+    # the shared MLP as the chain a decode step runs, from the f32 (normed) input: the reference's
+    # four launches (quantize_q8, gate|up GEMV, gelu_mul_q8, down GEMV; ft-model/src/lib.rs:
+    # 1368-1395) and this library's three (quantize_q8, gemv_gate_up_act, down GEMV), each over
+    # rotating weight copies, `args.steps` chains per graph
+    (gu_rows, H), (_, I) = moe_synth.DENSE["shared_gate_up"], moe_synth.DENSE["shared_down"]
+    gb, db = gu_rows * ft_hip.row_bytes(H, ft_hip.LAYOUT_Q4R), H * ft_hip.row_bytes(I, ft_hip.LAYOUT_Q4R)
+    gc, dc = max(2, -(-1_500_000_000 // gb)), max(2, -(-1_500_000_000 // db))
+    Wg = moe_synth.dense_weights(g, "shared_gate_up", copies=gc, device=dev)
+    Wd = moe_synth.dense_weights(g, "shared_down", copies=dc, device=dev)
+    xs = torch.from_numpy(np.random.default_rng(7).standard_normal(H).astype(np.float32)).to(dev)
+    q8x = torch.zeros(H // 32 * 40, dtype=torch.uint8, device=dev)
+    ygu = torch.zeros(gu_rows, dtype=torch.float32, device=dev)
+    q8a = torch.zeros(I // 32 * 40, dtype=torch.uint8, device=dev)
+    ys = torch.zeros(H, dtype=torch.float32, device=dev)
+    slots = torch.zeros(1, dtype=torch.int32, device=dev)
+    chains = {}
+    for cname in ("reference_4_launches", "fused_3_launches"):
+        def chain(n, cname=cname):
+            for i in range(n):
+                wg, wd = Wg[(i % gc) * gb:(i % gc + 1) * gb], Wd[(i % dc) * db:(i % dc + 1) * db]
+                g.quantize_q8(xs, 0, q8x, H, 1, stream=stream)
+                if cname == "reference_4_launches":
+                    g.gemv_grouped_slots(wg, 0, 0, slots, None, 1, q8x, 0, ygu, gu_rows, gu_rows, H, stream=stream)
+                    g.gelu_mul_q8(ygu, q8a, I, 1, stream=stream)
+                else:
+                    g.gemv_gate_up_act(wg, gb, slots, 1, 1, q8x, H, I, q8a, stream=stream)
+                g.gemv_grouped_slots(wd, 0, 0, slots, None, 1, q8a, 0, ys, H, H, I, stream=stream)
+
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            chain(args.warmup)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                chain(args.steps)
+            graph.replay()
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record(stream)
+            graph.replay()
+            ev1.record(stream)
+        torch.cuda.synchronize()
+        chains[cname] = round(ev0.elapsed_time(ev1) * 1000.0 / args.steps, 3)
+        log(f"[dense] shared MLP chain, {cname}: {chains[cname]:.2f} us")
+        del graph
+    del Wg, Wd
+    torch.cuda.empty_cache()
     # the floor of one launch in the graph: the same entry point on a 1 x 32 matrix
     Wf = torch.empty(ft_hip.row_bytes(32, ft_hip.LAYOUT_Q4R), dtype=torch.uint8, device=dev)
     g.gen_q4_rows(moe_synth.tensor_key(moe_synth.DENSE_CFG, 0, 0, 0), 0, 1, 32, moe_synth.gen_scale(0.02), Wf,
@@ -264,6 +313,9 @@ def bench_dense(args, g):
     L = moe_synth.GEMMA.n_layers
     layer = ["qkv", "o_proj", "shared_gate_up", "shared_down"]
     tok_us = L * sum(per[n]["us"] for n in layer) + per["lm_head"]["us"]
+    # the same token with the shared MLP as the faster of the two chains (its input q8 and GELU*up
+    # included, which the GEMV-only figure above leaves out)
+    tok_chain_us = L * (per["qkv"]["us"] + per["o_proj"]["us"] + min(chains.values())) + per["lm_head"]["us"]
     tok_bytes = L * sum(per[n]["bytes"] for n in layer) + per["lm_head"]["bytes"]
     dom = max(order, key=lambda n: per[n]["us"] * (L if n in layer else 1))
     d = per[dom]
@@ -275,7 +327,8 @@ def bench_dense(args, g):
         "data": "synthetic (seeded Irwin-Hall(4) values of sd 0.02 as q4r weights, sd 1 input)",
         "config": {"workload": "dense q4r GEMVs of the Gemma-4-26B-A4B-shaped decode step, batch 1",
                    "name": "dense", "gemvs": per, "layers": L, "gemv_lanes": args.gemv_lanes or "auto",
-                   "launch_floor_us": round(floor_us, 3)},
+                   "launch_floor_us": round(floor_us, 3), "shared_mlp_chain_us": chains,
+                   "us_per_token_with_shared_chain": round(tok_chain_us, 2)},
         "achieved_GBps": round(tok_bytes / (tok_us * 1e-6) / 1e9, 1),
         "hbm_frac": round(tok_bytes / (tok_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
         "roofline": {"bound": "hbm", "achieved": d["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",

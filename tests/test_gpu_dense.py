@@ -120,14 +120,28 @@ def test_shared_mlp_chain(gemv, orc):
     assert np.array_equal(blk[:, 8:].copy().view(np.int8).ravel(), aq)
     # one launch: gate|up GEMV with GELU*up and q8 (ft_hip_gemv_gate_up_act). Its f32 gate|up sums
     # run in another lane order than the GEMV above, so its q8 may differ from the two-launch one by
-    # the rounding of those sums only: per block d within 1e-5 relative and quants within 1
+    # the rounding of those sums only: per block d within 1e-5 relative and quants within 1. Teacher-
+    # forced on its own sums (the layer record) it is bit-exact: GELU*up q8 of those sums equals the
+    # launch's act q8, and its gate|up block dots equal the oracle's
     q8b = torch.zeros_like(q8a)
     slots = torch.zeros(1, dtype=torch.int32, device=DEV)
-    gemv.gemv_gate_up_act(Wgu, Wgu.numel(), slots, 1, 1, q8_dev(gemv, x), H, I, q8b)
+    gsum = torch.full((1, gu_rows), float("nan"), dtype=torch.float32, device=DEV)
+    gdots = torch.full((1, gu_rows, H // 32), -(2 ** 31), dtype=torch.int32, device=DEV)
+    gemv.set_layer_record(gu=gsum, gu_dots=gdots)
+    try:
+        gemv.gemv_gate_up_act(Wgu, Wgu.numel(), slots, 1, 1, q8_dev(gemv, x), H, I, q8b)
+        G, GD = host(gsum)[0], host(gdots)[0]
+    finally:
+        gemv.set_layer_record()
     b1 = host(q8b).reshape(I // 32, 40)
     d1 = b1[:, :4].copy().view(np.float32)[:, 0]
     assert np.all(np.abs(d1 - ad) <= 1e-5 * np.abs(ad))
     assert np.max(np.abs(b1[:, 8:].copy().view(np.int8).astype(int).ravel() - aq.astype(int))) <= 1
+    _, fd, fq = orc.gelu_mul_q8(G, I)
+    assert np.array_equal(d1.view(np.uint32), fd.view(np.uint32))
+    assert np.array_equal(b1[:, 8:].copy().view(np.int8).ravel(), fq)
+    _, xq8 = orc.q8_quantize(host(x))
+    assert np.array_equal(GD, orc.block_dots(q4r_to_q4_0(host(Wgu), gu_rows, H), xq8, H))
     # down from the act q8, through the grouped GEMV: dots bit-exact, f32 within tolerance
     nb = I // 32
     y = torch.zeros(H, dtype=torch.float32, device=DEV)
