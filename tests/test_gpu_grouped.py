@@ -144,16 +144,17 @@ def test_grouped_repeatable_and_empty(gemv, gstack):
                            gs.bank(0), gs.ids[0], gs.wts[0], gs.ws)
 
 
-@pytest.mark.parametrize("norm", [False, True])
-def test_grouped_large_expert_mfma(gemv, orc, norm):
-    """Config 5's shape (H 4096, 8 experts of I 14336, top-2), 12 tokens in
-    one grouped layer (MFMA kernels, K-split down rows): per token routing
-    bit-exact, act q8 bit-exact from the kernel's own gate|up sums, gate|up
-    sums and outputs within the north-star tolerance."""
+@pytest.mark.parametrize("norm,B", [(False, 12), (True, 12), (True, 32)])
+def test_grouped_large_expert_mfma(gemv, orc, norm, B):
+    """Config 5's shape (H 4096, 8 experts of I 14336, top-2), 12 tokens and
+    config 5's own batch of 32 in one grouped layer (MFMA kernels, K-split
+    down rows): per token routing bit-exact, act q8 bit-exact from the
+    kernel's own gate|up sums, gate|up sums and outputs within the
+    north-star tolerance."""
     m = moe_synth.SyntheticMoE(gemv, moe_synth.LARGE, n_layers=1)
     st = moe_synth.FusedStack(m, workspace=False)
     s = m.shape
-    H, I, E, K, B = s.hidden, s.inter, s.n_experts, s.top_k, 12
+    H, I, E, K = s.hidden, s.inter, s.n_experts, s.top_k
     gs = moe_synth.GroupedStack(st, B)
     x = _hidden(m, B, first=40)
     xo = torch.zeros_like(x)
