@@ -580,9 +580,12 @@ def main():
         torch.cuda.synchronize()
         log(f"[setup] banks repacked for the fused kernel in {time.time() - t1:.1f}s")
 
-        def run(t0_, n):
+        def run(t0_, n, marks=None):
             for t in range(t0_, t0_ + n):
                 stack.run(hidden[t, 0], outs[t, 0])
+                if marks is not None:
+                    marks.append(torch.cuda.Event(enable_timing=True))
+                    marks[-1].record()
     else:
         step = None
         if path == "grouped":
@@ -608,10 +611,13 @@ def main():
         runner = GraphRunner(model, B, C, layer, step)
         log(f"[setup] {C} step(s) per captured HIP graph")
 
-        def run(t0_, n):
+        def run(t0_, n, marks=None):
             for c in range(t0_, t0_ + n, C):
                 runner.run_chunk(hidden[c:c + C])
                 outs[c:c + C].copy_(runner.out)
+                if marks is not None:
+                    marks.append(torch.cuda.Event(enable_timing=True))
+                    marks[-1].record()
 
     if args.copy_calib > 0:
         n = args.copy_calib << 18
@@ -635,6 +641,16 @@ def main():
     ms = ev0.elapsed_time(ev1)
     us_step = ms * 1000.0 / args.steps
     us_tok = us_step / B
+    # the distribution, from a second pass over the same steps with an event after each token
+    # (fused) or captured chunk of steps (kept out of the timed pass above)
+    marks = []
+    ev2 = torch.cuda.Event(enable_timing=True)
+    ev2.record()
+    run(args.warmup, args.steps, marks)
+    torch.cuda.synchronize()
+    per = args.steps / max(1, len(marks))  # steps per mark
+    spans = [a.elapsed_time(b) * 1000.0 / (per * B) for a, b in zip([ev2] + marks[:-1], marks)]
+    us_tok_p50, us_tok_p90 = float(np.percentile(spans, 50)), float(np.percentile(spans, 90))
     e_bytes = moe_synth.algorithmic_expert_bytes(shape)
     router_bytes = E * H * 4 * model.L
     if B == 1:
@@ -740,6 +756,9 @@ def main():
         "metric": METRIC,
         "value": round(us_tok, 2),
         "unit": "us/token",
+        "us_per_token_p50": round(us_tok_p50, 2),
+        "us_per_token_p90": round(us_tok_p90, 2),
+        "p50_over": f"{len(marks)} spans of {per:g} step(s) each, HIP events between them, in a second pass",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
