@@ -138,6 +138,8 @@ __device__ __forceinline__ float swz_xor16_f(float v) {
     return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
 }
 __device__ __forceinline__ int swz_xor16_i(int v) { return __builtin_amdgcn_ds_swizzle(v, 0x401F); }
+// lane ^ 4 (bit-mask mode: xor 4, and 0x1F)
+__device__ __forceinline__ int swz_xor4_i(int v) { return __builtin_amdgcn_ds_swizzle(v, 0x101F); }
 
 // All-lane max / sum over the 32 lanes of a half-wave (every one active):
 // DPP within rows of 16 (quad xor 1, quad xor 2, half-row mirror, row

@@ -448,7 +448,9 @@ __device__ __forceinline__ void route_units(const FusedParams& P, Misc* m, const
             float ss = 0.0f;
 #pragma unroll
             for (int g = 0; g < NGROUP; ++g) ss = ss + gv[g];
-            ir = 1.0f / sqrtf(ss / (float)P.H + 1e-6f);  // correctly rounded (HIP default)
+            int Hs = P.H;
+            asm volatile("" : "+s"(Hs));  // (float)H formed here: hoisted, it was spilled and reloaded
+            ir = 1.0f / sqrtf(ss / (float)Hs + 1e-6f);  // correctly rounded (HIP default)
         }
         uint64_t key = 0xFFFFFFFFu - (uint32_t)t;  // indices >= E: distinct, below every real key
         if (t < E) {
@@ -500,7 +502,7 @@ __device__ __forceinline__ void route_units(const FusedParams& P, Misc* m, const
         }
         rk += quad_xor1i(rk);
         rk += quad_xor2i(rk);
-        rk += __shfl_xor(rk, 4);
+        rk += swz_xor4_i(rk);  // no lane-address register (a shuffle's was spilled and reloaded)
         if (pp == 0 && rk < K) {  // ranks are distinct: each slot written once
             const int i = (int)(0xFFFFFFFFu - (uint32_t)kc);
             m->sel_i[rk] = i;
@@ -1111,8 +1113,12 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                 int qsum;
                 const uint32_t wq = q8_quantize_lanes32(a, &d, &qsum);
                 uint64_t* dst = P.act_t + ((int64_t)u * nbj + j) * 10;
-                const int k = (t & 3) == 0 ? 2 + (t >> 2) : (t == 1 ? 0 : (t == 2 ? 1 : -1));
-                const uint32_t v = t == 1 ? __float_as_uint(d) : (t == 2 ? (uint32_t)qsum : wq);
+                // the word index from the opaque lane index: hoisted out of the
+                // layer loop, the store's address was spilled and reloaded (with a
+                // vmcnt(0) in front of the hand-over)
+                const int ta = tid_here();
+                const int k = (ta & 3) == 0 ? 2 + (ta >> 2) : (ta == 1 ? 0 : (ta == 2 ? 1 : -1));
+                const uint32_t v = ta == 1 ? __float_as_uint(d) : (ta == 2 ? (uint32_t)qsum : wq);
                 if (k >= 0) {
                     if (act_local) st_tag_local(dst + k, tag_a(l), v);
                     else st_tag(dst + k, tag_a(l), v);
@@ -1171,7 +1177,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         // now, checked after the down dots, when every older load of this wave
         // has landed anyway, so it never stalls the chain
         uint64_t pid_raw = 0;
-        if (pf && l + 1 < L && t < K) pid_raw = ld_tag(pid_buf(l + 1) + prep * PID_STRIDE + t);
+        if (pf && l + 1 < L && tid_here() < K) pid_raw = ld_tag(pid_buf(l + 1) + prep * PID_STRIDE + tid_here());
         // ---- down: the act blocks of unit group u, then y of 128 rows ----
         if (dm) {
             // act8: [nbj blocks x 32 B qs][nbj (d, qsum) pairs] (16-B aligned qs)
@@ -1217,9 +1223,10 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         // ---- prefetch: the predicted expert of layer l+1 for this unit group ----
         if (pf) {
             bool ok = true;
-            if (t < K) {
+            const int tq = tid_here();  // the lane tests and the LDS address formed here (hoisted, they spilled)
+            if (tq < K) {
                 ok = (uint32_t)(pid_raw >> 32) == tag_g(l + 1);
-                m->pid[(l + 1) & 1][t] = (int)(uint32_t)pid_raw;
+                m->pid[(l + 1) & 1][tq] = (int)(uint32_t)pid_raw;
             }
             // not yet published (late pred units): the bounded wait
             if (!__syncthreads_and(ok) &&
