@@ -83,6 +83,9 @@ def parse():
     ap.add_argument("--layers", type=int, default=0, help="0 = the config's layer count")
     ap.add_argument("--prefetch", type=int, choices=[0, 1], default=1,
                     help="fused path: stream the early-routed experts of the next layer ahead (1) or not (0)")
+    ap.add_argument("--refine", type=int, choices=[0, 1], default=1,
+                    help="fused path: prefetch the refined prediction (R_{l+1} x_l + sum_p w_p M_p a_p, from the "
+                         "table ft_hip_fused_build_predictor builds at setup) (1) or the early routing's alone (0)")
     ap.add_argument("--trace", default="", metavar="NPY",
                     help="fused path: after timing, run one more token recording every workgroup's phase stamps "
                          "(wall clock, 100 MHz) into this .npy file, shape [workgroups][layers+1][32]")
@@ -576,7 +579,7 @@ def main():
     if path == "fused":
         t1 = time.time()
         g.fused_set_prefetch(args.prefetch)
-        stack = moe_synth.FusedStack(model)
+        stack = moe_synth.FusedStack(model, predictor=bool(args.refine))
         torch.cuda.synchronize()
         log(f"[setup] banks repacked for the fused kernel in {time.time() - t1:.1f}s")
 
@@ -749,7 +752,8 @@ def main():
                "host_cpu": cpu_name, "host_logical_cpus": n_logical}
 
     workload = {1: "", 2: "", 3: ", Zipf(1.1) router bias", 4: "", 5: ""}[cfg_id]
-    profiled_opts = (args.path == "auto" and args.prefetch == 1 and args.input_norm == 1 and args.mfma_min == 0
+    profiled_opts = (args.path == "auto" and args.prefetch == 1 and args.refine == 1 and args.input_norm == 1
+                     and args.mfma_min == 0
                      and args.layers == 0 and not args.trace)
     traffic = MEASURED_TRAFFIC.get(args.config) if profiled_opts else None
     res = {
@@ -773,6 +777,8 @@ def main():
                    "baseline_config": cfg_id, "name": args.config,
                    "hidden": H, "inter": I, "experts": E, "top_k": k, "layers": model.L, "batch": B,
                    "path": path, "prefetch": bool(args.prefetch) if path == "fused" else None,
+                   "prediction": ("refined" if args.refine else "early routing") if path == "fused" and args.prefetch
+                   else None,
                    "input_norm": bool(args.input_norm),
                    "zipf_tau": moe_synth.ZIPF_TAU[(shape.name, zipf_s)] if zipf_s else None,
                    "mfma_min_tokens": args.mfma_min if path == "grouped" else None,

@@ -13,15 +13,17 @@
 // (the alternatives measured 1.4-20 us per barrier on this part).
 //
 // Why prefetch: a layer's hand-over chain (act -> y -> routing) is several
-// us during which HBM would sit idle. The router of layer l+1 applied to x_l
-// ("early routing") picks most of layer l+1's experts, so every unit group
-// streams the tiles of its PREDICTED expert of layer l+1 into registers as
-// soon as it has finished layer l's dots, overlapping the stream with the
-// chain. When the true routing arrives, predicted experts that were routed
-// stay with the unit group that holds them; only the remaining unit groups
-// load the experts nobody predicted (a miss).
+// us during which HBM would sit idle. Every unit group streams the tiles of
+// its PREDICTED expert of layer l+1 into registers as soon as it has
+// finished layer l's dots, overlapping the stream with the chain. When the
+// true routing arrives, predicted experts that were routed stay with the
+// unit group that holds them; only the remaining unit groups load the
+// experts nobody predicted (a miss). The prediction: the router of layer
+// l+1 applied to x_l ("early routing", ~88 % of experts), refined, when a
+// table M_{l,e} = R_{l+1} D_{l,e} is set, by the layer's own act blocks:
+// R_{l+1} x_{l+1} = R_{l+1} x_l + sum_p w_p M_p a_p (~99 %).
 //
-// Workgroups (G shape: H 2816, I 704, E 128, top-8): 200.
+// Workgroups (G shape: H 2816, I 704, E 128, top-8): 208.
 //   expert unit (u, j), 176 of them, unit group u = w % K, j = w / K:
 //     gate|up : 64 rows (32 gate, 32 up) of its expert for act block j
 //               (32 columns), H/32 blocks held in registers by 8 waves;
@@ -43,9 +45,14 @@
 //     of the rows and their sum of squares; publishes them (hop C),
 //     double-buffered by parity.
 //   pred unit g, 8 of them: the same combine of group g's rows, then the
-//     group sums of layer l+2's router over x_{l+1}; the pred units exchange
-//     them, rank them (the same top-k as the true routing) and publish the
-//     predicted experts of layer l+2, one copy per XCD.
+//     group sums of layer l+2's router over x_{l+1} (pp), published.
+//   refiner unit r, 8 of them (XCD r): per layer l, the early logits of
+//     l+1 from every pred unit's sums; without a table their top-k is the
+//     prediction of l+1; with one, their 16 best are candidates, and once
+//     unit group r has published its act blocks of layer l the refiner
+//     publishes its share w M a of the candidates' logits. Expert units
+//     form the prediction from the candidates and the 8 shares themselves;
+//     the refiner publishes it for the group and pred units of its XCD.
 //   every expert and group unit: reads the 8 group sums of every expert
 //     (and, expert units, the 88 q8 blocks of x_{l+1}) (hop C), logits =
 //     sum over groups in order + bias, top-k (and, group units, softmax),
@@ -75,6 +82,10 @@ constexpr int CTL_ABORT = 32;
 constexpr uint32_t ABORT_EPOCH_WRAP = 0xFFFFFFFFu;
 constexpr int TRACE_SLOTS = 32; // stamps per workgroup per layer in the debug trace
 constexpr int PID_STRIDE = 16;  // words per copy of the predicted experts
+constexpr int NCAND = 16;       // candidates of the refined prediction: the early routing's 16 best experts
+constexpr int CW = 3 * NCAND + 1;  // candidate words: ids, sums of R_{l+1} x_l, biases, the norm scale of x_l
+constexpr int CD_STRIDE = 64;   // words per refiner's copy of the candidate words
+constexpr int CP_WORDS = NGROUP * CD_STRIDE + NGROUP * NCAND;  // per layer parity: candidate copies, then shares
 
 struct FusedParams {
     const uint8_t* banks;       // [L][E][expert_bytes], fused layout
@@ -88,12 +99,15 @@ struct FusedParams {
     uint64_t* act_t;            // tagged [K][I/32][10]
     uint64_t* hp_t;             // tagged [K][I/32][8 wave slices][64 rows]: gate|up partials of missed tiles
     uint64_t* y_t;              // tagged [2][K][H], by layer parity
-    uint64_t* gq_t;             // tagged [2][NREP][NGROUP][gq_stride]: E group sums, the group's sum of
-                                // squares of x, then qw q8 words
+    uint64_t* gq_t;             // tagged [3][NREP][NGROUP][gq_stride] (by layer mod 3): E group sums, the
+                                // group's sum of squares of x, then qw q8 words
     uint64_t* pp_t;             // tagged [2][NGROUP][E+1]: group sums of the predicting router, then the
                                 // group's sum of squares of x
-    uint64_t* pid_t;            // tagged [2][NGROUP][PID_STRIDE]: predicted experts, one copy per pred unit
+    uint64_t* pid_t;            // tagged [2][NGROUP][PID_STRIDE]: predicted experts, one copy per refiner
     uint64_t* pl_t;             // tagged [grid]: the XCD each workgroup runs on
+    uint64_t* cp_t;             // tagged [2][CP_WORDS], by layer parity: each refiner's copy of the candidate
+                                // words of layer l+1 (CD_STRIDE apart), then the refiners' shares [NGROUP][NCAND]
+    const uint8_t* pred_tab;    // [L-1][E] refined-prediction records (pred_record_bytes each), or null
     int64_t rs_gq;              // replica stride (words); the parity stride is NREP * rs_gq
     uint32_t* ctl;              // [CTL_EPOCH] epoch, [CTL_ABORT] abort epoch
     float* dbg_gu;              // [L][K][2I] or null
@@ -317,13 +331,14 @@ __device__ __forceinline__ int key_slot(int i) { return (i / KEY_ROW) * (KEY_ROW
 //   the groups' sums of squares in row E of gs; else 1), then + bias (bias_t:
 //   this thread's expert's bias, read ahead by the caller). inv_r goes to
 //   m->inv_r (routing only). Then each logit's rank, and the top K in rank order:
-//   pred >= 0 (prediction): ids alone into m->pid[pred];
+//   pred >= 0 (prediction): ids alone into m->pid[pred] (or, with sel_out,
+//   the nsel best ids into sel_out);
 //   otherwise ids into m->sel_i, logits into m->sel_v and, for every unit
 //   group u whose held expert `held[u]` was routed, its slot into
 //   m->uslot[u] (-1: not routed). Two barriers; the caller reads after the
 //   second.
 __device__ __forceinline__ void route_rank(const FusedParams& P, Misc* m, const float* gs, float bias_t, int pred,
-                                           const int* held) {
+                                           const int* held, int* sel_out = nullptr, int nsel = 0) {
     static_assert(NGROUP == 8 && MAX_E == 128, "the logit and key layouts below assume these");
     const int E = P.E, K = P.K, t = tid_here();
     if (t < MAX_E) {  // whole wavefronts (MAX_E is a multiple of 64)
@@ -376,7 +391,9 @@ __device__ __forceinline__ void route_rank(const FusedParams& P, Misc* m, const 
         h1 = reinterpret_cast<const int4*>(held)[1];
     }
     const float li = m->logits[i];
-    if ((t >> 2) < E && part == 0 && rank < K) {  // ranks are distinct: each slot written once
+    if (sel_out) {  // (pred >= 0) the nsel best, in rank order
+        if ((t >> 2) < E && part == 0 && rank < nsel) sel_out[rank] = i;
+    } else if ((t >> 2) < E && part == 0 && rank < K) {  // ranks are distinct: each slot written once
         if (pred >= 0) {
             m->pid[pred][rank] = i;
         } else {
@@ -389,6 +406,34 @@ __device__ __forceinline__ void route_rank(const FusedParams& P, Misc* m, const 
         }
     }
     __syncthreads();
+}
+
+// The refined prediction of layer l+1 from the candidate words cw (the
+// early routing's NCAND best experts of l+1: ids, then their sums of
+// R_{l+1} x_l, then their biases, then the input norm's scale of x_l, or 1)
+// and the refiners' shares sh [NGROUP][NCAND] (w_p M_p a_p of the slot each
+// unit group ran in layer l): logit_c = (base_c + sh[0][c] + ... +
+// sh[7][c]) * ir + bias_c, each op rounded once; the K best candidates in
+// rank order into pid. Wavefront 0 (its lanes' LDS accesses complete in
+// program order); the caller synchronises before other waves read pid. Every
+// workgroup that needs the prediction runs this on the same words, so all
+// hold the same one.
+__device__ __forceinline__ void cand_pid(const uint32_t* cw, const uint32_t* sh, uint64_t* keys, int* pid, int K) {
+    const int c = tid_here();
+    uint64_t key = 0;
+    if (c < NCAND) {
+        float s = __uint_as_float(cw[NCAND + c]);
+#pragma unroll
+        for (int p = 0; p < NGROUP; ++p) s = s + __uint_as_float(sh[p * NCAND + c]);
+        key = rank_key(s * __uint_as_float(cw[3 * NCAND]) + __uint_as_float(cw[2 * NCAND + c]), (int)cw[c]);
+        keys[c] = key;
+    }
+    if (c < NCAND) {
+        int rank = 0;
+#pragma unroll
+        for (int q = 0; q < NCAND; ++q) rank += keys[q] > key ? 1 : 0;
+        if (rank < K) pid[rank] = (int)cw[c];
+    }
 }
 
 // Slot that unit group u runs (after route_rank with `held`): the slot of
@@ -711,9 +756,7 @@ template <int BPW, int DB, int CPT, bool DBG>
 __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P) {
     constexpr int C = 2 * BPW;  // router chunks per group = H/128
     // words per thread of each wait (H = 256 * BPW, E <= 128, K <= 8):
-    constexpr int UW_G = NGROUP * MAX_E / FT_THREADS;                              // group sums (prediction)
-    static_assert((NGROUP - 1) * (MAX_E + 1) <= UW_G * FT_THREADS, "pred units poll 7 groups' sums in UW_G rounds");
-    constexpr int UW_GA = (NGROUP * (MAX_E + 1) + FT_THREADS - 1) / FT_THREADS;       // all 8 groups' sums
+    constexpr int UW_GA = (NGROUP * (MAX_E + 1) + FT_THREADS - 1) / FT_THREADS;       // all 8 groups' sums (+ squares)
     // group units: the experts of one split, LPE threads each
     constexpr int LPE_G = FT_THREADS / (MAX_E / GSPLIT), CPT_G = (C + LPE_G - 1) / LPE_G;
     static_assert(CPT_G <= CPT, "a split's router registers fit the pred units' array");
@@ -760,39 +803,196 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     auto tag_g = [&](int l) { return epoch + 4u * l + 1u; };
     auto tag_a = [&](int l) { return epoch + 4u * l + 2u; };
     auto tag_y = [&](int l) { return epoch + 4u * l + 3u; };
-    auto gq_buf = [&](int l) { return P.gq_t + (int64_t)(l & 1) * NREP * P.rs_gq; };
+    auto gq_buf = [&](int l) { return P.gq_t + (int64_t)(l % 3) * NREP * P.rs_gq; };
+    auto cp_buf = [&](int l) { return P.cp_t + (int64_t)(l & 1) * CP_WORDS; };
     auto pp_buf = [&](int l) { return P.pp_t + (int64_t)(l & 1) * NGROUP * (E + 1); };
-    // the prediction: one copy per pred unit g (on XCD g), read by the units
+    // the prediction: one copy per refiner r (on XCD r), read by the units
     // of the same XCD
     auto pid_buf = [&](int l) { return P.pid_t + (int64_t)(l & 1) * NGROUP * PID_STRIDE; };
     auto y_buf = [&](int l) { return P.y_t + (int64_t)(l & 1) * K * H; };
-    const int prep = w % NGROUP;  // the pred unit whose copy this workgroup reads
+    const int prep = w % NGROUP;  // the refiner whose copies this workgroup reads
     auto ident = [](int i) { return (int64_t)i; };
     const int rep = w % NREP;  // workgroups are dealt to the 8 XCDs round-robin
     const bool pf = P.prefetch != 0;
     if (t == 0) st_tag(P.pl_t + w, tag_g(0), xcc_id());
 
+    if (w >= P.n_unit + (GSPLIT + 1) * NGROUP) {
+        // ============ refiner unit r: the prediction of layer l+1 ============
+        // Runs beside unit group r (workgroup n_unit + 3*NGROUP + r, on XCD r).
+        // Every pred unit's group sums of R_{l+1} x_l (pp) give the early
+        // logits of layer l+1 (times the input norm's scale of x_l, plus the
+        // bias of l+1). Without a table their K best are the prediction,
+        // published once the routing words of l are in. With a table
+        // (ft_hip_fused_build_predictor: M_{l,e} = R_{l+1} D_{l,e}, int8 per
+        // 32 columns with an f32 scale) the prediction is refined: layer l+1's
+        // logits are linear in x_{l+1} = x_l + sum_p w_p D_p a_p, so
+        // R_{l+1} x_{l+1} = R_{l+1} x_l + sum_p w_p M_p a_p. The refiner
+        // publishes the early logits' NCAND best as candidate words at once;
+        // once unit group r has published the act blocks of the slot it runs
+        // in layer l, it publishes its share w M a for the candidates; every
+        // expert unit then forms the prediction itself from the candidate
+        // words and the 8 shares (cand_pid), one hand-over after the shares,
+        // and the refiner does the same for the group and pred units (its pid
+        // copy). Results never depend on the prediction (it only decides
+        // which unit group holds which expert), so this f32 arithmetic is
+        // free-form; all that matters is that every workgroup computes the same.
+        const int r = w - P.n_unit - (GSPLIT + 1) * NGROUP;
+        if (!pf || L < 2) return;
+        const bool refine = P.pred_tab != nullptr;
+        const int ES = E + 1;
+        auto aidx = [=](int i) { return (int64_t)(i / ES) * P.gq_stride + i % ES; };
+        auto adst = [=](int i) { return (i % ES) * NGROUP + i / ES; };
+        auto act_dst = [=](int i) {
+            const int bi = i / 10, k = i - bi * 10;
+            return k >= 2 ? bi * 8 + (k - 2) : nbj * 8 + bi * 2 + k;
+        };
+        float* gs = reinterpret_cast<float*>(gq);         // [E+1][NGROUP]
+        float* lg = gy;                                     // [E][NGROUP]: the early logit in column 0
+        float* bs = gx;                                     // [E] the early sums
+        uint32_t* cwl = reinterpret_cast<uint32_t*>(red);  // candidate words, then (at +CD_STRIDE) the shares
+        int* cid = reinterpret_cast<int*>(gp);              // [NCAND] candidates in rank order
+        const uint4* aq4 = reinterpret_cast<const uint4*>(act8);
+        const int2* adp = reinterpret_cast<const int2*>(act8 + nbj * 32);
+        const int64_t rec_bytes = (int64_t)E * nbj * 36;
+        static_assert(NCAND * 32 <= FT_THREADS && CW <= CD_STRIDE, "32 lanes per candidate's share");
+        for (int l = 0; l + 1 < L; ++l) {
+            stamp<DBG>(P, l, 0);
+            const float bias_l = ld_bias(P, l), bias_n1 = ld_bias(P, l + 1);
+            // the early sums: every group's sums of R_{l+1} x_l and of x_l . x_l
+            if (!wait_words<DBG, UW_GA>(P, m, epoch, pp_buf(l + 1), NGROUP * ES, ident, tag_g(l + 1), gq, adst, l, 27))
+                return;
+            float ir = 1.0f;
+            if (tid_here() < E) {
+                const float4 a = reinterpret_cast<const float4*>(gs + tid_here() * NGROUP)[0];
+                const float4 b = reinterpret_cast<const float4*>(gs + tid_here() * NGROUP)[1];
+                const float base = ((((((a.x + a.y) + a.z) + a.w) + b.x) + b.y) + b.z) + b.w;
+                if (P.input_norm) {
+                    const float4 c = reinterpret_cast<const float4*>(gs + E * NGROUP)[0];
+                    const float4 d = reinterpret_cast<const float4*>(gs + E * NGROUP)[1];
+                    const float ss = ((((((c.x + c.y) + c.z) + c.w) + d.x) + d.y) + d.z) + d.w;
+                    int Hs = P.H;
+                    asm volatile("" : "+s"(Hs));
+                    ir = 1.0f / sqrtf(ss / (float)Hs + 1e-6f);
+                }
+                bs[tid_here()] = base;
+                float4* o = reinterpret_cast<float4*>(lg + tid_here() * NGROUP);
+                o[0] = make_float4(base * ir, 0.0f, 0.0f, 0.0f);
+                o[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+            __syncthreads();
+            // early prediction (no table) or the candidates (table): rank the early logits
+            route_rank(P, m, lg, bias_n1, (l + 1) & 1, nullptr, refine ? cid : nullptr, NCAND);
+            if (refine) {
+                const int k = tid_here();
+                if (k < CW) {
+                    const int c = k % NCAND, e = min(max(cid[c], 0), E - 1);
+                    const uint32_t v = k < NCAND ? (uint32_t)e
+                                     : k < 2 * NCAND ? __float_as_uint(bs[e])
+                                     : k < 3 * NCAND ? __float_as_uint(P.bias ? P.bias[(int64_t)(l + 1) * E + e] : 0.0f)
+                                     : __float_as_uint(ir);
+                    cwl[k] = v;
+                    st_tag(cp_buf(l) + r * CD_STRIDE + k, tag_a(l), v);
+                }
+            }
+            // the routing words of layer l: the slot unit group r runs; this
+            // wait also orders the writes below after every group unit's and
+            // expert unit's reads (the chains stated at the group units)
+            if (!wait_words<DBG, UW_GA>(P, m, epoch, gq_buf(l) + rep * P.rs_gq, NGROUP * ES, aidx, tag_g(l), gq, adst, l,
+                                        24))
+                return;
+            stamp<DBG>(P, l, 12);
+            if (refine) {
+                const bool first = l == 0;
+                route_rank(P, m, gs, bias_l, -1, first ? nullptr : m->pid[l & 1]);
+                route_weights(P, m, l, first, false);
+                __syncthreads();
+                const int slot = unit_slot(m, K, r, first);
+                const int eid = min(max(m->ids[slot], 0), E - 1);
+                const float wr = m->wts[slot];
+                // M_{l, eid} rows of the candidates: thread (candidate c, block b) for b < I/32
+                const int tq = tid_here();
+                const int c = tq >> 5, b = tq & 31, bb = min(b, nbj - 1);
+                const int ec = min(max((int)cwl[c], 0), E - 1);
+                const uint8_t* rec = P.pred_tab + ((int64_t)l * E + eid) * rec_bytes;
+                const uint4* q = reinterpret_cast<const uint4*>(rec + ((int64_t)ec * nbj + bb) * 32);
+                const uint4 mq0 = q[0], mq1 = q[1];
+                const float md = *reinterpret_cast<const float*>(rec + (int64_t)E * nbj * 32 + ((int64_t)ec * nbj + bb) * 4);
+                if (!wait_words<DBG, 1, true>(P, m, epoch, P.act_t + (int64_t)r * nbj * 10, nbj * 10, ident, tag_a(l),
+                                              reinterpret_cast<uint32_t*>(act8), act_dst, l, 25))
+                    return;
+                stamp<DBG>(P, l, 4);
+                const uint4 lo = aq4[bb * 2], hi = aq4[bb * 2 + 1];
+                const int2 ap = adp[bb];
+                int d = 0;
+                d = __builtin_amdgcn_sdot4((int)mq0.x, (int)lo.x, d, false);
+                d = __builtin_amdgcn_sdot4((int)mq0.y, (int)lo.y, d, false);
+                d = __builtin_amdgcn_sdot4((int)mq0.z, (int)lo.z, d, false);
+                d = __builtin_amdgcn_sdot4((int)mq0.w, (int)lo.w, d, false);
+                d = __builtin_amdgcn_sdot4((int)mq1.x, (int)hi.x, d, false);
+                d = __builtin_amdgcn_sdot4((int)mq1.y, (int)hi.y, d, false);
+                d = __builtin_amdgcn_sdot4((int)mq1.z, (int)hi.z, d, false);
+                d = __builtin_amdgcn_sdot4((int)mq1.w, (int)hi.w, d, false);
+                float v = b < nbj ? (float)d * (md * __int_as_float(ap.x)) : 0.0f;
+#pragma unroll
+                for (int o = 1; o < 32; o <<= 1) v += __shfl_xor(v, o, 32);
+                if (b == 0) st_tag(cp_buf(l) + NGROUP * CD_STRIDE + r * NCAND + c, tag_a(l), __float_as_uint(v * wr));
+                stamp<DBG>(P, l, 5);
+                // every refiner's share -> the prediction, as every expert unit forms it
+                if (!wait_words<DBG, 1>(P, m, epoch, cp_buf(l) + NGROUP * CD_STRIDE, NGROUP * NCAND, ident, tag_a(l),
+                                        cwl + CD_STRIDE, l, 26))
+                    return;
+                stamp<DBG>(P, l, 8);
+                if (tid_here() < 64) cand_pid(cwl, cwl + CD_STRIDE, m->keys, m->pid[(l + 1) & 1], K);
+                __syncthreads();
+            }
+            if (tid_here() < K)
+                st_tag(pid_buf(l + 1) + r * PID_STRIDE + tid_here(), tag_g(l + 1), (uint32_t)m->pid[(l + 1) & 1][tid_here()]);
+            stamp<DBG>(P, l, 14);
+        }
+        return;
+    }
+
     if (w >= P.n_unit) {
-        // ============ group unit (routing) or pred unit (prediction) ============
+        // ============ group unit (routing) or pred unit (early sums) ============
         // Both combine the same rows bit for bit. A group unit then applies the
         // router of layer l+1 (true routing of l+1, q8 of x_{l+1}); a pred unit
-        // the router of layer l+2 (the prediction of layer l+2).
+        // the router of layer l+2 and publishes its group's sums (pp), the base
+        // of the refiners' prediction of layer l+2.
         // Reused words are rewritten only after every reader has read them:
         //   act_t, hp_t (one buffer): rewritten for l+1 after the routing of
-        //     l+1, which needs every y of l, produced after the reads;
-        //   y_t (by parity): rewritten for l+2 after the writer saw the
-        //     prediction of l+2, which its pred unit publishes after every
-        //     pred unit's sums of l+2, each computed after reading y(l); group
-        //     units read y(l) before publishing the routing of l+1;
-        //   gq_t (by parity): rewritten for l+2 after every y(l+1), i.e. after
-        //     every expert unit took the prediction of l+1 from its XCD's pred
-        //     unit, which publishes it after reading gq(l);
-        //   pp_t (by parity): rewritten for l+2 after y(l), i.e. after the
-        //     prediction of l was read from all 8 copies, each published after
-        //     its pred unit read pp(l);
-        //   pid_t (by parity): rewritten for l+2 after the routing of l+1 from
-        //     every group unit (each read pid(l) before publishing it), and so
-        //     after every y(l), i.e. after every expert unit took pid(l).
+        //     l+1, which needs every y of l, produced after the down units'
+        //     reads; refiner u reads act(l) of unit group u before publishing
+        //     its share (table) or, without a table, does not read it; every
+        //     unit of u takes the shares before it writes act(l+1);
+        //   y_t (by parity): rewritten for l+2 after the writer took the
+        //     prediction of l+2 (or its candidate words) from its refiner,
+        //     published after reading every pred unit's sums of l+2, each
+        //     computed after reading y(l); group units read y(l) before
+        //     publishing the routing of l+1;
+        //   gq_t (by layer mod 3): rewritten for l+3 after every y(l+2). An
+        //     expert unit reads gq(l) before its y(l); a group unit before
+        //     publishing gq(l+1), which the routing of l+2 needs; every
+        //     refiner before publishing the prediction of l+1, and every
+        //     expert unit takes the prediction of l+2 (published after it)
+        //     before writing y(l+2); a pred unit before publishing its sums
+        //     of l+2, which every refiner reads before publishing the
+        //     prediction of l+2;
+        //   pp_t (by parity): rewritten for l+2 after every y(l); each expert
+        //     unit wrote y(l) after taking the prediction of l (or its
+        //     candidate words) from its refiner, which had read every group's
+        //     pp(l);
+        //   pid_t (by parity, one copy per refiner): refiner r rewrites it
+        //     for l+3 after the routing words of l+2 (every group unit read
+        //     pid(l+1) before publishing them, and they follow every y(l+1),
+        //     which each expert unit wrote after taking pid(l+1)) and after
+        //     every pred unit's sums of l+3 (each pred unit read pid(l+1)
+        //     before computing them);
+        //   cp_t (by parity): refiner r rewrites its candidate words for l+2
+        //     after every pred unit's sums of l+3, i.e. after every y(l+1),
+        //     which each expert unit wrote after reading cp(l); and its share
+        //     after the routing words of l+2, published by the group units
+        //     after the prediction of l+1 from every refiner, each formed
+        //     after reading every share of cp(l).
         // Group units: GSPLIT per group, w - n_unit = sp * NGROUP + g (all on
         // XCD g); split sp publishes the router sums of experts sp*E/GSPLIT..,
         // split 0 also the sum of squares and the q8 blocks, and it writes
@@ -811,68 +1011,51 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         if (pu && (!pf || L < 2)) return;    // nothing to predict
         uint32_t* q8w = reinterpret_cast<uint32_t*>(gp + (C + 1) * E);
         float4 wv[CPT][4];
-        // Group sums and sums of squares -> LDS [E+1][NGROUP] (row E: the
-        // sums of squares). Group units poll every group's row of the
-        // broadcast (aidx; their own group's too, which the other splits
-        // write). Pred units take their own group's row from gp (own_sums,
-        // before the wait) and poll the 7 other groups of the prediction
-        // exchange (opidx), which carries the same sums of squares (both
-        // combine the same x); they then poll the broadcast's E sums alone
-        // (gidx_e, into rows < E, keeping row E).
+        // The routing words -> LDS [E+1][NGROUP] (row E: the sums of squares):
+        // every group's slot of the broadcast (its own group's too, which the
+        // other splits write).
         const int ES = E + 1;
-        auto ogrp = [=](int i) { const int o = i / ES; return o < g ? o : o + 1; };
         auto aidx = [=](int i) { return (int64_t)(i / ES) * P.gq_stride + i % ES; };
         auto adst = [=](int i) { return (i % ES) * NGROUP + i / ES; };
-        auto opidx = [=](int i) { return (int64_t)ogrp(i) * ES + i % ES; };
-        auto odst = [=](int i) { return (i % ES) * NGROUP + ogrp(i); };
-        auto gidx_e = [=](int i) { return (int64_t)(i / E) * P.gq_stride + i % E; };
-        auto own_sums = [&]() __attribute__((always_inline)) {
-            const float* sq = reinterpret_cast<const float*>(q8w + P.qw);
-            if (t <= E) gq[t * NGROUP + g] = __float_as_uint(t < E ? gp[C * E + t] : sq[C]);
-        };
-        auto pdst = [=](int i) { return (i % E) * NGROUP + i / E; };  // E sums of 8 groups -> LDS rows < E
         // a split's router weights: the first CPT_G rows of wv
         auto& wvg = reinterpret_cast<float4(&)[CPT_G][4]>(wv);
         auto load_router = [&](int layer) __attribute__((always_inline)) {
             if (pu) group_load_router<CPT, C, 4>(P, layer, g, 0, wv);
             else group_load_router<CPT_G, C, LPE_G>(P, layer, g, e0, wvg);
         };
+        // publishes the sums of the router just applied to x (gx): a pred unit
+        // layer rl's sums to pp, a group unit its broadcast words
+        auto publish = [&](int rl, int sl) __attribute__((always_inline)) {
+            if (pu) group_publish<CPT, C, 4, DBG>(P, g, 0, wv, gx, gp, q8w, pp_buf(rl), tag_g(rl), sl, true, true);
+            else group_publish<CPT_G, C, LPE_G, DBG>(P, g, e0, wvg, gx, gp, q8w, gq_buf(rl), tag_g(rl), sl, false,
+                                                     primary);
+        };
         stamp<DBG>(P, -1, 0);
         load_router(pu ? 1 : 0);
-        float bias_n = ld_bias(P, 0), bias_p = pu ? ld_bias(P, 1) : 0.0f;
+        float bias_n = ld_bias(P, 0);
         for (int i = t; i < HG; i += FT_THREADS) {
             gx[i] = P.x_in[r0 + i];
             if (DBG && P.dbg_x && primary) P.dbg_x[r0 + i] = gx[i];
         }
         __syncthreads();
-        if (pu) {
-            group_publish<CPT, C, 4, DBG>(P, g, 0, wv, gx, gp, q8w, pp_buf(1), tag_g(1), -1, true, true);
-            own_sums();
-            if (!wait_words<DBG, UW_G>(P, m, epoch, pp_buf(1), (NGROUP - 1) * ES, opidx, tag_g(1), gq, odst)) { fail(); return; }
-            route_rank(P, m, reinterpret_cast<const float*>(gq), bias_p, 1, nullptr);
-            if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * E, gidx_e, tag_g(0), gq, pdst)) { fail(); return; }
-            if (t < K) st_tag(pid_buf(1) + g * PID_STRIDE + t, tag_g(1), (uint32_t)m->pid[1][t]);
-        } else {
-            group_publish<CPT_G, C, LPE_G, DBG>(P, g, e0, wvg, gx, gp, q8w, gq_buf(0), tag_g(0), -1, false, primary);
-            stamp<DBG>(P, -1, 11);
-            if (!wait_words<DBG, UW_GA>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * ES, aidx, tag_g(0), gq, adst)) {
-                fail();
-                return;
-            }
+        publish(pu ? 1 : 0, -1);
+        stamp<DBG>(P, -1, 11);
+        if (!wait_words<DBG, UW_GA>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * ES, aidx, tag_g(0), gq, adst)) {
+            fail();
+            return;
         }
         stamp<DBG>(P, -1, 12);
         route_rank(P, m, reinterpret_cast<const float*>(gq), bias_n, -1, nullptr);
         route_weights(P, m, 0, true, record);
         stamp<DBG>(P, -1, 14);
         for (int l = 0; l < L; ++l) {
-            // a pred unit's last prediction (of layer L-1) was published at
+            // a pred unit's last sums (layer L-1's router) were published at
             // l = L-3: nothing of its work after that is read
             if (pu && l + 2 >= L) return;
             stamp<DBG>(P, l, 0);
             const int rl = pu ? l + 2 : l + 1;  // the router layer applied after this layer's combine
             if (rl < L) load_router(rl);
             if (l + 1 < L) bias_n = ld_bias(P, l + 1);
-            if (pu && l + 2 < L) bias_p = ld_bias(P, l + 2);
             stamp<DBG>(P, l, 1);
             // y of every unit group for this group's rows, [u][HG] in LDS
             auto yidx = [=](int i) { return (int64_t)(i / HG) * H + r0 + i % HG; };
@@ -906,39 +1089,19 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
             __syncthreads();
             stamp<DBG>(P, l, 9);
             if (l + 1 == L) break;
-            if (pu) {  // here l + 2 < L
-                group_publish<CPT, C, 4, DBG>(P, g, 0, wv, gx, gp, q8w, pp_buf(l + 2), tag_g(l + 2), l, true, true);
-                stamp<DBG>(P, l, 11);
-                own_sums();
-                if (!wait_words<DBG, UW_G>(P, m, epoch, pp_buf(l + 2), (NGROUP - 1) * ES, opidx, tag_g(l + 2), gq, odst, l,
-                                           24)) {
-                    fail();
-                    return;
-                }
-                route_rank(P, m, reinterpret_cast<const float*>(gq), bias_p, l & 1, nullptr);
-                if (!wait_words<DBG, UW_G>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * E, gidx_e, tag_g(l + 1), gq,
-                                           pdst)) {
-                    fail();
-                    return;
-                }
-                stamp<DBG>(P, l, 12);
-                if (t < K) st_tag(pid_buf(l + 2) + g * PID_STRIDE + t, tag_g(l + 2), (uint32_t)m->pid[l & 1][t]);
-            } else {
-                group_publish<CPT_G, C, LPE_G, DBG>(P, g, e0, wvg, gx, gp, q8w, gq_buf(l + 1), tag_g(l + 1), l, false,
-                                                    primary);
-                stamp<DBG>(P, l, 11);
-                if (!wait_words<DBG, UW_GA>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * ES, aidx, tag_g(l + 1),
-                                            gq, adst, l, 24)) {
-                    fail();
-                    return;
-                }
-                stamp<DBG>(P, l, 12);
-                // the prediction of layer l+1, for the slot -> unit group map
-                if (pf && !wait_words<DBG, 1>(P, m, epoch, pid_buf(l + 1) + prep * PID_STRIDE, K, ident, tag_g(l + 1),
-                                      reinterpret_cast<uint32_t*>(m->pid[(l + 1) & 1]), l, 27)) {
-                    fail();
-                    return;
-                }
+            publish(rl, l);
+            stamp<DBG>(P, l, 11);
+            if (!wait_words<DBG, UW_GA>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * ES, aidx, tag_g(l + 1), gq,
+                                        adst, l, 24)) {
+                fail();
+                return;
+            }
+            stamp<DBG>(P, l, 12);
+            // the prediction of layer l+1, for the slot -> unit group map
+            if (pf && !wait_words<DBG, 1>(P, m, epoch, pid_buf(l + 1) + prep * PID_STRIDE, K, ident, tag_g(l + 1),
+                                          reinterpret_cast<uint32_t*>(m->pid[(l + 1) & 1]), l, 27)) {
+                fail();
+                return;
             }
             route_rank(P, m, reinterpret_cast<const float*>(gq), bias_n, -1, pf ? m->pid[(l + 1) & 1] : nullptr);
             route_weights(P, m, l + 1, !pf, record);
@@ -949,6 +1112,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
 
     // ======================= expert unit =======================
     const int u = w % K, j = w / K;
+    const bool refine = P.pred_tab != nullptr;  // the refined prediction (see the refiner units)
     const bool gm = w < P.n_gu, dm = w < P.n_dn;  // false: that part of the unit is idle
     const int dn_tile = nbj * 288;               // bytes of one 16-row down tile
     const int ES = E + 1, nq = ES + P.qw;  // per group: E sums, the sum of squares, q8 words
@@ -965,14 +1129,18 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     float bias_n = ld_bias(P, 0);
     if (!wait_words<DBG, UW_X>(P, m, epoch, gq_buf(0) + rep * P.rs_gq, NGROUP * nq, xidx, tag_g(0), gq, xdst)) return;
     // The act hand-over of unit group u stays in the XCD's L2 (plain stores,
-    // agent-scope polls) when every unit of group u runs on this workgroup's
-    // XCD; otherwise its stores write through.
+    // agent-scope polls) when every unit of group u, and refiner u (which
+    // reads the act too), runs on this workgroup's XCD; otherwise its stores
+    // write through.
     bool act_local;
     {
         const int upe = P.n_unit / K;  // units per unit group
+        const int64_t ref_w = P.n_unit + (GSPLIT + 1) * NGROUP + u;
         uint32_t* xw = reinterpret_cast<uint32_t*>(red);
-        if (!wait_words<DBG, 1>(P, m, epoch, P.pl_t, upe, [=](int i) { return (int64_t)(u + K * i); }, tag_g(0), xw)) return;
-        act_local = __syncthreads_and(t >= upe || xw[t] == xcc_id()) != 0;
+        if (!wait_words<DBG, 1>(P, m, epoch, P.pl_t, upe + 1,
+                                [=](int i) { return i < upe ? (int64_t)(u + K * i) : ref_w; }, tag_g(0), xw))
+            return;
+        act_local = __syncthreads_and(t > upe || xw[t] == xcc_id()) != 0;
         trace_value<DBG>(P, -1, 27, act_local ? 1u : 0u);
         trace_value<DBG>(P, -1, 28, xcc_id());
     }
@@ -1173,11 +1341,12 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
             }
             stamp<DBG>(P, l, 3);
         }
-        // the prediction of layer l+1 (published early in this layer): loaded
-        // now, checked after the down dots, when every older load of this wave
-        // has landed anyway, so it never stalls the chain
+        // the early prediction of layer l+1 (published before this layer
+        // started): loaded now, checked after the down dots, when every older
+        // load of this wave has landed anyway, so it never stalls the chain
         uint64_t pid_raw = 0;
-        if (pf && l + 1 < L && tid_here() < K) pid_raw = ld_tag(pid_buf(l + 1) + prep * PID_STRIDE + tid_here());
+        if (pf && !refine && l + 1 < L && tid_here() < K)
+            pid_raw = ld_tag(pid_buf(l + 1) + prep * PID_STRIDE + tid_here());
         // ---- down: the act blocks of unit group u, then y of 128 rows ----
         if (dm) {
             // act8: [nbj blocks x 32 B qs][nbj (d, qsum) pairs] (16-B aligned qs)
@@ -1222,17 +1391,32 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         bias_n = ld_bias(P, l + 1);
         // ---- prefetch: the predicted expert of layer l+1 for this unit group ----
         if (pf) {
-            bool ok = true;
-            const int tq = tid_here();  // the lane tests and the LDS address formed here (hoisted, they spilled)
-            if (tq < K) {
-                ok = (uint32_t)(pid_raw >> 32) == tag_g(l + 1);
-                m->pid[(l + 1) & 1][tq] = (int)(uint32_t)pid_raw;
+            if (refine) {
+                // the refined prediction, formed here from this XCD's copy of
+                // the candidate words and every refiner's share (one hand-over
+                // after the shares, as the refiners form it)
+                auto cidx = [=](int i) {
+                    return (int64_t)(i < CW ? prep * CD_STRIDE + i : NGROUP * CD_STRIDE + (i - CW));
+                };
+                auto cdst = [=](int i) { return i < CW ? i : CD_STRIDE + (i - CW); };
+                uint32_t* cw = reinterpret_cast<uint32_t*>(red);
+                if (!wait_words<DBG, 1>(P, m, epoch, cp_buf(l), CW + NGROUP * NCAND, cidx, tag_a(l), cw, cdst, l, 27))
+                    return;
+                if (tid_here() < 64) cand_pid(cw, cw + CD_STRIDE, m->keys, m->pid[(l + 1) & 1], K);
+                __syncthreads();
+            } else {
+                bool ok = true;
+                const int tq = tid_here();  // the lane tests and the LDS address formed here (hoisted, they spilled)
+                if (tq < K) {
+                    ok = (uint32_t)(pid_raw >> 32) == tag_g(l + 1);
+                    m->pid[(l + 1) & 1][tq] = (int)(uint32_t)pid_raw;
+                }
+                // not yet published (late refiner): the bounded wait
+                if (!__syncthreads_and(ok) &&
+                    !wait_words<DBG, 1>(P, m, epoch, pid_buf(l + 1) + prep * PID_STRIDE, K, ident, tag_g(l + 1),
+                                     reinterpret_cast<uint32_t*>(m->pid[(l + 1) & 1]), l, 27))
+                    return;
             }
-            // not yet published (late pred units): the bounded wait
-            if (!__syncthreads_and(ok) &&
-                !wait_words<DBG, 1>(P, m, epoch, pid_buf(l + 1) + prep * PID_STRIDE, K, ident, tag_g(l + 1),
-                                 reinterpret_cast<uint32_t*>(m->pid[(l + 1) & 1]), l, 27))
-                return;
             const int pe = min(max(m->pid[(l + 1) & 1][u], 0), E - 1);
             load_gu(l + 1, pe, wave, qv, sc);
             load_dn(l + 1, pe);
@@ -1331,6 +1515,93 @@ __global__ __launch_bounds__(256) void k_pack_router(const float* src, float* ds
     dst[g] = src[l * per_l + (int64_t)e * H + c * DN_ROWS + i];
 }
 
+// Refined-prediction table (setup): record (l, e), l < L-1, holds
+// M = R_{l+1} D_{l,e} (E router rows x I columns; R_{l+1} from the fused
+// router layout, D_{l,e} the expert's down rows dequantized from the fused
+// layout), each row quantized per 32 columns like a q8 block: [E][I/32][32]
+// int8, then [E][I/32] f32 scales (d = amax / 127, q = rint(v / d)). One
+// workgroup per (l, e, 64 columns); f32 products summed over the H rows in
+// steps of 32. Only the refiners' predictions read it, so its rounding is
+// free-form.
+constexpr int PT_STEP = 32;  // D rows (R columns) per step
+__global__ __launch_bounds__(256) void k_pred_table(const uint8_t* banks, const float* routers, uint8_t* out, int H,
+                                                    int I, int64_t expert_bytes, int64_t gu_bytes) {
+    constexpr int E = MAX_E;  // the fused shape's expert count (checked by the host)
+    __shared__ float Rs[E][PT_STEP + 1];
+    __shared__ float Ds[PT_STEP][64];
+    __shared__ float Ms[E][65];
+    const int kt = blockIdx.x, e = blockIdx.y, l = blockIdx.z, t = threadIdx.x;
+    const int nbj = I >> 5, C = H / DN_ROWS;
+    const uint8_t* D0 = banks + ((int64_t)l * E + e) * expert_bytes + gu_bytes;
+    const float* R = routers + (int64_t)(l + 1) * C * E * DN_ROWS;
+    const int tr = t >> 4, tc = t & 15;  // router rows tr*8.., columns tc*4..
+    float acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+    for (int h0 = 0; h0 < H; h0 += PT_STEP) {
+        for (int i = t; i < E * PT_STEP; i += 256) {  // chunks h0/16 and h0/16+1, [E][16] each
+            const int c = i / (E * DN_ROWS), rem = i % (E * DN_ROWS), er = rem / DN_ROWS, ii = rem % DN_ROWS;
+            Rs[er][c * DN_ROWS + ii] = R[((int64_t)(h0 / DN_ROWS + c) * E + er) * DN_ROWS + ii];
+        }
+        if (t < 64) {  // D rows h0.., blocks 2kt and 2kt+1: one (row, block) per thread
+            const int rrow = t >> 1, blk = t & 1, h = h0 + rrow, jt = h / DN_ROWS, rr = h % DN_ROWS, b = 2 * kt + blk;
+            const uint8_t* T = D0 + (int64_t)jt * nbj * 288;
+            const float d = h2f(*reinterpret_cast<const uint16_t*>(T + b * 32 + rr * 2));
+            const uint4 q = *reinterpret_cast<const uint4*>(T + nbj * 32 + b * 256 + rr * 16);
+            const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int byte = (int)((qw[i >> 2] >> ((i & 3) * 8)) & 0xFF);
+                Ds[rrow][blk * 32 + i] = d * (float)((byte & 15) - 8);
+                Ds[rrow][blk * 32 + i + 16] = d * (float)((byte >> 4) - 8);
+            }
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int hh = 0; hh < PT_STEP; ++hh) {
+            float a[8], b[4];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a[i] = Rs[tr * 8 + i][hh];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = Ds[hh][tc * 4 + j];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) Ms[tr * 8 + i][tc * 4 + j] = acc[i][j];
+    __syncthreads();
+    // row er, block 2kt + blk: amax, scale, quants
+    const int er = t >> 1, blk = t & 1, b = 2 * kt + blk;
+    float amax = 0.0f;
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(Ms[er][blk * 32 + i]));
+    const float d = amax / 127.0f;
+    uint32_t w[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float x = Ms[er][blk * 32 + 4 * k + i];
+            const int q = d > 0.0f ? (int)fminf(fmaxf(rintf(x / d), -127.0f), 127.0f) : 0;
+            v |= (uint32_t)(q & 0xFF) << (8 * i);
+        }
+        w[k] = v;
+    }
+    uint8_t* rec = out + ((int64_t)l * E + e) * ((int64_t)E * nbj * 36);
+    uint4* qd = reinterpret_cast<uint4*>(rec + ((int64_t)er * nbj + b) * 32);
+    qd[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    qd[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    *reinterpret_cast<float*>(rec + (int64_t)E * nbj * 32 + ((int64_t)er * nbj + b) * 4) = d;
+}
+
 __global__ void k_fill_u32(uint32_t* p, int64_t n, uint32_t v) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
@@ -1340,7 +1611,7 @@ __global__ void k_fill_u32(uint32_t* p, int64_t n, uint32_t v) {
 // host side
 // ---------------------------------------------------------------------------
 struct WsLayout {
-    int64_t ctl, act, hp, y, gq, pp, pid, pl, total;
+    int64_t ctl, act, hp, y, gq, pp, pid, pl, cp, total;
     int gq_stride, qw;
     int64_t rs_gq;  // words
 };
@@ -1356,10 +1627,11 @@ WsLayout ws_layout(int64_t H, int64_t I, int64_t E, int64_t K) {
     w.act = off; off += up(K * (I / 32) * 10 * 8);
     w.hp = off; off += up(K * (I / 32) * FT_WAVES * 64 * 8);
     w.y = off; off += 2 * up(K * H * 8);
-    w.gq = off; off += 2 * NREP * up(w.rs_gq * 8);
+    w.gq = off; off += 3 * NREP * up(w.rs_gq * 8);
     w.pp = off; off += 2 * up(NGROUP * (E + 1) * 8);
     w.pid = off; off += 2 * up(NGROUP * PID_STRIDE * 8);
-    w.pl = off; off += up(((int64_t)std::max(K * (I / 32), K * (H / DN_UNIT)) + (GSPLIT + 1) * NGROUP) * 8);
+    w.pl = off; off += up(((int64_t)std::max(K * (I / 32), K * (H / DN_UNIT)) + (GSPLIT + 2) * NGROUP) * 8);
+    w.cp = off; off += 2 * up(CP_WORDS * 8);
     w.total = off;
     return w;
 }
@@ -1398,7 +1670,7 @@ extern "C" size_t ft_hip_fused_workspace_bytes(int64_t hidden, int64_t inter, in
 extern "C" int ft_hip_fused_workgroups(int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k) {
     if (hidden <= 0 || hidden % 256 || inter <= 0 || inter % 32 || n_experts <= 0 || top_k <= 0) return -1;
     int n_gu, n_dn;
-    return fused_units(hidden, inter, top_k, &n_gu, &n_dn) + (GSPLIT + 1) * NGROUP;
+    return fused_units(hidden, inter, top_k, &n_gu, &n_dn) + (GSPLIT + 2) * NGROUP;
 }
 
 extern "C" int ft_hip_fused_workspace_init(ft_hip_ctx* ctx, void* stream, void* workspace, size_t workspace_bytes) {
@@ -1471,6 +1743,42 @@ extern "C" int ft_hip_pack_router_fused(ft_hip_ctx* ctx, void* stream, const flo
     return launch_status(nm);
 }
 
+extern "C" int64_t ft_hip_fused_predictor_bytes(int64_t hidden, int64_t inter, int64_t n_experts, int64_t n_layers) {
+    if (hidden <= 0 || hidden % 32 || inter <= 0 || inter % 64 || n_experts <= 0 || n_layers <= 0) return -1;
+    return (n_layers - 1) * n_experts * n_experts * (inter / 32) * 36;
+}
+
+extern "C" int ft_hip_fused_build_predictor(ft_hip_ctx* ctx, void* stream, const void* banks, const float* routers,
+                                            int64_t hidden, int64_t inter, int64_t n_experts, int64_t n_layers,
+                                            void* table, size_t table_bytes) {
+    clear_error();
+    const char* nm = "fused_build_predictor";
+    if (int rc = check_fused_shape(nm, hidden, inter, n_experts, MAX_K, n_layers)) return rc;
+    const int64_t need = ft_hip_fused_predictor_bytes(hidden, inter, n_experts, n_layers);
+    if ((int64_t)table_bytes < need)
+        return fail(FT_HIP_E_SHAPE, "%s: table_bytes=%zu < %lld", nm, table_bytes, (long long)need);
+    if (!ctx || !banks || !routers || (need > 0 && !table)) return fail(FT_HIP_E_INVALID, "%s: null argument", nm);
+    if ((reinterpret_cast<uintptr_t>(banks) | reinterpret_cast<uintptr_t>(routers) | reinterpret_cast<uintptr_t>(table)) & 15)
+        return fail(FT_HIP_E_SHAPE, "%s: banks, routers and table must be 16-byte aligned", nm);
+    if (need == 0) return FT_HIP_OK;
+    hipLaunchKernelGGL(k_pred_table, dim3((unsigned)(inter / 64), (unsigned)n_experts, (unsigned)(n_layers - 1)),
+                       dim3(256), 0, reinterpret_cast<hipStream_t>(stream), (const uint8_t*)banks, routers,
+                       (uint8_t*)table, (int)hidden, (int)inter, ft_hip_fused_expert_bytes(hidden, inter),
+                       2 * inter * (hidden / 32) * 18);
+    return launch_status(nm);
+}
+
+extern "C" int ft_hip_fused_set_predictor(ft_hip_ctx* ctx, const void* table, size_t table_bytes, int64_t n_layers) {
+    clear_error();
+    if (!ctx) return fail(FT_HIP_E_INVALID, "fused_set_predictor: null ctx");
+    if (table && (n_layers <= 0 || (reinterpret_cast<uintptr_t>(table) & 15)))
+        return fail(FT_HIP_E_SHAPE, "fused_set_predictor: n_layers must be positive and the table 16-byte aligned");
+    ctx->fused_pred = table;
+    ctx->fused_pred_bytes = table ? table_bytes : 0;
+    ctx->fused_pred_layers = table ? n_layers : 0;
+    return FT_HIP_OK;
+}
+
 extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float* x_in, float* x_out, int64_t hidden,
                                       int64_t inter, int64_t n_experts, int64_t top_k, int64_t n_layers,
                                       const void* banks, const float* routers, const float* bias,
@@ -1490,7 +1798,7 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
     P.K = (int)top_k;
     P.L = (int)n_layers;
     P.n_unit = fused_units(hidden, inter, top_k, &P.n_gu, &P.n_dn);
-    const int nw = P.n_unit + (GSPLIT + 1) * NGROUP;
+    const int nw = P.n_unit + (GSPLIT + 2) * NGROUP;  // + group, pred and refiner units
     P.gq_stride = wl.gq_stride;
     P.qw = wl.qw;
     P.rs_gq = (wl.rs_gq * 8 + 255) / 256 * 256 / 8;
@@ -1529,6 +1837,7 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
     P.pp_t = (uint64_t*)(ws + wl.pp);
     P.pid_t = (uint64_t*)(ws + wl.pid);
     P.pl_t = (uint64_t*)(ws + wl.pl);
+    P.cp_t = (uint64_t*)(ws + wl.cp);
     P.ctl = (uint32_t*)(ws + wl.ctl);
     P.dbg_gu = dbg_gu;
     P.dbg_act = (uint8_t*)dbg_act;
@@ -1540,6 +1849,15 @@ extern "C" int ft_hip_moe_stack_fused(ft_hip_ctx* ctx, void* stream, const float
     P.gu_bytes = 2 * inter * (hidden / 32) * 18;
     P.spin_limit = ctx->fused_spin_limit;
     P.prefetch = ctx->fused_prefetch;
+    // the refined-prediction table (ft_hip_fused_set_predictor): it must cover
+    // this launch's layers; it only steers the prefetch, never the results
+    if (ctx->fused_pred) {
+        const int64_t need = ft_hip_fused_predictor_bytes(hidden, inter, n_experts, n_layers);
+        if (n_layers > ctx->fused_pred_layers || (int64_t)ctx->fused_pred_bytes < need)
+            return fail(FT_HIP_E_SHAPE, "%s: the predictor table was built for %lld layers (%zu B); this launch has %lld",
+                        nm, (long long)ctx->fused_pred_layers, ctx->fused_pred_bytes, (long long)n_layers);
+        P.pred_tab = (const uint8_t*)ctx->fused_pred;
+    }
     P.input_norm = ctx->input_norm;
     // The epoch guard: a launch advances the workspace's epoch by 4(L+1) and
     // its tags must stay below 2^32. For a workspace this context initialised

@@ -27,6 +27,9 @@ struct ft_hip_ctx {
     int fused_spin_limit;  // polls before a fused-kernel wait gives up
     int fused_prefetch;    // fused kernel: stream predicted experts ahead (1) or not (0)
     int fused_cooperative; // fused kernel: cooperative launch (1) or plain (0)
+    const void* fused_pred;      // fused kernel: refined-prediction table (ft_hip_fused_set_predictor), or null
+    size_t fused_pred_bytes;     // its size
+    int64_t fused_pred_layers;   // the n_layers it was built for
     int input_norm;        // layer entry points run on rmsnorm(x) (1) or x (0)
     int grouped_mfma_min;  // grouped layer: experts with at least this many tokens take the MFMA kernels (0: auto)
     int gemv_lanes;        // q4r GEMV lanes per row (ft_hip_set_gemv_lanes): 0 automatic, 8, 16, 32 or 64

@@ -92,6 +92,9 @@ extern "C" {
     pub fn ft_hip_fused_set_spin_limit(ctx: *mut FtHipCtx, polls: c_int) -> c_int;
     pub fn ft_hip_fused_set_prefetch(ctx: *mut FtHipCtx, on: c_int) -> c_int;
     pub fn ft_hip_fused_set_cooperative(ctx: *mut FtHipCtx, on: c_int) -> c_int;
+    pub fn ft_hip_fused_predictor_bytes(hidden: i64, inter: i64, n_experts: i64, n_layers: i64) -> i64;
+    pub fn ft_hip_fused_build_predictor(ctx: *mut FtHipCtx, stream: *mut c_void, banks: *const c_void, routers: *const f32, hidden: i64, inter: i64, n_experts: i64, n_layers: i64, table: *mut c_void, table_bytes: usize) -> c_int;
+    pub fn ft_hip_fused_set_predictor(ctx: *mut FtHipCtx, table: *const c_void, table_bytes: usize, n_layers: i64) -> c_int;
     pub fn ft_hip_fused_status(ctx: *mut FtHipCtx, workspace: *mut c_void, aborted: *mut c_int) -> c_int;
     pub fn ft_gguf_open(path: *const c_char, out: *mut *mut FtGguf) -> c_int;
     pub fn ft_gguf_close(g: *mut FtGguf) -> c_int;

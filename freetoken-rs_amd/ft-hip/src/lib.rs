@@ -363,6 +363,28 @@ impl Q4Gemv {
         })
     }
 
+    /// Bytes of the fused kernel's refined-prediction table for n_layers layers.
+    pub fn fused_predictor_bytes(hidden: usize, inter: usize, n_experts: usize, n_layers: usize) -> Option<usize> {
+        let n = unsafe { ffi::ft_hip_fused_predictor_bytes(hidden as i64, inter as i64, n_experts as i64, n_layers as i64) };
+        if n < 0 { None } else { Some(n as usize) }
+    }
+
+    /// Build the refined-prediction table (M = R_{l+1} D_{l,e}) from fused banks and routers (setup).
+    #[allow(clippy::too_many_arguments)]
+    pub fn fused_build_predictor(&self, s: Stream, banks: DevPtr, routers: DevPtr, hidden: usize, inter: usize,
+                                 n_experts: usize, n_layers: usize, table: DevPtr, table_bytes: usize) -> Result<()> {
+        check(unsafe {
+            ffi::ft_hip_fused_build_predictor(self.ctx, s.0, p(banks), p(routers), hidden as i64, inter as i64,
+                                              n_experts as i64, n_layers as i64, pm(table), table_bytes)
+        })
+    }
+
+    /// Later fused launches prefetch the refined prediction (None: the early routing's alone).
+    pub fn fused_set_predictor(&self, table: Option<(DevPtr, usize)>, n_layers: usize) -> Result<()> {
+        let (t, n) = table.map_or((std::ptr::null(), 0), |(t, n)| (p(t), n));
+        check(unsafe { ffi::ft_hip_fused_set_predictor(self.ctx, t, n, n_layers as i64) })
+    }
+
     /// After synchronising the stream: Err if a fused launch on `workspace`
     /// gave up a bounded wait (its outputs are NaN / id -1).
     pub fn fused_status(&self, workspace: DevPtr) -> Result<bool> {

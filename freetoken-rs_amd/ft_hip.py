@@ -70,6 +70,9 @@ SIGNATURES = {
     "ft_hip_fused_set_spin_limit": (_I, [_P, _I]),
     "ft_hip_fused_set_prefetch": (_I, [_P, _I]),
     "ft_hip_fused_set_cooperative": (_I, [_P, _I]),
+    "ft_hip_fused_predictor_bytes": (_I64, [_I64, _I64, _I64, _I64]),
+    "ft_hip_fused_build_predictor": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _SZ]),
+    "ft_hip_fused_set_predictor": (_I, [_P, _P, _SZ, _I64]),
     "ft_hip_set_input_norm": (_I, [_P, _I]),
     "ft_hip_set_grouped_mfma_min": (_I, [_P, _I]),
     "ft_hip_set_gemv_lanes": (_I, [_P, _I]),
@@ -356,6 +359,22 @@ class Q4Gemv:
     def fused_set_prefetch(self, on):
         """1: stream early-routed experts ahead (default); 0: load each layer's experts once routed."""
         check(lib().ft_hip_fused_set_prefetch(self._ctx, int(on)))
+
+    @staticmethod
+    def fused_predictor_bytes(hidden, inter, n_experts, n_layers):
+        return lib().ft_hip_fused_predictor_bytes(hidden, inter, n_experts, n_layers)
+
+    def fused_build_predictor(self, banks, routers, hidden, inter, n_experts, n_layers, table, stream=None):
+        """Refined-prediction table M = R_{l+1} D_{l,e} from fused banks and routers (setup)."""
+        check(lib().ft_hip_fused_build_predictor(self._ctx, _stream(stream), _ptr(banks), _ptr(routers), hidden, inter,
+                                                 n_experts, n_layers, _ptr(table),
+                                                 0 if table is None else table.numel() * table.element_size()))
+
+    def fused_set_predictor(self, table, n_layers=0):
+        """Later fused launches prefetch the refined prediction from `table` (None: early routing only)."""
+        check(lib().ft_hip_fused_set_predictor(self._ctx, _ptr(table),
+                                               0 if table is None else table.numel() * table.element_size(),
+                                               n_layers))
 
     def set_input_norm(self, on):
         """1: the layer entry points run on rmsnorm(x) (logits and gate|up sums times

@@ -260,9 +260,11 @@ class FusedStack:
     kernel (ft_hip_moe_stack_fused): one launch runs all layers of one token.
     The packed banks also serve the grouped batched path (GroupedStack)."""
 
-    def __init__(self, model, workspace=True):
+    def __init__(self, model, workspace=True, predictor=True):
         """workspace=False: the packed banks and routers only (for the grouped
-        path on shapes the fused kernel does not take)."""
+        path on shapes the fused kernel does not take). predictor: build the
+        refined-prediction table (ft_hip_fused_build_predictor) and use it in
+        run(); False: the early routing's prediction alone."""
         g, s = model.g, model.shape
         H, I, E, K = s.hidden, s.inter, s.n_experts, s.top_k
         self.m, self.g = model, g
@@ -275,6 +277,10 @@ class FusedStack:
         if workspace:
             self.ws = torch.empty(g.fused_workspace_bytes(H, I, E, K), dtype=torch.uint8, device=model.device)
             g.fused_workspace_init(self.ws)
+        self.pred = None
+        if workspace and predictor and model.L > 1:
+            self.pred = torch.empty(g.fused_predictor_bytes(H, I, E, model.L), dtype=torch.uint8, device=model.device)
+            g.fused_build_predictor(self.banks, self.routers, H, I, E, model.L, self.pred)
 
     def n_workgroups(self):
         s = self.m.shape
@@ -283,6 +289,7 @@ class FusedStack:
     def run(self, x_in, x_out, ids=None, wts=None, dbg_gu=None, dbg_act=None, dbg_x=None, trace=None,
             stream=None):
         s = self.m.shape
+        self.g.fused_set_predictor(self.pred, self.m.L)  # the context's setting is shared by every stack
         self.g.moe_stack_fused(x_in, x_out, s.hidden, s.inter, s.n_experts, s.top_k, self.m.L, self.banks,
                                self.routers, self.m.bias, None, ids, wts, self.ws, dbg_gu, dbg_act, dbg_x, trace,
                                stream)

@@ -487,6 +487,30 @@ int ft_hip_fused_set_spin_limit(ft_hip_ctx* ctx, int polls);
  * routing; it predicts nothing). */
 int ft_hip_fused_set_prefetch(ft_hip_ctx* ctx, int on);
 
+/* Refined prediction for the fused kernel's prefetch (no reference
+ * counterpart; the reference predicts nothing). Layer l+1's router logits
+ * are linear in x_{l+1} = x_l + sum_p w_p D_p a_p, so with the table
+ * M_{l,e} = R_{l+1} D_{l,e} (E router rows x inter columns per expert, int8
+ * per 32 columns with an f32 scale, [n_layers-1][E] records) refiner units
+ * rank R_{l+1} x_l + sum_p w_p M_p a_p as soon as layer l's act blocks are
+ * published, and every unit group prefetches that prediction instead of the
+ * early routing's (R_{l+1} x_l alone). Results are identical with or without
+ * it: the prediction only decides which unit group holds which expert.
+ * Bytes of the table for these banks (-1 on a bad shape). */
+int64_t ft_hip_fused_predictor_bytes(int64_t hidden, int64_t inter, int64_t n_experts, int64_t n_layers);
+
+/* Build the table from fused-layout banks and fused-layout routers (those
+ * ft_hip_moe_stack_fused takes), on `stream`. Setup only. */
+int ft_hip_fused_build_predictor(ft_hip_ctx* ctx, void* stream, const void* banks, const float* routers,
+                                 int64_t hidden, int64_t inter, int64_t n_experts, int64_t n_layers, void* table,
+                                 size_t table_bytes);
+
+/* Use `table` (built for n_layers layers of the banks later launches take)
+ * in every later ft_hip_moe_stack_fused on this context; NULL returns to the
+ * early routing's prediction (the default). A launch with more layers than
+ * the table covers returns FT_HIP_E_SHAPE. */
+int ft_hip_fused_set_predictor(ft_hip_ctx* ctx, const void* table, size_t table_bytes, int64_t n_layers);
+
 /* Fused kernel launch mode. 0 (default): a plain launch, whose workgroups
  * (one per CU, fewer than the device's CUs) are all resident only while no
  * kernel of another stream occupies CUs; the fastest mode for a device the

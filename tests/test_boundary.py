@@ -128,8 +128,24 @@ def test_new_surface_shape_errors():
 
 def test_fused_workgroups_formula():
     """K*max(I/32, H/128) expert units, two group units (each with half of
-    the experts' router sums) and a pred unit per R-order group."""
-    assert ft_hip.Q4Gemv.fused_workgroups(2816, 704, 128, 8) == 8 * 22 + 3 * 8
-    assert ft_hip.Q4Gemv.fused_workgroups(2816, 352, 128, 4) == 4 * 22 + 3 * 8
-    assert ft_hip.Q4Gemv.fused_workgroups(4096, 512, 64, 2) == 2 * 32 + 3 * 8
+    the experts' router sums), a pred unit and a refiner unit per R-order group."""
+    assert ft_hip.Q4Gemv.fused_workgroups(2816, 704, 128, 8) == 8 * 22 + 4 * 8
+    assert ft_hip.Q4Gemv.fused_workgroups(2816, 352, 128, 4) == 4 * 22 + 4 * 8
+    assert ft_hip.Q4Gemv.fused_workgroups(4096, 512, 64, 2) == 2 * 32 + 4 * 8
     assert ft_hip.Q4Gemv.fused_workgroups(2816, 700, 128, 8) == -1
+
+
+def test_fused_predictor_sizes_and_errors():
+    """The refined-prediction table: (L-1) * E records of E x I/32 blocks of
+    36 B; bad shapes and null arguments are refused before any GPU call."""
+    L = ft_hip.lib()
+    P = ctypes.c_void_p(16)
+    assert ft_hip.Q4Gemv.fused_predictor_bytes(2816, 704, 128, 30) == 29 * 128 * 128 * 22 * 36
+    assert ft_hip.Q4Gemv.fused_predictor_bytes(2816, 704, 128, 1) == 0
+    assert ft_hip.Q4Gemv.fused_predictor_bytes(2816, 700, 128, 4) == -1
+    assert ft_hip.Q4Gemv.fused_predictor_bytes(2816, 704, 128, 0) == -1
+    need = ft_hip.Q4Gemv.fused_predictor_bytes(2816, 704, 128, 4)
+    assert _err(L.ft_hip_fused_build_predictor(None, None, P, P, 2880, 704, 128, 4, P, need))[0] == ft_hip.E_SHAPE
+    assert _err(L.ft_hip_fused_build_predictor(None, None, P, P, 2816, 704, 128, 4, P, need - 1))[0] == ft_hip.E_SHAPE
+    assert _err(L.ft_hip_fused_build_predictor(None, None, P, P, 2816, 704, 128, 4, P, need))[0] == ft_hip.E_INVALID
+    assert _err(L.ft_hip_fused_set_predictor(None, P, need, 4))[0] == ft_hip.E_INVALID

@@ -148,6 +148,106 @@ def test_fused_zipf_prefetch_does_not_change_results(gemv, zstack):
         assert np.array_equal(u.view(np.uint32), v.view(np.uint32))
 
 
+def _table_record(stack, l, e):
+    """Record (l, e) of the refined-prediction table -> (values [E, I] dequantized, scales [E, I/32])."""
+    s = stack.m.shape
+    E, nbj = s.n_experts, s.inter // 32
+    rec = E * nbj * 36
+    b = host(stack.pred[(l * E + e) * rec:(l * E + e + 1) * rec])
+    q = b[:E * nbj * 32].view(np.int8).reshape(E, nbj, 32).astype(np.float64)
+    d = b[E * nbj * 32:].view(np.float32).reshape(E, nbj)
+    return (q * d[:, :, None].astype(np.float64)).reshape(E, -1), d
+
+
+@pytest.mark.parametrize("l,e", [(0, 0), (0, 77), (2, 127)])
+def test_fused_predictor_table(gemv, stack, l, e):
+    """Record (l, e) of the refined-prediction table is R_{l+1} D_{l,e}
+    quantized per 32 columns: against the f64 product of the model's router
+    and the expert's down rows (read back from the fused banks and
+    dequantized independently), each value within half a quantization step
+    (and the rounding of v/d) plus the f32 sum's error bound n*u*sum|r*d|,
+    and each block's scale within that bound of its amax / 127."""
+    from test_oracle import unpack_q4
+    m = stack.m
+    s = m.shape
+    H, I, E = s.hidden, s.inter, s.n_experts
+    eb = stack.expert_bytes
+    _, dn = unpack_fused_expert(host(stack.banks[(l * E + e) * eb:(l * E + e + 1) * eb]), H, I)
+    nib, d4 = unpack_q4(dn, I)
+    D = (nib.astype(np.float64) - 8) * np.repeat(d4.astype(np.float64), 32, axis=1)  # [H, I]
+    R = host(m.routers[l + 1]).astype(np.float64)                                      # [E, H]
+    ref, mag = R @ D, np.abs(R) @ np.abs(D)
+    gam = H * 2.0 ** -24
+    got, d = _table_record(stack, l, e)
+    step = np.repeat(d.astype(np.float64), 32, axis=1)
+    assert np.all(np.abs(got - ref) <= 0.5 * step * (1 + 1e-5) + gam * mag)
+    amax = np.abs(ref).reshape(E, I // 32, 32).max(axis=2)
+    bmag = mag.reshape(E, I // 32, 32).max(axis=2)
+    assert np.all(np.abs(d - amax / 127) <= gam * bmag / 127 + 1e-7 * amax)
+    assert np.all(d > 0)
+
+
+def _run_pred(stack, token, pred, prefetch=1):
+    saved = stack.pred
+    stack.pred = saved if pred else None
+    try:
+        return _run_plain(stack, token, prefetch)
+    finally:
+        stack.pred = saved
+
+
+@pytest.mark.parametrize("which,norm", [("uniform", False), ("zipf", True)])
+def test_fused_predictor_does_not_change_results(gemv, stack, zstack, which, norm):
+    """The refined prediction only decides which unit group holds which
+    expert: outputs, ids and weights are bit-identical with it, with the
+    early routing's prediction alone, and with no prefetch."""
+    st = stack if which == "uniform" else zstack
+    with input_norm(gemv, norm):
+        for token in (31, 32):
+            a = _run_pred(st, token, True)
+            b = _run_pred(st, token, False)
+            c = _run_pred(st, token, False, prefetch=0)
+            for u, v, w in zip(a, b, c):
+                assert np.array_equal(u.view(np.uint32), v.view(np.uint32))
+                assert np.array_equal(u.view(np.uint32), w.view(np.uint32))
+
+
+def _misses(stack, token, pred, norm=False):
+    """Held experts not routed, summed over unit groups and the predicted
+    layers 1..L-1, from the debug trace: expert unit u (tile 0, workgroup u)
+    records per layer whether its held expert was routed (slot 10 of row
+    l+1; layer 0 holds nothing)."""
+    m = stack.m
+    nw = stack.n_workgroups()
+    tr = torch.zeros(nw * (m.L + 1) * 32, dtype=torch.int64, device=DEV)
+    x = m.hidden(token)
+    saved = stack.pred
+    stack.pred = saved if pred else None
+    try:
+        with input_norm(m.g, norm):
+            stack.run(x, torch.zeros_like(x), trace=tr)
+        stack.check()
+    finally:
+        stack.pred = saved
+    t = host(tr).reshape(nw, m.L + 1, 32)
+    return int(t[:m.shape.top_k, 2:, 10].sum())
+
+
+@pytest.mark.parametrize("which,norm", [("uniform", False), ("zipf", True)])
+def test_fused_predictor_removes_misses(gemv, stack, zstack, which, norm):
+    """With the table nearly every held expert is routed: at most 3.5 % of
+    the 8 tokens x 3 predicted layers x 8 unit groups miss (measured: 1 and
+    4 of 192; the early routing alone misses 10-20 of them). Under the input
+    norm the table's logits take x_l's norm scale for x_{l+1}'s, which with
+    the Zipf bias decides a few close ranks."""
+    st = stack if which == "uniform" else zstack
+    n = 8 * (st.m.L - 1) * st.m.shape.top_k
+    with_t = sum(_misses(st, 40 + i, True, norm) for i in range(8))
+    without = sum(_misses(st, 40 + i, False, norm) for i in range(8))
+    print(f"misses with the table {with_t}/{n}, early routing alone {without}/{n}")
+    assert with_t <= 0.035 * n
+
+
 def _weights_diag(orc, Wr, x, bias, K, got, want):
     """Which scale of the logits reproduces the kernel's weights (a failure report)."""
     lg = orc.router_logits(Wr, x)
