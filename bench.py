@@ -39,7 +39,7 @@ HBM_PEAK_GBPS = 8000.0
 # 256 MiB torch copy in the same run reads and writes over what the counters report for it.
 # Summaries and commands: profiles/hbm_traffic.md. Reported only for runs with those options.
 MEASURED_TRAFFIC = {
-    "gemma30": 969518821,    # k_moe_stack_fused, one launch (algorithmic 846,151,680 B)
+    "gemma30": 883615384,    # k_moe_stack_fused, one launch (algorithmic 846,151,680 B)
     "zipf": 991925124,       # k_moe_stack_fused, one launch
     "batch16": 7918487317,   # whole step, 30 grouped layers
     "batch64": 11704224180,  # whole step, 30 grouped layers (MFMA)

@@ -59,6 +59,8 @@
 //     then the assignment of routed slots to unit groups.
 // Weight layouts are lossless repacks of q4_0 with its byte count.
 
+#include <type_traits>
+
 #include "ft_device.hpp"
 #include "ft_runtime.hpp"
 
@@ -82,6 +84,7 @@ constexpr int CTL_ABORT = 32;
 constexpr uint32_t ABORT_EPOCH_WRAP = 0xFFFFFFFFu;
 constexpr int TRACE_SLOTS = 32; // stamps per workgroup per layer in the debug trace
 constexpr int PID_STRIDE = 16;  // words per copy of the predicted experts
+template <int N> using IC = std::integral_constant<int, N>;
 constexpr int NCAND = 16;       // candidates of the refined prediction: the early routing's 16 best experts
 constexpr int CW = 3 * NCAND + 1;  // candidate words: ids, sums of R_{l+1} x_l, biases, the norm scale of x_l
 constexpr int CD_STRIDE = 64;   // words per refiner's copy of the candidate words
@@ -754,6 +757,14 @@ __device__ __forceinline__ void poison_outputs(const FusedParams& P, int g) {
 // unconditional so that they issue back to back.
 template <int BPW, int DB, int CPT, bool DBG>
 __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P) {
+    // Gate|up blocks per wave prefetched before the broadcast wait; the rest
+    // are issued once the broadcast is in, and land during the routing. A
+    // CU returns loads in order, so every prefetch load issued before the
+    // broadcast polls delays them; the whole prefetch there held the
+    // broadcast read ~2 us behind its publication. Measured (us/token):
+    // all 11 blocks early 396, 10: 392, 9: 383, 8: 374, 7: 381, 6: 383;
+    // the down rows late as well: 387 (with 8 early).
+    constexpr int PF_EARLY = BPW > 3 ? BPW - 3 : BPW;
     constexpr int C = 2 * BPW;  // router chunks per group = H/128
     // words per thread of each wait (H = 256 * BPW, E <= 128, K <= 8):
     constexpr int UW_GA = (NGROUP * (MAX_E + 1) + FT_THREADS - 1) / FT_THREADS;       // all 8 groups' sums (+ squares)
@@ -1171,8 +1182,10 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     const bool helpers = K == FT_WAVES;
     // per-thread offsets from an opaque thread index: hoisted out of the layer
     // loop they would stay live (and spill) for the whole kernel
-    auto load_gu = [&](int layer, int eid, int s, uint4 (&q)[BPW], uint32_t (&c)[BPW])
+    // blocks [i0, i1) of the wave's share (compile-time bounds)
+    auto load_gu = [&](int layer, int eid, int s, uint4 (&q)[BPW], uint32_t (&c)[BPW], auto i0, auto i1)
                        __attribute__((always_inline)) {
+        constexpr int I0 = decltype(i0)::value, I1 = decltype(i1)::value;
         const int tl = tid_here();
         const uint8_t* xb = P.banks + ((int64_t)layer * E + eid) * P.expert_bytes;
         const int r = tl & 63, b0 = s * BPW;
@@ -1188,9 +1201,9 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         // half in the dots: a 2-byte load is widened by a separate
         // instruction, which makes the wave wait for the load at once.
 #pragma unroll
-        for (int i = 0; i < BPW; ++i) q[i] = *reinterpret_cast<const uint4*>(Tq + i * 1024);
+        for (int i = I0; i < I1; ++i) q[i] = *reinterpret_cast<const uint4*>(Tq + i * 1024);
 #pragma unroll
-        for (int i = 0; i < BPW; ++i) c[i] = *reinterpret_cast<const uint32_t*>(Ts - (r & 1) * 2 + i * 128);
+        for (int i = I0; i < I1; ++i) c[i] = *reinterpret_cast<const uint32_t*>(Ts - (r & 1) * 2 + i * 128);
         asm volatile("" ::: "memory");  // issued here, not sunk towards the first use
     };
     auto load_dn = [&](int layer, int eid) __attribute__((always_inline)) {
@@ -1233,15 +1246,16 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                 hm = true;
                 hug = m->mlist[mi];
                 if (DBG) hslot = m->mslot[mi];
-                load_gu(layer, min(max(m->mexp[mi], 0), E - 1), (u - hug) & (FT_WAVES - 1), hq, hs);
+                load_gu(layer, min(max(m->mexp[mi], 0), E - 1), (u - hug) & (FT_WAVES - 1), hq, hs, IC<0>{}, IC<BPW>{});
             }
         } else if (own_miss) {
-            load_gu(layer, eid, tid_here() >> 6, qv, sc);
+            load_gu(layer, eid, tid_here() >> 6, qv, sc, IC<0>{}, IC<BPW>{});
             load_dn(layer, eid);
         }
     };
     decide(0, true);
     trace_value<DBG>(P, 0, 10, own_miss ? 1u : 0u);
+    int pe = 0;  // the predicted expert of the next layer
     stamp<DBG>(P, -1, 14);
 
     for (int l = 0; l < L; ++l) {
@@ -1417,8 +1431,8 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
                                      reinterpret_cast<uint32_t*>(m->pid[(l + 1) & 1]), l, 27))
                     return;
             }
-            const int pe = min(max(m->pid[(l + 1) & 1][u], 0), E - 1);
-            load_gu(l + 1, pe, wave, qv, sc);
+            pe = min(max(m->pid[(l + 1) & 1][u], 0), E - 1);
+            load_gu(l + 1, pe, wave, qv, sc, IC<0>{}, IC<PF_EARLY>{});
             load_dn(l + 1, pe);
             stamp<DBG>(P, l, 7);
         }
@@ -1426,6 +1440,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
         if (!wait_words<DBG, UW_X>(P, m, epoch, gq_buf(l + 1) + rep * P.rs_gq, NGROUP * nq, xidx, tag_g(l + 1), gq, xdst, l, 24))
             return;
         stamp<DBG>(P, l, 12);
+        if (pf && PF_EARLY < BPW) load_gu(l + 1, pe, wave, qv, sc, IC<PF_EARLY>{}, IC<BPW>{});  // the rest
         route_units(P, m, reinterpret_cast<const float*>(gq), bias_n, pf ? m->pid[(l + 1) & 1] : nullptr);
         stamp<DBG>(P, l, 13);
         decide(l + 1, !pf);
