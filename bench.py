@@ -40,7 +40,7 @@ HBM_PEAK_GBPS = 8000.0
 # Summaries and commands: profiles/hbm_traffic.md. Reported only for runs with those options.
 MEASURED_TRAFFIC = {
     "gemma30": 883615384,    # k_moe_stack_fused, one launch (algorithmic 846,151,680 B)
-    "zipf": 991925124,       # k_moe_stack_fused, one launch
+    "zipf": 888320417,       # k_moe_stack_fused, one launch
     "batch16": 7918487317,   # whole step, 30 grouped layers
     "batch64": 11704224180,  # whole step, 30 grouped layers (MFMA)
     "large32": 25249082752,  # whole step, 32 grouped layers

@@ -407,8 +407,10 @@ int ft_hip_set_input_norm(ft_hip_ctx* ctx, int on);
  * Workgroups: K*max(I/32, H/128) expert units (routed slot p, index j: the
  * gate|up rows of act block j and the down rows 128j..128j+127 of expert
  * ids[p]) plus 16 group units (two per R-order group of H/8 rows: combine,
- * the router sums of half of the experts, q8 of x) and 8 prediction
- * units -- see ft_hip_fused_workgroups. Supported shape: the Gemma expert section (hidden
+ * the router sums of half of the experts, q8 of x), 8 prediction units
+ * (layer l+2's router sums over x_{l+1}) and 8 refiner units (the
+ * prediction of layer l+1, see ft_hip_fused_set_predictor) -- see
+ * ft_hip_fused_workgroups. Supported shape: the Gemma expert section (hidden
  * 2816, inter 704, 128 experts, top-8), the one its tests cover; other
  * shapes return FT_HIP_E_SHAPE (use ft_hip_moe_layer).
  *
@@ -491,11 +493,12 @@ int ft_hip_fused_set_prefetch(ft_hip_ctx* ctx, int on);
  * counterpart; the reference predicts nothing). Layer l+1's router logits
  * are linear in x_{l+1} = x_l + sum_p w_p D_p a_p, so with the table
  * M_{l,e} = R_{l+1} D_{l,e} (E router rows x inter columns per expert, int8
- * per 32 columns with an f32 scale, [n_layers-1][E] records) refiner units
- * rank R_{l+1} x_l + sum_p w_p M_p a_p as soon as layer l's act blocks are
+ * per 32 columns with an f32 scale, [n_layers-1][E] records) the early
+ * routing's 16 best experts (R_{l+1} x_l) are re-ranked by
+ * R_{l+1} x_l + sum_p w_p M_p a_p as soon as layer l's act blocks are
  * published, and every unit group prefetches that prediction instead of the
- * early routing's (R_{l+1} x_l alone). Results are identical with or without
- * it: the prediction only decides which unit group holds which expert.
+ * early routing's. Results are identical with or without it: the prediction
+ * only decides which unit group holds which expert.
  * Bytes of the table for these banks (-1 on a bad shape). */
 int64_t ft_hip_fused_predictor_bytes(int64_t hidden, int64_t inter, int64_t n_experts, int64_t n_layers);
 
