@@ -212,6 +212,29 @@ def test_fused_predictor_does_not_change_results(gemv, stack, zstack, which, nor
                 assert np.array_equal(u.view(np.uint32), w.view(np.uint32))
 
 
+def test_fused_predictor_layer_mismatch_rejected(gemv, stack):
+    """A table built for fewer layers than the launch runs is refused before
+    the launch (FT_HIP_E_SHAPE); building one for 2 layers of the same banks
+    works, and clearing it (None) returns to the early routing."""
+    m = stack.m
+    s = m.shape
+    small = torch.empty(gemv.fused_predictor_bytes(s.hidden, s.inter, s.n_experts, 2), dtype=torch.uint8,
+                        device=DEV)
+    gemv.fused_build_predictor(stack.banks, stack.routers, s.hidden, s.inter, s.n_experts, 2, small)
+    x = m.hidden(0)
+    gemv.fused_set_predictor(small, 2)
+    try:
+        with pytest.raises(ft_hip.FtHipError) as ei:
+            gemv.moe_stack_fused(x, torch.zeros_like(x), s.hidden, s.inter, s.n_experts, s.top_k, m.L, stack.banks,
+                                 stack.routers, m.bias, None, None, None, stack.ws)
+        assert ei.value.code == ft_hip.E_SHAPE
+        with pytest.raises(ft_hip.FtHipError):
+            gemv.fused_set_predictor(small[1:], 2)  # not 16-byte aligned
+    finally:
+        gemv.fused_set_predictor(None)
+    stack.check()
+
+
 def _misses(stack, token, pred, norm=False):
     """Held experts not routed, summed over unit groups and the predicted
     layers 1..L-1, from the debug trace: expert unit u (tile 0, workgroup u)
