@@ -110,7 +110,7 @@ struct FusedParams {
     uint64_t* pl_t;             // tagged [grid]: the XCD each workgroup runs on
     uint64_t* cp_t;             // tagged [2][CP_WORDS], by layer parity: each refiner's copy of the candidate
                                 // words of layer l+1 (CD_STRIDE apart), then the refiners' shares [NGROUP][NCAND]
-    const uint8_t* pred_tab;    // [L-1][E] refined-prediction records (pred_record_bytes each), or null
+    const uint8_t* pred_tab;    // [L-1][E] refined-prediction records (E*(I/32)*36 bytes each), or null
     int64_t rs_gq;              // replica stride (words); the parity stride is NREP * rs_gq
     uint32_t* ctl;              // [CTL_EPOCH] epoch, [CTL_ABORT] abort epoch
     float* dbg_gu;              // [L][K][2I] or null

@@ -509,9 +509,10 @@ int ft_hip_fused_build_predictor(ft_hip_ctx* ctx, void* stream, const void* bank
                                  size_t table_bytes);
 
 /* Use `table` (built for n_layers layers of the banks later launches take)
- * in every later ft_hip_moe_stack_fused on this context; NULL returns to the
- * early routing's prediction (the default). A launch with more layers than
- * the table covers returns FT_HIP_E_SHAPE. */
+ * in every later ft_hip_moe_stack_fused on this context; it must stay
+ * allocated while set. NULL returns to the early routing's prediction (the
+ * default). A launch with more layers than the table covers returns
+ * FT_HIP_E_SHAPE. */
 int ft_hip_fused_set_predictor(ft_hip_ctx* ctx, const void* table, size_t table_bytes, int64_t n_layers);
 
 /* Fused kernel launch mode. 0 (default): a plain launch, whose workgroups
