@@ -469,16 +469,27 @@ def teacher_forced(model, gpu_states, gpu_ids, threads, input_norm, n_tok):
 
 
 def host_cpu():
-    """(model name, logical CPUs) of this host."""
-    name = "unknown"
+    """(model name with its family/model/stepping and vector extensions, logical CPUs) of this host.
+    Virtualised hosts often report a bare "AMD EPYC" as the model name; the CPUID family and model
+    and the AVX2 / AVX-512 flags (the reference's CPU path is AVX2) identify the part further."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    name = line.split(":", 1)[1].strip()
-                    break
+                if not line.strip():
+                    break  # the first processor's block
+                k, _, v = line.partition(":")
+                fields[k.strip()] = v.strip()
     except OSError:
         pass
+    name = fields.get("model name", "unknown")
+    flags = fields.get("flags", "").split()
+    extra = [f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields]
+    if flags:
+        extra.append("AVX2 " + ("yes" if "avx2" in flags else "no"))
+        extra.append("AVX-512 " + ("yes" if "avx512f" in flags else "no"))
+    if extra:
+        name += " (" + ", ".join(extra) + ")"
     return name, os.cpu_count() or 1
 
 
