@@ -485,6 +485,9 @@ __global__ __launch_bounds__(GT, 1) void k_grouped_down(const uint8_t* bank, int
 // ---------------------------------------------------------------------------
 typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int MT = 16;  // tokens per MFMA tile
+// token stride of the gate|up wave partials in LDS: one more than MT, so the
+// wave-order sums (consecutive lanes: consecutive rows) read distinct banks
+constexpr int MTP = MT + 1;
 static_assert(MT * 10 <= GT, "k_mfma_gu stores a chunk's q8 words with one thread each");
 
 struct ActOp {
@@ -605,12 +608,12 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
     const int per = (n_items + (int)gridDim.x - 1) / (int)gridDim.x;
     const int it0 = (int)blockIdx.x * per, it1 = min(n_items, it0 + per);
     if (it0 >= it1) return;
-    // LDS: scales [nb][64] f32 | wave partials [GW][64][MT] | sums [MT][64] |
+    // LDS: scales [nb][64] f32 | wave partials [GW][64][MTP] | sums [MT][64] |
     // act [MT][32] | act q8 [MT][10] | the chunk's tokens (pair, norm scale)
     // [MT] x2 | the chunk's q8 rows [MT][nb*10 + 1] u32
     float* scl = reinterpret_cast<float*>(lds);
     float* red = reinterpret_cast<float*>(lds + nb * 256);
-    float* rows = red + GW * 64 * MT;
+    float* rows = red + GW * 64 * MTP;
     float* actv = rows + MT * 64;
     uint32_t* ablk = reinterpret_cast<uint32_t*>(actv + MT * 32);
     int* tok_p = reinterpret_cast<int*>(ablk + MT * 10);
@@ -763,14 +766,14 @@ __global__ __launch_bounds__(GT, 1) void k_mfma_gu(const uint8_t* __restrict__ b
 #pragma unroll
         for (int m = 0; m < 4; ++m)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) red[(wave * 64 + 16 * m + 4 * lg + v) * MT + li] = acc[m][v];
+            for (int v = 0; v < 4; ++v) red[(wave * 64 + 16 * m + 4 * lg + v) * MTP + li] = acc[m][v];
         __syncthreads();  // every wave is past its MFMAs: act rows and scl may change below
         if (nxt_scales) load_scales(nxt);
         for (int i = t; i < cur.nt * 64; i += GT) {  // (token, row) sums over the waves, in wave order
             const int tt = i >> 6, rr = i & 63;
             float sv = 0.0f;
 #pragma unroll
-            for (int v = 0; v < GW; ++v) sv = sv + red[(v * 64 + rr) * MT + tt];
+            for (int v = 0; v < GW; ++v) sv = sv + red[(v * 64 + rr) * MTP + tt];
             const int pp = tok_p[tt];
             if (in_scale) sv = sv * tok_s[tt];
             rows[tt * 64 + rr] = sv;
@@ -1099,7 +1102,7 @@ extern "C" int ft_hip_moe_layer_grouped(ft_hip_ctx* ctx, void* stream, const flo
         if ((rc = launch_status("moe_layer_grouped/gate_up"))) return rc;
     }
     if (mfma) {
-        const size_t lds_mg = (size_t)nb * 256 + sizeof(float) * (GW * 64 * MT + MT * 64 + MT * 32) + 4 * MT * 10 +
+        const size_t lds_mg = (size_t)nb * 256 + sizeof(float) * (GW * 64 * MTP + MT * 64 + MT * 32) + 4 * MT * 10 +
                               8 * MT + 4 * (size_t)MT * (nb * 10 + 1);
         auto kern = H == 2816 ? (rec ? k_mfma_gu<11, true> : k_mfma_gu<11, false>)
                               : (rec ? k_mfma_gu<16, true> : k_mfma_gu<16, false>);
