@@ -1008,6 +1008,88 @@ __global__ __launch_bounds__(256) void k_route_prep_n(const float* W, const floa
         quantize_block_quad(xs + 32 * b, l & 3, reinterpret_cast<uint32_t*>(q8 + ((int64_t)s * nb + b) * Q8_BLK));
 }
 
+// k_route_prep_n for SQ seqs per workgroup as well (larger batches): workgroup
+// (eg, sg) computes logits EG*eg..+EG-1 of seqs SQ*sg..+SQ-1, each in the
+// R-order as k_route_prep (the same bits), holding the EG router chunks in
+// registers across the SQ seqs, so the router is read n_seqs/SQ times
+// instead of n_seqs; and quantizes q8 blocks [eg*Q, eg*Q+Q) of each of its
+// seqs, Q = ceil(nb / gridDim.x). Workgroup eg == 0 stores inv of its seqs.
+// Grid (n_rows/EG, n_seqs/SQ), 256 threads.
+template <int EG, int SQ>
+__global__ __launch_bounds__(256) void k_route_prep_m(const float* W, const float* x, const float* bias, int norm,
+                                                      float* inv, uint8_t* q8, float* y, int dim, int n_rows) {
+    extern __shared__ float P[];  // [SQ][EG+1][nch + 1] chunk partials: the EG logits', then x.x
+    __shared__ float G[SQ * (EG + 1) * 8], tot[SQ * (EG + 1)];
+    const int eg = blockIdx.x, s0 = blockIdx.y * SQ, l = threadIdx.x;
+    const int nch = dim >> 4, ps = nch + 1;  // odd row stride: the group sums' lanes read different banks
+    const float* w0 = W + (int64_t)eg * EG * dim;
+    for (int c = l; c < nch; c += blockDim.x) {
+        float4 wv[EG][4];
+#pragma unroll
+        for (int j = 0; j < EG; ++j)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) wv[j][k] = reinterpret_cast<const float4*>(w0 + (int64_t)j * dim + 16 * c)[k];
+#pragma unroll
+        for (int q = 0; q < SQ; ++q) {
+            const float4* x4 = reinterpret_cast<const float4*>(x + (int64_t)(s0 + q) * dim + 16 * c);
+            float4 xv[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) xv[k] = x4[k];
+            float* Pq = P + q * (EG + 1) * ps;
+#pragma unroll
+            for (int j = 0; j < EG; ++j) {
+                float p = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float4 a = wv[j][k], b = xv[k];
+                    p = fmaf(a.x, b.x, p);
+                    p = fmaf(a.y, b.y, p);
+                    p = fmaf(a.z, b.z, p);
+                    p = fmaf(a.w, b.w, p);
+                }
+                Pq[j * ps + c] = p;
+            }
+            float pss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float4 b = xv[k];
+                pss = fmaf(b.x, b.x, pss);
+                pss = fmaf(b.y, b.y, pss);
+                pss = fmaf(b.z, b.z, pss);
+                pss = fmaf(b.w, b.w, pss);
+            }
+            Pq[EG * ps + c] = pss;
+        }
+    }
+    __syncthreads();
+    const int C = dim >> 7;
+    for (int i = l; i < SQ * (EG + 1) * 8; i += blockDim.x) G[i] = group_sum(P + (i >> 3) * ps + (i & 7) * C, C);
+    __syncthreads();
+    if (l < SQ * (EG + 1)) {
+        float t = 0.0f;
+        for (int g = 0; g < 8; ++g) t = t + G[l * 8 + g];
+        tot[l] = t;
+    }
+    __syncthreads();
+    if (l < SQ * EG) {
+        const int q = l / EG, jj = l - q * EG;
+        const float ir = norm ? 1.0f / sqrtf(tot[q * (EG + 1) + EG] / (float)dim + 1e-6f) : 1.0f;  // correctly rounded
+        const int e = eg * EG + jj, s = s0 + q;
+        float t = tot[q * (EG + 1) + jj];
+        if (norm) t = t * ir;
+        if (bias) t = t + bias[e];
+        y[(int64_t)s * n_rows + e] = t;
+        if (norm && e == 0) inv[s] = ir;
+    }
+    const int nb = dim >> 5, Q = (nb + gridDim.x - 1) / gridDim.x;
+    for (int i = l; i < SQ * Q * 4; i += blockDim.x) {  // whole quads: 4 consecutive lanes per block
+        const int q = i / (Q * 4), rem = i - q * Q * 4, b = eg * Q + (rem >> 2);
+        if (b < nb)
+            quantize_block_quad(x + (int64_t)(s0 + q) * dim + 32 * b, rem & 3,
+                                reinterpret_cast<uint32_t*>(q8 + ((int64_t)(s0 + q) * nb + b) * Q8_BLK));
+    }
+}
+
 // Scale of the input RMS norm per seq: inv[s] = 1 / sqrt(ss / dim + 1e-6),
 // ss = x_s.x_s in the R-order, each op rounded once. Grid n_seqs.
 __global__ __launch_bounds__(256) void k_rms_inv(const float* x, float* inv, int dim) {
@@ -1505,6 +1587,18 @@ int launch_route_prep(void* stream, const float* w, const float* x, const float*
     // when the rows split into groups that still cover the q8 blocks at up to
     // 64 per workgroup: 8 from 32 seqs (measured faster at 64), 4 from 16
     const int eg = n_seqs >= 32 ? 8 : (n_seqs >= 16 ? 4 : 1);
+    // from 32 seqs also 4 seqs per workgroup (the router read n_seqs/4
+    // times), when that still makes at least 128 workgroups (256 at 64 seqs
+    // of 128 experts: 65.8-66.8 vs 66.2-67.2 us/token on two boxes; at 16
+    // seqs 2 per workgroup measured no faster)
+    constexpr int sq = 4;
+    if (eg == 8 && n_rows % eg == 0 && n_seqs % sq == 0 && (n_rows / eg) * (n_seqs / sq) >= 128) {
+        const size_t lds = sizeof(float) * (size_t)sq * (eg + 1) * (dim / 16 + 1);
+        auto kern = k_route_prep_m<8, sq>;
+        hipLaunchKernelGGL(kern, dim3((unsigned)(n_rows / eg), (unsigned)(n_seqs / sq)), dim3(256), lds, S(stream), w,
+                           x, bias, norm, inv, (uint8_t*)q8, y, (int)dim, (int)n_rows);
+        return launch_status("route_prep_m");
+    }
     if (eg > 1 && n_rows % eg == 0 && (n_rows / eg) * 64 >= dim / 32) {
         hipLaunchKernelGGL(eg == 8 ? k_route_prep_n<8> : k_route_prep_n<4>, dim3((unsigned)(n_rows / eg),
                            (unsigned)n_seqs), dim3(256), (size_t)(dim / 16) * (eg + 1) * 4, S(stream), w, x, bias,
