@@ -993,12 +993,23 @@ __global__ __launch_bounds__(256) void k_grouped_combine(const float* y, const f
                                                          int H, int K) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x, s = blockIdx.y;
     if (i >= H) return;
+    const float xv = x[(int64_t)s * H + i];
     float h = 0.0f;
-    for (int k = 0; k < K; ++k) {
-        const float part = y[((int64_t)s * K + k) * H + i] * wts[s * K + k];
-        h = h + part;
+    for (int k0 = 0; k0 < K; k0 += 8) {  // the loads of 8 slots issued together, then the sum in slot order
+        float yv[8], wv[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int k = min(k0 + q, K - 1);
+            yv[q] = y[((int64_t)s * K + k) * H + i];
+            wv[q] = wts[s * K + k];
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float part = yv[q] * wv[q];
+            h = k0 + q < K ? h + part : h;
+        }
     }
-    out[(int64_t)s * H + i] = x[(int64_t)s * H + i] + h;
+    out[(int64_t)s * H + i] = xv + h;
 }
 
 int check_grouped_shape(const char* nm, int64_t B, int64_t H, int64_t I, int64_t E, int64_t K) {

@@ -954,17 +954,30 @@ __global__ __launch_bounds__(256) void k_route_prep_n(const float* W, const floa
     const float* w0 = W + (int64_t)eg * EG * dim;
     for (int c = l; c < nch; c += blockDim.x) {
         const float4* x4 = reinterpret_cast<const float4*>(xs + 16 * c);
-        float4 xv[4];
+        float4 xv[4], wv[EG][4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) xv[k] = x4[k];
+#pragma unroll
+        for (int j = 0; j < EG; ++j)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) wv[j][k] = reinterpret_cast<const float4*>(w0 + (int64_t)j * dim + 16 * c)[k];
+        // every value held at once here: the loads are all issued before the
+        // chains (the scheduler otherwise interleaved them, a load latency
+        // per few loads)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            asm volatile("" : "+v"(xv[k].x), "+v"(xv[k].y), "+v"(xv[k].z), "+v"(xv[k].w));
+#pragma unroll
+            for (int j = 0; j < EG; ++j)
+                asm volatile("" : "+v"(wv[j][k].x), "+v"(wv[j][k].y), "+v"(wv[j][k].z), "+v"(wv[j][k].w));
+        }
         float pe[EG], ps = 0.0f;
 #pragma unroll
         for (int j = 0; j < EG; ++j) {
-            const float4* w4 = reinterpret_cast<const float4*>(w0 + (int64_t)j * dim + 16 * c);
             float p = 0.0f;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const float4 a = w4[k], b = xv[k];
+                const float4 a = wv[j][k], b = xv[k];
                 p = fmaf(a.x, b.x, p);
                 p = fmaf(a.y, b.y, p);
                 p = fmaf(a.z, b.z, p);
@@ -1024,24 +1037,38 @@ __global__ __launch_bounds__(256) void k_route_prep_m(const float* W, const floa
     const int nch = dim >> 4, ps = nch + 1;  // odd row stride: the group sums' lanes read different banks
     const float* w0 = W + (int64_t)eg * EG * dim;
     for (int c = l; c < nch; c += blockDim.x) {
-        float4 wv[EG][4];
+        // every load of the chunk issued before the first fma (one load
+        // latency), then the chains: each (logit, seq) partial and each seq's
+        // x.x over the 16 elements in order
+        float4 wv[EG][4], xv[SQ][4];
 #pragma unroll
-        for (int j = 0; j < EG; ++j)
+        for (int k = 0; k < 4; ++k) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) wv[j][k] = reinterpret_cast<const float4*>(w0 + (int64_t)j * dim + 16 * c)[k];
+            for (int j = 0; j < EG; ++j) wv[j][k] = reinterpret_cast<const float4*>(w0 + (int64_t)j * dim + 16 * c)[k];
+#pragma unroll
+            for (int q = 0; q < SQ; ++q) xv[q][k] = reinterpret_cast<const float4*>(x + (int64_t)(s0 + q) * dim + 16 * c)[k];
+        }
+        // every value held at once here: the loads cannot be sunk towards
+        // their first use (the scheduler otherwise interleaved them with the
+        // chains, one load latency per few loads)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+#pragma unroll
+            for (int j = 0; j < EG; ++j)
+                asm volatile("" : "+v"(wv[j][k].x), "+v"(wv[j][k].y), "+v"(wv[j][k].z), "+v"(wv[j][k].w));
+#pragma unroll
+            for (int q = 0; q < SQ; ++q)
+                asm volatile("" : "+v"(xv[q][k].x), "+v"(xv[q][k].y), "+v"(xv[q][k].z), "+v"(xv[q][k].w));
+        }
 #pragma unroll
         for (int q = 0; q < SQ; ++q) {
-            const float4* x4 = reinterpret_cast<const float4*>(x + (int64_t)(s0 + q) * dim + 16 * c);
-            float4 xv[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) xv[k] = x4[k];
             float* Pq = P + q * (EG + 1) * ps;
 #pragma unroll
             for (int j = 0; j < EG; ++j) {
                 float p = 0.0f;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    const float4 a = wv[j][k], b = xv[k];
+                    const float4 a = wv[j][k], b = xv[q][k];
                     p = fmaf(a.x, b.x, p);
                     p = fmaf(a.y, b.y, p);
                     p = fmaf(a.z, b.z, p);
@@ -1052,7 +1079,7 @@ __global__ __launch_bounds__(256) void k_route_prep_m(const float* W, const floa
             float pss = 0.0f;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const float4 b = xv[k];
+                const float4 b = xv[q][k];
                 pss = fmaf(b.x, b.x, pss);
                 pss = fmaf(b.y, b.y, pss);
                 pss = fmaf(b.z, b.z, pss);
