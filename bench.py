@@ -42,8 +42,8 @@ MEASURED_TRAFFIC = {
     "gemma30": 883615384,    # k_moe_stack_fused, one launch (algorithmic 846,151,680 B)
     "zipf": 888320417,       # k_moe_stack_fused, one launch
     "batch16": 7918487317,   # whole step, 30 grouped layers
-    "batch64": 11704224180,  # whole step, 30 grouped layers (MFMA)
-    "large32": 25249082752,  # whole step, 32 grouped layers
+    "batch64": 12209286449,  # whole step, 30 grouped layers (MFMA)
+    "large32": 25578821695,  # whole step, 32 grouped layers
     "large1": 132300061,     # k_gemv_gu_long, one launch (algorithmic 132,120,576 B)
 }
 METRIC = "MoE expert-FFN µs/token at batch 1 + achieved HBM GB/s (% of MI355X peak)"
