@@ -337,16 +337,19 @@ __device__ __forceinline__ void head_prologue(const HeadArgs& h, int s, int H, i
 // Layer-record helpers of the REC instantiations (tests only).
 // The q8 row of x_s that a head prologue left in LDS, stored by the seq's
 // first workgroup (blockIdx.x 0 of pair s*div).
-__device__ __forceinline__ void record_x8(const GemvArgs& a, int e, int s, int div, const int* lds) {
-    if (!a.x8rec || blockIdx.x != 0 || e != s * div) return;
+__device__ __forceinline__ void record_x8(const GemvArgs& a, int e, int s, int div, const int* lds,
+                                          int jb = -1) {
+    if (!a.x8rec || (jb < 0 ? (int)blockIdx.x : jb) != 0 || e != s * div) return;
     const int nw = (a.k >> 5) * 10;
     int* dst = reinterpret_cast<int*>(a.x8rec + (int64_t)s * (a.k >> 5) * Q8_BLK);
     for (int i = threadIdx.x; i < nw; i += blockDim.x) dst[i] = lds[i];
 }
 // Lane l < 32 of the tail: the scaled gate and up sums of act block blockIdx.x.
-__device__ __forceinline__ void record_sums(const GemvArgs& a, int e, int inter, float gate, float up) {
-    if (!a.sums || threadIdx.x >= 32) return;
-    float* dst = a.sums + (int64_t)e * 2 * inter + (int)blockIdx.x * 32 + threadIdx.x;
+__device__ __forceinline__ void record_sums(const GemvArgs& a, int e, int inter, float gate, float up, int jb = -1,
+                                            int tl = -1) {
+    const int t = tl < 0 ? (int)threadIdx.x : tl;
+    if (!a.sums || t >= 32) return;
+    float* dst = a.sums + (int64_t)e * 2 * inter + (jb < 0 ? (int)blockIdx.x : jb) * 32 + t;
     dst[0] = gate;
     dst[inter] = up;
 }
@@ -610,21 +613,35 @@ __device__ __forceinline__ float long_row_dot(const LongRow<BPL>& r, const LongA
 }
 
 // k_gemv_gu_act for rows of 64*BPL blocks (q4r): the same work per (act
-// block j, pair) workgroup and the same prologues (logits or head, top-k)
-// and tail (GELU*up, q8). 256 threads: wave w owns gate rows 32j+8w..+7 and
-// up rows I+32j+8w..+7, four rows in flight, a row's slot refilled with the
-// row four later once its dots are done. The activation row's loads go out
-// before the weights' (loads complete in order), their LDS stores after.
-// REC: the test record of k_gemv_gu_act (block dots, sums, head q8 row).
-template <bool TOPK, int BPL, bool HEAD = false, bool REC = false>
-__global__ __launch_bounds__(256, 4) void k_gemv_gu_long(GemvArgs a, int inter, uint8_t* q8a, const float* in_scale,
-                                                         int div, const float* logits, const float* escale,
-                                                         int32_t* ids, float* wts, int E, HeadArgs h) {
+// block j, pair) unit and the same prologues (logits or head, top-k) and
+// tail (GELU*up, q8). 256 threads per unit: wave w owns gate rows 32j+8w..+7
+// and up rows I+32j+8w..+7, four rows in flight, a row's slot refilled with
+// the row four later once its dots are done. The activation row's loads go
+// out before the weights' (loads complete in order), their LDS stores after.
+// UPB units per workgroup (256*UPB threads, grid (inter/32)*pairs/UPB):
+// sub-group g takes unit blockIdx.x*UPB + g, act block j = unit % (inter/32)
+// of pair unit / (inter/32), so the UPB units share their pair (inter/32 is a
+// multiple of UPB) and the prologue is computed once for them; with UPB 1 the
+// grid is (inter/32, pairs). REC: the test record of k_gemv_gu_act (block
+// dots, sums, head q8 row).
+template <bool TOPK, int BPL, bool HEAD = false, bool REC = false, int UPB = 1>
+__global__ __launch_bounds__(256 * UPB, UPB == 1 ? 4 : 1) void k_gemv_gu_long(GemvArgs a, int inter, uint8_t* q8a,
+                                                                             const float* in_scale, int div,
+                                                                             const float* logits, const float* escale,
+                                                                             int32_t* ids, float* wts, int E,
+                                                                             HeadArgs h) {
     static_assert(TOPK || !HEAD, "the head's logits are ranked in the launch");
     constexpr int RPW = 16, RIF = 4;  // rows per wave, rows in flight
     extern __shared__ int lds[];
-    __shared__ float gs[64];
-    const int e = blockIdx.y, t = threadIdx.x;
+    __shared__ float gs[UPB][64];
+    const int tw = threadIdx.x;  // thread of the workgroup (prologue)
+    const int g = UPB > 1 ? tw >> 8 : 0, t = UPB > 1 ? tw & 255 : tw;  // sub-group, thread of the unit
+    const int nblk = inter >> 5, unit = (int)blockIdx.x * UPB + g;
+    const int jb = UPB > 1 ? unit % nblk : (int)blockIdx.x;   // act block
+    const int e = UPB > 1 ? unit / nblk : (int)blockIdx.y;    // pair (the same for the workgroup's units)
+    // the workgroup's first act block: the conditions below that guard
+    // barriers depend on it, not on jb, so they are uniform per workgroup
+    const int jw = UPB > 1 ? ((int)blockIdx.x * UPB) % nblk : (int)blockIdx.x;
     __shared__ float sv[TOPK ? 256 : 1], selv[TOPK ? 32 : 1];
     __shared__ int seli[TOPK ? 32 : 1];
     __shared__ uint64_t key[TOPK ? 256 : 1];
@@ -636,7 +653,7 @@ __global__ __launch_bounds__(256, 4) void k_gemv_gu_long(GemvArgs a, int inter, 
     constexpr int RB = (64 * BPL * 2 + 15) / 16 * 16 + 64 * BPL * 16;  // q4r row bytes
     LongRow<BPL> rr[RIF];
     const uint8_t* eb = nullptr;
-    auto row_of = [&](int i) { return (i < 8 ? 0 : inter) + (int)blockIdx.x * 32 + 8 * wave + (i & 7); };
+    auto row_of = [&](int i) { return (i < 8 ? 0 : inter) + jb * 32 + 8 * wave + (i & 7); };
     auto load_row = [&](int i) __attribute__((always_inline)) {
         long_row_load<BPL>(eb + (int64_t)row_of(i) * RB, lane, rr[i % RIF]);
     };
@@ -647,29 +664,29 @@ __global__ __launch_bounds__(256, 4) void k_gemv_gu_long(GemvArgs a, int inter, 
     };
     if constexpr (HEAD) {
         head_prologue(h, s, a.k, E, sv, lds, reinterpret_cast<float*>(lds + (a.k >> 5) * 10), hg, &irs);
-        if (REC) record_x8(a, e, s, div, lds);
+        if (REC) record_x8(a, e, s, div, lds, jw);  // every thread of the workgroup holding block 0
     } else {
         // the q8 row of x (10 words per block: 64*BPL*10 words, XW per thread)
-        constexpr int XW = (64 * BPL * 10 + 255) / 256;
+        constexpr int XW = (64 * BPL * 10 + 256 * UPB - 1) / (256 * UPB);
         const int nw = (a.k >> 5) * 10;
         const int* src = reinterpret_cast<const int*>(a.q8 + (int64_t)entry_xrow(a, e) * a.q8_stride_blocks * Q8_BLK);
         int v[XW];
 #pragma unroll
-        for (int r = 0; r < XW; ++r) v[r] = t + 256 * r < nw ? src[t + 256 * r] : 0;
-        if (TOPK && t < E) sv[t] = logits[(int64_t)s * E + t];
+        for (int r = 0; r < XW; ++r) v[r] = tw + 256 * UPB * r < nw ? src[tw + 256 * UPB * r] : 0;
+        if (TOPK && tw < E) sv[tw] = logits[(int64_t)s * E + tw];
         if constexpr (!TOPK) issue(a.slots[e]);  // the pair's expert is known: weights behind the q8 row
 #pragma unroll
         for (int r = 0; r < XW; ++r)
-            if (t + 256 * r < nw) lds[t + 256 * r] = v[r];
+            if (tw + 256 * UPB * r < nw) lds[tw + 256 * UPB * r] = v[r];
         __syncthreads();
     }
     if constexpr (TOPK) {
         topk_rank_select(sv, E, div, key, selv, seli);
-        if (blockIdx.x == 0 && e == s * div) {  // the seq's writer (uniform per workgroup): the weights too
+        if (jw == 0 && e == s * div) {  // the seq's writer (uniform per workgroup; a barrier inside): the weights too
             const float w = topk_softmax(selv, seli, div, escale, exv);
-            if (t < div) {
-                ids[(int64_t)s * div + t] = seli[t];
-                wts[(int64_t)s * div + t] = w;
+            if (tw < div) {
+                ids[(int64_t)s * div + tw] = seli[tw];
+                wts[(int64_t)s * div + tw] = w;
             }
         }
         issue(seli[e - s * div]);
@@ -680,22 +697,22 @@ __global__ __launch_bounds__(256, 4) void k_gemv_gu_long(GemvArgs a, int inter, 
     for (int i = 0; i < RPW; ++i) {
         int32_t* rec = REC && a.dots ? a.dots + ((int64_t)e * 2 * inter + row_of(i)) * (64 * BPL) : nullptr;
         const float acc = long_row_dot<BPL>(rr[i % RIF], xa, lane, rec);
-        if (lane == 0) gs[(i < 8 ? 0 : 32) + 8 * wave + (i & 7)] = acc;
+        if (lane == 0) gs[g][(i < 8 ? 0 : 32) + 8 * wave + (i & 7)] = acc;
         if (i + RIF < RPW) load_row(i + RIF);
     }
     __syncthreads();
-    if (threadIdx.x < 64) {  // both half-waves compute block j; the first stores it
-        const int l = threadIdx.x & 31;
-        float gate = gs[l], up = gs[32 + l];
+    if (t < 64) {  // both half-waves compute block j; the first stores it
+        const int l = t & 31;
+        float gate = gs[g][l], up = gs[g][32 + l];
         if (HEAD ? h.norm != 0 : in_scale != nullptr) {
             const float sc = HEAD ? irs : in_scale[e / div];
             gate = gate * sc;
             up = up * sc;
         }
-        if (REC) record_sums(a, e, inter, gate, up);
+        if (REC) record_sums(a, e, inter, gate, up, jb, t);
         const float v = gelu_tanh(gate) * up;
         const Q8Lane r = q8_quantize_half(v);
-        if (threadIdx.x < 32) q8_store_half(q8a + ((int64_t)e * (inter >> 5) + blockIdx.x) * Q8_BLK, l, r);
+        if (t < 32) q8_store_half(q8a + ((int64_t)e * (inter >> 5) + jb) * Q8_BLK, l, r);
     }
 }
 
@@ -1371,10 +1388,19 @@ static int short_lanes(const ft_hip_ctx* ctx, int layout, int64_t n_rows, int64_
 static int gu_long_bpl(int layout, int64_t hidden) {
     return layout == FT_LAYOUT_Q4R && (hidden == 2048 || hidden == 4096) ? (int)(hidden / 2048) : 0;
 }
+// Launches of (inter/32, pairs) units: four units per workgroup (one per
+// CU: the workgroups then spread evenly, 224 for the large-expert layer's
+// 896 units, instead of 3 or 4 of the 256-thread form per CU) when 4 divides
+// inter/32 and the layer has at least 128 such workgroups.
 template <bool TOPK, bool HEAD, bool REC = false>
 static void launch_gu_long_r(int bpl, dim3 grid, size_t lds, hipStream_t st, const GemvArgs& a, int inter,
                              uint8_t* q8a, const float* in_scale, int div, const float* logits, const float* escale,
                              int32_t* ids, float* wts, int E, const HeadArgs& h) {
+    if (bpl == 2 && grid.x % 4 == 0 && grid.x * grid.y / 4 >= 128) {
+        hipLaunchKernelGGL((k_gemv_gu_long<TOPK, 2, HEAD, REC, 4>), dim3(grid.x * grid.y / 4), dim3(1024), lds, st, a,
+                           inter, q8a, in_scale, div, logits, escale, ids, wts, E, h);
+        return;
+    }
     if (bpl == 1)
         hipLaunchKernelGGL((k_gemv_gu_long<TOPK, 1, HEAD, REC>), grid, dim3(256), lds, st, a, inter, q8a, in_scale,
                            div, logits, escale, ids, wts, E, h);
