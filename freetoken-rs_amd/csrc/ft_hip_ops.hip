@@ -631,7 +631,9 @@ __global__ __launch_bounds__(256 * UPB, UPB == 1 ? 4 : 1) void k_gemv_gu_long(Ge
                                                                              int32_t* ids, float* wts, int E,
                                                                              HeadArgs h) {
     static_assert(TOPK || !HEAD, "the head's logits are ranked in the launch");
-    constexpr int RPW = 16, RIF = 4;  // rows per wave, rows in flight
+    // rows per wave, rows in flight (with one workgroup per CU, 3 measured faster than 2, 4 or 6:
+    // large1 1438.7-1439.0 vs 1448.1-1448.5, 1443.3-1448.4 and 1466.9-1467.6 us/token, same box)
+    constexpr int RPW = 16, RIF = UPB > 1 ? 3 : 4;
     extern __shared__ int lds[];
     __shared__ float gs[UPB][64];
     const int tw = threadIdx.x;  // thread of the workgroup (prologue)
