@@ -44,7 +44,7 @@ MEASURED_TRAFFIC = {
     "batch16": 7918487317,   # whole step, 30 grouped layers
     "batch64": 12209286449,  # whole step, 30 grouped layers (MFMA)
     "large32": 25578821695,  # whole step, 32 grouped layers
-    "large1": 132300061,     # k_gemv_gu_long, one launch (algorithmic 132,120,576 B)
+    "large1": 132269060,     # k_gemv_gu_long, one launch (algorithmic 132,120,576 B)
 }
 METRIC = "MoE expert-FFN µs/token at batch 1 + achieved HBM GB/s (% of MI355X peak)"
 # name -> (shape, tokens per step, Zipf exponent of the router bias, BASELINE.json config)
