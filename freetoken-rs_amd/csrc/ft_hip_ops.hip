@@ -905,6 +905,17 @@ __global__ __launch_bounds__(256) void k_route_prep(const float* W, const float*
     __shared__ float irs;
     const int e = blockIdx.x, s = blockIdx.y, l = threadIdx.x;
     const float* xs = x + (int64_t)s * dim;
+    // this lane's part of the q8 block it quantizes at the end, loaded with
+    // the first loads (one load latency for the launch, not two)
+    const int nb = dim >> 5, b = e * 16 + (l >> 2);
+    const bool qz = e * 16 < nb && l < 64 && b < nb;  // quads of blocks beyond nb idle
+    float4 qa = make_float4(0.f, 0.f, 0.f, 0.f), qb = qa;
+    if (qz) {
+        const float4* v4 = reinterpret_cast<const float4*>(xs + 32 * b);
+        qa = v4[2 * (l & 3)];
+        qb = v4[2 * (l & 3) + 1];
+    }
+    const float bv = bias && l == 0 ? bias[e] : 0.0f;  // the logit's bias, loaded with them
     float t;
     if (norm) {  // both R-order dots in one pass: x.x (P) and w.x (Q), each in its own order
         const float* w = W + (int64_t)e * dim;
@@ -945,15 +956,11 @@ __global__ __launch_bounds__(256) void k_route_prep(const float* W, const float*
     const float ir = norm ? irs : 1.0f;
     if (l == 0) {
         if (norm) t = t * ir;
-        if (bias) t = t + bias[e];
+        if (bias) t = t + bv;
         y[(int64_t)s * n_rows + e] = t;
         if (norm && e == 0) inv[s] = ir;
     }
-    const int nb = dim >> 5, b = e * 16 + (l >> 2);
-    if (e * 16 < nb) {  // uniform per workgroup; the quads of blocks beyond nb idle
-        if (l < 64 && b < nb)
-            quantize_block_quad(xs + 32 * b, l & 3, reinterpret_cast<uint32_t*>(q8 + ((int64_t)s * nb + b) * Q8_BLK));
-    }
+    if (qz) quantize_block_quad_v(qa, qb, l & 3, reinterpret_cast<uint32_t*>(q8 + ((int64_t)s * nb + b) * Q8_BLK));
 }
 
 // k_route_prep for EG logits per workgroup (batched decode): workgroup
