@@ -517,6 +517,15 @@ __global__ __launch_bounds__(NT) void k_gemv_down_head(GemvArgs a, const float* 
         }
     };
     if (EARLY) load_w();
+    // the combine's operands (this row's x and the seq's pair weights), loaded
+    // first: read only after the GEMV, they would add a load latency there
+    constexpr int KW = NT / (16 * 8);  // k <= NT / (16 * LPR) <= NT / 128 pairs
+    float xr = 0.0f, wk[KW];
+    if (t < 16) {
+        xr = x[(int64_t)s * H + c * 16 + t];
+#pragma unroll
+        for (int q = 0; q < KW; ++q) wk[q] = q < k ? wts[(int64_t)s * k + q] : 0.0f;
+    }
     stage_words<40>(reinterpret_cast<const int*>(a.q8 + (int64_t)s * k * a.q8_stride_blocks * Q8_BLK), k * nb * 10,
                     lds);
     const int lane = t & 63, wave = t >> 6;
@@ -533,11 +542,12 @@ __global__ __launch_bounds__(NT) void k_gemv_down_head(GemvArgs a, const float* 
     if (t < 16) {
         const int i = c * 16 + t;
         float hsum = 0.0f;
-        for (int q = 0; q < k; ++q) {
-            const float p = ys[q * 16 + t] * wts[(int64_t)s * k + q];
-            hsum = hsum + p;
+#pragma unroll
+        for (int q = 0; q < KW; ++q) {
+            const float p = ys[min(q, k - 1) * 16 + t] * wk[q];
+            hsum = q < k ? hsum + p : hsum;
         }
-        const float v = x[(int64_t)s * H + i] + hsum;
+        const float v = xr + hsum;
         out[(int64_t)s * H + i] = v;
         xs[t] = v;
     }
