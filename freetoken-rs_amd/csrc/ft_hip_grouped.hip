@@ -290,6 +290,7 @@ __global__ __launch_bounds__(GT, 2) void k_grouped_gu(const uint8_t* bank, int64
         for (int i = 0; i < BPW; ++i) sc[i] = *reinterpret_cast<const uint16_t*>(T + (b0 + i) * 128 + r * 2);
     }
     __shared__ int ctok[NT];
+    __shared__ float cscl[NT];  // the tokens' input-norm scales, loaded with the chunk's staging
     for (int c0 = 0; c0 < n; c0 += NT) {
         const int nt = min(NT, n - c0);
         __syncthreads();  // the previous chunk's LDS is consumed
@@ -313,6 +314,8 @@ __global__ __launch_bounds__(GT, 2) void k_grouped_gu(const uint8_t* bank, int64
                     v[tt][m] = (tt < nt && wi < W) ? src[wi] : 0u;
                 }
             }
+            const float sct = in_scale && t < nt ? in_scale[ctok[t]] : 1.0f;  // with the row loads
+            if (t < NT) cscl[t] = sct;
 #pragma unroll
             for (int tt = 0; tt < NT; ++tt) {
 #pragma unroll
@@ -356,7 +359,7 @@ __global__ __launch_bounds__(GT, 2) void k_grouped_gu(const uint8_t* bank, int64
             float sv = 0.0f;
 #pragma unroll
             for (int v = 0; v < GW; ++v) sv = sv + red[(v * NT + tt) * 64 + rr];
-            if (in_scale) sv = sv * in_scale[lst[c0 + tt] / K];
+            if (in_scale) sv = sv * cscl[tt];
             rows[tt * 64 + rr] = sv;
             if (dbg_gu) {
                 const int p = lst[c0 + tt];
