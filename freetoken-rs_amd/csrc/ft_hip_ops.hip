@@ -988,6 +988,7 @@ __global__ __launch_bounds__(256) void k_route_prep_n(const float* W, const floa
     const int nch = dim >> 4;
     const float* xs = x + (int64_t)s * dim;
     const float* w0 = W + (int64_t)eg * EG * dim;
+    const float bv = bias && l < EG ? bias[eg * EG + l] : 0.0f;  // the logit's bias, loaded with the chunks
     for (int c = l; c < nch; c += blockDim.x) {
         const float4* x4 = reinterpret_cast<const float4*>(xs + 16 * c);
         float4 xv[4], wv[EG][4];
@@ -1048,7 +1049,7 @@ __global__ __launch_bounds__(256) void k_route_prep_n(const float* W, const floa
         const int e = eg * EG + l;
         float t = tot[l];
         if (norm) t = t * ir;
-        if (bias) t = t + bias[e];
+        if (bias) t = t + bv;
         y[(int64_t)s * n_rows + e] = t;
         if (norm && e == 0) inv[s] = ir;
     }
@@ -1072,6 +1073,7 @@ __global__ __launch_bounds__(256) void k_route_prep_m(const float* W, const floa
     const int eg = blockIdx.x, s0 = blockIdx.y * SQ, l = threadIdx.x;
     const int nch = dim >> 4, ps = nch + 1;  // odd row stride: the group sums' lanes read different banks
     const float* w0 = W + (int64_t)eg * EG * dim;
+    const float bv = bias && l < SQ * EG ? bias[eg * EG + l % EG] : 0.0f;  // loaded with the chunks
     for (int c = l; c < nch; c += blockDim.x) {
         // every load of the chunk issued before the first fma (one load
         // latency), then the chains: each (logit, seq) partial and each seq's
@@ -1140,7 +1142,7 @@ __global__ __launch_bounds__(256) void k_route_prep_m(const float* W, const floa
         const int e = eg * EG + jj, s = s0 + q;
         float t = tot[q * (EG + 1) + jj];
         if (norm) t = t * ir;
-        if (bias) t = t + bias[e];
+        if (bias) t = t + bv;
         y[(int64_t)s * n_rows + e] = t;
         if (norm && e == 0) inv[s] = ir;
     }
