@@ -200,8 +200,10 @@ def bench_dense(args, g):
     GEMV time of one decoded token. The shared MLP is also timed as the chain
     a step runs (its input q8 and GELU*up included): the reference's four
     launches and this library's three with the gate|up launch applying
-    GELU*up and the q8 (config.shared_mlp_chain_us; the token with the faster
-    chain: config.us_per_token_with_shared_chain)."""
+    GELU*up and the q8, and two (ft_hip_gemv_q4r_f32in: the gate|up GEMV with
+    the q8 of x in its launch and GELU*up as its f32 second output, the down
+    GEMV with the q8 of that in its launch) (config.shared_mlp_chain_us; the
+    token with the fastest chain: config.us_per_token_with_shared_chain)."""
     import numpy as np
     import torch
     import ft_hip
@@ -250,7 +252,8 @@ def bench_dense(args, g):
         torch.cuda.empty_cache()
     # the shared MLP as the chain a decode step runs, from the f32 (normed) input: the reference's
     # four launches (quantize_q8, gate|up GEMV, gelu_mul_q8, down GEMV; ft-model/src/lib.rs:
-    # 1368-1395) and this library's three (quantize_q8, gemv_gate_up_act, down GEMV), each over
+    # 1368-1395), this library's three (quantize_q8, gemv_gate_up_act, down GEMV) and two
+    # (gemv_q4r_f32in for gate|up from x with GELU*up out, then for down from that), each over
     # rotating weight copies, `args.steps` chains per graph
     (gu_rows, H), (_, I) = moe_synth.DENSE["shared_gate_up"], moe_synth.DENSE["shared_down"]
     gb, db = gu_rows * ft_hip.row_bytes(H, ft_hip.LAYOUT_Q4R), H * ft_hip.row_bytes(I, ft_hip.LAYOUT_Q4R)
@@ -262,12 +265,17 @@ def bench_dense(args, g):
     ygu = torch.zeros(gu_rows, dtype=torch.float32, device=dev)
     q8a = torch.zeros(I // 32 * 40, dtype=torch.uint8, device=dev)
     ys = torch.zeros(H, dtype=torch.float32, device=dev)
+    actf = torch.zeros(I, dtype=torch.float32, device=dev)
     slots = torch.zeros(1, dtype=torch.int32, device=dev)
     chains = {}
-    for cname in ("reference_4_launches", "fused_3_launches"):
+    for cname in ("reference_4_launches", "fused_3_launches", "f32in_2_launches"):
         def chain(n, cname=cname):
             for i in range(n):
                 wg, wd = Wg[(i % gc) * gb:(i % gc + 1) * gb], Wd[(i % dc) * db:(i % dc + 1) * db]
+                if cname == "f32in_2_launches":
+                    g.gemv_q4r_f32in(wg, xs, ygu, actf, gu_rows, H, stream=stream)
+                    g.gemv_q4r_f32in(wd, actf, ys, None, H, I, stream=stream)
+                    continue
                 g.quantize_q8(xs, 0, q8x, H, 1, stream=stream)
                 if cname == "reference_4_launches":
                     g.gemv_grouped_slots(wg, 0, 0, slots, None, 1, q8x, 0, ygu, gu_rows, gu_rows, H, stream=stream)
@@ -316,7 +324,7 @@ def bench_dense(args, g):
     L = moe_synth.GEMMA.n_layers
     layer = ["qkv", "o_proj", "shared_gate_up", "shared_down"]
     tok_us = L * sum(per[n]["us"] for n in layer) + per["lm_head"]["us"]
-    # the same token with the shared MLP as the faster of the two chains (its input q8 and GELU*up
+    # the same token with the shared MLP as the fastest of the chains (its input q8 and GELU*up
     # included, which the GEMV-only figure above leaves out)
     tok_chain_us = L * (per["qkv"]["us"] + per["o_proj"]["us"] + min(chains.values())) + per["lm_head"]["us"]
     tok_bytes = L * sum(per[n]["bytes"] for n in layer) + per["lm_head"]["bytes"]

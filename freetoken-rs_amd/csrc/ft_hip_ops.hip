@@ -36,11 +36,14 @@ struct GemvArgs {
     int64_t y_stride;
     int n_rows;
     int k;
+    const float* xf;           // f32 input row of the short GEMV's XIN mode (k floats), quantized in the launch
+    float* act;                // gate|up launch of the short GEMV (ACT): gelu_tanh(gate) * up per column
 };
 
 __device__ __forceinline__ const uint8_t* entry_base(const GemvArgs& a, int e) {
+    // no slots: one dense matrix at base
     const uint8_t* p = a.bases ? reinterpret_cast<const uint8_t*>(a.bases[e])
-                               : a.base + (uint64_t)a.slots[e] * a.expert_bytes;
+                               : a.base + (a.slots ? (uint64_t)a.slots[e] * a.expert_bytes : 0);
     return p + a.bank_off;
 }
 
@@ -96,6 +99,29 @@ __device__ __forceinline__ void stage_words(const int* src, int n, int* lds) {
 __device__ __forceinline__ void stage_q8(const GemvArgs& a, int e, int* lds) {
     stage_words(reinterpret_cast<const int*>(a.q8 + (int64_t)entry_xrow(a, e) * a.q8_stride_blocks * Q8_BLK),
                 (a.k >> 5) * 10, lds);
+}
+
+// The q8 row of the f32 row x computed into LDS (nb blocks of 40 B, 4 lanes
+// per block, 8 values each; the loads of two rounds issued before their
+// arithmetic), with k_quantize_q8's arithmetic.
+__device__ __forceinline__ void stage_f32_q8(const float* x, int nb, int* lds) {
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    for (int base = 0; base < nb * 4; base += 2 * 256) {
+        float4 va[2], vb[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int i = base + h * 256 + (int)threadIdx.x, f = i < nb * 4 ? 2 * i : 0;
+            va[h] = x4[f];
+            vb[h] = x4[f + 1];
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int i = base + h * 256 + (int)threadIdx.x;
+            if (i < nb * 4)  // whole quads: nb * 4 and the strides are multiples of 4
+                quantize_block_quad_v(va[h], vb[h], i & 3, reinterpret_cast<uint32_t*>(lds + (i >> 2) * 10));
+        }
+    }
+    __syncthreads();
 }
 
 // Top-k of E <= 256 logits sv (LDS) in the router's order (larger first,
@@ -224,15 +250,22 @@ __global__ __launch_bounds__(256) void k_gemv_q4_grouped(GemvArgs a) {
 // the weight loads and the q8 staging share one latency. The lane's fma chain
 // runs in block order and the LPR lanes are summed by xor 1, 2, ..., LPR/2.
 // REC: every block's int32 dot is also stored to a.dots[e][row][block] (test
-// record). Grid (ceil(n_rows / (256/LPR)), n_entries).
-template <int LPR, int NBL, bool REC>
+// record). XIN: the q8 activation from the q8 row a.q8 (0, the reference's
+// gemv_q4r) or computed in the launch from the f32 row a.xf (1, its
+// quantize_q8 then gemv_q4r). ACT (a gate|up matrix, n_rows = 2I): a
+// workgroup takes RPW/2 gate rows c.. and the up rows I+c.. of the same
+// columns, and also stores a.act[c] = gelu_tanh(gate) * up (the f32 of its
+// gelu_mul_q8). Grid (ceil(n_rows / (256/LPR)), n_entries).
+template <int LPR, int NBL, bool REC, int XIN = 0, bool ACT = false>
 __global__ __launch_bounds__(256) void k_gemv_q4r_short(GemvArgs a) {
     extern __shared__ int lds[];
     constexpr int RPW = 256 / LPR;
     const int e = blockIdx.y;
     const int nb = a.k >> 5;
     const int qs_off = (nb * 2 + 15) / 16 * 16;
-    const int row = blockIdx.x * RPW + (int)threadIdx.x / LPR;
+    const int lr = (int)threadIdx.x / LPR, half = a.n_rows >> 1;
+    const int col = blockIdx.x * (RPW / 2) + lr % (RPW / 2);  // ACT: the row's column
+    const int row = ACT ? (col < half ? (lr < RPW / 2 ? col : half + col) : a.n_rows) : blockIdx.x * RPW + lr;
     const int sub = (int)threadIdx.x % LPR;
     const bool live = row < a.n_rows;
     const uint8_t* wr = entry_base(a, e) + (int64_t)(live ? row : 0) * row_bytes_of(FT_LAYOUT_Q4R, a.k);
@@ -248,7 +281,8 @@ __global__ __launch_bounds__(256) void k_gemv_q4r_short(GemvArgs a) {
             q[u] = make_uint4(0u, 0u, 0u, 0u);
         }
     }
-    stage_q8(a, e, lds);
+    if constexpr (XIN == 0) stage_q8(a, e, lds);
+    else stage_f32_q8(a.xf + (int64_t)entry_xrow(a, e) * a.k, nb, lds);
     float acc = 0.0f;
 #pragma unroll
     for (int u = 0; u < NBL; ++u) {
@@ -266,6 +300,14 @@ __global__ __launch_bounds__(256) void k_gemv_q4r_short(GemvArgs a) {
 #pragma unroll
     for (int m = 1; m < LPR; m <<= 1) acc += __shfl_xor(acc, m);
     if (live && sub == 0) a.y[(int64_t)e * a.y_stride + row] = acc;
+    if constexpr (ACT) {  // the rows' sums to the lanes of their columns
+        __shared__ float rs[RPW];
+        if (sub == 0) rs[lr] = acc;
+        __syncthreads();
+        const int c = blockIdx.x * (RPW / 2) + (int)threadIdx.x;
+        if ((int)threadIdx.x < RPW / 2 && c < half)
+            a.act[(int64_t)e * half + c] = gelu_tanh(rs[threadIdx.x]) * rs[RPW / 2 + threadIdx.x];
+    }
 }
 
 // The head of a layer taken from the previous layer's down launch
@@ -1457,17 +1499,23 @@ static void launch_gu_act(int layout, bool rec, dim3 grid, size_t lds, hipStream
                        wts, E, h);
 }
 
-template <int LPR, bool REC>
+template <int LPR, bool REC, int XIN = 0, bool ACT = false>
 static void launch_short_rec(int nbl, dim3 grid, size_t lds, hipStream_t s, const GemvArgs& a) {
-    if (nbl <= 2) hipLaunchKernelGGL((k_gemv_q4r_short<LPR, 2, REC>), grid, dim3(256), lds, s, a);
-    else if (nbl <= 4) hipLaunchKernelGGL((k_gemv_q4r_short<LPR, 4, REC>), grid, dim3(256), lds, s, a);
-    else hipLaunchKernelGGL((k_gemv_q4r_short<LPR, 8, REC>), grid, dim3(256), lds, s, a);
+    if (nbl <= 2) hipLaunchKernelGGL((k_gemv_q4r_short<LPR, 2, REC, XIN, ACT>), grid, dim3(256), lds, s, a);
+    else if (nbl <= 4) hipLaunchKernelGGL((k_gemv_q4r_short<LPR, 4, REC, XIN, ACT>), grid, dim3(256), lds, s, a);
+    else hipLaunchKernelGGL((k_gemv_q4r_short<LPR, 8, REC, XIN, ACT>), grid, dim3(256), lds, s, a);
+}
+
+template <int LPR, int XIN = 0, bool ACT = false>
+static void launch_short(bool rec, int nbl, dim3 grid, size_t lds, hipStream_t s, const GemvArgs& a) {
+    if (rec) launch_short_rec<LPR, true, XIN, ACT>(nbl, grid, lds, s, a);
+    else launch_short_rec<LPR, false, XIN, ACT>(nbl, grid, lds, s, a);
 }
 
 template <int LPR>
-static void launch_short(bool rec, int nbl, dim3 grid, size_t lds, hipStream_t s, const GemvArgs& a) {
-    if (rec) launch_short_rec<LPR, true>(nbl, grid, lds, s, a);
-    else launch_short_rec<LPR, false>(nbl, grid, lds, s, a);
+static void launch_short_f32in(bool rec, bool act, int nbl, dim3 grid, size_t lds, hipStream_t s, const GemvArgs& a) {
+    if (act) launch_short<LPR, 1, true>(rec, nbl, grid, lds, s, a);
+    else launch_short<LPR, 1, false>(rec, nbl, grid, lds, s, a);
 }
 
 static int gemv_common(ft_hip_ctx* ctx, void* stream, GemvArgs& a, int64_t n_entries, int64_t n_rows, int64_t k,
@@ -1551,6 +1599,47 @@ extern "C" int ft_hip_gemv_q4_grouped_slots(ft_hip_ctx* ctx, void* stream, const
     a.y = y;
     a.y_stride = y_stride;
     return gemv_common(ctx, stream, a, n_entries, n_rows, k, layout, false, "gemv_q4_grouped_slots");
+}
+
+extern "C" int ft_hip_gemv_q4r_f32in(ft_hip_ctx* ctx, void* stream, const void* w, const float* x, float* y,
+                                     float* act, int64_t n_rows, int64_t k) {
+    clear_error();
+    const char* nm = "gemv_q4r_f32in";
+    if (k <= 0 || k % 32 || k > 32 * 8 * 64)
+        return fail(FT_HIP_E_SHAPE, "%s: k=%lld must be a positive multiple of 32 up to 16384", nm, (long long)k);
+    if (n_rows < 0 || n_rows > (1 << 30)) return fail(FT_HIP_E_SHAPE, "%s: n_rows out of range", nm);
+    if (act && n_rows % 2) return fail(FT_HIP_E_SHAPE, "%s: a gate|up matrix (act given) has an even n_rows", nm);
+    if (!ctx || !w || !x || !y) return fail(FT_HIP_E_INVALID, "%s: null argument", nm);
+    if ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15)
+        return fail(FT_HIP_E_SHAPE, "%s: w and x must be 16-byte aligned", nm);
+    if (n_rows == 0) return FT_HIP_OK;
+    GemvArgs a{};
+    a.base = (const uint8_t*)w;  // no slots: the one matrix at base
+    a.x_div = 1;
+    a.xf = x;
+    a.y = y;
+    a.act = act;
+    a.y_stride = n_rows;
+    a.n_rows = (int)n_rows;
+    a.k = (int)k;
+    const bool rec = ctx->rec_gu != nullptr;  // the block-dot record (tests)
+    a.dots = ctx->rec_gu;
+    const int nb = (int)(k / 32);
+    // the lanes the q8-input GEMV takes for this shape (the same sums, bit for
+    // bit), or where that is the 8-lane kernel, the fewest that hold the row;
+    // with act (unless forced) 32 where the row fits: 8 rows, 4 columns per
+    // workgroup, so the GELU tail runs on half as many workgroups (Gemma's
+    // shared gate|up: 7.50 vs 8.16 us at 64 lanes)
+    int lpr = short_lanes(ctx, FT_LAYOUT_Q4R, n_rows, 1, nb);
+    if (act && !ctx->gemv_lanes && nb <= 8 * 32) lpr = 32;
+    if (!lpr) lpr = nb <= 8 * 16 ? 16 : (nb <= 8 * 32 ? 32 : 64);
+    const int nbl = (nb + lpr - 1) / lpr;
+    const dim3 grid((unsigned)((n_rows + 256 / lpr - 1) / (256 / lpr)), 1);
+    const size_t lds = (size_t)nb * Q8_BLK;
+    if (lpr == 16) launch_short_f32in<16>(rec, act != nullptr, nbl, grid, lds, S(stream), a);
+    else if (lpr == 32) launch_short_f32in<32>(rec, act != nullptr, nbl, grid, lds, S(stream), a);
+    else launch_short_f32in<64>(rec, act != nullptr, nbl, grid, lds, S(stream), a);
+    return launch_status(nm);
 }
 
 extern "C" int ft_hip_q4q8_block_dots(ft_hip_ctx* ctx, void* stream, const void* base, uint64_t expert_bytes,

@@ -52,6 +52,7 @@ extern "C" {
     pub fn ft_hip_reduce_expert_weighted(ctx: *mut FtHipCtx, stream: *mut c_void, y: *const f32, wts: *const f32, out: *mut f32, hidden: i64, n_experts: i64) -> c_int;
     pub fn ft_hip_reduce_weighted(ctx: *mut FtHipCtx, stream: *mut c_void, y: *const f32, out: *mut f32, a: f32, hidden: i64, n_experts: i64) -> c_int;
     pub fn ft_hip_gemv_gate_up_act(ctx: *mut FtHipCtx, stream: *mut c_void, base: *const c_void, expert_bytes: u64, slots: *const i32, n_pairs: i64, x_div: i64, q8x: *const c_void, hidden: i64, inter: i64, layout: c_int, in_scale: *const f32, q8_act: *mut c_void) -> c_int;
+    pub fn ft_hip_gemv_q4r_f32in(ctx: *mut FtHipCtx, stream: *mut c_void, w: *const c_void, x: *const f32, y: *mut f32, act: *mut f32, n_rows: i64, k: i64) -> c_int;
     pub fn ft_hip_router_logits(ctx: *mut FtHipCtx, stream: *mut c_void, w: *const f32, x: *const f32, bias: *const f32, y: *mut f32, dim: i64, n_rows: i64, n_seqs: i64) -> c_int;
     pub fn ft_hip_topk_router(ctx: *mut FtHipCtx, stream: *mut c_void, logits: *const f32, expert_scale: *const f32, ids: *mut i32, wts: *mut f32, e_count: i64, k: i64, n_seqs: i64) -> c_int;
     pub fn ft_hip_reduce_pairs_weighted(ctx: *mut FtHipCtx, stream: *mut c_void, y: *const f32, wts: *const f32, seq_of: *const i32, out: *mut f32, hidden: i64, n_pairs: i64, n_seqs: i64) -> c_int;

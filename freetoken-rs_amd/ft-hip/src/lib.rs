@@ -225,6 +225,20 @@ impl Q4Gemv {
         })
     }
 
+    /// Dense q4r GEMV from an f32 row, its q8 computed in the launch
+    /// (`quantize_q8` + `gemv_q4r_idx`); with `act`, a gate|up matrix whose
+    /// launch also stores gelu_tanh(gate) * up per column, the f32 of
+    /// `gelu_mul_q8` (ft-model/src/lib.rs:1368-1395).
+    #[allow(clippy::too_many_arguments)]
+    pub fn gemv_q4r_f32in(&self, s: Stream, w: DevPtr, x: DevPtr, y: DevPtr, act: Option<DevPtr>, n_rows: usize,
+                          k: usize) -> Result<()> {
+        let a: *mut f32 = match act {
+            Some(v) => pm(v),
+            None => std::ptr::null_mut(),
+        };
+        check(unsafe { ffi::ft_hip_gemv_q4r_f32in(self.ctx, s.0, p(w), p(x), pm(y), a, n_rows as i64, k as i64) })
+    }
+
     /// Gate|up GEMV with GELU*up and q8 in one launch (the `gemv_q4r_ptr` +
     /// `gelu_mul_q8` pair of ft-model/src/lib.rs:1584-1593).
     #[allow(clippy::too_many_arguments)]

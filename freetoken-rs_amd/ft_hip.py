@@ -44,6 +44,7 @@ SIGNATURES = {
     "ft_hip_reduce_expert_weighted": (_I, [_P, _P, _P, _P, _P, _I64, _I64]),
     "ft_hip_reduce_weighted": (_I, [_P, _P, _P, _P, ctypes.c_float, _I64, _I64]),
     "ft_hip_gemv_gate_up_act": (_I, [_P, _P, _P, _U64, _P, _I64, _I64, _P, _I64, _I64, _I, _P, _P]),
+    "ft_hip_gemv_q4r_f32in": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64]),
     "ft_hip_router_logits": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64]),
     "ft_hip_topk_router": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64]),
     "ft_hip_reduce_pairs_weighted": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64]),
@@ -229,6 +230,12 @@ class Q4Gemv:
                                            _ptr(out), n_rows, k, layout))
 
     # -- ft-cuda/src/lib.rs:354-374 --
+    def gemv_q4r_f32in(self, w, x, y, act, n_rows, k, stream=None):
+        """y = w . q8(x), the q8 of the f32 row x computed in the launch; act (or
+        None): for a gate|up matrix, also gelu_tanh(gate) * up per column."""
+        check(lib().ft_hip_gemv_q4r_f32in(self._ctx, _stream(stream), _ptr(w), _ptr(x), _ptr(y), _ptr(act), n_rows,
+                                          k))
+
     def gelu_mul_q8(self, gu, q8, inter, n, stream=None):
         check(lib().ft_hip_gelu_mul_q8(self._ctx, _stream(stream), _ptr(gu), _ptr(q8), inter, n))
 

@@ -165,6 +165,24 @@ int ft_hip_gemv_gate_up_act(ft_hip_ctx* ctx, void* stream, const void* base, uin
                             int64_t hidden, int64_t inter, int layout, const float* in_scale,
                             void* q8_act);
 
+/* A dense q4r GEMV from an f32 input row, its q8 computed in the same launch
+ * with the bits of ft_hip_quantize_q8; the shared MLP's chain (ft-model/src/
+ * lib.rs:1368-1395: quantize_q8, gemv_q4r gate|up, gelu_mul_q8, gemv_q4r
+ * down; ft-cuda/src/lib.rs:329-374, :736-767) then runs as two launches:
+ *   gate|up: x [k] -> y [2I] gate and up sums, act [I] f32 = gelu_tanh(gate)
+ *     * up, the f32 that gelu_mul_q8 quantizes (replaces quantize_q8 +
+ *     gemv_q4r_idx + the f32 half of gelu_mul_q8);
+ *   down: x = act, act NULL (replaces the q8 half of gelu_mul_q8 +
+ *     gemv_q4r_idx).
+ * y[r] = row r of w ([n_rows x k] q4r) against q8(x), with the sums of
+ * ft_hip_gemv_q4_grouped_slots (one entry, that q8) at the same lanes per
+ * row bit for bit: the lanes that GEMV takes, except with act (unless
+ * ft_hip_set_gemv_lanes forces them) 32 for rows up to 256 blocks. act:
+ * NULL, or for a gate|up matrix (n_rows = 2I, even) its [n_rows/2] outputs.
+ * w and x 16-byte aligned; k <= 16384. */
+int ft_hip_gemv_q4r_f32in(ft_hip_ctx* ctx, void* stream, const void* w, const float* x, float* y,
+                          float* act, int64_t n_rows, int64_t k);
+
 /* Replaces gemv_f32_rows_dev (ft-cuda/src/lib.rs:674-694): router logits
  * y[s][e] = sum_i W[e][i] * x[s][i] in this library's R-order (chunks of 16
  * elements by fma, 8 groups of dim/128 chunks, summed in order), plus bias[e]

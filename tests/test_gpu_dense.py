@@ -152,3 +152,101 @@ def test_shared_mlp_chain(gemv, orc):
     assert np.array_equal(host(dots).reshape(H, nb), orc.block_dots(raw, aq, I))
     ref = orc.gemv_q8(raw, H, ad, aq, I, threads=8)
     assert np.max(np.abs(host(y) - ref)) <= 1e-3 * np.linalg.norm(ref)
+
+
+def _q4r(gemv, rows, k, seed):
+    W = torch.empty(rows * ft_hip.row_bytes(k, ft_hip.LAYOUT_Q4R), dtype=torch.uint8, device=DEV)
+    gemv.gen_q4_rows(moe_synth.tensor_key(moe_synth.DENSE_CFG, seed, rows, k), 0, rows, k,
+                     moe_synth.gen_scale(0.02), W, ft_hip.LAYOUT_Q4R)
+    return W
+
+
+@pytest.mark.parametrize("lanes", [0, 16, 32, 64])
+@pytest.mark.parametrize("act", [False, True])
+@pytest.mark.parametrize("rows,k", [(4224, 2816), (2816, 2112), (8, 64), (34, 2048), (258, 4096)])
+def test_gemv_q4r_f32in(gemv, orc, rows, k, act, lanes):
+    """ft_hip_gemv_q4r_f32in: the q8 of the f32 row x computed in the launch. y
+    equals the reference's two calls (quantize_q8, then the GEMV at the same lane
+    count) bit for bit; the launch's own block dots (block-dot record) equal the
+    oracle's integer dots against the oracle's q8 of x; with act (the matrix as
+    gate|up rows), act equals the oracle's GELU*up of the launch's own sums, and
+    gelu_mul_q8 of those sums quantizes exactly what q8(act) gives."""
+    W = _q4r(gemv, rows, k, 50 + rows)
+    xin = np.random.default_rng(rows * 7 + k).standard_normal(k).astype(np.float32)
+    x = torch.from_numpy(xin).to(DEV)
+    q8 = q8_dev(gemv, x)
+    slots = torch.zeros(1, dtype=torch.int32, device=DEV)
+    y2 = torch.zeros(rows, dtype=torch.float32, device=DEV)
+    y1 = torch.full((rows,), float("nan"), dtype=torch.float32, device=DEV)
+    a1 = torch.full((rows // 2,), float("nan"), dtype=torch.float32, device=DEV) if act else None
+    nb = k // 32
+    rec = torch.full((rows * nb,), -(1 << 30), dtype=torch.int32, device=DEV)
+    unused = torch.zeros(1, dtype=torch.int32, device=DEV)
+    try:
+        # the same lanes per row: with act (automatic) 32 where the row fits
+        gemv.set_gemv_lanes(lanes or (32 if act and nb <= 256 else 0))
+        gemv.gemv_grouped_slots(W, 0, 0, slots, None, 1, q8, 0, y2, rows, rows, k)
+        gemv.set_gemv_lanes(lanes)
+        gemv.set_block_dot_record(rec, unused)
+        try:
+            gemv.gemv_q4r_f32in(W, x, y1, a1, rows, k)
+        finally:
+            gemv.set_block_dot_record(None, None)
+        y3 = torch.full_like(y1, float("nan"))
+        a3 = torch.full_like(a1, float("nan")) if act else None
+        gemv.gemv_q4r_f32in(W, x, y3, a3, rows, k)  # without the record: the same bits
+    finally:
+        gemv.set_gemv_lanes(0)
+    Y = host(y2)
+    assert np.array_equal(host(y1).view(np.uint32), Y.view(np.uint32))
+    assert np.array_equal(host(y3).view(np.uint32), Y.view(np.uint32))
+    _, qs8 = orc.q8_quantize(xin)
+    raw = q4r_to_q4_0(host(W), rows, k)
+    assert np.array_equal(host(rec).reshape(rows, nb), orc.block_dots(raw, qs8, k))
+    if act:
+        A = host(a1)
+        assert np.array_equal(host(a3).view(np.uint32), A.view(np.uint32))
+        if rows // 2 % 32 == 0:  # whole q8 blocks: the oracle's GELU*up (and its q8) of the launch's sums
+            ref_a, ad, aq = orc.gelu_mul_q8(Y, rows // 2)
+            assert np.array_equal(A.view(np.uint32), ref_a.view(np.uint32))
+            d8, q8a = orc.q8_quantize(A)
+            assert np.array_equal(d8.view(np.uint32), ad.view(np.uint32)) and np.array_equal(q8a, aq)
+
+
+def test_gemv_q4r_f32in_rejects(gemv):
+    W = _q4r(gemv, 4, 64, 1)
+    x = torch.zeros(128, dtype=torch.float32, device=DEV)
+    y = torch.zeros(4, dtype=torch.float32, device=DEV)
+    a = torch.zeros(2, dtype=torch.float32, device=DEV)
+    for args in [(W, x, y, None, 4, 48), (W, x, y, None, 4, 32 * 513), (W, x[1:], y, None, 4, 64),
+                 (W, x, y, None, -1, 64), (W, x, y, a, 3, 64), (W, x, None, None, 4, 64)]:
+        with pytest.raises(ft_hip.FtHipError):
+            gemv.gemv_q4r_f32in(*args)
+
+
+def test_shared_mlp_two_launches(gemv, orc):
+    """The shared MLP from its f32 input in two launches (gate|up from x with act,
+    down from act, each with its q8 in the launch) gives the bits of the
+    reference's four (quantize_q8, gate|up GEMV, gelu_mul_q8, down GEMV) with
+    the gate|up GEMV at the lanes per row of the launch with act."""
+    (gu_rows, H), (_, I) = moe_synth.DENSE["shared_gate_up"], moe_synth.DENSE["shared_down"]
+    Wgu = moe_synth.dense_weights(gemv, "shared_gate_up")
+    Wdn = moe_synth.dense_weights(gemv, "shared_down")
+    x = torch.from_numpy(np.random.default_rng(12).standard_normal(H).astype(np.float32)).to(DEV)
+    slots = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ygu, y4 = torch.zeros(gu_rows, dtype=torch.float32, device=DEV), torch.zeros(H, dtype=torch.float32, device=DEV)
+    q8a = torch.zeros(I // 32 * 40, dtype=torch.uint8, device=DEV)
+    gemv.set_gemv_lanes(32)  # the lanes per row the gate|up launch with act takes
+    try:
+        gemv.gemv_grouped_slots(Wgu, 0, 0, slots, None, 1, q8_dev(gemv, x), 0, ygu, gu_rows, gu_rows, H)
+    finally:
+        gemv.set_gemv_lanes(0)
+    gemv.gelu_mul_q8(ygu, q8a, I, 1)
+    gemv.gemv_grouped_slots(Wdn, 0, 0, slots, None, 1, q8a, 0, y4, H, H, I)
+    gu2, y2 = torch.zeros_like(ygu), torch.zeros_like(y4)
+    act = torch.zeros(I, dtype=torch.float32, device=DEV)
+    gemv.gemv_q4r_f32in(Wgu, x, gu2, act, gu_rows, H)
+    gemv.gemv_q4r_f32in(Wdn, act, y2, None, H, I)
+    assert np.array_equal(host(gu2).view(np.uint32), host(ygu).view(np.uint32))
+    assert np.array_equal(host(y2).view(np.uint32), host(y4).view(np.uint32))
+    assert np.all(np.isfinite(host(y2)))
