@@ -9,8 +9,12 @@ integer dots (ft-core/src/q4_0.rs:105-118); outputs within 1e-3 * ||y||_2
 and 1e-5 * sum|w*x| per row. The shared MLP runs gate|up -> GELU*up q8 ->
 down: the q8 activation bit-exact against the oracle's GELU*up q8 of the
 GPU's own gate|up sums, in two launches (gemv + gelu_mul_q8, as the reference)
-and in one (ft_hip_gemv_gate_up_act). lm_head is checked on a slice of its
-262,144 rows (the launch covers all of them).
+and in one (ft_hip_gemv_gate_up_act). The f32-input GEMV
+(ft_hip_gemv_q4r_f32in: the q8 of its f32 row computed in the launch, and on
+a gate|up matrix GELU*up as a second output) equals quantize_q8 + the GEMV bit
+for bit, and the shared MLP in its two launches equals the reference's four.
+lm_head is checked on a slice of its 262,144 rows (the launch covers all of
+them).
 """
 import numpy as np
 import pytest
