@@ -764,8 +764,8 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_moe_stack_fused(FusedParams P
     // broadcast read ~2 us behind its publication. Measured (us/token):
     // all 11 blocks early 396, 10: 392, 9: 383, 8: 374, 7: 381, 6: 383;
     // the down rows late as well: 387 (with 8 early; with 9, 10, 11 early:
-    // 383, 387, 388): issued after the broadcast, they sit in front of the
-    // act hand-over's polls instead.
+    // 383, 387, 388), half or a third of them late: 383 or 380: issued after
+    // the broadcast, they sit in front of the act hand-over's polls instead.
     constexpr int PF_EARLY = BPW > 3 ? BPW - 3 : BPW;
     constexpr int C = 2 * BPW;  // router chunks per group = H/128
     // words per thread of each wait (H = 256 * BPW, E <= 128, K <= 8):
