@@ -176,8 +176,10 @@ int ft_hip_gemv_gate_up_act(ft_hip_ctx* ctx, void* stream, const void* base, uin
  *     gemv_q4r_idx).
  * y[r] = row r of w ([n_rows x k] q4r) against q8(x), with the sums of
  * ft_hip_gemv_q4_grouped_slots (one entry, that q8) at the same lanes per
- * row bit for bit: the lanes that GEMV takes, except with act (unless
- * ft_hip_set_gemv_lanes forces them) 32 for rows up to 256 blocks. act:
+ * row bit for bit: the 16, 32 or 64 lanes that GEMV takes, except with act
+ * (unless ft_hip_set_gemv_lanes forces them) 32 for rows up to 256 blocks;
+ * where that GEMV takes 8 lanes (65,536 rows and more, or forced), 16, 32 or
+ * 64 by row length (sums within rounding of its). act:
  * NULL, or for a gate|up matrix (n_rows = 2I, even) its [n_rows/2] outputs.
  * w and x 16-byte aligned; k <= 16384. */
 int ft_hip_gemv_q4r_f32in(ft_hip_ctx* ctx, void* stream, const void* w, const float* x, float* y,
